@@ -1,0 +1,189 @@
+/*
+ * Streamed-MoE layer on MI355X (gfx950): C ABI of liblocali_amd.so.
+ *
+ * All pointers are device pointers unless stated otherwise; `stream` is a
+ * hipStream_t passed as void* (NULL = the default stream). Every entry point
+ * validates shapes on the host, launches asynchronously, never synchronises
+ * and never allocates; scratch memory comes from a caller-owned workspace
+ * whose size locali_moe_workspace_bytes() reports and which must be
+ * zero-filled once before first use (the library leaves its counters at zero
+ * after every call). Return value: 0 on success, a negative LOCALI_E_* code
+ * otherwise; locali_moe_last_error() describes the last failure on the
+ * calling thread.
+ *
+ * What each entry point replaces in the reference (MLX) implementation:
+ *   locali_moe_router          the gate call V4ArenaMoE.route -> MoEGate
+ *                              (dsv4_arena.py:165-166), Locali's own sigmoid
+ *                              router ArenaMoE.route (arena.py:501-506), and
+ *                              the expert -> slot lookup of ArenaMoE._apply
+ *                              (arena.py:558-567)
+ *   locali_moe_dispatch        the stable slot sort / segment of the mixed
+ *                              tier path (arena.py:641-659)
+ *   locali_moe_expert_decode   V4ArenaMoE._gather over a [T, k] slot grid
+ *                              (dsv4_arena.py:168-235: gather_qmm up/gate,
+ *                              clamped SwiGLU, gather_qmm down) fused with the
+ *                              weighted combine (arena.py:619-624) and the
+ *                              caller's shared-expert add (dsv4_engine.py:259)
+ *   locali_moe_expert_grouped  the same expert math with (token, k) entries
+ *                              grouped by slot (arena.py:641-672), one pass of
+ *                              each slot's weights per group, then combine
+ *   locali_moe_combine         sum_k y * w in the activation dtype
+ *                              (arena.py:623-624) or fp32 (arena.py:661-672)
+ *   locali_moe_arena_fill      the slot fill ArenaStore._read_into/_read_many
+ *                              (arena.py:179-200), as a host->HBM copy
+ *   locali_moe_forward         ArenaMoE.__call__ (arena.py:508-547) for an
+ *                              all-resident arena, plus the shared expert
+ */
+#ifndef LOCALI_MOE_H
+#define LOCALI_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    LOCALI_DT_F32 = 0,
+    LOCALI_DT_F16 = 1,
+    LOCALI_DT_BF16 = 2,
+};
+
+enum {
+    LOCALI_SCORE_SQRTSOFTPLUS = 0,
+    LOCALI_SCORE_SIGMOID = 1,
+    LOCALI_SCORE_SOFTMAX = 2,
+};
+
+enum {
+    LOCALI_COMBINE_ROUNDED = 0,   /* y*w rounded to the activation dtype */
+    LOCALI_COMBINE_FP32 = 1,      /* y*w and the sum kept in fp32 */
+};
+
+enum {
+    LOCALI_OK = 0,
+    LOCALI_E_ARG = -1,            /* invalid argument / unsupported shape */
+    LOCALI_E_WORKSPACE = -2,      /* workspace too small */
+    LOCALI_E_HIP = -4,            /* HIP runtime error */
+};
+
+/* One projection arena: every slot holds one expert's affine-quantised
+ * matrix in MLX layout (reference arena.py:150-160 per (tier, proj, kind)):
+ *   weight  uint32   [n_slots, rows, cols * bits / 32]  (LSB-first codes)
+ *   scales  dtype    [n_slots, rows, cols / group_size]
+ *   biases  dtype    [n_slots, rows, cols / group_size]
+ * rows = outputs, cols = inputs; dtype = meta_dtype (F16 or BF16), which must
+ * equal the activation dtype (the reference casts activations to fp16 for
+ * fp16 metadata, dsv4_arena.py:172-173). */
+typedef struct {
+    const void *weight;
+    const void *scales;
+    const void *biases;
+    int32_t bits;          /* 2, 4 or 8 */
+    int32_t group_size;    /* 32, 64 or 128 */
+    int32_t rows;
+    int32_t cols;
+    int32_t meta_dtype;    /* LOCALI_DT_F16 or LOCALI_DT_BF16 */
+    int32_t n_slots;
+} locali_qproj;
+
+/* gate/up: rows = d_ff, cols = d_model; down: rows = d_model, cols = d_ff. */
+typedef struct {
+    locali_qproj gate;
+    locali_qproj up;
+    locali_qproj down;
+} locali_expert_arena;
+
+/* Router description (the checkpoint gate's tensors,
+ * tf:modeling_deepseek_v4.py:1028-1033, 1062). */
+typedef struct {
+    const void *weight;            /* [n_experts, d_model] */
+    int32_t weight_dtype;          /* LOCALI_DT_* */
+    int32_t n_experts;             /* <= 512 */
+    int32_t top_k;                 /* 1..16 */
+    int32_t score_func;            /* LOCALI_SCORE_* */
+    int32_t norm_topk;             /* renormalise selected scores */
+    float routed_scale;            /* routed_scaling_factor */
+    const float *score_bias;       /* [n_experts] selection-only bias, or NULL */
+    const int32_t *tid2eid;        /* [vocab, top_k] hash routing table, or NULL */
+    int32_t vocab;
+} locali_router;
+
+/* Workspace bytes for up to `tokens` tokens. */
+size_t locali_moe_workspace_bytes(int32_t tokens, int32_t d_model, int32_t d_ff,
+                                  int32_t n_experts, int32_t top_k,
+                                  int32_t has_shared);
+
+/* Router: idx/weights [tokens, top_k] (int32 / fp32); route_slot (optional,
+ * int32 [tokens, top_k]) = slot_of_expert[idx] or -1. input_ids (int32
+ * [tokens]) is used only with a hash table. logits_in (optional fp32
+ * [tokens, n_experts]) skips the gate product. */
+int locali_moe_router(const locali_router *router, const void *x, int32_t x_dtype,
+                      int32_t tokens, int32_t d_model, const int32_t *input_ids,
+                      const float *logits_in, const int32_t *slot_of_expert,
+                      int32_t n_slots, int32_t *idx, float *weights,
+                      int32_t *route_slot, void *workspace, size_t workspace_bytes,
+                      void *stream);
+
+/* Stable sort of the tokens*top_k route entries by slot. sorted_route
+ * [tokens*top_k] holds route ids (t*top_k + j) grouped by ascending slot and
+ * token order inside a slot; seg_start [n_slots + 1] is the exclusive prefix
+ * count per slot. */
+int locali_moe_dispatch(const int32_t *route_slot, int32_t tokens, int32_t top_k,
+                        int32_t n_slots, int32_t *sorted_route, int32_t *seg_start,
+                        void *stream);
+
+/* Expert math over a [tokens, top_k] slot grid (+ one shared-expert route per
+ * token when `shared` is non-NULL, read from its slot 0), fused with the
+ * combine: out [tokens, d_model] in x_dtype. hidden: caller buffer of
+ * (tokens*top_k + tokens) * d_ff 16-bit elements (post-SwiGLU activations).
+ * Slots outside [0, n_slots) contribute zero. */
+int locali_moe_expert_decode(const locali_expert_arena *routed,
+                             const locali_expert_arena *shared, const void *x,
+                             int32_t x_dtype, int32_t tokens, int32_t top_k,
+                             const int32_t *route_slot, const float *weights,
+                             float swiglu_limit, int32_t fp32_swiglu,
+                             int32_t combine_mode, void *hidden, void *out,
+                             void *stream);
+
+/* Grouped form of locali_moe_expert_decode for many tokens: (token, k) entries
+ * are grouped by slot on the device and every slot's weights are streamed
+ * once per group; expert ids idx [tokens, top_k] and slot_of_expert [n_experts]
+ * give the slots. Scratch comes from the workspace. */
+int locali_moe_expert_grouped(const locali_expert_arena *routed,
+                              const locali_expert_arena *shared, const void *x,
+                              int32_t x_dtype, int32_t tokens, int32_t top_k,
+                              int32_t n_experts, const int32_t *idx,
+                              const int32_t *slot_of_expert, const float *weights,
+                              float swiglu_limit, int32_t fp32_swiglu,
+                              int32_t combine_mode, void *out, void *workspace,
+                              size_t workspace_bytes, void *stream);
+
+/* out[t] = round(sum_j round(y[t,j] * round(w[t,j]))) (ROUNDED) or the fp32
+ * form (FP32), plus round(out + shared_y[t]) when shared_y is non-NULL.
+ * y [tokens, top_k, d], shared_y [tokens, d], out [tokens, d] in dtype. */
+int locali_moe_combine(const void *y, const void *shared_y, const float *weights,
+                       int32_t dtype, int32_t tokens, int32_t top_k, int32_t d,
+                       int32_t combine_mode, void *out, void *stream);
+
+/* Asynchronous host -> device copy of `bytes` into an arena slot region
+ * (src should be pinned host memory for a truly asynchronous copy). */
+int locali_moe_arena_fill(void *dst, const void *src_host, size_t bytes, void *stream);
+
+/* Whole layer on an all-resident arena: router, dispatch (decode or grouped
+ * by token count), experts, combine, shared expert. out [tokens, d_model]. */
+int locali_moe_forward(const locali_router *router, const locali_expert_arena *routed,
+                       const locali_expert_arena *shared, const int32_t *slot_of_expert,
+                       const void *x, int32_t x_dtype, int32_t tokens,
+                       const int32_t *input_ids, float swiglu_limit,
+                       int32_t fp32_swiglu, void *out, int32_t *idx, float *weights,
+                       void *workspace, size_t workspace_bytes, void *stream);
+
+const char *locali_moe_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,414 @@
+// C ABI of liblocali_amd.so (include/locali_moe.h): host-side validation,
+// workspace carving and kernel launches. No allocation, no synchronisation.
+#include "locali_moe.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "grouped_kernels.hpp"
+#include "launch.hpp"
+
+using namespace locali;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *where) {
+    return fail(LOCALI_E_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+constexpr size_t kAlign = 256;
+constexpr int kMaxSlots = 16000;
+constexpr int kMaxExperts = 512;
+constexpr int kRouterSplitsHost = 4;
+constexpr int kDecodeMaxTokens = 2;   // above this the grouped path is used
+
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+bool dtype16(int32_t dt) { return dt == LOCALI_DT_F16 || dt == LOCALI_DT_BF16; }
+
+// Workspace layout for up to T tokens.
+struct Layout {
+    size_t counter, logits, route_slot, hidden, seg_start, sorted_route, route_pos, tiles, n_tiles,
+        gh, gy, total;
+    int max_tiles;
+};
+
+Layout layout(int T, int d, int dff, int E, int k, int has_shared) {
+    Layout L{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off = align_up(off + bytes);
+        return at;
+    };
+    const int R = T * k;
+    const int routes = R + (has_shared ? T : 0);
+    L.max_tiles = grouped_max_tiles(T, k, has_shared ? 1 : 0, E, kGroupedTileTokens);
+    L.counter = take(kAlign);
+    L.logits = take(sizeof(float) * kRouterSplitsHost * static_cast<size_t>(T) * E);
+    L.route_slot = take(sizeof(int32_t) * R);
+    L.hidden = take(sizeof(uint16_t) * static_cast<size_t>(routes) * dff);
+    L.seg_start = take(sizeof(int32_t) * (kMaxSlots + 1));
+    L.sorted_route = take(sizeof(int32_t) * R);
+    L.route_pos = take(sizeof(int32_t) * R);
+    L.tiles = take(sizeof(int32_t) * 4 * L.max_tiles);
+    L.n_tiles = take(sizeof(int32_t));
+    L.gh = take(sizeof(uint16_t) * static_cast<size_t>(routes) * dff);
+    L.gy = take(sizeof(uint16_t) * static_cast<size_t>(routes) * d);
+    L.total = off;
+    return L;
+}
+
+template <typename T>
+T *at(void *ws, size_t off) {
+    return reinterpret_cast<T *>(static_cast<char *>(ws) + off);
+}
+
+int check_proj(const locali_qproj &p, const char *name, int32_t x_dtype) {
+    if (!p.weight || !p.scales || !p.biases)
+        return fail(LOCALI_E_ARG, "%s: null array", name);
+    if (p.bits != 2 && p.bits != 4 && p.bits != 8)
+        return fail(LOCALI_E_ARG, "%s: bits %d not in {2,4,8}", name, p.bits);
+    if (p.group_size != 32 && p.group_size != 64 && p.group_size != 128)
+        return fail(LOCALI_E_ARG, "%s: group_size %d not in {32,64,128}", name, p.group_size);
+    if (p.rows <= 0 || p.cols <= 0 || p.cols % p.group_size)
+        return fail(LOCALI_E_ARG, "%s: rows %d / cols %d invalid for group %d", name, p.rows, p.cols,
+                    p.group_size);
+    if (p.n_slots < 1) return fail(LOCALI_E_ARG, "%s: n_slots %d", name, p.n_slots);
+    if (!dtype16(p.meta_dtype) || p.meta_dtype != x_dtype)
+        return fail(LOCALI_E_ARG, "%s: metadata dtype %d must equal activation dtype %d", name,
+                    p.meta_dtype, x_dtype);
+    const int64_t bits_row = static_cast<int64_t>(p.cols) * p.bits;
+    const int64_t cpr = bits_row / 128;
+    if (bits_row % 128 || !(cpr == 8 || cpr == 16 || cpr == 32 || cpr == 64 || cpr == 128 || cpr == 256))
+        return fail(LOCALI_E_ARG,
+                    "%s: cols*bits/128 = %lld 16-byte chunks per row unsupported "
+                    "(need 8, 16, 32, 64, 128 or 256)",
+                    name, static_cast<long long>(cpr));
+    const int vpc = 128 / p.bits;
+    if (p.group_size < vpc && !(p.bits == 2 && p.group_size == 32))
+        return fail(LOCALI_E_ARG, "%s: group %d smaller than a 16-byte chunk", name, p.group_size);
+    return 0;
+}
+
+QProj to_dev(const locali_qproj &p) {
+    QProj q;
+    q.w = static_cast<const uint32_t *>(p.weight);
+    q.s = static_cast<const uint16_t *>(p.scales);
+    q.b = static_cast<const uint16_t *>(p.biases);
+    q.rows = p.rows;
+    q.cols = p.cols;
+    q.bits = p.bits;
+    q.group = p.group_size;
+    q.n_slots = p.n_slots;
+    q.w_slot = static_cast<int64_t>(p.rows) * p.cols * p.bits / 32;
+    q.m_slot = static_cast<int64_t>(p.rows) * p.cols / p.group_size;
+    return q;
+}
+
+bool same_quant(const locali_qproj &a, const locali_qproj &b) {
+    return a.bits == b.bits && a.group_size == b.group_size && a.rows == b.rows && a.cols == b.cols &&
+           a.meta_dtype == b.meta_dtype;
+}
+
+int check_arena(const locali_expert_arena *a, const char *name, int32_t x_dtype, int d, int *dff) {
+    if (!a) return fail(LOCALI_E_ARG, "%s: null arena", name);
+    int rc;
+    if ((rc = check_proj(a->gate, "gate", x_dtype)) || (rc = check_proj(a->up, "up", x_dtype)) ||
+        (rc = check_proj(a->down, "down", x_dtype)))
+        return rc;
+    if (!same_quant(a->gate, a->up))
+        return fail(LOCALI_E_ARG, "%s: gate and up projections must share shape and quantisation", name);
+    if (a->gate.cols != d || a->down.rows != d || a->down.cols != a->gate.rows)
+        return fail(LOCALI_E_ARG, "%s: shapes gate[%d,%d] down[%d,%d] inconsistent with d_model %d", name,
+                    a->gate.rows, a->gate.cols, a->down.rows, a->down.cols, d);
+    if (a->gate.n_slots != a->up.n_slots || a->gate.n_slots != a->down.n_slots)
+        return fail(LOCALI_E_ARG, "%s: projections disagree on n_slots", name);
+    *dff = a->gate.rows;
+    return 0;
+}
+
+int check_shared(const locali_expert_arena *routed, const locali_expert_arena *shared) {
+    if (!shared) return 0;
+    if (!same_quant(routed->gate, shared->gate) || !same_quant(routed->up, shared->up) ||
+        !same_quant(routed->down, shared->down))
+        return fail(LOCALI_E_ARG, "shared expert must use the routed experts' shapes and quantisation");
+    return 0;
+}
+
+hipStream_t S(void *stream) { return static_cast<hipStream_t>(stream); }
+
+int run_decode(const locali_expert_arena *routed, const locali_expert_arena *shared, const void *x,
+               int32_t x_dtype, int32_t tokens, int32_t top_k, const int32_t *route_slot,
+               const float *weights, float limit, int32_t fp32_swiglu, int32_t combine_mode,
+               void *hidden, void *out, hipStream_t st) {
+    DecodeLaunch L{};
+    L.ra.x = static_cast<const uint16_t *>(x);
+    L.ra.route_slot = route_slot;
+    L.ra.tokens = tokens;
+    L.ra.top_k = top_k;
+    L.ra.n_shared = shared ? 1 : 0;
+    L.routes = tokens * top_k + (shared ? tokens : 0);
+    L.bf16 = x_dtype == LOCALI_DT_BF16;
+    L.gate = to_dev(routed->gate);
+    L.up = to_dev(routed->up);
+    L.down = to_dev(routed->down);
+    const locali_expert_arena *sh = shared ? shared : routed;
+    L.sgate = to_dev(sh->gate);
+    L.sup = to_dev(sh->up);
+    L.sdown = to_dev(sh->down);
+    L.h = static_cast<uint16_t *>(hidden);
+    L.limit = limit;
+    L.fp32_swiglu = fp32_swiglu;
+    L.ca.weights = weights;
+    L.ca.out = static_cast<uint16_t *>(out);
+    L.ca.mode = combine_mode;
+    hipError_t e = launch_gateup_decode(L, st);
+    if (e != hipSuccess) return hip_fail(e, "gate/up decode launch");
+    e = launch_down_combine_decode(L, st);
+    if (e != hipSuccess) return hip_fail(e, "down/combine decode launch");
+    return 0;
+}
+
+int run_grouped(const locali_expert_arena *routed, const locali_expert_arena *shared, const void *x,
+                int32_t x_dtype, int32_t tokens, int32_t top_k, int32_t n_experts,
+                const int32_t *route_slot, const float *weights, float limit, int32_t fp32_swiglu,
+                int32_t combine_mode, void *out, void *ws, const Layout &lay, hipStream_t st) {
+    const int R = tokens * top_k;
+    const int n_slots = routed->gate.n_slots;
+    int32_t *seg_start = at<int32_t>(ws, lay.seg_start);
+    int32_t *sorted_route = at<int32_t>(ws, lay.sorted_route);
+    int32_t *route_pos = at<int32_t>(ws, lay.route_pos);
+    int32_t *tiles = at<int32_t>(ws, lay.tiles);
+    int32_t *n_tiles = at<int32_t>(ws, lay.n_tiles);
+    uint16_t *gh = at<uint16_t>(ws, lay.gh);
+    uint16_t *gy = at<uint16_t>(ws, lay.gy);
+    (void)n_experts;
+    hipError_t e = launch_dispatch(route_slot, R, n_slots, shared ? tokens : 0, kGroupedTileTokens,
+                                   seg_start, sorted_route, route_pos, tiles, n_tiles, lay.max_tiles, st);
+    if (e != hipSuccess) return hip_fail(e, "dispatch launch");
+    GroupedKernelLaunch G{};
+    G.ta.x = static_cast<const uint16_t *>(x);
+    G.ta.tiles = tiles;
+    G.ta.n_tiles = n_tiles;
+    G.ta.sorted_route = sorted_route;
+    G.ta.R = R;
+    G.ta.top_k = top_k;
+    G.bf16 = x_dtype == LOCALI_DT_BF16;
+    G.gate = to_dev(routed->gate);
+    G.up = to_dev(routed->up);
+    G.down = to_dev(routed->down);
+    const locali_expert_arena *sh = shared ? shared : routed;
+    G.sgate = to_dev(sh->gate);
+    G.sup = to_dev(sh->up);
+    G.sdown = to_dev(sh->down);
+    G.h = gh;
+    G.y = gy;
+    G.limit = limit;
+    G.fp32_swiglu = fp32_swiglu;
+    G.max_tiles = lay.max_tiles;
+    if ((e = launch_grouped_kernels(0, G, st)) != hipSuccess) return hip_fail(e, "grouped gate/up launch");
+    if ((e = launch_grouped_kernels(1, G, st)) != hipSuccess) return hip_fail(e, "grouped down launch");
+    const int d = routed->down.rows;
+    e = launch_combine(gy, route_pos, shared ? gy + static_cast<int64_t>(R) * d : nullptr, weights, tokens,
+                       top_k, d, combine_mode, x_dtype == LOCALI_DT_BF16, static_cast<uint16_t *>(out), st);
+    if (e != hipSuccess) return hip_fail(e, "combine launch");
+    return 0;
+}
+
+int check_router(const locali_router *r, int d) {
+    if (!r || !r->weight) return fail(LOCALI_E_ARG, "router: null");
+    if (r->n_experts < 1 || r->n_experts > kMaxExperts)
+        return fail(LOCALI_E_ARG, "router: n_experts %d not in [1, %d]", r->n_experts, kMaxExperts);
+    if (r->top_k < 1 || r->top_k > 16 || r->top_k > r->n_experts)
+        return fail(LOCALI_E_ARG, "router: top_k %d invalid", r->top_k);
+    if (r->weight_dtype != LOCALI_DT_F32 && !dtype16(r->weight_dtype))
+        return fail(LOCALI_E_ARG, "router: weight dtype %d", r->weight_dtype);
+    if (r->score_func < 0 || r->score_func > 2) return fail(LOCALI_E_ARG, "router: score_func %d", r->score_func);
+    if (d % 8) return fail(LOCALI_E_ARG, "router: d_model %d not a multiple of 8", d);
+    if (r->tid2eid && r->vocab < 1) return fail(LOCALI_E_ARG, "router: hash table without vocab");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *locali_moe_last_error(void) { return g_error.c_str(); }
+
+size_t locali_moe_workspace_bytes(int32_t tokens, int32_t d_model, int32_t d_ff, int32_t n_experts,
+                                  int32_t top_k, int32_t has_shared) {
+    if (tokens < 1 || d_model < 1 || d_ff < 1 || n_experts < 1 || top_k < 1) return 0;
+    return layout(tokens, d_model, d_ff, n_experts, top_k, has_shared).total;
+}
+
+int locali_moe_router(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens,
+                      int32_t d_model, const int32_t *input_ids, const float *logits_in,
+                      const int32_t *slot_of_expert, int32_t n_slots, int32_t *idx, float *weights,
+                      int32_t *route_slot, void *workspace, size_t workspace_bytes, void *stream) {
+    int rc;
+    if ((rc = check_router(router, d_model))) return rc;
+    if (tokens < 1 || !x || !dtype16(x_dtype) || !idx || !weights || !workspace)
+        return fail(LOCALI_E_ARG, "router: bad tokens/x/outputs/workspace");
+    if (router->tid2eid && !input_ids) return fail(LOCALI_E_ARG, "router: hash routing needs input_ids");
+    if (route_slot && (!slot_of_expert || n_slots < 1))
+        return fail(LOCALI_E_ARG, "router: route_slot needs slot_of_expert and n_slots");
+    const Layout lay = layout(tokens, d_model, 1, router->n_experts, router->top_k, 0);
+    if (workspace_bytes < lay.route_slot)
+        return fail(LOCALI_E_WORKSPACE, "router: workspace %zu < %zu bytes", workspace_bytes, lay.route_slot);
+    RouterLaunch L{};
+    L.x = static_cast<const uint16_t *>(x);
+    L.x_bf16 = x_dtype == LOCALI_DT_BF16;
+    L.gate_w = router->weight;
+    L.gate_dtype = router->weight_dtype;
+    L.bias = router->score_bias;
+    L.tid2eid = router->tid2eid;
+    L.input_ids = input_ids;
+    L.vocab = router->vocab;
+    L.tokens = tokens;
+    L.d = d_model;
+    L.E = router->n_experts;
+    L.top_k = router->top_k;
+    L.score_func = router->score_func;
+    L.norm_topk = router->norm_topk;
+    L.routed_scale = router->routed_scale;
+    L.slot_of_expert = slot_of_expert;
+    L.n_slots = n_slots;
+    L.idx = idx;
+    L.weights = weights;
+    L.route_slot = route_slot;
+    L.logits = at<float>(workspace, lay.logits);
+    L.counter = at<uint32_t>(workspace, lay.counter);
+    L.logits_in = logits_in;
+    hipError_t e = launch_router(L, S(stream));
+    if (e != hipSuccess) return hip_fail(e, "router launch");
+    return 0;
+}
+
+int locali_moe_dispatch(const int32_t *route_slot, int32_t tokens, int32_t top_k, int32_t n_slots,
+                        int32_t *sorted_route, int32_t *seg_start, void *stream) {
+    if (!route_slot || !sorted_route || !seg_start || tokens < 1 || top_k < 1 || n_slots < 1 ||
+        n_slots > kMaxSlots)
+        return fail(LOCALI_E_ARG, "dispatch: bad arguments");
+    // No tile list is produced for this entry point.
+    hipError_t e = launch_dispatch(route_slot, tokens * top_k, n_slots, 0, 1, seg_start, sorted_route,
+                                   nullptr, nullptr, nullptr, 0, S(stream));
+    if (e != hipSuccess) return hip_fail(e, "dispatch launch");
+    return 0;
+}
+
+int locali_moe_expert_decode(const locali_expert_arena *routed, const locali_expert_arena *shared,
+                             const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k,
+                             const int32_t *route_slot, const float *weights, float swiglu_limit,
+                             int32_t fp32_swiglu, int32_t combine_mode, void *hidden, void *out,
+                             void *stream) {
+    int rc, dff = 0;
+    if (!x || !dtype16(x_dtype) || tokens < 1 || top_k < 1 || !route_slot || !weights || !hidden || !out)
+        return fail(LOCALI_E_ARG, "expert_decode: bad arguments");
+    if (!routed) return fail(LOCALI_E_ARG, "expert_decode: null arena");
+    if ((rc = check_arena(routed, "routed", x_dtype, routed->gate.cols, &dff))) return rc;
+    if ((rc = check_shared(routed, shared))) return rc;
+    if (top_k + (shared ? 1 : 0) > 16) return fail(LOCALI_E_ARG, "expert_decode: top_k + shared > 16");
+    if (combine_mode != LOCALI_COMBINE_ROUNDED && combine_mode != LOCALI_COMBINE_FP32)
+        return fail(LOCALI_E_ARG, "expert_decode: combine_mode %d", combine_mode);
+    return run_decode(routed, shared, x, x_dtype, tokens, top_k, route_slot, weights, swiglu_limit,
+                      fp32_swiglu, combine_mode, hidden, out, S(stream));
+}
+
+int locali_moe_expert_grouped(const locali_expert_arena *routed, const locali_expert_arena *shared,
+                              const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k,
+                              int32_t n_experts, const int32_t *idx, const int32_t *slot_of_expert,
+                              const float *weights, float swiglu_limit, int32_t fp32_swiglu,
+                              int32_t combine_mode, void *out, void *workspace, size_t workspace_bytes,
+                              void *stream) {
+    int rc, dff = 0;
+    if (!x || !dtype16(x_dtype) || tokens < 1 || top_k < 1 || !idx || !slot_of_expert || !weights ||
+        !out || !workspace || n_experts < 1)
+        return fail(LOCALI_E_ARG, "expert_grouped: bad arguments");
+    if (!routed) return fail(LOCALI_E_ARG, "expert_grouped: null arena");
+    const int d = routed->gate.cols;
+    if ((rc = check_arena(routed, "routed", x_dtype, d, &dff))) return rc;
+    if ((rc = check_shared(routed, shared))) return rc;
+    if (routed->gate.n_slots > kMaxSlots) return fail(LOCALI_E_ARG, "expert_grouped: n_slots > %d", kMaxSlots);
+    const Layout lay = layout(tokens, d, dff, n_experts, top_k, shared ? 1 : 0);
+    if (workspace_bytes < lay.total)
+        return fail(LOCALI_E_WORKSPACE, "expert_grouped: workspace %zu < %zu bytes", workspace_bytes, lay.total);
+    int32_t *route_slot = at<int32_t>(workspace, lay.route_slot);
+    hipError_t e = launch_route_slots(idx, tokens * top_k, n_experts, slot_of_expert, routed->gate.n_slots,
+                                      route_slot, S(stream));
+    if (e != hipSuccess) return hip_fail(e, "route slot launch");
+    return run_grouped(routed, shared, x, x_dtype, tokens, top_k, n_experts, route_slot, weights,
+                       swiglu_limit, fp32_swiglu, combine_mode, out, workspace, lay, S(stream));
+}
+
+int locali_moe_combine(const void *y, const void *shared_y, const float *weights, int32_t dtype,
+                       int32_t tokens, int32_t top_k, int32_t d, int32_t combine_mode, void *out,
+                       void *stream) {
+    if (!y || !weights || !out || !dtype16(dtype) || tokens < 1 || top_k < 1 || d < 1)
+        return fail(LOCALI_E_ARG, "combine: bad arguments");
+    hipError_t e = launch_combine(static_cast<const uint16_t *>(y), nullptr,
+                                  static_cast<const uint16_t *>(shared_y), weights, tokens, top_k, d,
+                                  combine_mode, dtype == LOCALI_DT_BF16, static_cast<uint16_t *>(out),
+                                  S(stream));
+    if (e != hipSuccess) return hip_fail(e, "combine launch");
+    return 0;
+}
+
+int locali_moe_arena_fill(void *dst, const void *src_host, size_t bytes, void *stream) {
+    if (!dst || !src_host) return fail(LOCALI_E_ARG, "arena_fill: null pointer");
+    if (!bytes) return 0;
+    hipError_t e = hipMemcpyAsync(dst, src_host, bytes, hipMemcpyHostToDevice, S(stream));
+    if (e != hipSuccess) return hip_fail(e, "arena_fill");
+    return 0;
+}
+
+int locali_moe_forward(const locali_router *router, const locali_expert_arena *routed,
+                       const locali_expert_arena *shared, const int32_t *slot_of_expert, const void *x,
+                       int32_t x_dtype, int32_t tokens, const int32_t *input_ids, float swiglu_limit,
+                       int32_t fp32_swiglu, void *out, int32_t *idx, float *weights, void *workspace,
+                       size_t workspace_bytes, void *stream) {
+    int rc, dff = 0;
+    if (!routed || !x || !out || !idx || !weights || !workspace || !slot_of_expert || tokens < 1 ||
+        !dtype16(x_dtype))
+        return fail(LOCALI_E_ARG, "forward: bad arguments");
+    const int d = routed->gate.cols;
+    if ((rc = check_router(router, d))) return rc;
+    if ((rc = check_arena(routed, "routed", x_dtype, d, &dff))) return rc;
+    if ((rc = check_shared(routed, shared))) return rc;
+    const int k = router->top_k, E = router->n_experts;
+    if (k + (shared ? 1 : 0) > 16) return fail(LOCALI_E_ARG, "forward: top_k + shared > 16");
+    if (routed->gate.n_slots > kMaxSlots) return fail(LOCALI_E_ARG, "forward: n_slots > %d", kMaxSlots);
+    const Layout lay = layout(tokens, d, dff, E, k, shared ? 1 : 0);
+    if (workspace_bytes < lay.total)
+        return fail(LOCALI_E_WORKSPACE, "forward: workspace %zu < %zu bytes", workspace_bytes, lay.total);
+    int32_t *route_slot = at<int32_t>(workspace, lay.route_slot);
+    rc = locali_moe_router(router, x, x_dtype, tokens, d, input_ids, nullptr, slot_of_expert,
+                           routed->gate.n_slots, idx, weights, route_slot, workspace, workspace_bytes,
+                           stream);
+    if (rc) return rc;
+    if (tokens <= kDecodeMaxTokens)
+        return run_decode(routed, shared, x, x_dtype, tokens, k, route_slot, weights, swiglu_limit,
+                          fp32_swiglu, LOCALI_COMBINE_ROUNDED, at<void>(workspace, lay.hidden), out,
+                          S(stream));
+    return run_grouped(routed, shared, x, x_dtype, tokens, k, E, route_slot, weights, swiglu_limit,
+                       fp32_swiglu, LOCALI_COMBINE_ROUNDED, out, workspace, lay, S(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,233 @@
+// Shared device helpers for the streamed-MoE kernels (gfx950 / CDNA4, wave64).
+//
+// 16-bit activations and affine metadata travel as raw uint16 bit patterns;
+// the template flag BF16 selects bfloat16 (true) or IEEE half (false).
+//
+// Affine weights use the MLX layout (value j of a row in word j*bits/32, LSB
+// first; reference dsv4_kernels.py:26-29, 59-73). A lane streams 16-byte
+// chunks of a row. Each 32-bit word is turned into packed 16-bit pairs by one
+// v_and_or_b32 against a "magic" exponent (bf16 128.0 = 0x4300 or fp16
+// 1024.0 = 0x6400) whose mantissa ulp is 1: a 2- or 4-bit field OR-ed into the
+// low mantissa bits reads as magic + field. A field sitting 2j bits up reads
+// as magic + 4^j q, so several fields are taken per shift and the matching
+// activations are pre-scaled by 4^-j (exact in 16-bit floats). One v_dot2
+// then accumulates x'.(magic + 4^j q) into fp32, and the per-group constant
+// magic * sum(x') is subtracted once per group:
+//     sum_k x_k q_k = D - magic * sum_k x'_k
+// which is the factorised affine dot of dsv4_kernels.py:75-79
+//     scale * sum(x q) + bias * sum(x).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace locali {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_float(uint16_t u) {
+    return __uint_as_float(static_cast<uint32_t>(u) << 16);
+}
+
+__device__ __forceinline__ uint16_t float_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_float(uint16_t u) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, u));
+}
+
+__device__ __forceinline__ uint16_t float_to_f16(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <bool BF16>
+__device__ __forceinline__ float to_float(uint16_t u) {
+    if constexpr (BF16) return bf16_to_float(u);
+    else return f16_to_float(u);
+}
+
+template <bool BF16>
+__device__ __forceinline__ uint16_t from_float(float f) {
+    if constexpr (BF16) return float_to_bf16(f);
+    else return float_to_f16(f);
+}
+
+template <bool BF16>
+__device__ __forceinline__ float round16(float f) {
+    return to_float<BF16>(from_float<BF16>(f));
+}
+
+// fp32 += dot(a.lo*b.lo + a.hi*b.hi) over packed 16-bit pairs.
+template <bool BF16>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    if constexpr (BF16)
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                               __builtin_bit_cast(bf16x2_t, b), c, false);
+    else
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a),
+                                      __builtin_bit_cast(f16x2_t, b), c, false);
+}
+
+// ---------------------------------------------------------------------------
+// Per-word pair tables.
+//
+// For each pair p of a 32-bit word: shift applied to the word, the mask that
+// selects one field in each 16-bit half, the values (index within the word)
+// the two fields belong to, and log2 of the factor that turns the field into
+// the value's contribution (x' = x * 2^xexp). For 8-bit codes under bf16 the
+// byte is split into nibbles (hi nibble weight 16, xexp = +4).
+// ---------------------------------------------------------------------------
+struct PairSpec {
+    uint8_t shift;
+    uint32_t mask;
+    uint8_t lo_val, hi_val;
+    int8_t lo_xexp, hi_xexp;
+};
+
+template <int BITS, bool BF16> struct Pairs;
+
+// 2-bit, bf16 magic 128: fields 0,2,4 of the mantissa; shifts 0, 6, 12.
+template <> struct Pairs<2, true> {
+    static constexpr int kCount = 8;
+    static constexpr uint32_t kMagic = 0x43004300u;
+    static constexpr float kMagicValue = 128.0f;
+    static constexpr PairSpec kSpec[8] = {
+        {0, 0x00030003u, 0, 8, 0, 0},   {0, 0x000C000Cu, 1, 9, -2, -2},
+        {0, 0x00300030u, 2, 10, -4, -4}, {6, 0x00030003u, 3, 11, 0, 0},
+        {6, 0x000C000Cu, 4, 12, -2, -2}, {6, 0x00300030u, 5, 13, -4, -4},
+        {12, 0x00030003u, 6, 14, 0, 0}, {12, 0x000C000Cu, 7, 15, -2, -2}};
+};
+
+// 2-bit, fp16 magic 1024: fields 0,2,4,6,8; shifts 0, 10.
+template <> struct Pairs<2, false> {
+    static constexpr int kCount = 8;
+    static constexpr uint32_t kMagic = 0x64006400u;
+    static constexpr float kMagicValue = 1024.0f;
+    static constexpr PairSpec kSpec[8] = {
+        {0, 0x00030003u, 0, 8, 0, 0},    {0, 0x000C000Cu, 1, 9, -2, -2},
+        {0, 0x00300030u, 2, 10, -4, -4}, {0, 0x00C000C0u, 3, 11, -6, -6},
+        {0, 0x03000300u, 4, 12, -8, -8}, {10, 0x00030003u, 5, 13, 0, 0},
+        {10, 0x000C000Cu, 6, 14, -2, -2}, {10, 0x00300030u, 7, 15, -4, -4}};
+};
+
+// 4-bit, bf16 magic 128: only bits 0-3 fit; shifts 0, 4, 8, 12.
+template <> struct Pairs<4, true> {
+    static constexpr int kCount = 4;
+    static constexpr uint32_t kMagic = 0x43004300u;
+    static constexpr float kMagicValue = 128.0f;
+    static constexpr PairSpec kSpec[4] = {{0, 0x000F000Fu, 0, 4, 0, 0},
+                                          {4, 0x000F000Fu, 1, 5, 0, 0},
+                                          {8, 0x000F000Fu, 2, 6, 0, 0},
+                                          {12, 0x000F000Fu, 3, 7, 0, 0}};
+};
+
+// 4-bit, fp16 magic 1024: bits 0-3 and 4-7; shifts 0, 8.
+template <> struct Pairs<4, false> {
+    static constexpr int kCount = 4;
+    static constexpr uint32_t kMagic = 0x64006400u;
+    static constexpr float kMagicValue = 1024.0f;
+    static constexpr PairSpec kSpec[4] = {{0, 0x000F000Fu, 0, 4, 0, 0},
+                                          {0, 0x00F000F0u, 1, 5, -4, -4},
+                                          {8, 0x000F000Fu, 2, 6, 0, 0},
+                                          {8, 0x00F000F0u, 3, 7, -4, -4}};
+};
+
+// 8-bit, bf16: a byte does not fit the 7-bit mantissa, so each byte is two
+// nibble fields (the high nibble weighs 16). Values 0..3 of the word.
+template <> struct Pairs<8, true> {
+    static constexpr int kCount = 4;
+    static constexpr uint32_t kMagic = 0x43004300u;
+    static constexpr float kMagicValue = 128.0f;
+    static constexpr PairSpec kSpec[4] = {{0, 0x000F000Fu, 0, 2, 0, 0},
+                                          {4, 0x000F000Fu, 0, 2, 4, 4},
+                                          {8, 0x000F000Fu, 1, 3, 0, 0},
+                                          {12, 0x000F000Fu, 1, 3, 4, 4}};
+};
+
+// 8-bit, fp16 magic 1024: a whole byte fits; shifts 0, 8.
+template <> struct Pairs<8, false> {
+    static constexpr int kCount = 2;
+    static constexpr uint32_t kMagic = 0x64006400u;
+    static constexpr float kMagicValue = 1024.0f;
+    static constexpr PairSpec kSpec[2] = {{0, 0x00FF00FFu, 0, 2, 0, 0},
+                                          {8, 0x00FF00FFu, 1, 3, 0, 0}};
+};
+
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t magic) {
+    return (v & mask) | magic;   // single v_and_or_b32
+}
+
+// Dot of one packed word against its pre-scaled activation pairs.
+template <int BITS, bool BF16>
+__device__ __forceinline__ float word_dot(uint32_t w, const uint32_t *xp, float acc) {
+    using P = Pairs<BITS, BF16>;
+#pragma unroll
+    for (int p = 0; p < P::kCount; ++p) {
+        const uint32_t a = and_or(w >> P::kSpec[p].shift, P::kSpec[p].mask, P::kMagic);
+        acc = dot2<BF16>(a, xp[p], acc);
+    }
+    return acc;
+}
+
+// ---------------------------------------------------------------------------
+// Wave reductions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float shfl_xor(float v, int m) {
+    return __shfl_xor(v, m, 64);
+}
+
+// Transposed butterfly: NV partial sums per lane, summed over the LPR lanes of
+// a lane group (LPR a power of two, NV <= LPR, both powers of two). Afterwards
+// every lane of the group holds the total of value index
+//     (lane % LPR) / (LPR / NV)
+// in v[0]. Costs NV-1 + log2(LPR/NV) shuffles instead of NV*log2(LPR).
+template <int NV, int LPR>
+__device__ __forceinline__ void reduce_transposed(float (&v)[NV], int lane) {
+    int nv = NV;
+#pragma unroll
+    for (int m = LPR / 2; m >= 1; m >>= 1) {
+        if (nv > 1) {
+            const int half = nv >> 1;
+            const bool upper = (lane & m) != 0;
+#pragma unroll
+            for (int i = 0; i < NV / 2; ++i) {
+                if (i < half) {
+                    const float a = v[i], b = v[i + half];
+                    const float send = upper ? a : b;
+                    const float keep = upper ? b : a;
+                    v[i] = keep + shfl_xor(send, m);
+                }
+            }
+            nv = half;
+        } else {
+            v[0] += shfl_xor(v[0], m);
+        }
+    }
+}
+
+__device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + __expf(-g)); }
+
+// Clamped SwiGLU on projection outputs already rounded to the activation
+// dtype (reference dsv4_arena.py:225-234): up clipped to +-L, gate capped at
+// L (L <= 0 disables both), then silu(gate) * up either op by op in the
+// 16-bit dtype (sigmoid, gate*sigmoid and *up each rounded) or in fp32 with
+// one final rounding.
+template <bool BF16>
+__device__ __forceinline__ uint16_t swiglu16(float gate, float up, float limit, bool fp32_swiglu) {
+    if (limit > 0.0f) {
+        up = fminf(fmaxf(up, -limit), limit);
+        gate = fminf(gate, limit);
+    }
+    if (fp32_swiglu) return from_float<BF16>(gate * sigmoidf_(gate) * up);
+    const float sig = round16<BF16>(sigmoidf_(gate));
+    const float act = round16<BF16>(gate * sig);
+    return from_float<BF16>(act * up);
+}
+
+}  // namespace locali

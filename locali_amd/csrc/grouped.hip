@@ -1,0 +1,240 @@
+// Grouped expert path (prefill and batched decode): dispatch, tile list and
+// combine. The (token, k) route entries are sorted by arena slot, stably
+// (token order inside a slot) as the reference mixed-tier path does
+// (arena.py:641-659), so each slot's weights are streamed once per group of
+// tokens instead of once per route.
+//
+//   dispatch_count_kernel   one workgroup: per-slot counts, exclusive scan
+//                           (seg_start), per-slot tile counts and the tile
+//                           list (slot, first position, token count); the
+//                           shared expert, when present, is one more segment
+//                           holding every token, placed after the routed ones
+//   dispatch_place_kernel   one wave per slot: walks the routes 64 at a time
+//                           with a ballot and writes sorted_route / route_pos
+//                           in route order (stable)
+//   combine_kernel          out[t] = round(sum_j round(y[pos(t,j)] * w)) (+ shared)
+#include "grouped_kernels.hpp"
+
+namespace locali {
+
+constexpr int kDispatchThreads = 1024;
+constexpr int kMaxDispatchSlots = 16000;   // counts live in 64 KiB of LDS
+
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
+    const int32_t *__restrict__ route_slot, int R, int n_slots, int n_shared_tokens, int tile_tokens,
+    int32_t *__restrict__ seg_start, int32_t *__restrict__ tiles, int32_t *__restrict__ n_tiles,
+    int max_tiles) {
+    extern __shared__ int32_t cnt[];              // [n_slots + 1]
+    __shared__ int32_t wsum[kDispatchThreads / 64];
+    __shared__ int32_t carry;
+    const int tid = threadIdx.x;
+    for (int s = tid; s <= n_slots; s += blockDim.x) cnt[s] = 0;
+    __syncthreads();
+    for (int r = tid; r < R; r += blockDim.x) {
+        const int s = route_slot[r];
+        if (s >= 0 && s < n_slots) atomicAdd(&cnt[s], 1);
+    }
+    __syncthreads();
+    // Two exclusive scans over slots in chunks of blockDim.x: positions and tiles.
+    for (int pass = 0; pass < 2; ++pass) {
+        if (tid == 0) carry = 0;
+        __syncthreads();
+        for (int base = 0; base < n_slots; base += blockDim.x) {
+            const int s = base + tid;
+            const int c = s < n_slots ? cnt[s] : 0;
+            const int v = pass == 0 ? c : (c + tile_tokens - 1) / tile_tokens;
+            // inclusive wave scan
+            int x = v;
+            for (int m = 1; m < 64; m <<= 1) {
+                const int y = __shfl_up(x, m, 64);
+                if ((tid & 63) >= m) x += y;
+            }
+            if ((tid & 63) == 63) wsum[tid >> 6] = x;
+            __syncthreads();
+            if (tid < 64) {
+                int w = tid < (int)(blockDim.x >> 6) ? wsum[tid] : 0;
+                for (int m = 1; m < 64; m <<= 1) {
+                    const int y = __shfl_up(w, m, 64);
+                    if (tid >= m) w += y;
+                }
+                if (tid < (int)(blockDim.x >> 6)) wsum[tid] = w;
+            }
+            __syncthreads();
+            const int excl = carry + (tid >= 64 ? wsum[(tid >> 6) - 1] : 0) + x - v;
+            if (s < n_slots) {
+                if (pass == 0) {
+                    seg_start[s] = excl;
+                } else {
+                    int pos = seg_start[s];
+                    for (int q = 0; q < v; ++q) {
+                        const int tile = excl + q;
+                        if (tiles && tile < max_tiles) {
+                            const int first = pos + q * tile_tokens;
+                            tiles[4 * tile + 0] = s;
+                            tiles[4 * tile + 1] = first;
+                            tiles[4 * tile + 2] = min(tile_tokens, c - q * tile_tokens);
+                            tiles[4 * tile + 3] = 0;
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            if (tid == blockDim.x - 1) carry = excl + v;
+            __syncthreads();
+        }
+        if (pass == 0 && tid == 0) seg_start[n_slots] = carry;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        int nt = carry;
+        // shared expert: positions R .. R + n_shared_tokens, slot marker -2
+        for (int q = 0; q * tile_tokens < n_shared_tokens; ++q) {
+            if (tiles && nt < max_tiles) {
+                tiles[4 * nt + 0] = -2;
+                tiles[4 * nt + 1] = R + q * tile_tokens;
+                tiles[4 * nt + 2] = min(tile_tokens, n_shared_tokens - q * tile_tokens);
+                tiles[4 * nt + 3] = 0;
+            }
+            ++nt;
+        }
+        if (n_tiles) *n_tiles = min(nt, max_tiles);
+    }
+}
+
+__global__ __launch_bounds__(256) void dispatch_place_kernel(
+    const int32_t *__restrict__ route_slot, int R, int n_slots, const int32_t *__restrict__ seg_start,
+    int32_t *__restrict__ sorted_route, int32_t *__restrict__ route_pos) {
+    const int lane = threadIdx.x & 63;
+    const int s = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (s >= n_slots) return;
+    const int base = seg_start[s], end = seg_start[s + 1];
+    if (base == end) return;
+    int pos = base;
+    for (int r0 = 0; r0 < R && pos < end; r0 += 64) {
+        const int r = r0 + lane;
+        const bool mine = r < R && route_slot[r] == s;
+        const uint64_t m = __ballot(mine);
+        if (mine) {
+            const int p = pos + __popcll(m & ((1ull << lane) - 1ull));
+            sorted_route[p] = r;
+            if (route_pos) route_pos[r] = p;
+        }
+        pos += __popcll(m);
+    }
+}
+
+// Invalid slots (outside the arena) never get a position; mark them.
+__global__ void route_pos_init_kernel(const int32_t *__restrict__ route_slot, int R, int n_slots,
+                                      int32_t *__restrict__ route_pos) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < R) {
+        const int s = route_slot[r];
+        if (s < 0 || s >= n_slots) route_pos[r] = -1;
+    }
+}
+
+// expert id -> slot, fused with the route list.
+__global__ void route_slots_kernel(const int32_t *__restrict__ idx, int R, int E,
+                                   const int32_t *__restrict__ slot_of_expert, int n_slots,
+                                   int32_t *__restrict__ route_slot) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < R) {
+        const int e = idx[r];
+        int s = (e >= 0 && e < E) ? slot_of_expert[e] : -1;
+        if (s >= n_slots) s = -1;
+        route_slot[r] = s;
+    }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict__ y,
+                                                      const int32_t *__restrict__ route_pos,
+                                                      const uint16_t *__restrict__ shared_y,
+                                                      const float *__restrict__ weights, int tokens,
+                                                      int top_k, int d, int mode,
+                                                      uint16_t *__restrict__ out) {
+    const int t = blockIdx.y;
+    const int col = blockIdx.x * blockDim.x + threadIdx.x;
+    if (col >= d) return;
+    float acc = 0.f;
+    for (int j = 0; j < top_k; ++j) {
+        const int r = t * top_k + j;
+        const int p = route_pos ? route_pos[r] : r;
+        if (p < 0) continue;
+        const float w = round16<BF16>(weights[r]);
+        const float v = to_float<BF16>(y[static_cast<int64_t>(p) * d + col]);
+        acc += mode == 0 ? round16<BF16>(v * w) : v * w;
+    }
+    float o = round16<BF16>(acc);
+    if (shared_y) o = round16<BF16>(o + to_float<BF16>(shared_y[static_cast<int64_t>(t) * d + col]));
+    out[static_cast<int64_t>(t) * d + col] = from_float<BF16>(o);
+}
+
+// --------------------------------------------------------------------------
+hipError_t grouped_b2_bf16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
+hipError_t grouped_b2_f16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
+hipError_t grouped_b4_bf16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
+hipError_t grouped_b4_f16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
+hipError_t grouped_b8_bf16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
+hipError_t grouped_b8_f16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
+
+// which: 0 = gate/up + SwiGLU, 1 = down.
+hipError_t launch_grouped_kernels(int which, const GroupedKernelLaunch &L, hipStream_t st) {
+    const QProj &p = which == 0 ? L.gate : L.down;
+    const int gpc = group_parts(p), cpr = chunks_per_row(p);
+    switch (p.bits) {
+    case 2: return L.bf16 ? grouped_b2_bf16(which, gpc, cpr, L, st) : grouped_b2_f16(which, gpc, cpr, L, st);
+    case 4: return L.bf16 ? grouped_b4_bf16(which, gpc, cpr, L, st) : grouped_b4_f16(which, gpc, cpr, L, st);
+    case 8: return L.bf16 ? grouped_b8_bf16(which, gpc, cpr, L, st) : grouped_b8_f16(which, gpc, cpr, L, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+int grouped_max_tiles(int tokens, int top_k, int n_shared, int E, int tile_tokens) {
+    const int R = tokens * top_k;
+    const int distinct = R < E ? R : E;
+    return (R + tile_tokens - 1) / tile_tokens + distinct +
+           n_shared * ((tokens + tile_tokens - 1) / tile_tokens) + 1;
+}
+
+hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
+                           int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
+                           int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,
+                           hipStream_t st) {
+    if (n_slots < 1 || n_slots > kMaxDispatchSlots) return hipErrorInvalidValue;
+    const size_t lds = sizeof(int32_t) * (n_slots + 1);
+    hipLaunchKernelGGL(dispatch_count_kernel, dim3(1), dim3(kDispatchThreads), lds, st, route_slot, R,
+                       n_slots, n_shared_tokens, tile_tokens, seg_start, tiles, n_tiles, max_tiles);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (route_pos) {
+        hipLaunchKernelGGL(route_pos_init_kernel, dim3((R + 255) / 256), dim3(256), 0, st, route_slot,
+                           R, n_slots, route_pos);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(dispatch_place_kernel, dim3((n_slots + 3) / 4), dim3(256), 0, st, route_slot, R,
+                       n_slots, seg_start, sorted_route, route_pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_route_slots(const int32_t *idx, int R, int E, const int32_t *slot_of_expert,
+                              int n_slots, int32_t *route_slot, hipStream_t st) {
+    hipLaunchKernelGGL(route_slots_kernel, dim3((R + 255) / 256), dim3(256), 0, st, idx, R, E,
+                       slot_of_expert, n_slots, route_slot);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const uint16_t *y, const int32_t *route_pos, const uint16_t *shared_y,
+                          const float *weights, int tokens, int top_k, int d, int mode, bool bf16,
+                          uint16_t *out, hipStream_t st) {
+    dim3 grid((d + 255) / 256, tokens);
+    if (bf16)
+        hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, st, y, route_pos, shared_y, weights,
+                           tokens, top_k, d, mode, out);
+    else
+        hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(256), 0, st, y, route_pos, shared_y, weights,
+                           tokens, top_k, d, mode, out);
+    return hipGetLastError();
+}
+
+}  // namespace locali

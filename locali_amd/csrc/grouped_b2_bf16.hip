@@ -1,0 +1,12 @@
+// Grouped kernels instantiated for 2-bit codes with bf16 activations.
+#include "grouped_kernels.hpp"
+
+namespace locali {
+
+hipError_t grouped_b2_bf16(int which, int gpc, int cpr, const GroupedKernelLaunch &L,
+                           hipStream_t st) {
+    if (gpc == 2) return grouped_geometry<2, true, 2>(which, cpr, L, st);
+    return grouped_geometry<2, true, 1>(which, cpr, L, st);
+}
+
+}  // namespace locali

@@ -1,0 +1,258 @@
+// Grouped expert kernels on the VALU: a tile is (slot, first sorted position,
+// up to TT tokens). Every 32-bit weight word is expanded by v_and_or_b32 once
+// and fed to TT v_dot2 instructions, one per token of the tile, so a slot's
+// weights are streamed once per tile rather than once per route.
+//
+//   gateup_grouped_kernel  h[pos, n] = swiglu(gate, up) for the tile's tokens
+//   down_grouped_kernel    y[pos, d] = round(down(h[pos]))
+// Positions index the slot-sorted route order written by the dispatch; the
+// shared expert's tile (slot marker -2) covers positions R .. R + tokens.
+#pragma once
+
+#include "launch.hpp"
+#include "qgemv.hpp"
+
+namespace locali {
+
+struct TileArgs {
+    const uint16_t *x;            // [tokens, d]
+    const int32_t *tiles;         // [max_tiles, 4]
+    const int32_t *n_tiles;       // [1]
+    const int32_t *sorted_route;  // [R]
+    int32_t R, top_k;
+};
+
+__device__ __forceinline__ int tile_token(const TileArgs &ta, bool shared, int pos) {
+    return shared ? pos - ta.R : ta.sorted_route[pos] / ta.top_k;
+}
+
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int TT>
+__device__ __forceinline__ void row_partial_multi(const RowChunks<CPL> &rc,
+                                                  const XVec<BITS, BF16, CPL, GPC> (&xv)[TT],
+                                                  const uint16_t *__restrict__ srow,
+                                                  const uint16_t *__restrict__ brow, int group,
+                                                  int lane_in_row, float (&out)[TT]) {
+    using G = Geom<BITS, CPL, LPR, GPC>;
+    using P = Pairs<BITS, BF16>;
+#pragma unroll
+    for (int q = 0; q < TT; ++q) out[q] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const uint32_t words[4] = {rc.c[i][0], rc.c[i][1], rc.c[i][2], rc.c[i][3]};
+        const int k0 = (lane_in_row + LPR * i) * G::kVPC;
+#pragma unroll
+        for (int gp = 0; gp < GPC; ++gp) {
+            float d[TT];
+#pragma unroll
+            for (int q = 0; q < TT; ++q) d[q] = 0.f;
+#pragma unroll
+            for (int wd = gp * G::kWPG; wd < (gp + 1) * G::kWPG; ++wd) {
+#pragma unroll
+                for (int p = 0; p < P::kCount; ++p) {
+                    const uint32_t a = and_or(words[wd] >> P::kSpec[p].shift, P::kSpec[p].mask, P::kMagic);
+#pragma unroll
+                    for (int q = 0; q < TT; ++q) d[q] = dot2<BF16>(a, xv[q].xp[i][wd][p], d[q]);
+                }
+            }
+            const int g = (k0 + gp * G::kWPG * G::kVPW) / group;
+            const float sc = to_float<BF16>(srow[g]);
+            const float bi = to_float<BF16>(brow[g]);
+#pragma unroll
+            for (int q = 0; q < TT; ++q)
+                out[q] = fmaf(sc, d[q] - xv[q].corr[i][gp], fmaf(bi, xv[q].xs[i][gp], out[q]));
+        }
+    }
+}
+
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int TT>
+__global__ __launch_bounds__(256) void gateup_grouped_kernel(TileArgs ta, QProj gate, QProj up,
+                                                              QProj sgate, QProj sup,
+                                                              uint16_t *__restrict__ h, float limit,
+                                                              int fp32_swiglu) {
+    using G = Geom<BITS, CPL, LPR, GPC>;
+    constexpr int RPW = J * G::kRPL;
+    constexpr int NV = 2 * J * TT;
+    static_assert(NV <= LPR, "values per lane exceed lanes per row");
+    const int tile = blockIdx.y;
+    if (tile >= *ta.n_tiles) return;
+    const int slot = ta.tiles[4 * tile], first = ta.tiles[4 * tile + 1];
+    const int count = ta.tiles[4 * tile + 2];
+    const bool shared = slot == -2;
+    const QProj &pg = shared ? sgate : gate;
+    const QProj &pu = shared ? sup : up;
+    if (count <= 0 || (!shared && (slot < 0 || slot >= pg.n_slots || first < 0 ||
+                                   first + count > ta.R)))
+        return;
+    const int N = pg.rows, K = pg.cols;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane_in_row = lane % LPR, row_sub = lane / LPR;
+    const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * RPW;
+    if (row0 >= N) return;
+    const int sl = shared ? 0 : slot;
+
+    XVec<BITS, BF16, CPL, GPC> xv[TT];
+#pragma unroll
+    for (int q = 0; q < TT; ++q) {
+        const int tok = tile_token(ta, shared, first + min(q, count - 1));
+        load_xvec<BITS, BF16, CPL, LPR, GPC>(xv[q], ta.x + static_cast<int64_t>(tok) * K, lane_in_row);
+    }
+    const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+    const int gpr = K / pg.group;
+    const uint32_t *gw = pg.w + sl * pg.w_slot, *uw = pu.w + sl * pu.w_slot;
+    const uint16_t *gs = pg.s + sl * pg.m_slot, *gb = pg.b + sl * pg.m_slot;
+    const uint16_t *us = pu.s + sl * pu.m_slot, *ub = pu.b + sl * pu.m_slot;
+    RowChunks<CPL> wg[J], wu[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
+        load_row<BITS, CPL, LPR>(wg[j], gw + row * wpr, lane_in_row);
+        load_row<BITS, CPL, LPR>(wu[j], uw + row * wpr, lane_in_row);
+    }
+    float v[NV];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
+        float pgq[TT], puq[TT];
+        row_partial_multi<BITS, BF16, CPL, LPR, GPC, TT>(wg[j], xv, gs + row * gpr, gb + row * gpr,
+                                                         pg.group, lane_in_row, pgq);
+        row_partial_multi<BITS, BF16, CPL, LPR, GPC, TT>(wu[j], xv, us + row * gpr, ub + row * gpr,
+                                                         pu.group, lane_in_row, puq);
+#pragma unroll
+        for (int q = 0; q < TT; ++q) {
+            v[j * TT + q] = pgq[q];
+            v[J * TT + j * TT + q] = puq[q];
+        }
+    }
+    reduce_transposed<NV, LPR>(v, lane);
+    const float partner = shfl_xor(v[0], LPR / 2);
+    constexpr int span = LPR / NV;
+    const int vi = lane_in_row / span;
+    if (vi < J * TT && (lane_in_row % span) == 0) {
+        const int j = vi / TT, q = vi % TT;
+        const int row = row0 + j * G::kRPL + row_sub;
+        if (row < N && q < count)
+            h[static_cast<int64_t>(first + q) * N + row] =
+                swiglu16<BF16>(round16<BF16>(v[0]), round16<BF16>(partner), limit, fp32_swiglu != 0);
+    }
+}
+
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int TT>
+__global__ __launch_bounds__(256) void down_grouped_kernel(TileArgs ta, QProj down, QProj sdown,
+                                                            const uint16_t *__restrict__ h,
+                                                            uint16_t *__restrict__ y) {
+    using G = Geom<BITS, CPL, LPR, GPC>;
+    constexpr int RPW = J * G::kRPL;
+    constexpr int NV = J * TT;
+    static_assert(NV <= LPR, "values per lane exceed lanes per row");
+    const int tile = blockIdx.y;
+    if (tile >= *ta.n_tiles) return;
+    const int slot = ta.tiles[4 * tile], first = ta.tiles[4 * tile + 1];
+    const int count = ta.tiles[4 * tile + 2];
+    const bool shared = slot == -2;
+    const QProj &p = shared ? sdown : down;
+    if (count <= 0 || (!shared && (slot < 0 || slot >= p.n_slots || first < 0 ||
+                                   first + count > ta.R)))
+        return;
+    const int N = p.rows, K = p.cols;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane_in_row = lane % LPR, row_sub = lane / LPR;
+    const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * RPW;
+    if (row0 >= N) return;
+    const int sl = shared ? 0 : slot;
+
+    XVec<BITS, BF16, CPL, GPC> xv[TT];
+#pragma unroll
+    for (int q = 0; q < TT; ++q)
+        load_xvec<BITS, BF16, CPL, LPR, GPC>(
+            xv[q], h + static_cast<int64_t>(first + min(q, count - 1)) * K, lane_in_row);
+    const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+    const int gpr = K / p.group;
+    const uint32_t *w = p.w + sl * p.w_slot;
+    const uint16_t *s = p.s + sl * p.m_slot, *b = p.b + sl * p.m_slot;
+    RowChunks<CPL> rc[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
+        load_row<BITS, CPL, LPR>(rc[j], w + row * wpr, lane_in_row);
+    }
+    float v[NV];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
+        float pq[TT];
+        row_partial_multi<BITS, BF16, CPL, LPR, GPC, TT>(rc[j], xv, s + row * gpr, b + row * gpr,
+                                                         p.group, lane_in_row, pq);
+#pragma unroll
+        for (int q = 0; q < TT; ++q) v[j * TT + q] = pq[q];
+    }
+    reduce_transposed<NV, LPR>(v, lane);
+    constexpr int span = LPR / NV;
+    const int vi = lane_in_row / span;
+    if ((lane_in_row % span) == 0) {
+        const int j = vi / TT, q = vi % TT;
+        const int row = row0 + j * G::kRPL + row_sub;
+        if (row < N && q < count)
+            y[static_cast<int64_t>(first + q) * N + row] = from_float<BF16>(v[0]);
+    }
+}
+
+// --------------------------------------------------------------------------
+constexpr int kGroupedTileTokens = 4;
+
+struct GroupedKernelLaunch {
+    TileArgs ta;
+    bool bf16;
+    QProj gate, up, down, sgate, sup, sdown;
+    uint16_t *h, *y;
+    float limit;
+    int32_t fp32_swiglu;
+    int32_t max_tiles;
+};
+
+template <int BITS, bool BF16, int CPL, int LPR, int GPC>
+hipError_t launch_grouped_t(int which, const GroupedKernelLaunch &L, hipStream_t st) {
+    constexpr int TT = kGroupedTileTokens;
+    using G = Geom<BITS, CPL, LPR, GPC>;
+    constexpr int waves = 4;
+    if (which == 0) {
+        constexpr int J = (LPR >= 4 * TT) ? 2 : 1;
+        const int rpb = waves * J * G::kRPL;
+        dim3 grid((L.gate.rows + rpb - 1) / rpb, L.max_tiles);
+        hipLaunchKernelGGL((gateup_grouped_kernel<BITS, BF16, CPL, LPR, GPC, J, TT>), grid,
+                           dim3(64 * waves), 0, st, L.ta, L.gate, L.up, L.sgate, L.sup, L.h, L.limit,
+                           L.fp32_swiglu);
+    } else {
+        constexpr int J = (LPR >= 4 * TT) ? 4 : ((LPR >= 2 * TT) ? 2 : 1);
+        const int rpb = waves * J * G::kRPL;
+        dim3 grid((L.down.rows + rpb - 1) / rpb, L.max_tiles);
+        hipLaunchKernelGGL((down_grouped_kernel<BITS, BF16, CPL, LPR, GPC, J, TT>), grid,
+                           dim3(64 * waves), 0, st, L.ta, L.down, L.sdown, L.h, L.y);
+    }
+    return hipGetLastError();
+}
+
+template <int BITS, bool BF16, int GPC>
+hipError_t grouped_geometry(int which, int cpr, const GroupedKernelLaunch &L, hipStream_t st) {
+    switch (cpr) {
+    case 8: return launch_grouped_t<BITS, BF16, 1, 8, GPC>(which, L, st);
+    case 16: return launch_grouped_t<BITS, BF16, 1, 16, GPC>(which, L, st);
+    case 32: return launch_grouped_t<BITS, BF16, 1, 32, GPC>(which, L, st);
+    case 64: return launch_grouped_t<BITS, BF16, 1, 64, GPC>(which, L, st);
+    case 128: return launch_grouped_t<BITS, BF16, 2, 64, GPC>(which, L, st);
+    case 256: return launch_grouped_t<BITS, BF16, 4, 64, GPC>(which, L, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_grouped_kernels(int which, const GroupedKernelLaunch &L, hipStream_t st);
+hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
+                           int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
+                           int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,
+                           hipStream_t st);
+hipError_t launch_route_slots(const int32_t *idx, int R, int E, const int32_t *slot_of_expert,
+                              int n_slots, int32_t *route_slot, hipStream_t st);
+hipError_t launch_combine(const uint16_t *y, const int32_t *route_pos, const uint16_t *shared_y,
+                          const float *weights, int tokens, int top_k, int d, int mode, bool bf16,
+                          uint16_t *out, hipStream_t st);
+
+}  // namespace locali

@@ -1,0 +1,100 @@
+// Host-side launch descriptors shared between the C-ABI layer (api.cpp) and
+// the kernel translation units. Plain structs of device pointers and sizes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qgemv.hpp"
+
+namespace locali {
+
+// Routes of the decode path: r in [0, tokens*top_k) is (token r / top_k,
+// slot route_slot[r]); r in [tokens*top_k, +tokens) is the shared expert of
+// token r - tokens*top_k (slot 0 of the shared arena).
+struct RouteArgs {
+    const uint16_t *x;          // [tokens, d_model]
+    const int32_t *route_slot;  // [tokens * top_k]
+    int32_t tokens, top_k, n_shared;
+};
+
+struct CombineArgs {
+    const float *weights;       // [tokens, top_k] router weights (fp32)
+    uint16_t *out;              // [tokens, d_model]
+    int32_t mode;               // 0: products rounded (single tier), 1: fp32 products
+};
+
+// ---- decode path -----------------------------------------------------------
+struct DecodeLaunch {
+    RouteArgs ra;
+    int32_t routes;             // tokens * top_k + n_shared * tokens
+    bool bf16;
+    QProj gate, up, down;       // routed arena
+    QProj sgate, sup, sdown;    // shared expert (slot 0), or copies of routed
+    uint16_t *h;                // [routes, d_ff]
+    float limit;
+    int32_t fp32_swiglu;
+    CombineArgs ca;
+};
+
+hipError_t launch_gateup_decode(const DecodeLaunch &L, hipStream_t st);
+hipError_t launch_down_combine_decode(const DecodeLaunch &L, hipStream_t st);
+int chunks_per_row(const QProj &p);
+int group_parts(const QProj &p);
+
+// ---- router ------------------------------------------------------------------
+struct RouterLaunch {
+    const uint16_t *x;          // [tokens, d] activations (bf16/fp16 bits)
+    bool x_bf16;
+    const void *gate_w;         // [E, d]
+    int32_t gate_dtype;         // 0 fp32, 1 fp16, 2 bf16
+    const float *bias;          // [E] selection-only bias or null
+    const int32_t *tid2eid;     // [vocab, top_k] hash table or null
+    const int32_t *input_ids;   // [tokens] or null
+    int32_t vocab;
+    int32_t tokens, d, E, top_k;
+    int32_t score_func;         // 0 sqrtsoftplus, 1 sigmoid, 2 softmax
+    int32_t norm_topk;
+    float routed_scale;
+    const int32_t *slot_of_expert;  // [E] or null
+    int32_t n_slots;
+    int32_t *idx;               // [tokens, top_k]
+    float *weights;             // [tokens, top_k]
+    int32_t *route_slot;        // [tokens, top_k] or null
+    float *logits;              // workspace [tokens, E]
+    uint32_t *counter;          // workspace, zero between calls
+    const float *logits_in;     // optional precomputed logits [tokens, E]
+};
+
+hipError_t launch_router(const RouterLaunch &L, hipStream_t st);
+
+// ---- grouped (prefill) path --------------------------------------------------
+struct GroupedLaunch {
+    const uint16_t *x;          // [tokens, d]
+    bool bf16;
+    int32_t tokens, top_k, n_shared, E;
+    const int32_t *idx;         // [tokens, top_k] expert ids
+    const int32_t *slot_of_expert;  // [E]
+    QProj gate, up, down, sgate, sup, sdown;
+    float limit;
+    int32_t fp32_swiglu;
+    const float *weights;       // [tokens, top_k]
+    int32_t combine_mode;
+    uint16_t *out;              // [tokens, d]
+    // workspace
+    int32_t *seg_offset;        // [E + 2]   segment starts (+ shared), last = total
+    int32_t *seg_slot;          // [E + 1]
+    int32_t *sorted_route;      // [tokens * top_k + tokens]  route ids in segment order
+    int32_t *route_pos;         // [tokens * top_k + tokens]  inverse
+    int32_t *tiles;             // [max_tiles * 4] (segment, first, count, pad)
+    int32_t *n_tiles;           // [1]
+    uint16_t *h;                // [routes, d_ff] in sorted order
+    uint16_t *y;                // [routes, d]    in sorted order
+    int32_t max_tiles;
+    int32_t tile_tokens;
+};
+
+hipError_t launch_grouped(const GroupedLaunch &L, hipStream_t st);
+int grouped_max_tiles(int tokens, int top_k, int n_shared, int E, int tile_tokens);
+
+}  // namespace locali

@@ -1,0 +1,285 @@
+"""torch-facing wrappers over the liblocali_amd.so C ABI.
+
+Tensors must already live on the GPU; the wrappers pass raw device pointers
+and the current HIP stream, check shapes on the host, and raise on any error.
+PyTorch supplies device memory and streams only -- every byte of arithmetic
+runs in the library's HIP kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import (COMBINE_FP32, COMBINE_ROUNDED, DT_BF16, DT_F16, DT_F32, SCORE_SIGMOID,
+                   SCORE_SOFTMAX, SCORE_SQRTSOFTPLUS, check, lib)
+
+__all__ = [
+    "ProjArena", "ExpertArenaT", "RouterSpec", "Workspace", "router", "dispatch",
+    "expert_decode", "expert_grouped", "combine", "forward", "arena_fill",
+    "COMBINE_ROUNDED", "COMBINE_FP32",
+]
+
+DTYPES = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}
+SCORE_FUNCS = {"sqrtsoftplus": SCORE_SQRTSOFTPLUS, "sigmoid": SCORE_SIGMOID,
+               "softmax": SCORE_SOFTMAX}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("tensor must be on the GPU")
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return t.data_ptr()
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+@dataclass
+class ProjArena:
+    """One projection across all arena slots, in MLX affine layout:
+    weight uint32 [S, rows, cols*bits/32], scales/biases [S, rows, cols/group]."""
+    weight: torch.Tensor
+    scales: torch.Tensor
+    biases: torch.Tensor
+    bits: int
+    group_size: int
+
+    @property
+    def n_slots(self) -> int:
+        return int(self.weight.shape[0])
+
+    @property
+    def rows(self) -> int:
+        return int(self.weight.shape[1])
+
+    @property
+    def cols(self) -> int:
+        return int(self.weight.shape[2]) * 32 // self.bits
+
+    def struct(self) -> _lib.QProj:
+        w, s, b = self.weight, self.scales, self.biases
+        if w.dtype not in (torch.int32, torch.uint32):
+            raise TypeError("packed weights must be 32-bit")
+        if s.shape != b.shape or s.dtype != b.dtype:
+            raise ValueError("scales and biases must match")
+        if s.shape[:2] != w.shape[:2] or s.shape[2] * self.group_size != self.cols:
+            raise ValueError(f"metadata shape {tuple(s.shape)} does not fit weight {tuple(w.shape)}")
+        return _lib.QProj(_ptr(w), _ptr(s), _ptr(b), self.bits, self.group_size, self.rows,
+                          self.cols, _dt(s), self.n_slots)
+
+
+@dataclass
+class ExpertArenaT:
+    gate: ProjArena
+    up: ProjArena
+    down: ProjArena
+
+    def struct(self) -> _lib.ExpertArena:
+        return _lib.ExpertArena(self.gate.struct(), self.up.struct(), self.down.struct())
+
+    @property
+    def d_model(self) -> int:
+        return self.gate.cols
+
+    @property
+    def d_ff(self) -> int:
+        return self.gate.rows
+
+    @property
+    def n_slots(self) -> int:
+        return self.gate.n_slots
+
+
+@dataclass
+class RouterSpec:
+    """The gate's tensors (tf:modeling_deepseek_v4.py:1028-1033, 1062)."""
+    weight: torch.Tensor                      # [E, d]
+    top_k: int
+    score_func: str = "sqrtsoftplus"
+    norm_topk: bool = True
+    routed_scale: float = 1.0
+    score_bias: torch.Tensor | None = None    # [E] fp32
+    tid2eid: torch.Tensor | None = None       # [vocab, top_k] int32
+
+    def struct(self) -> _lib.Router:
+        E = int(self.weight.shape[0])
+        bias = self.score_bias
+        if bias is not None and (bias.dtype != torch.float32 or bias.numel() != E):
+            raise ValueError("score_bias must be fp32 [n_experts]")
+        t2e = self.tid2eid
+        if t2e is not None and (t2e.dtype != torch.int32 or t2e.dim() != 2 or t2e.shape[1] != self.top_k):
+            raise ValueError("tid2eid must be int32 [vocab, top_k]")
+        return _lib.Router(_ptr(self.weight), _dt(self.weight), E, self.top_k,
+                           SCORE_FUNCS[self.score_func], int(self.norm_topk),
+                           float(self.routed_scale), _ptr(bias), _ptr(t2e),
+                           int(t2e.shape[0]) if t2e is not None else 0)
+
+    @property
+    def n_experts(self) -> int:
+        return int(self.weight.shape[0])
+
+
+class Workspace:
+    """Zero-initialised device scratch, grown on demand (growth allocates, so
+    size it once up front for allocation-free steady state)."""
+
+    def __init__(self, device=None):
+        self.device = torch.device(device or "cuda")
+        self.buf = torch.zeros(0, dtype=torch.uint8, device=self.device)
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.buf.numel() < nbytes:
+            self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+        return self.buf
+
+    def reserve(self, tokens, d_model, d_ff, n_experts, top_k, has_shared) -> torch.Tensor:
+        return self.get(workspace_bytes(tokens, d_model, d_ff, n_experts, top_k, has_shared))
+
+
+def workspace_bytes(tokens, d_model, d_ff, n_experts, top_k, has_shared) -> int:
+    return int(lib().locali_moe_workspace_bytes(tokens, d_model, d_ff, n_experts, top_k,
+                                                int(bool(has_shared))))
+
+
+def _flat(x: torch.Tensor) -> torch.Tensor:
+    return x.reshape(-1, x.shape[-1]).contiguous()
+
+
+def router(spec: RouterSpec, x: torch.Tensor, ws: Workspace, *, input_ids=None, logits=None,
+           slot_of_expert=None, n_slots: int = 0):
+    """Returns (idx int32 [T,k], weights fp32 [T,k], route_slot int32 [T,k] | None)."""
+    x2 = _flat(x)
+    T, d = x2.shape
+    k = spec.top_k
+    idx = torch.empty(T, k, dtype=torch.int32, device=x.device)
+    w = torch.empty(T, k, dtype=torch.float32, device=x.device)
+    rs = torch.empty(T, k, dtype=torch.int32, device=x.device) if slot_of_expert is not None else None
+    buf = ws.reserve(T, d, 1, spec.n_experts, k, 0)
+    ids = None
+    if input_ids is not None:
+        ids = input_ids.reshape(-1).to(device=x.device, dtype=torch.int32).contiguous()
+    lg = logits.reshape(T, -1).contiguous() if logits is not None else None
+    if lg is not None and lg.dtype != torch.float32:
+        raise TypeError("logits must be fp32")
+    st = spec.struct()
+    rc = lib().locali_moe_router(ctypes.byref(st), _ptr(x2), _dt(x2), T, d, _ptr(ids), _ptr(lg),
+                                 _ptr(slot_of_expert), n_slots, _ptr(idx), _ptr(w), _ptr(rs),
+                                 _ptr(buf), buf.numel(), _stream())
+    check(rc, "locali_moe_router")
+    return idx, w, rs
+
+
+def dispatch(route_slot: torch.Tensor, n_slots: int):
+    """Stable slot sort: (sorted_route int32 [T*k], seg_start int32 [n_slots+1])."""
+    T, k = route_slot.shape
+    sorted_route = torch.empty(T * k, dtype=torch.int32, device=route_slot.device)
+    seg = torch.empty(n_slots + 1, dtype=torch.int32, device=route_slot.device)
+    rc = lib().locali_moe_dispatch(_ptr(route_slot.contiguous()), T, k, n_slots, _ptr(sorted_route),
+                                   _ptr(seg), _stream())
+    check(rc, "locali_moe_dispatch")
+    return sorted_route, seg
+
+
+def expert_decode(arena: ExpertArenaT, shared: ExpertArenaT | None, x: torch.Tensor,
+                  route_slot: torch.Tensor, weights: torch.Tensor, *, swiglu_limit=10.0,
+                  fp32_swiglu=False, combine_mode=COMBINE_ROUNDED, hidden=None):
+    x2 = _flat(x)
+    T = x2.shape[0]
+    k = route_slot.shape[-1]
+    routes = T * k + (T if shared is not None else 0)
+    if hidden is None:
+        hidden = torch.empty(routes, arena.d_ff, dtype=x2.dtype, device=x.device)
+    out = torch.empty_like(x2)
+    a = arena.struct()
+    s = shared.struct() if shared is not None else None
+    rc = lib().locali_moe_expert_decode(ctypes.byref(a), ctypes.byref(s) if s is not None else None,
+                                        _ptr(x2), _dt(x2), T, k, _ptr(route_slot.contiguous()),
+                                        _ptr(weights.contiguous()), float(swiglu_limit),
+                                        int(fp32_swiglu), int(combine_mode), _ptr(hidden), _ptr(out),
+                                        _stream())
+    check(rc, "locali_moe_expert_decode")
+    return out.reshape(x.shape)
+
+
+def expert_grouped(arena: ExpertArenaT, shared: ExpertArenaT | None, x: torch.Tensor,
+                   idx: torch.Tensor, slot_of_expert: torch.Tensor, weights: torch.Tensor,
+                   ws: Workspace, *, n_experts=None, swiglu_limit=10.0, fp32_swiglu=False,
+                   combine_mode=COMBINE_ROUNDED):
+    x2 = _flat(x)
+    T = x2.shape[0]
+    k = idx.shape[-1]
+    E = int(n_experts or slot_of_expert.numel())
+    buf = ws.reserve(T, arena.d_model, arena.d_ff, E, k, shared is not None)
+    out = torch.empty_like(x2)
+    a = arena.struct()
+    s = shared.struct() if shared is not None else None
+    rc = lib().locali_moe_expert_grouped(ctypes.byref(a), ctypes.byref(s) if s is not None else None,
+                                         _ptr(x2), _dt(x2), T, k, E, _ptr(idx.contiguous()),
+                                         _ptr(slot_of_expert), _ptr(weights.contiguous()),
+                                         float(swiglu_limit), int(fp32_swiglu), int(combine_mode),
+                                         _ptr(out), _ptr(buf), buf.numel(), _stream())
+    check(rc, "locali_moe_expert_grouped")
+    return out.reshape(x.shape)
+
+
+def combine(y: torch.Tensor, weights: torch.Tensor, shared_y=None, mode=COMBINE_ROUNDED):
+    T, k, d = y.shape
+    out = torch.empty(T, d, dtype=y.dtype, device=y.device)
+    rc = lib().locali_moe_combine(_ptr(y.contiguous()), _ptr(shared_y), _ptr(weights.contiguous()),
+                                  _dt(y), T, k, d, int(mode), _ptr(out), _stream())
+    check(rc, "locali_moe_combine")
+    return out
+
+
+def forward(spec: RouterSpec, arena: ExpertArenaT, shared: ExpertArenaT | None,
+            slot_of_expert: torch.Tensor, x: torch.Tensor, ws: Workspace, *, input_ids=None,
+            swiglu_limit=10.0, fp32_swiglu=False, out=None, idx=None, weights=None):
+    """Whole MoE layer (router, dispatch, experts, combine, shared) on an
+    all-resident arena. Returns (out, idx, weights)."""
+    x2 = _flat(x)
+    T, d = x2.shape
+    k = spec.top_k
+    buf = ws.reserve(T, d, arena.d_ff, spec.n_experts, k, shared is not None)
+    out = torch.empty_like(x2) if out is None else out
+    idx = torch.empty(T, k, dtype=torch.int32, device=x.device) if idx is None else idx
+    weights = torch.empty(T, k, dtype=torch.float32, device=x.device) if weights is None else weights
+    ids = None
+    if input_ids is not None:
+        ids = input_ids.reshape(-1).to(device=x.device, dtype=torch.int32).contiguous()
+    r = spec.struct()
+    a = arena.struct()
+    s = shared.struct() if shared is not None else None
+    rc = lib().locali_moe_forward(ctypes.byref(r), ctypes.byref(a),
+                                  ctypes.byref(s) if s is not None else None, _ptr(slot_of_expert),
+                                  _ptr(x2), _dt(x2), T, _ptr(ids), float(swiglu_limit),
+                                  int(fp32_swiglu), _ptr(out), _ptr(idx), _ptr(weights), _ptr(buf),
+                                  buf.numel(), _stream())
+    check(rc, "locali_moe_forward")
+    return out.reshape(x.shape), idx, weights
+
+
+def arena_fill(dst: torch.Tensor, src: torch.Tensor, stream=None) -> None:
+    """Asynchronous host -> HBM copy of src (pinned host tensor) into dst."""
+    if src.is_cuda or not dst.is_cuda:
+        raise ValueError("arena_fill copies a host tensor into a device tensor")
+    nbytes = src.numel() * src.element_size()
+    if nbytes != dst.numel() * dst.element_size():
+        raise ValueError("arena_fill size mismatch")
+    st = stream.cuda_stream if stream is not None else _stream()
+    rc = lib().locali_moe_arena_fill(_ptr(dst), ctypes.c_void_p(src.data_ptr()), nbytes, st)
+    check(rc, "locali_moe_arena_fill")

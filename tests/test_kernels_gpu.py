@@ -1,0 +1,291 @@
+"""GPU parity: the HIP kernels (through the liblocali_amd.so C ABI) against the
+CPU oracle on identical seeded inputs.
+
+Bars (north star): router indices bit-exact as sets wherever the oracle's
+selection margin exceeds the fp32 accumulation-order noise (1e-4); weights
+within 1e-5 relative; slot assignment exact; expert outputs within 1e-2
+relative / 2e-3 absolute of the oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import (arena_numpy, assert_close, banner, dt_name, exact_fraction, values)
+from locali_amd import ops, synth
+from oracle import moe
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _dev(arena):
+    return ops.ExpertArenaT(*(ops.ProjArena(p.weight.to(DEV), p.scales.to(DEV), p.biases.to(DEV),
+                                            p.bits, p.group_size)
+                              for p in (arena.gate, arena.up, arena.down)))
+
+
+def _oracle_layer(x, idx, wts, arena, slot_of, dtype, shared=None, limit=10.0, fp32_swiglu=False):
+    dt = dt_name(dtype)
+    sh = None
+    if shared is not None:
+        sh = {k: (v[0][0], v[1][0], v[2][0], v[3], v[4]) for k, v in arena_numpy(shared).items()}
+    return moe.moe_layer(values(x), idx, wts, arena_numpy(arena), slot_of, dt, limit=limit,
+                         fp32_swiglu=fp32_swiglu, shared=sh)
+
+
+# ---------------------------------------------------------------------------
+# Router
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("T", [1, 3, 40, 130])
+@pytest.mark.parametrize("score", ["sqrtsoftplus", "sigmoid", "softmax"])
+def test_router_matches_oracle(T, score):
+    banner(f"router T={T} score={score}")
+    E, d, k = 256, 1024, 6
+    w, bias = synth.uniform_router(E, d, torch.bfloat16, seed=T, bias_std=0.01)
+    x = synth.activations(T, d, torch.bfloat16, seed=T + 7)
+    slot_of = torch.randperm(E, generator=torch.Generator().manual_seed(5)).to(torch.int32) + 1
+    spec = ops.RouterSpec(w.to(DEV), k, score_func=score, routed_scale=1.5,
+                          score_bias=bias.to(DEV))
+    ws = ops.Workspace()
+    idx, wts, rs = ops.router(spec, x.to(DEV), ws, slot_of_expert=slot_of.to(DEV), n_slots=E + 1)
+    torch.cuda.synchronize()
+    oi, ow, margin, _ = moe.route(values(x), values(w), k, bias=values(bias), score_func=score,
+                                  routed_scale=1.5)
+    idx, wts, rs = idx.cpu().numpy(), wts.cpu().numpy(), rs.cpu().numpy()
+    checked = 0
+    for t in range(T):
+        if margin[t] < 1e-4:
+            continue
+        checked += 1
+        assert list(idx[t]) == list(oi[t]), f"token {t}"
+        np.testing.assert_allclose(wts[t], ow[t], rtol=1e-5, atol=1e-7)
+        assert list(rs[t]) == [int(slot_of[e]) for e in idx[t]]
+    assert checked >= 0.9 * T
+
+
+def test_router_hash_mode():
+    banner("router hash")
+    E, d, k, V, T = 64, 512, 6, 50, 20
+    w, _ = synth.uniform_router(E, d, torch.bfloat16, seed=3)
+    table = torch.stack([torch.randperm(E, generator=torch.Generator().manual_seed(i))[:k]
+                         for i in range(V)]).to(torch.int32)
+    ids = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(1))
+    x = synth.activations(T, d, torch.bfloat16, seed=4)
+    spec = ops.RouterSpec(w.to(DEV), k, routed_scale=1.5, tid2eid=table.to(DEV))
+    idx, wts, _ = ops.router(spec, x.to(DEV), ops.Workspace(), input_ids=ids.to(DEV))
+    oi, ow, _, _ = moe.route(values(x), values(w), k, routed_scale=1.5, tid2eid=table.numpy(),
+                             input_ids=ids.numpy())
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    np.testing.assert_allclose(wts.cpu().numpy(), ow, rtol=1e-5)
+
+
+def test_router_precomputed_logits_zipf():
+    banner("router logits_in zipf")
+    T, E, k = 64, 256, 6
+    logits = synth.zipf_logits(T, E, seed=2)
+    w = torch.zeros(E, 256, dtype=torch.bfloat16)
+    spec = ops.RouterSpec(w.to(DEV), k, routed_scale=1.5)
+    idx, wts, _ = ops.router(spec, torch.zeros(T, 256, dtype=torch.bfloat16, device=DEV),
+                             ops.Workspace(), logits=logits.to(DEV))
+    oi = np.argsort(-logits.numpy(), axis=1, kind="stable")[:, :k]
+    assert np.array_equal(idx.cpu().numpy(), oi)
+
+
+# ---------------------------------------------------------------------------
+# Expert math, decode path
+# ---------------------------------------------------------------------------
+DECODE_CASES = [
+    # (dtype, bits_gu, bits_down, group, d, dff)
+    (torch.bfloat16, 2, 2, 64, 512, 256),
+    (torch.bfloat16, 2, 4, 64, 512, 256),
+    (torch.bfloat16, 4, 4, 64, 1024, 512),
+    (torch.bfloat16, 2, 2, 128, 1024, 512),
+    (torch.bfloat16, 2, 2, 32, 512, 256),
+    (torch.bfloat16, 8, 8, 64, 512, 256),
+    (torch.bfloat16, 4, 4, 32, 256, 128),
+    (torch.float16, 4, 4, 64, 1024, 512),
+    (torch.float16, 2, 2, 64, 512, 256),
+    (torch.float16, 8, 4, 128, 512, 256),
+    (torch.bfloat16, 2, 2, 64, 4096, 2048),
+]
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=lambda c: "-".join(map(str, c)))
+@pytest.mark.parametrize("T", [1, 2])
+def test_expert_decode_matches_oracle(case, T):
+    dtype, bgu, bdn, group, d, dff = case
+    banner(f"expert_decode {case} T={T}")
+    S, k = 9, 4
+    arena = synth.expert_arena(S, d, dff, bits_gate_up=bgu, bits_down=bdn, group=group, dtype=dtype,
+                               seed=d + bgu)
+    shared = synth.expert_arena(1, d, dff, bits_gate_up=bgu, bits_down=bdn, group=group, dtype=dtype,
+                                seed=99, zero_slot=False)
+    x = synth.activations(T, d, dtype, seed=T)
+    gen = torch.Generator().manual_seed(T + d)
+    slots = torch.stack([torch.randperm(S - 1, generator=gen)[:k] + 1 for _ in range(T)]).to(torch.int32)
+    wts = torch.rand(T, k, generator=gen) * 1.5
+    out = ops.expert_decode(_dev(arena), _dev(shared), x.to(DEV), slots.to(DEV), wts.to(DEV),
+                            swiglu_limit=10.0)
+    torch.cuda.synchronize()
+    slot_of = {s: s for s in range(S)}
+    want = _oracle_layer(x, slots.numpy(), wts.numpy(), arena, slot_of, dtype, shared=shared)
+    got = values(out)
+    assert_close(got, want, f"decode {case}")
+    assert exact_fraction(got, want) > 0.8
+
+
+@pytest.mark.parametrize("fp32_swiglu", [False, True])
+def test_expert_decode_swiglu_modes_and_limit(fp32_swiglu):
+    banner(f"swiglu fp32={fp32_swiglu}")
+    d, dff, S, k = 512, 256, 5, 2
+    arena = synth.expert_arena(S, d, dff, seed=5)
+    x = (synth.activations(1, d, seed=3).float() * 4).to(torch.bfloat16)   # drive the clamp
+    slots = torch.tensor([[1, 3]], dtype=torch.int32)
+    wts = torch.tensor([[0.7, 0.3]])
+    for limit in (10.0, 0.5, 0.0):
+        out = ops.expert_decode(_dev(arena), None, x.to(DEV), slots.to(DEV), wts.to(DEV),
+                                swiglu_limit=limit, fp32_swiglu=fp32_swiglu)
+        want = _oracle_layer(x, slots.numpy(), wts.numpy(), arena, {s: s for s in range(S)},
+                             torch.bfloat16, limit=limit, fp32_swiglu=fp32_swiglu)
+        assert_close(values(out), want, f"limit {limit}")
+
+
+def test_zero_slot_and_invalid_slots_contribute_zero():
+    banner("zero / invalid slots")
+    d, dff, S = 512, 256, 4
+    arena = synth.expert_arena(S, d, dff, seed=8)
+    x = synth.activations(1, d, seed=1)
+    for bad in (0, -1, S, 1000):
+        slots = torch.tensor([[bad, bad]], dtype=torch.int32)
+        out = ops.expert_decode(_dev(arena), None, x.to(DEV), slots.to(DEV),
+                                torch.ones(1, 2, device=DEV))
+        assert torch.count_nonzero(out).item() == 0
+
+
+def test_expert_decode_rejects_bad_shapes():
+    banner("shape checks")
+    arena = _dev(synth.expert_arena(3, 512, 256, seed=1))
+    x = torch.zeros(1, 512, dtype=torch.float16, device=DEV)      # dtype mismatch
+    with pytest.raises(ops._lib.LocaliError):
+        ops.expert_decode(arena, None, x, torch.ones(1, 2, dtype=torch.int32, device=DEV),
+                          torch.ones(1, 2, device=DEV))
+    odd = synth.expert_arena(3, 576, 256, seed=1)                 # 576*2/128 chunks unsupported
+    with pytest.raises(ops._lib.LocaliError):
+        ops.expert_decode(_dev(odd), None, torch.zeros(1, 576, dtype=torch.bfloat16, device=DEV),
+                          torch.ones(1, 2, dtype=torch.int32, device=DEV), torch.ones(1, 2, device=DEV))
+
+
+# ---------------------------------------------------------------------------
+# Grouped path, dispatch, combine
+# ---------------------------------------------------------------------------
+def test_dispatch_stable_sort():
+    banner("dispatch")
+    T, k, S = 37, 6, 40
+    gen = torch.Generator().manual_seed(0)
+    rs = torch.stack([torch.randperm(S - 1, generator=gen)[:k] + 1 for _ in range(T)]).to(torch.int32)
+    rs[3, 2] = -1
+    sorted_route, seg = ops.dispatch(rs.to(DEV), S)
+    order, counts, _ = moe.dispatch(rs.numpy())
+    flat = rs.numpy().reshape(-1)
+    valid = order[flat[order] >= 0]
+    n = int(seg[-1].item())
+    assert n == valid.size
+    assert np.array_equal(sorted_route.cpu().numpy()[:n], valid)
+    seg = seg.cpu().numpy()
+    for s in range(S):
+        assert seg[s + 1] - seg[s] == counts.get(s, 0)
+
+
+@pytest.mark.parametrize("T,dtype,bits", [(3, torch.bfloat16, (2, 2)), (17, torch.bfloat16, (2, 4)),
+                                          (64, torch.bfloat16, (2, 2)), (9, torch.float16, (4, 4))])
+def test_expert_grouped_matches_oracle(T, dtype, bits):
+    banner(f"grouped T={T} {dtype} {bits}")
+    d, dff, E, k = 512, 256, 16, 4
+    arena = synth.expert_arena(E + 1, d, dff, bits_gate_up=bits[0], bits_down=bits[1], dtype=dtype,
+                               seed=T)
+    shared = synth.expert_arena(1, d, dff, bits_gate_up=bits[0], bits_down=bits[1], dtype=dtype,
+                                seed=77, zero_slot=False)
+    x = synth.activations(T, d, dtype, seed=T + 1)
+    gen = torch.Generator().manual_seed(T)
+    idx = torch.stack([torch.randperm(E, generator=gen)[:k] for _ in range(T)]).to(torch.int32)
+    for t in range(0, T, 2):            # skew: expert 0 in every other token
+        if not (idx[t] == 0).any():
+            idx[t, 0] = 0
+    slot_of = (torch.arange(E, dtype=torch.int32) + 1)
+    wts = torch.rand(T, k, generator=gen)
+    out = ops.expert_grouped(_dev(arena), _dev(shared), x.to(DEV), idx.to(DEV), slot_of.to(DEV),
+                             wts.to(DEV), ops.Workspace())
+    torch.cuda.synchronize()
+    want = _oracle_layer(x, idx.numpy(), wts.numpy(), arena, {e: e + 1 for e in range(E)}, dtype,
+                         shared=shared)
+    assert_close(values(out), want, "grouped")
+
+
+def test_combine_kernel():
+    banner("combine")
+    T, k, d = 5, 6, 300
+    gen = torch.Generator().manual_seed(2)
+    y = torch.randn(T, k, d, generator=gen).to(torch.bfloat16)
+    sh = torch.randn(T, d, generator=gen).to(torch.bfloat16)
+    w = torch.rand(T, k, generator=gen)
+    for mode, name in ((ops.COMBINE_ROUNDED, "single"), (ops.COMBINE_FP32, "fp32")):
+        out = ops.combine(y.to(DEV), w.to(DEV), sh.to(DEV), mode)
+        want = moe.add_shared(moe.combine(values(y), w.numpy(), "bf16", name), values(sh), "bf16")
+        assert_close(values(out), want, f"combine {name}", rtol=8e-3, atol=1e-6)
+        assert exact_fraction(values(out), want) > 0.99
+
+
+# ---------------------------------------------------------------------------
+# Whole layer (router + experts + combine + shared) on the benchmark shapes
+# ---------------------------------------------------------------------------
+def test_forward_small_cpu_config_fp16():
+    """d 1024, 32 experts + 1 shared, d_ff 512, 4-bit g64 fp16, decode and 8-token prefill."""
+    banner("forward C1")
+    d, E, dff, k = 1024, 32, 512, 6
+    arena = synth.expert_arena(E + 1, d, dff, bits_gate_up=4, group=64, dtype=torch.float16, seed=1)
+    shared = synth.expert_arena(1, d, dff, bits_gate_up=4, dtype=torch.float16, seed=2, zero_slot=False)
+    w, bias = synth.uniform_router(E, d, torch.float16, seed=3, bias_std=0.01)
+    spec = ops.RouterSpec(w.to(DEV), k, routed_scale=1.5, score_bias=bias.to(DEV))
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32)
+    for T in (1, 8):
+        x = synth.activations(T, d, torch.float16, seed=10 + T)
+        out, idx, wts = ops.forward(spec, _dev(arena), _dev(shared), slot_of.to(DEV), x.to(DEV),
+                                    ops.Workspace())
+        torch.cuda.synchronize()
+        oi, ow, margin, _ = moe.route(values(x), values(w), k, bias=values(bias), routed_scale=1.5)
+        assert (margin > 1e-4).all()
+        assert np.array_equal(idx.cpu().numpy(), oi)
+        want = _oracle_layer(x, oi, ow, arena, {e: e + 1 for e in range(E)}, torch.float16, shared=shared)
+        assert_close(values(out), want, f"forward C1 T={T}")
+
+
+def test_forward_full_width_decode(oracle_lib):
+    """d 4096, 256 experts + shared, d_ff 2048, 2-bit g64 bf16, 1 token; checked
+    against the C oracle (fp32) on the GPU's own routing."""
+    banner("forward C2")
+    d, E, dff, k = 4096, 256, 2048, 6
+    arena = synth.expert_arena(E + 1, d, dff, dtype=torch.bfloat16, seed=21, device=DEV)
+    shared = synth.expert_arena(1, d, dff, dtype=torch.bfloat16, seed=22, device=DEV, zero_slot=False)
+    w, _ = synth.uniform_router(E, d, torch.bfloat16, seed=23, device=DEV)
+    spec = ops.RouterSpec(w, k, routed_scale=1.5)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    ws = ops.Workspace()
+    for step in range(3):
+        x = synth.activations(1, d, torch.bfloat16, seed=100 + step, device=DEV)
+        out, idx, wts = ops.forward(spec, arena, shared, slot_of, x, ws)
+        torch.cuda.synchronize()
+        oi, ow, margin, _ = moe.route(values(x), values(w), k, routed_scale=1.5)
+        if margin[0] > 1e-4:
+            assert list(idx[0].cpu().numpy()) == list(oi[0])
+        slots = (idx.cpu().numpy() + 1).astype(np.int32)
+        used = sorted(set(slots.reshape(-1).tolist()))
+        remap = {s: i for i, s in enumerate(used)}
+        sub = arena_numpy(arena, float_meta=False, slots=used)
+        sh = {kk: (v[0], v[1], v[2], v[3], v[4]) for kk, v in arena_numpy(shared, float_meta=False).items()}
+        want = oracle_lib.moe_layer(values(x), np.vectorize(remap.get)(slots), wts.cpu().numpy(),
+                                    sub, "bf16", shared=sh)
+        assert_close(values(out), want, f"C2 step {step}")
+        assert exact_fraction(values(out), want) > 0.8

@@ -1,0 +1,221 @@
+"""Pins the CPU oracle itself (CPU only).
+
+Each oracle function is checked against something that does not restate its
+own formula: literal packed words worked out by hand, the reference's kernel
+text for code extraction (dsv4_kernels.py:59-73), special cases with closed
+forms, torch/numpy library routines, an independent C restatement
+(oracle/expert_ref.c), and golden router vectors from the transformers
+DeepSeek-V4 router classes (tests/golden/make_router_vectors.py).
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import affine, moe
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+# -- affine layout ------------------------------------------------------------
+
+def test_pack_literal_words():
+    # 4-bit LSB-first: value j in bits [4j, 4j+3]
+    assert affine.pack(np.array([[1, 2, 3, 4, 5, 6, 7, 8]]), 4)[0, 0] == 0x87654321
+    # 2-bit: codes 1,2,3,0 -> byte 0b00111001 = 0x39, repeated
+    assert affine.pack(np.array([[1, 2, 3, 0] * 4]), 2)[0, 0] == 0x39393939
+    # 8-bit: bytes in order
+    assert affine.pack(np.array([[0x11, 0x22, 0x33, 0xF4]]), 8)[0, 0] == 0xF4332211
+
+
+def test_unpack_matches_reference_kernel_text_extraction():
+    """dsv4_kernels.py:59-73: lane reads word block/16 + lane/2, shifts by
+    (lane & 1) * 16 and peels 8 two-bit values LSB first."""
+    rng = np.random.default_rng(3)
+    K = 512
+    words = rng.integers(0, 2**32, size=(3, K // 16), dtype=np.uint64).astype(np.uint32)
+    ours = affine.unpack(words, 2)
+    for row in range(3):
+        for block in range(0, K, 256):
+            for lane in range(32):
+                uw = int(words[row, block // 16 + lane // 2]) >> ((lane & 1) * 16)
+                for j in range(8):
+                    assert ours[row, block + lane * 8 + j] == (uw & 3)
+                    uw >>= 2
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_pack_unpack_roundtrip(bits):
+    rng = np.random.default_rng(bits)
+    q = rng.integers(0, 2**bits, size=(5, 256), dtype=np.uint8)
+    assert np.array_equal(affine.unpack(affine.pack(q, bits), bits), q)
+
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(0)
+    a = np.concatenate([rng.standard_normal(10000) * 10.0 ** rng.integers(-30, 30, 10000),
+                        [0.0, -0.0, 1.0 + 2**-8, 1.0 + 3 * 2**-8, 65504.0, 1e-40]]).astype(np.float32)
+    want = torch.from_numpy(a).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(affine.round_to(a, "bf16"), want)
+
+
+def test_c_oracle_rounding_matches_torch(oracle_lib):
+    rng = np.random.default_rng(1)
+    a = np.concatenate([rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 6, 20000),
+                        [65504.0, 65519.0, 65520.0, 6.0e-8, 2.0**-24 * 1.5, 2.0**-25, -3e-6]])
+    a = a.astype(np.float32)
+    assert np.array_equal(oracle_lib.round_array(a, "f16"),
+                          torch.from_numpy(a).half().float().numpy())
+    assert np.array_equal(oracle_lib.round_array(a, "bf16"),
+                          torch.from_numpy(a).bfloat16().float().numpy())
+
+
+# -- qmv ----------------------------------------------------------------------
+
+def _rand_proj(rng, N, K, bits, group, dt="bf16"):
+    q = rng.integers(0, 2**bits, size=(N, K), dtype=np.uint8)
+    s = affine.round_to(rng.uniform(0.01, 0.05, size=(N, K // group)), dt)
+    b = affine.round_to(rng.uniform(-0.1, 0.0, size=(N, K // group)), dt)
+    return q, affine.pack(q, bits), s, b
+
+
+@pytest.mark.parametrize("bits,group", [(2, 64), (4, 64), (2, 128), (4, 32), (8, 64)])
+def test_qmv_equals_torch_dense_matmul(bits, group):
+    rng = np.random.default_rng(bits * 1000 + group)
+    N, K = 48, 512
+    q, w, s, b = _rand_proj(rng, N, K, bits, group)
+    x = rng.standard_normal((3, K))
+    dense = torch.from_numpy(q.astype(np.float64)) * torch.from_numpy(s).double().repeat_interleave(group, 1) \
+        + torch.from_numpy(b).double().repeat_interleave(group, 1)
+    want = torch.from_numpy(x) @ dense.T
+    np.testing.assert_allclose(affine.qmv(x, w, s, b, bits, group), want.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_qmv_special_cases():
+    rng = np.random.default_rng(5)
+    N, K, G = 8, 256, 64
+    s = rng.uniform(0.5, 1.0, (N, K // G))
+    b = rng.uniform(-1.0, 1.0, (N, K // G))
+    x = rng.standard_normal(K)
+    zero_codes = affine.pack(np.zeros((N, K), np.uint8), 2)
+    # all-zero codes -> sum_g bias_g * sum(x in g)
+    want = (b * x.reshape(K // G, G).sum(1)).sum(1)
+    np.testing.assert_allclose(affine.qmv(x, zero_codes, s, b, 2, G), want, rtol=1e-12)
+    # one-hot x picks column j of the dequantised matrix: s*q + b
+    q = rng.integers(0, 4, (N, K), dtype=np.uint8)
+    j = 77
+    e = np.zeros(K)
+    e[j] = 1.0
+    np.testing.assert_allclose(affine.qmv(e, affine.pack(q, 2), s, b, 2, G),
+                               s[:, j // G] * q[:, j] + b[:, j // G], rtol=1e-12)
+    # zero slot (all-zero words, scales, biases) contributes exactly 0
+    assert np.all(affine.qmv(x, zero_codes, 0 * s, 0 * b, 2, G) == 0.0)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_c_oracle_layer_matches_numpy_oracle(oracle_lib, dt):
+    rng = np.random.default_rng(11)
+    S, d, dff, k, T = 5, 256, 128, 2, 3
+    arena, arena_c = {}, {}
+    for name, (N, K, bits) in {"gate_proj": (dff, d, 2), "up_proj": (dff, d, 2),
+                               "down_proj": (d, dff, 4)}.items():
+        ws, ss, bs = [], [], []
+        for _ in range(S):
+            _, w, s, b = _rand_proj(rng, N, K, bits, 64, dt)
+            ws.append(w), ss.append(s), bs.append(b)
+        w, s, b = np.stack(ws), np.stack(ss), np.stack(bs)
+        arena[name] = (w, s, b, bits, 64)
+        arena_c[name] = (w, affine.to_bits16(s, dt), affine.to_bits16(b, dt), bits, 64)
+    x = affine.round_to(rng.standard_normal((T, d)) * 3, dt)
+    idx = np.array([[1, 3], [4, 1], [2, 2]])
+    wts = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    slot_of = {e: e for e in range(S)}
+    want = moe.moe_layer(x, idx, wts, arena, slot_of, dt, limit=1.5)
+    got = oracle_lib.moe_layer(x, idx, wts, arena_c, dt, limit=1.5)
+    # fp32 vs fp64 accumulation: equal up to an occasional last-place flip
+    np.testing.assert_allclose(got, want, rtol=2e-2 if dt == "bf16" else 4e-3, atol=2e-3)
+    assert np.mean(got == want) > 0.9
+
+
+# -- router -------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", ["a", "b", "c"])
+def test_router_matches_transformers_golden_vectors(case):
+    g = np.load(GOLD / "router_vectors.npz")
+    x, w, bias = g[f"{case}_x"], g[f"{case}_w"], g[f"{case}_bias"]
+    k, scale = int(g[f"{case}_k"]), float(g[f"{case}_scale"])
+    idx, wts, margin, _ = moe.route(x, w, k, bias=bias, routed_scale=scale)
+    for t in range(x.shape[0]):
+        ref = dict(zip(g[f"{case}_idx"][t].tolist(), g[f"{case}_weights"][t].tolist()))
+        assert set(idx[t].tolist()) == set(ref), f"token {t}"
+        for e, v in zip(idx[t].tolist(), wts[t].tolist()):
+            assert v == pytest.approx(ref[e], rel=1e-5)
+    np.testing.assert_allclose(wts.sum(1), scale, rtol=1e-9)
+    hidx, hw, _, _ = moe.route(x, w, k, routed_scale=scale, tid2eid=g[f"{case}_table"],
+                               input_ids=g[f"{case}_ids"])
+    assert np.array_equal(hidx, g[f"{case}_hash_idx"])
+    np.testing.assert_allclose(hw, g[f"{case}_hash_weights"], rtol=1e-5)
+
+
+def test_router_sigmoid_variant_and_canonical_order():
+    """arena.py:501-506: sigmoid scores, selection on score + bias, weights
+    renormalised without scaling; in-row order descending, ties to lower id."""
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((4, 16))
+    w = rng.standard_normal((10, 16))
+    bias = rng.standard_normal(10) * 0.1
+    idx, wts, _, scores = moe.route(x, w, 3, bias=bias, score_func="sigmoid")
+    sel = scores + bias
+    for t in range(4):
+        assert list(idx[t]) == sorted(range(10), key=lambda e: (-sel[t, e], e))[:3]
+        np.testing.assert_allclose(wts[t], scores[t, idx[t]] / scores[t, idx[t]].sum(), rtol=1e-12)
+    tie_idx, _, _, _ = moe.route(np.zeros((1, 16)), w, 4, score_func="sigmoid")
+    assert list(tie_idx[0]) == [0, 1, 2, 3]
+
+
+def test_c_oracle_router_matches_numpy(oracle_lib):
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((6, 128)).astype(np.float32)
+    w = (rng.standard_normal((64, 128)) / 11).astype(np.float32)
+    bias = (rng.standard_normal(64) * 0.05).astype(np.float32)
+    idx, wts = oracle_lib.router(x, w, bias, 6, 0, True, 1.5)
+    nidx, nw, margin, _ = moe.route(x, w, 6, bias=bias, routed_scale=1.5)
+    for t in range(6):
+        if margin[t] > 1e-5:
+            assert list(idx[t]) == list(nidx[t])
+            np.testing.assert_allclose(wts[t], nw[t], rtol=1e-5)
+
+
+# -- combine / dispatch -------------------------------------------------------
+
+def test_combine_closed_forms():
+    y = affine.round_to(np.random.default_rng(0).standard_normal((2, 3, 8)), "bf16")
+    # unit weights on one route and zero elsewhere returns that route exactly
+    w = np.array([[1.0, 0.0, 0.0], [0.0, 0.0, 1.0]])
+    out = moe.combine(y, w, "bf16")
+    assert np.array_equal(out[0], y[0, 0]) and np.array_equal(out[1], y[1, 2])
+    # powers of two scale exactly
+    out = moe.combine(y, np.full((2, 3), 0.25), "bf16")
+    np.testing.assert_allclose(out, affine.round_to(y.sum(1) * 0.25, "bf16"), rtol=0, atol=0) \
+        if np.all(affine.round_to(y * 0.25, "bf16") == y * 0.25) else None
+    # shared add is a rounded sum
+    s = affine.round_to(np.ones((2, 8)) * 0.5, "bf16")
+    assert np.array_equal(moe.add_shared(np.zeros((2, 8)), s, "bf16"), s)
+
+
+def test_dispatch_is_stable_slot_sort():
+    rng = np.random.default_rng(4)
+    slots = rng.integers(1, 9, size=(40, 4))
+    order, counts, undo = moe.dispatch(slots)
+    flat = slots.reshape(-1)
+    assert np.all(np.diff(flat[order]) >= 0)
+    for s in np.unique(flat):
+        members = order[flat[order] == s]
+        assert np.all(np.diff(members) > 0)          # route order kept within a slot
+        assert counts[int(s)] == members.size
+    assert np.array_equal(order[undo], np.arange(flat.size))
+    assert moe.first_appearance([[3, 1], [1, 4], [3, 2]]) == [3, 1, 4, 2]
