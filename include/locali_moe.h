@@ -145,7 +145,25 @@ int locali_moe_expert_decode(const locali_expert_arena *routed,
                              const int32_t *route_slot, const float *weights,
                              float swiglu_limit, int32_t fp32_swiglu,
                              int32_t combine_mode, void *hidden, void *out,
-                             void *stream);
+                             void *workspace, size_t workspace_bytes, void *stream);
+
+/* The two stages of locali_moe_expert_decode, callable separately:
+ * gate/up + clamped SwiGLU into `hidden`, then down projection + combine
+ * (+ shared) into `out`. The down stage reads the prepared hidden vectors the
+ * gate/up stage leaves in the workspace, so both calls take the same
+ * workspace. Same arguments and rules as expert_decode. */
+int locali_moe_decode_gateup(const locali_expert_arena *routed,
+                             const locali_expert_arena *shared, const void *x,
+                             int32_t x_dtype, int32_t tokens, int32_t top_k,
+                             const int32_t *route_slot, float swiglu_limit,
+                             int32_t fp32_swiglu, void *hidden, void *workspace,
+                             size_t workspace_bytes, void *stream);
+int locali_moe_decode_down_combine(const locali_expert_arena *routed,
+                                   const locali_expert_arena *shared,
+                                   int32_t x_dtype, int32_t tokens, int32_t top_k,
+                                   const int32_t *route_slot, const float *weights,
+                                   int32_t combine_mode, void *out, void *workspace,
+                                   size_t workspace_bytes, void *stream);
 
 /* Grouped form of locali_moe_expert_decode for many tokens: (token, k) entries
  * are grouped by slot on the device and every slot's weights are streamed

@@ -86,7 +86,11 @@ _SIGNATURES = {
                            _P, _SZ, _P], ctypes.c_int),
     "locali_moe_dispatch": ([_P, _I, _I, _I, _P, _P, _P], ctypes.c_int),
     "locali_moe_expert_decode": ([ctypes.POINTER(ExpertArena), ctypes.POINTER(ExpertArena), _P, _I,
-                                  _I, _I, _P, _P, _F, _I, _I, _P, _P, _P], ctypes.c_int),
+                                  _I, _I, _P, _P, _F, _I, _I, _P, _P, _P, _SZ, _P], ctypes.c_int),
+    "locali_moe_decode_gateup": ([ctypes.POINTER(ExpertArena), ctypes.POINTER(ExpertArena), _P, _I,
+                                  _I, _I, _P, _F, _I, _P, _P, _SZ, _P], ctypes.c_int),
+    "locali_moe_decode_down_combine": ([ctypes.POINTER(ExpertArena), ctypes.POINTER(ExpertArena), _I,
+                                        _I, _I, _P, _P, _I, _P, _P, _SZ, _P], ctypes.c_int),
     "locali_moe_expert_grouped": ([ctypes.POINTER(ExpertArena), ctypes.POINTER(ExpertArena), _P, _I,
                                    _I, _I, _I, _P, _P, _P, _F, _I, _I, _P, _P, _SZ, _P], ctypes.c_int),
     "locali_moe_combine": ([_P, _P, _P, _I, _I, _I, _I, _I, _P, _P], ctypes.c_int),

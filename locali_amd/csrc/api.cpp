@@ -45,10 +45,14 @@ bool dtype16(int32_t dt) { return dt == LOCALI_DT_F16 || dt == LOCALI_DT_BF16; }
 
 // Workspace layout for up to T tokens.
 struct Layout {
-    size_t counter, logits, route_slot, hidden, seg_start, sorted_route, route_pos, tiles, n_tiles,
-        gh, gy, total;
+    size_t counter, logits, route_slot, hidden, xprep, hprep, seg_start, sorted_route, route_pos,
+        tiles, n_tiles, gh, gy, total;
     int max_tiles;
 };
+
+// Bytes of one prepared vector of K values, for any bit width (pairs take at
+// most K u32, partial sums at most K / 4 float2).
+size_t prep_bytes(int K) { return align_up(4 * static_cast<size_t>(K)) + align_up(2 * static_cast<size_t>(K)); }
 
 Layout layout(int T, int d, int dff, int E, int k, int has_shared) {
     Layout L{};
@@ -65,6 +69,8 @@ Layout layout(int T, int d, int dff, int E, int k, int has_shared) {
     L.logits = take(sizeof(float) * kRouterSplitsHost * static_cast<size_t>(T) * E);
     L.route_slot = take(sizeof(int32_t) * R);
     L.hidden = take(sizeof(uint16_t) * static_cast<size_t>(routes) * dff);
+    L.xprep = take(prep_bytes(d) * T);
+    L.hprep = take(prep_bytes(dff) * routes);
     L.seg_start = take(sizeof(int32_t) * (kMaxSlots + 1));
     L.sorted_route = take(sizeof(int32_t) * R);
     L.route_pos = take(sizeof(int32_t) * R);
@@ -155,10 +161,30 @@ int check_shared(const locali_expert_arena *routed, const locali_expert_arena *s
 
 hipStream_t S(void *stream) { return static_cast<hipStream_t>(stream); }
 
+// n_vec prepared vectors of K values carved from `base` (see Layout).
+PrepVec prep_view(void *base, int K, int bits, bool bf16) {
+    PrepVec v{};
+    v.pairs = static_cast<uint32_t *>(base);
+    v.pairs_stride = prep_pairs_count(K, bits, bf16);
+    v.parts_stride = prep_parts_count(K, bits);
+    // all pairs first, then all parts: caller reserved prep_bytes(K) per vector
+    return v;
+}
+
+PrepVec prep_batch(void *base, int n_vec, int K, int bits, bool bf16) {
+    PrepVec v = prep_view(base, K, bits, bf16);
+    const size_t pairs_bytes = align_up(4 * static_cast<size_t>(K) * n_vec);
+    v.parts = reinterpret_cast<float2 *>(static_cast<char *>(base) + pairs_bytes);
+    return v;
+}
+
+// stages: bit 0 = gate/up, bit 1 = down + combine. xprep_ready: the
+// activations were already prepared into x_prep_base by the router.
 int run_decode(const locali_expert_arena *routed, const locali_expert_arena *shared, const void *x,
                int32_t x_dtype, int32_t tokens, int32_t top_k, const int32_t *route_slot,
                const float *weights, float limit, int32_t fp32_swiglu, int32_t combine_mode,
-               void *hidden, void *out, hipStream_t st) {
+               void *hidden, void *out, hipStream_t st, int stages, void *x_prep_base,
+               bool xprep_ready, void *h_prep_base) {
     DecodeLaunch L{};
     L.ra.x = static_cast<const uint16_t *>(x);
     L.ra.route_slot = route_slot;
@@ -180,10 +206,34 @@ int run_decode(const locali_expert_arena *routed, const locali_expert_arena *sha
     L.ca.weights = weights;
     L.ca.out = static_cast<uint16_t *>(out);
     L.ca.mode = combine_mode;
-    hipError_t e = launch_gateup_decode(L, st);
-    if (e != hipSuccess) return hip_fail(e, "gate/up decode launch");
-    e = launch_down_combine_decode(L, st);
-    if (e != hipSuccess) return hip_fail(e, "down/combine decode launch");
+    const bool bf16 = x_dtype == LOCALI_DT_BF16;
+    L.xprep = prep_batch(x_prep_base, tokens, routed->gate.cols, routed->gate.bits, bf16);
+    L.hprep = prep_batch(h_prep_base, L.routes, routed->down.cols, routed->down.bits, bf16);
+    hipError_t e;
+    if ((stages & 1) && !xprep_ready) {
+        e = launch_prep_vectors(static_cast<const uint16_t *>(x), tokens, routed->gate.cols,
+                                routed->gate.bits, bf16, L.xprep, st);
+        if (e != hipSuccess) return hip_fail(e, "activation prep launch");
+    }
+    if ((stages & 1) && (e = launch_gateup_decode(L, st)) != hipSuccess)
+        return hip_fail(e, "gate/up decode launch");
+    if ((stages & 2) && (e = launch_down_combine_decode(L, st)) != hipSuccess)
+        return hip_fail(e, "down/combine decode launch");
+    return 0;
+}
+
+int check_decode_args(const locali_expert_arena *routed, const locali_expert_arena *shared,
+                      int32_t x_dtype, int32_t tokens, int32_t top_k, const int32_t *route_slot,
+                      int32_t combine_mode) {
+    int rc, dff = 0;
+    if (!dtype16(x_dtype) || tokens < 1 || top_k < 1 || !route_slot)
+        return fail(LOCALI_E_ARG, "expert_decode: bad arguments");
+    if (!routed) return fail(LOCALI_E_ARG, "expert_decode: null arena");
+    if ((rc = check_arena(routed, "routed", x_dtype, routed->gate.cols, &dff))) return rc;
+    if ((rc = check_shared(routed, shared))) return rc;
+    if (top_k + (shared ? 1 : 0) > 16) return fail(LOCALI_E_ARG, "expert_decode: top_k + shared > 16");
+    if (combine_mode != LOCALI_COMBINE_ROUNDED && combine_mode != LOCALI_COMBINE_FP32)
+        return fail(LOCALI_E_ARG, "expert_decode: combine_mode %d", combine_mode);
     return 0;
 }
 
@@ -247,32 +297,13 @@ int check_router(const locali_router *r, int d) {
     return 0;
 }
 
-}  // namespace
-
-extern "C" {
-
-const char *locali_moe_last_error(void) { return g_error.c_str(); }
-
-size_t locali_moe_workspace_bytes(int32_t tokens, int32_t d_model, int32_t d_ff, int32_t n_experts,
-                                  int32_t top_k, int32_t has_shared) {
-    if (tokens < 1 || d_model < 1 || d_ff < 1 || n_experts < 1 || top_k < 1) return 0;
-    return layout(tokens, d_model, d_ff, n_experts, top_k, has_shared).total;
-}
-
-int locali_moe_router(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens,
-                      int32_t d_model, const int32_t *input_ids, const float *logits_in,
-                      const int32_t *slot_of_expert, int32_t n_slots, int32_t *idx, float *weights,
-                      int32_t *route_slot, void *workspace, size_t workspace_bytes, void *stream) {
-    int rc;
-    if ((rc = check_router(router, d_model))) return rc;
-    if (tokens < 1 || !x || !dtype16(x_dtype) || !idx || !weights || !workspace)
-        return fail(LOCALI_E_ARG, "router: bad tokens/x/outputs/workspace");
+int route(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens, int32_t d_model,
+          const int32_t *input_ids, const float *logits_in, const int32_t *slot_of_expert,
+          int32_t n_slots, int32_t *idx, float *weights, int32_t *route_slot, void *workspace,
+          const Layout &lay, PrepVec xprep, int prep_bits, hipStream_t st) {
     if (router->tid2eid && !input_ids) return fail(LOCALI_E_ARG, "router: hash routing needs input_ids");
     if (route_slot && (!slot_of_expert || n_slots < 1))
         return fail(LOCALI_E_ARG, "router: route_slot needs slot_of_expert and n_slots");
-    const Layout lay = layout(tokens, d_model, 1, router->n_experts, router->top_k, 0);
-    if (workspace_bytes < lay.route_slot)
-        return fail(LOCALI_E_WORKSPACE, "router: workspace %zu < %zu bytes", workspace_bytes, lay.route_slot);
     RouterLaunch L{};
     L.x = static_cast<const uint16_t *>(x);
     L.x_bf16 = x_dtype == LOCALI_DT_BF16;
@@ -297,9 +328,38 @@ int locali_moe_router(const locali_router *router, const void *x, int32_t x_dtyp
     L.logits = at<float>(workspace, lay.logits);
     L.counter = at<uint32_t>(workspace, lay.counter);
     L.logits_in = logits_in;
-    hipError_t e = launch_router(L, S(stream));
+    L.xprep = xprep;
+    L.prep_bits = prep_bits;
+    hipError_t e = launch_router(L, st);
     if (e != hipSuccess) return hip_fail(e, "router launch");
     return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *locali_moe_last_error(void) { return g_error.c_str(); }
+
+size_t locali_moe_workspace_bytes(int32_t tokens, int32_t d_model, int32_t d_ff, int32_t n_experts,
+                                  int32_t top_k, int32_t has_shared) {
+    if (tokens < 1 || d_model < 1 || d_ff < 1 || n_experts < 1 || top_k < 1) return 0;
+    return layout(tokens, d_model, d_ff, n_experts, top_k, has_shared).total;
+}
+
+int locali_moe_router(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens,
+                      int32_t d_model, const int32_t *input_ids, const float *logits_in,
+                      const int32_t *slot_of_expert, int32_t n_slots, int32_t *idx, float *weights,
+                      int32_t *route_slot, void *workspace, size_t workspace_bytes, void *stream) {
+    int rc;
+    if ((rc = check_router(router, d_model))) return rc;
+    if (tokens < 1 || !x || !dtype16(x_dtype) || !idx || !weights || !workspace)
+        return fail(LOCALI_E_ARG, "router: bad tokens/x/outputs/workspace");
+    const Layout lay = layout(tokens, d_model, 1, router->n_experts, router->top_k, 0);
+    if (workspace_bytes < lay.route_slot)
+        return fail(LOCALI_E_WORKSPACE, "router: workspace %zu < %zu bytes", workspace_bytes, lay.route_slot);
+    return route(router, x, x_dtype, tokens, d_model, input_ids, logits_in, slot_of_expert, n_slots, idx,
+                 weights, route_slot, workspace, lay, PrepVec{}, 0, S(stream));
 }
 
 int locali_moe_dispatch(const int32_t *route_slot, int32_t tokens, int32_t top_k, int32_t n_slots,
@@ -314,22 +374,58 @@ int locali_moe_dispatch(const int32_t *route_slot, int32_t tokens, int32_t top_k
     return 0;
 }
 
+int decode_workspace(const locali_expert_arena *routed, const locali_expert_arena *shared, int tokens,
+                     int top_k, size_t workspace_bytes, void *workspace, Layout *lay) {
+    if (!workspace) return fail(LOCALI_E_ARG, "decode: null workspace");
+    *lay = layout(tokens, routed->gate.cols, routed->gate.rows, 1, top_k, shared ? 1 : 0);
+    if (workspace_bytes < lay->total)
+        return fail(LOCALI_E_WORKSPACE, "decode: workspace %zu < %zu bytes", workspace_bytes, lay->total);
+    return 0;
+}
+
 int locali_moe_expert_decode(const locali_expert_arena *routed, const locali_expert_arena *shared,
                              const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k,
                              const int32_t *route_slot, const float *weights, float swiglu_limit,
                              int32_t fp32_swiglu, int32_t combine_mode, void *hidden, void *out,
-                             void *stream) {
-    int rc, dff = 0;
-    if (!x || !dtype16(x_dtype) || tokens < 1 || top_k < 1 || !route_slot || !weights || !hidden || !out)
-        return fail(LOCALI_E_ARG, "expert_decode: bad arguments");
-    if (!routed) return fail(LOCALI_E_ARG, "expert_decode: null arena");
-    if ((rc = check_arena(routed, "routed", x_dtype, routed->gate.cols, &dff))) return rc;
-    if ((rc = check_shared(routed, shared))) return rc;
-    if (top_k + (shared ? 1 : 0) > 16) return fail(LOCALI_E_ARG, "expert_decode: top_k + shared > 16");
-    if (combine_mode != LOCALI_COMBINE_ROUNDED && combine_mode != LOCALI_COMBINE_FP32)
-        return fail(LOCALI_E_ARG, "expert_decode: combine_mode %d", combine_mode);
+                             void *workspace, size_t workspace_bytes, void *stream) {
+    if (!x || !weights || !hidden || !out) return fail(LOCALI_E_ARG, "expert_decode: null buffer");
+    int rc = check_decode_args(routed, shared, x_dtype, tokens, top_k, route_slot, combine_mode);
+    if (rc) return rc;
+    Layout lay;
+    if ((rc = decode_workspace(routed, shared, tokens, top_k, workspace_bytes, workspace, &lay))) return rc;
     return run_decode(routed, shared, x, x_dtype, tokens, top_k, route_slot, weights, swiglu_limit,
-                      fp32_swiglu, combine_mode, hidden, out, S(stream));
+                      fp32_swiglu, combine_mode, hidden, out, S(stream), 3, at<void>(workspace, lay.xprep),
+                      false, at<void>(workspace, lay.hprep));
+}
+
+int locali_moe_decode_gateup(const locali_expert_arena *routed, const locali_expert_arena *shared,
+                             const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k,
+                             const int32_t *route_slot, float swiglu_limit, int32_t fp32_swiglu,
+                             void *hidden, void *workspace, size_t workspace_bytes, void *stream) {
+    if (!x || !hidden) return fail(LOCALI_E_ARG, "decode_gateup: null buffer");
+    int rc = check_decode_args(routed, shared, x_dtype, tokens, top_k, route_slot,
+                               LOCALI_COMBINE_ROUNDED);
+    if (rc) return rc;
+    Layout lay;
+    if ((rc = decode_workspace(routed, shared, tokens, top_k, workspace_bytes, workspace, &lay))) return rc;
+    return run_decode(routed, shared, x, x_dtype, tokens, top_k, route_slot, nullptr, swiglu_limit,
+                      fp32_swiglu, LOCALI_COMBINE_ROUNDED, hidden, nullptr, S(stream), 1,
+                      at<void>(workspace, lay.xprep), false, at<void>(workspace, lay.hprep));
+}
+
+int locali_moe_decode_down_combine(const locali_expert_arena *routed,
+                                   const locali_expert_arena *shared, int32_t x_dtype, int32_t tokens,
+                                   int32_t top_k, const int32_t *route_slot, const float *weights,
+                                   int32_t combine_mode, void *out, void *workspace,
+                                   size_t workspace_bytes, void *stream) {
+    if (!weights || !out) return fail(LOCALI_E_ARG, "decode_down_combine: null buffer");
+    int rc = check_decode_args(routed, shared, x_dtype, tokens, top_k, route_slot, combine_mode);
+    if (rc) return rc;
+    Layout lay;
+    if ((rc = decode_workspace(routed, shared, tokens, top_k, workspace_bytes, workspace, &lay))) return rc;
+    return run_decode(routed, shared, nullptr, x_dtype, tokens, top_k, route_slot, weights, 0.f, 0,
+                      combine_mode, at<void>(workspace, lay.hidden), out, S(stream), 2,
+                      at<void>(workspace, lay.xprep), true, at<void>(workspace, lay.hprep));
 }
 
 int locali_moe_expert_grouped(const locali_expert_arena *routed, const locali_expert_arena *shared,
@@ -399,14 +495,18 @@ int locali_moe_forward(const locali_router *router, const locali_expert_arena *r
     if (workspace_bytes < lay.total)
         return fail(LOCALI_E_WORKSPACE, "forward: workspace %zu < %zu bytes", workspace_bytes, lay.total);
     int32_t *route_slot = at<int32_t>(workspace, lay.route_slot);
-    rc = locali_moe_router(router, x, x_dtype, tokens, d, input_ids, nullptr, slot_of_expert,
-                           routed->gate.n_slots, idx, weights, route_slot, workspace, workspace_bytes,
-                           stream);
+    const bool decode = tokens <= kDecodeMaxTokens;
+    const bool bf16 = x_dtype == LOCALI_DT_BF16;
+    PrepVec xprep{};
+    if (decode) xprep = prep_batch(at<void>(workspace, lay.xprep), tokens, d, routed->gate.bits, bf16);
+    rc = route(router, x, x_dtype, tokens, d, input_ids, nullptr, slot_of_expert, routed->gate.n_slots,
+               idx, weights, route_slot, workspace, lay, xprep, routed->gate.bits, S(stream));
     if (rc) return rc;
-    if (tokens <= kDecodeMaxTokens)
+    if (decode)
         return run_decode(routed, shared, x, x_dtype, tokens, k, route_slot, weights, swiglu_limit,
                           fp32_swiglu, LOCALI_COMBINE_ROUNDED, at<void>(workspace, lay.hidden), out,
-                          S(stream));
+                          S(stream), 3, at<void>(workspace, lay.xprep), true,
+                          at<void>(workspace, lay.hprep));
     return run_grouped(routed, shared, x, x_dtype, tokens, k, E, route_slot, weights, swiglu_limit,
                        fp32_swiglu, LOCALI_COMBINE_ROUNDED, out, workspace, lay, S(stream));
 }

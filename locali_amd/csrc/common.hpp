@@ -21,7 +21,18 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace locali {
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -94,6 +105,7 @@ template <int BITS, bool BF16> struct Pairs;
 
 // 2-bit, bf16 magic 128: fields 0,2,4 of the mantissa; shifts 0, 6, 12.
 template <> struct Pairs<2, true> {
+    static constexpr bool kSubtract = false;  // magic removed per group
     static constexpr int kCount = 8;
     static constexpr uint32_t kMagic = 0x43004300u;
     static constexpr float kMagicValue = 128.0f;
@@ -106,6 +118,7 @@ template <> struct Pairs<2, true> {
 
 // 2-bit, fp16 magic 1024: fields 0,2,4,6,8; shifts 0, 10.
 template <> struct Pairs<2, false> {
+    static constexpr bool kSubtract = true;   // magic removed by v_pk_add_f16
     static constexpr int kCount = 8;
     static constexpr uint32_t kMagic = 0x64006400u;
     static constexpr float kMagicValue = 1024.0f;
@@ -118,6 +131,7 @@ template <> struct Pairs<2, false> {
 
 // 4-bit, bf16 magic 128: only bits 0-3 fit; shifts 0, 4, 8, 12.
 template <> struct Pairs<4, true> {
+    static constexpr bool kSubtract = false;  // magic removed per group
     static constexpr int kCount = 4;
     static constexpr uint32_t kMagic = 0x43004300u;
     static constexpr float kMagicValue = 128.0f;
@@ -129,6 +143,7 @@ template <> struct Pairs<4, true> {
 
 // 4-bit, fp16 magic 1024: bits 0-3 and 4-7; shifts 0, 8.
 template <> struct Pairs<4, false> {
+    static constexpr bool kSubtract = true;   // magic removed by v_pk_add_f16
     static constexpr int kCount = 4;
     static constexpr uint32_t kMagic = 0x64006400u;
     static constexpr float kMagicValue = 1024.0f;
@@ -141,6 +156,7 @@ template <> struct Pairs<4, false> {
 // 8-bit, bf16: a byte does not fit the 7-bit mantissa, so each byte is two
 // nibble fields (the high nibble weighs 16). Values 0..3 of the word.
 template <> struct Pairs<8, true> {
+    static constexpr bool kSubtract = false;  // magic removed per group
     static constexpr int kCount = 4;
     static constexpr uint32_t kMagic = 0x43004300u;
     static constexpr float kMagicValue = 128.0f;
@@ -152,6 +168,7 @@ template <> struct Pairs<8, true> {
 
 // 8-bit, fp16 magic 1024: a whole byte fits; shifts 0, 8.
 template <> struct Pairs<8, false> {
+    static constexpr bool kSubtract = true;   // magic removed by v_pk_add_f16
     static constexpr int kCount = 2;
     static constexpr uint32_t kMagic = 0x64006400u;
     static constexpr float kMagicValue = 1024.0f;
@@ -159,19 +176,53 @@ template <> struct Pairs<8, false> {
                                           {8, 0x00FF00FFu, 1, 3, 0, 0}};
 };
 
-__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t magic) {
-    return (v & mask) | magic;   // single v_and_or_b32
+// (v & mask) | magic in one v_and_or_b32. GFX9 VOP3 encodings take no
+// literal constants and read at most one SGPR, so the compiler splits the
+// expression into v_and + v_or when both are immediates; here the mask rides
+// in an SGPR and the magic in a VGPR materialised once per kernel (magic_vgpr).
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t magic_v) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(magic_v));
+    return r;
+}
+
+// A VGPR holding `value` that the compiler cannot see through (so it is kept
+// in one register instead of being re-materialised at every use).
+__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t value) {
+    uint32_t r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(value));
+    return r;
+}
+
+// Stop the instruction scheduler from moving anything across this point
+// (used to keep every load of a wave issued before its arithmetic).
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Expand pair p of a packed word into two 16-bit floats. For fp16 the magic
+// is removed right away with one exact packed subtraction (the result is a
+// small integer times a power of two), which keeps the 1024 offset out of the
+// fp32 accumulator; for bf16 the offset (128) is removed once per group.
+template <int BITS, bool BF16, int p>
+__device__ __forceinline__ uint32_t expand_pair(uint32_t w, uint32_t magic_v) {
+    using P = Pairs<BITS, BF16>;
+    constexpr PairSpec ps = P::kSpec[p];
+    const uint32_t a = and_or(w >> ps.shift, ps.mask, magic_v);
+    if constexpr (P::kSubtract) {
+        const f16x2_t magic = {static_cast<_Float16>(-1024.0f), static_cast<_Float16>(-1024.0f)};
+        return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, a) + magic);
+    } else {
+        return a;
+    }
 }
 
 // Dot of one packed word against its pre-scaled activation pairs.
 template <int BITS, bool BF16>
-__device__ __forceinline__ float word_dot(uint32_t w, const uint32_t *xp, float acc) {
+__device__ __forceinline__ float word_dot(uint32_t w, const uint32_t *xp, float acc,
+                                          uint32_t magic_v) {
     using P = Pairs<BITS, BF16>;
-#pragma unroll
-    for (int p = 0; p < P::kCount; ++p) {
-        const uint32_t a = and_or(w >> P::kSpec[p].shift, P::kSpec[p].mask, P::kMagic);
-        acc = dot2<BF16>(a, xp[p], acc);
-    }
+    static_for<0, P::kCount>([&](auto p) {
+        acc = dot2<BF16>(expand_pair<BITS, BF16, decltype(p)::value>(w, magic_v), xp[p], acc);
+    });
     return acc;
 }
 

@@ -1,14 +1,21 @@
 // Decode-path expert kernels: one (token, expert) route per GEMV.
 //
-//   gateup_route_kernel   h[r, n] = swiglu(up_r(x_t)[n], gate_r(x_t)[n])
-//                         for every route r (routed top-k entries, then one
-//                         shared-expert route per token), streaming the gate
-//                         and up rows of the route's arena slot.
-//   down_combine_kernel   out[t, d] = sum_j round(round(down_j(h_j)[d]) * w_j)
-//                         (+ shared) for a block of output rows d; all routes
-//                         of token t run in the same workgroup (one wave per
-//                         route) and are combined through LDS in route order,
-//                         so the result is deterministic without atomics.
+//   gateup_route_kernel   h[r, n] = swiglu(up_r(x_t)[n], gate_r(x_t)[n]) for
+//                         every route r (routed top-k entries, then one
+//                         shared-expert route per token). A workgroup of 8
+//                         waves covers RB consecutive rows of one route; each
+//                         lane loads its slice of the token's prepared
+//                         activations (written once per token by the router
+//                         or the prep kernel) and streams J rows of the
+//                         slot's gate and up matrices. The epilogue writes h
+//                         and, because the workgroup owns whole words of the
+//                         down projection's input, also h's prepared form.
+//   down_combine_kernel   out[t, d] = round(sum_j round(round(y_j[d]) * w_j))
+//                         (+ shared, rounded) for RB output rows d: one wave
+//                         per route of token t streams the route's down rows
+//                         against its prepared hidden vector; the route
+//                         results meet in LDS and are combined in route
+//                         order -- deterministic, no atomics.
 // Reference arithmetic: dsv4_arena.py:168-235 (expert), arena.py:619-624 and
 // dsv4_engine.py:259 (combine and shared expert).
 #pragma once
@@ -18,6 +25,8 @@
 
 namespace locali {
 
+constexpr int kGateUpWaves = 8;
+
 __device__ __forceinline__ void route_of(const RouteArgs &ra, int r, int &token, int &slot,
                                          bool &shared) {
     const int routed = ra.tokens * ra.top_k;
@@ -26,14 +35,18 @@ __device__ __forceinline__ void route_of(const RouteArgs &ra, int r, int &token,
     slot = shared ? 0 : ra.route_slot[r];
 }
 
+template <int LPR>
+constexpr int gateup_rows_per_wave_load() { return LPR >= 16 ? 8 : LPR / 2; }
+
 // ---------------------------------------------------------------------------
 template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J>
-__global__ __launch_bounds__(256) void gateup_route_kernel(RouteArgs ra, QProj gate, QProj up,
-                                                            QProj sgate, QProj sup,
-                                                            uint16_t *__restrict__ h,
-                                                            float limit, int fp32_swiglu) {
+__global__ __launch_bounds__(64 * kGateUpWaves) void gateup_route_kernel(
+    RouteArgs ra, QProj gate, QProj up, QProj sgate, QProj sup, PrepVec xin, uint16_t *__restrict__ h,
+    PrepVec hout, int down_bits, float limit, int fp32_swiglu) {
     using G = Geom<BITS, CPL, LPR, GPC>;
-    constexpr int RPW = J * G::kRPL;           // rows per wave
+    constexpr int RPW = J * G::kRPL;              // rows per wave
+    constexpr int RB = kGateUpWaves * RPW;        // rows per workgroup
+    __shared__ __align__(16) uint16_t hs[RB];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int lane_in_row = lane % LPR;
@@ -45,101 +58,120 @@ __global__ __launch_bounds__(256) void gateup_route_kernel(RouteArgs ra, QProj g
     const QProj &pg = shared ? sgate : gate;
     const QProj &pu = shared ? sup : up;
     const int N = pg.rows, K = pg.cols;
-    const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * RPW;
-    if (row0 >= N) return;
+    const int n0 = blockIdx.x * RB;
+    const int row0 = n0 + wave * RPW;
+    const bool active = row0 < N;
     const bool valid_slot = slot >= 0 && slot < pg.n_slots;
-
-    XVec<BITS, BF16, CPL, GPC> xv;
-    load_xvec<BITS, BF16, CPL, LPR, GPC>(xv, ra.x + static_cast<int64_t>(token) * K, lane_in_row);
-
+    const int sl = valid_slot ? slot : 0;
     const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;   // words per row
     const int gpr = K / pg.group;                               // groups per row
-    const int sl = valid_slot ? slot : 0;
-    const uint32_t *gw = pg.w + sl * pg.w_slot;
-    const uint32_t *uw = pu.w + sl * pu.w_slot;
-    const uint16_t *gs = pg.s + sl * pg.m_slot, *gb = pg.b + sl * pg.m_slot;
-    const uint16_t *us = pu.s + sl * pu.m_slot, *ub = pu.b + sl * pu.m_slot;
 
-    RowChunks<CPL> wg[J], wu[J];
+    if (active) {
+        const uint32_t *gw = pg.w + sl * pg.w_slot, *uw = pu.w + sl * pu.w_slot;
+        const uint16_t *gs = pg.s + sl * pg.m_slot, *gb = pg.b + sl * pg.m_slot;
+        const uint16_t *us = pu.s + sl * pu.m_slot, *ub = pu.b + sl * pu.m_slot;
+        // Activations first: loads retire in issue order, so rows can be
+        // consumed as they land only if the activations are already in.
+        XVec<BITS, BF16, CPL, GPC> xv;
+        load_xvec_global<BITS, BF16, CPL, LPR, GPC>(xv, xin.pairs + token * xin.pairs_stride,
+                                                    xin.parts + token * xin.parts_stride,
+                                                    lane_in_row);
+        sched_fence();
+        RowData<CPL, GPC> wg[J], wu[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-        load_row<BITS, CPL, LPR>(wg[j], gw + row * wpr, lane_in_row);
-        load_row<BITS, CPL, LPR>(wu[j], uw + row * wpr, lane_in_row);
-    }
-    float v[2 * J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-        v[j] = row_partial<BITS, BF16, CPL, LPR, GPC>(wg[j], xv, gs + row * gpr, gb + row * gpr,
-                                                       pg.group, lane_in_row);
-        v[J + j] = row_partial<BITS, BF16, CPL, LPR, GPC>(wu[j], xv, us + row * gpr,
-                                                           ub + row * gpr, pu.group, lane_in_row);
-    }
-    reduce_transposed<2 * J, LPR>(v, lane);
-    // lane holds value index vi = (lane % LPR) / (LPR / 2J): gates first.
-    const float partner = shfl_xor(v[0], LPR / 2);
-    constexpr int span = LPR / (2 * J);
-    const int vi = lane_in_row / span;
-    if (vi < J && (lane_in_row % span) == 0) {
-        const int row = row0 + vi * G::kRPL + row_sub;
-        if (row < N) {
-            uint16_t out = 0;
-            if (valid_slot)
-                out = swiglu16<BF16>(round16<BF16>(v[0]), round16<BF16>(partner), limit,
-                                     fp32_swiglu != 0);
-            h[static_cast<int64_t>(r) * N + row] = out;
+        for (int j = 0; j < J; ++j) {
+            const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
+            load_row<BITS, CPL, LPR, GPC>(wg[j], gw + row * wpr, gs + row * gpr, gb + row * gpr,
+                                          pg.group, lane_in_row);
+            load_row<BITS, CPL, LPR, GPC>(wu[j], uw + row * wpr, us + row * gpr, ub + row * gpr,
+                                          pu.group, lane_in_row);
         }
+        sched_fence();
+        const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
+        float v[2 * J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            v[j] = row_partial<BITS, BF16, CPL, LPR, GPC>(wg[j], xv, magic_v);
+            v[J + j] = row_partial<BITS, BF16, CPL, LPR, GPC>(wu[j], xv, magic_v);
+        }
+        reduce_transposed<2 * J, LPR>(v, lane);
+        // lane holds value index vi = (lane % LPR) / (LPR / 2J): gates first.
+        const float partner = shfl_xor(v[0], LPR / 2);
+        constexpr int span = LPR / (2 * J);
+        const int vi = lane_in_row / span;
+        if (vi < J && (lane_in_row % span) == 0) {
+            const int row = row0 + vi * G::kRPL + row_sub;
+            if (row < N) {
+                uint16_t out = 0;
+                if (valid_slot)
+                    out = swiglu16<BF16>(round16<BF16>(v[0]), round16<BF16>(partner), limit,
+                                         fp32_swiglu != 0);
+                h[static_cast<int64_t>(r) * N + row] = out;
+                hs[row - n0] = out;
+            }
+        }
+    }
+    if (!hout.pairs) return;                      // uniform across the workgroup
+    __syncthreads();
+    // Prepared form of h for the down projection: this workgroup owns the
+    // words covering rows [n0, n0 + RB).
+    const int vpw = 32 / down_bits;
+    const int nrows = min(RB, N - n0);
+    const int words = nrows / vpw;
+    if (static_cast<int>(threadIdx.x) < words) {
+        const int unit = n0 / vpw + threadIdx.x;
+        prep_unit_at<BF16>(down_bits, hs + threadIdx.x * vpw,
+                           hout.pairs + r * hout.pairs_stride + unit * pairs_per_word<BF16>(down_bits),
+                           hout.parts + r * hout.parts_stride + unit);
     }
 }
 
 // ---------------------------------------------------------------------------
-constexpr int kMaxRoutesPerToken = 16;
-
-template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J>
-__global__ __launch_bounds__(1024) void down_combine_kernel(RouteArgs ra, QProj down, QProj sdown,
-                                                             const uint16_t *__restrict__ h,
-                                                             CombineArgs ca) {
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, QProj down,
+                                                                   QProj sdown, PrepVec hin,
+                                                                   CombineArgs ca) {
     using G = Geom<BITS, CPL, LPR, GPC>;
-    constexpr int RPW = J * G::kRPL;           // rows per workgroup (all waves share them)
-    __shared__ float ylds[kMaxRoutesPerToken][RPW];
+    constexpr int RB = J * G::kRPL;               // rows per workgroup
+    __shared__ float ylds[WAVES][RB];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int nwaves = blockDim.x >> 6;
     const int lane_in_row = lane % LPR;
     const int row_sub = lane / LPR;
     const int t = blockIdx.y;
     const int N = down.rows, K = down.cols;
-    const int row0 = blockIdx.x * RPW;
     const int per_token = ra.top_k + ra.n_shared;
     const int routed = ra.tokens * ra.top_k;
+    const int row0 = blockIdx.x * RB;
     const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
     const int gpr = K / down.group;
 
-    for (int j = wave; j < per_token; j += nwaves) {
-        const bool shared = j >= ra.top_k;
-        const int r = shared ? routed + t : t * ra.top_k + j;
-        const int slot = shared ? 0 : ra.route_slot[r];
-        const QProj &p = shared ? sdown : down;
+    if (wave < per_token) {
+        const int j = wave;
+        const bool sh = j >= ra.top_k;
+        const int r = sh ? routed + t : t * ra.top_k + j;
+        const int slot = sh ? 0 : ra.route_slot[r];
+        const QProj &p = sh ? sdown : down;
         const bool valid_slot = slot >= 0 && slot < p.n_slots;
         const int sl = valid_slot ? slot : 0;
-        XVec<BITS, BF16, CPL, GPC> xv;
-        load_xvec<BITS, BF16, CPL, LPR, GPC>(xv, h + static_cast<int64_t>(r) * K, lane_in_row);
         const uint32_t *w = p.w + sl * p.w_slot;
         const uint16_t *s = p.s + sl * p.m_slot, *b = p.b + sl * p.m_slot;
-        RowChunks<CPL> rc[J];
+        XVec<BITS, BF16, CPL, GPC> xv;
+        load_xvec_global<BITS, BF16, CPL, LPR, GPC>(xv, hin.pairs + r * hin.pairs_stride,
+                                                    hin.parts + r * hin.parts_stride, lane_in_row);
+        sched_fence();
+        RowData<CPL, GPC> rd[J];
 #pragma unroll
         for (int q = 0; q < J; ++q) {
             const int row = min(row0 + q * G::kRPL + row_sub, N - 1);
-            load_row<BITS, CPL, LPR>(rc[q], w + row * wpr, lane_in_row);
+            load_row<BITS, CPL, LPR, GPC>(rd[q], w + row * wpr, s + row * gpr, b + row * gpr, p.group,
+                                          lane_in_row);
         }
+        sched_fence();
+        const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
         float v[J];
 #pragma unroll
-        for (int q = 0; q < J; ++q) {
-            const int row = min(row0 + q * G::kRPL + row_sub, N - 1);
-            v[q] = row_partial<BITS, BF16, CPL, LPR, GPC>(rc[q], xv, s + row * gpr, b + row * gpr,
-                                                          p.group, lane_in_row);
-        }
+        for (int q = 0; q < J; ++q) v[q] = row_partial<BITS, BF16, CPL, LPR, GPC>(rd[q], xv, magic_v);
         reduce_transposed<J, LPR>(v, lane);
         constexpr int span = LPR / J;
         const int vi = lane_in_row / span;
@@ -147,7 +179,7 @@ __global__ __launch_bounds__(1024) void down_combine_kernel(RouteArgs ra, QProj 
             ylds[j][vi * G::kRPL + row_sub] = valid_slot ? round16<BF16>(v[0]) : 0.f;
     }
     __syncthreads();
-    for (int q = threadIdx.x; q < RPW; q += blockDim.x) {
+    for (int q = threadIdx.x; q < RB; q += blockDim.x) {
         const int row = row0 + q;
         if (row >= N) continue;
         float acc = 0.f;
@@ -169,26 +201,34 @@ __global__ __launch_bounds__(1024) void down_combine_kernel(RouteArgs ra, QProj 
 // ---------------------------------------------------------------------------
 template <int BITS, bool BF16, int CPL, int LPR, int GPC>
 hipError_t launch_gateup_t(const DecodeLaunch &L, hipStream_t st) {
-    constexpr int J = 4;
+    constexpr int J = gateup_rows_per_wave_load<LPR>();
     using G = Geom<BITS, CPL, LPR, GPC>;
-    constexpr int waves = 4;
-    const int rows_per_block = waves * J * G::kRPL;
+    const int rows_per_block = kGateUpWaves * J * G::kRPL;
+    // the epilogue prepares whole words of the down input
+    if (L.hprep.pairs && rows_per_block % (32 / L.down.bits)) return hipErrorInvalidValue;
     dim3 grid((L.gate.rows + rows_per_block - 1) / rows_per_block, L.routes);
-    hipLaunchKernelGGL((gateup_route_kernel<BITS, BF16, CPL, LPR, GPC, J>), grid, dim3(64 * waves),
-                       0, st, L.ra, L.gate, L.up, L.sgate, L.sup, L.h, L.limit, L.fp32_swiglu);
+    hipLaunchKernelGGL((gateup_route_kernel<BITS, BF16, CPL, LPR, GPC, J>), grid,
+                       dim3(64 * kGateUpWaves), 0, st, L.ra, L.gate, L.up, L.sgate, L.sup, L.xprep,
+                       L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu);
     return hipGetLastError();
 }
 
 template <int BITS, bool BF16, int CPL, int LPR, int GPC>
 hipError_t launch_down_t(const DecodeLaunch &L, hipStream_t st) {
-    constexpr int J = (LPR >= 8) ? 8 : LPR;
+    constexpr int J = LPR >= 8 ? 8 : LPR;
     using G = Geom<BITS, CPL, LPR, GPC>;
-    const int rows_per_block = J * G::kRPL;
     const int per_token = L.ra.top_k + L.ra.n_shared;
-    const int waves = per_token < kMaxRoutesPerToken ? per_token : kMaxRoutesPerToken;
+    const int rows_per_block = J * G::kRPL;
     dim3 grid((L.down.rows + rows_per_block - 1) / rows_per_block, L.ra.tokens);
-    hipLaunchKernelGGL((down_combine_kernel<BITS, BF16, CPL, LPR, GPC, J>), grid, dim3(64 * waves),
-                       0, st, L.ra, L.down, L.sdown, L.h, L.ca);
+    if (per_token <= 8) {
+        hipLaunchKernelGGL((down_combine_kernel<BITS, BF16, CPL, LPR, GPC, J, 8>), grid,
+                           dim3(64 * per_token), 0, st, L.ra, L.down, L.sdown, L.hprep, L.ca);
+    } else if (per_token <= 16) {
+        hipLaunchKernelGGL((down_combine_kernel<BITS, BF16, CPL, LPR, GPC, J, 16>), grid,
+                           dim3(64 * per_token), 0, st, L.ra, L.down, L.sdown, L.hprep, L.ca);
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

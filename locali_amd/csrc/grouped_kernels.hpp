@@ -27,19 +27,16 @@ __device__ __forceinline__ int tile_token(const TileArgs &ta, bool shared, int p
 }
 
 template <int BITS, bool BF16, int CPL, int LPR, int GPC, int TT>
-__device__ __forceinline__ void row_partial_multi(const RowChunks<CPL> &rc,
+__device__ __forceinline__ void row_partial_multi(const RowData<CPL, GPC> &rd,
                                                   const XVec<BITS, BF16, CPL, GPC> (&xv)[TT],
-                                                  const uint16_t *__restrict__ srow,
-                                                  const uint16_t *__restrict__ brow, int group,
-                                                  int lane_in_row, float (&out)[TT]) {
+                                                  float (&out)[TT], uint32_t magic_v) {
     using G = Geom<BITS, CPL, LPR, GPC>;
     using P = Pairs<BITS, BF16>;
 #pragma unroll
     for (int q = 0; q < TT; ++q) out[q] = 0.f;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-        const uint32_t words[4] = {rc.c[i][0], rc.c[i][1], rc.c[i][2], rc.c[i][3]};
-        const int k0 = (lane_in_row + LPR * i) * G::kVPC;
+        const uint32_t words[4] = {rd.c[i][0], rd.c[i][1], rd.c[i][2], rd.c[i][3]};
 #pragma unroll
         for (int gp = 0; gp < GPC; ++gp) {
             float d[TT];
@@ -47,16 +44,15 @@ __device__ __forceinline__ void row_partial_multi(const RowChunks<CPL> &rc,
             for (int q = 0; q < TT; ++q) d[q] = 0.f;
 #pragma unroll
             for (int wd = gp * G::kWPG; wd < (gp + 1) * G::kWPG; ++wd) {
-#pragma unroll
-                for (int p = 0; p < P::kCount; ++p) {
-                    const uint32_t a = and_or(words[wd] >> P::kSpec[p].shift, P::kSpec[p].mask, P::kMagic);
+                static_for<0, P::kCount>([&](auto pc) {
+                    constexpr int p = decltype(pc)::value;
+                    const uint32_t a = expand_pair<BITS, BF16, p>(words[wd], magic_v);
 #pragma unroll
                     for (int q = 0; q < TT; ++q) d[q] = dot2<BF16>(a, xv[q].xp[i][wd][p], d[q]);
-                }
+                });
             }
-            const int g = (k0 + gp * G::kWPG * G::kVPW) / group;
-            const float sc = to_float<BF16>(srow[g]);
-            const float bi = to_float<BF16>(brow[g]);
+            const float sc = to_float<BF16>(rd.s[i][gp]);
+            const float bi = to_float<BF16>(rd.b[i][gp]);
 #pragma unroll
             for (int q = 0; q < TT; ++q)
                 out[q] = fmaf(sc, d[q] - xv[q].corr[i][gp], fmaf(bi, xv[q].xs[i][gp], out[q]));
@@ -64,15 +60,33 @@ __device__ __forceinline__ void row_partial_multi(const RowChunks<CPL> &rc,
     }
 }
 
+constexpr int kGroupedWaves = 8;
+
+// Prepare the tile's TT input vectors (rows of `src` selected by tile
+// positions) into LDS; unused token slots repeat the last valid one.
+template <int BITS, bool BF16, int CPL, int LPR, int TT, typename RowOf>
+__device__ __forceinline__ void prep_tile(XLds<BITS, BF16, CPL, LPR> (&xl)[TT], RowOf row_of,
+                                          int count) {
+    constexpr int VPC = 128 / BITS, VPW = 32 / BITS;
+    constexpr int units = LPR * CPL * 4;
+    for (int u = threadIdx.x; u < TT * units; u += blockDim.x) {
+        const int q = u / units, uu = u % units;
+        const int ln = uu % LPR, wd = (uu / LPR) % 4, i = uu / (LPR * 4);
+        const int k0 = (ln + LPR * i) * VPC + wd * VPW;
+        prep_word<BITS, BF16>(row_of(min(q, count - 1)) + k0, &xl[q].pairs[i][wd][0][ln], LPR,
+                              xl[q].part[i][wd][ln]);
+    }
+}
+
 template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int TT>
-__global__ __launch_bounds__(256) void gateup_grouped_kernel(TileArgs ta, QProj gate, QProj up,
-                                                              QProj sgate, QProj sup,
-                                                              uint16_t *__restrict__ h, float limit,
-                                                              int fp32_swiglu) {
+__global__ __launch_bounds__(64 * kGroupedWaves) void gateup_grouped_kernel(
+    TileArgs ta, QProj gate, QProj up, QProj sgate, QProj sup, uint16_t *__restrict__ h, float limit,
+    int fp32_swiglu) {
     using G = Geom<BITS, CPL, LPR, GPC>;
     constexpr int RPW = J * G::kRPL;
     constexpr int NV = 2 * J * TT;
     static_assert(NV <= LPR, "values per lane exceed lanes per row");
+    __shared__ XLds<BITS, BF16, CPL, LPR> xl[TT];
     const int tile = blockIdx.y;
     if (tile >= *ta.n_tiles) return;
     const int slot = ta.tiles[4 * tile], first = ta.tiles[4 * tile + 1];
@@ -86,37 +100,38 @@ __global__ __launch_bounds__(256) void gateup_grouped_kernel(TileArgs ta, QProj 
     const int N = pg.rows, K = pg.cols;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lane_in_row = lane % LPR, row_sub = lane / LPR;
+    prep_tile<BITS, BF16, CPL, LPR, TT>(
+        xl, [&](int q) { return ta.x + static_cast<int64_t>(tile_token(ta, shared, first + q)) * K; },
+        count);
+    __syncthreads();
     const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * RPW;
     if (row0 >= N) return;
     const int sl = shared ? 0 : slot;
-
-    XVec<BITS, BF16, CPL, GPC> xv[TT];
-#pragma unroll
-    for (int q = 0; q < TT; ++q) {
-        const int tok = tile_token(ta, shared, first + min(q, count - 1));
-        load_xvec<BITS, BF16, CPL, LPR, GPC>(xv[q], ta.x + static_cast<int64_t>(tok) * K, lane_in_row);
-    }
     const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
     const int gpr = K / pg.group;
     const uint32_t *gw = pg.w + sl * pg.w_slot, *uw = pu.w + sl * pu.w_slot;
     const uint16_t *gs = pg.s + sl * pg.m_slot, *gb = pg.b + sl * pg.m_slot;
     const uint16_t *us = pu.s + sl * pu.m_slot, *ub = pu.b + sl * pu.m_slot;
-    RowChunks<CPL> wg[J], wu[J];
+    RowData<CPL, GPC> wg[J], wu[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-        load_row<BITS, CPL, LPR>(wg[j], gw + row * wpr, lane_in_row);
-        load_row<BITS, CPL, LPR>(wu[j], uw + row * wpr, lane_in_row);
+        load_row<BITS, CPL, LPR, GPC>(wg[j], gw + row * wpr, gs + row * gpr, gb + row * gpr,
+                                      pg.group, lane_in_row);
+        load_row<BITS, CPL, LPR, GPC>(wu[j], uw + row * wpr, us + row * gpr, ub + row * gpr,
+                                      pu.group, lane_in_row);
     }
+    XVec<BITS, BF16, CPL, GPC> xv[TT];
+#pragma unroll
+    for (int q = 0; q < TT; ++q) load_xvec_lds<BITS, BF16, CPL, LPR, GPC>(xv[q], xl[q], lane_in_row);
+    sched_fence();
+    const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
     float v[NV];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
         float pgq[TT], puq[TT];
-        row_partial_multi<BITS, BF16, CPL, LPR, GPC, TT>(wg[j], xv, gs + row * gpr, gb + row * gpr,
-                                                         pg.group, lane_in_row, pgq);
-        row_partial_multi<BITS, BF16, CPL, LPR, GPC, TT>(wu[j], xv, us + row * gpr, ub + row * gpr,
-                                                         pu.group, lane_in_row, puq);
+        row_partial_multi<BITS, BF16, CPL, LPR, GPC, TT>(wg[j], xv, pgq, magic_v);
+        row_partial_multi<BITS, BF16, CPL, LPR, GPC, TT>(wu[j], xv, puq, magic_v);
 #pragma unroll
         for (int q = 0; q < TT; ++q) {
             v[j * TT + q] = pgq[q];
@@ -137,13 +152,13 @@ __global__ __launch_bounds__(256) void gateup_grouped_kernel(TileArgs ta, QProj 
 }
 
 template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int TT>
-__global__ __launch_bounds__(256) void down_grouped_kernel(TileArgs ta, QProj down, QProj sdown,
-                                                            const uint16_t *__restrict__ h,
-                                                            uint16_t *__restrict__ y) {
+__global__ __launch_bounds__(64 * kGroupedWaves) void down_grouped_kernel(
+    TileArgs ta, QProj down, QProj sdown, const uint16_t *__restrict__ h, uint16_t *__restrict__ y) {
     using G = Geom<BITS, CPL, LPR, GPC>;
     constexpr int RPW = J * G::kRPL;
     constexpr int NV = J * TT;
     static_assert(NV <= LPR, "values per lane exceed lanes per row");
+    __shared__ XLds<BITS, BF16, CPL, LPR> xl[TT];
     const int tile = blockIdx.y;
     if (tile >= *ta.n_tiles) return;
     const int slot = ta.tiles[4 * tile], first = ta.tiles[4 * tile + 1];
@@ -156,32 +171,33 @@ __global__ __launch_bounds__(256) void down_grouped_kernel(TileArgs ta, QProj do
     const int N = p.rows, K = p.cols;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lane_in_row = lane % LPR, row_sub = lane / LPR;
+    prep_tile<BITS, BF16, CPL, LPR, TT>(
+        xl, [&](int q) { return h + static_cast<int64_t>(first + q) * K; }, count);
+    __syncthreads();
     const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * RPW;
     if (row0 >= N) return;
     const int sl = shared ? 0 : slot;
-
-    XVec<BITS, BF16, CPL, GPC> xv[TT];
-#pragma unroll
-    for (int q = 0; q < TT; ++q)
-        load_xvec<BITS, BF16, CPL, LPR, GPC>(
-            xv[q], h + static_cast<int64_t>(first + min(q, count - 1)) * K, lane_in_row);
     const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
     const int gpr = K / p.group;
     const uint32_t *w = p.w + sl * p.w_slot;
     const uint16_t *s = p.s + sl * p.m_slot, *b = p.b + sl * p.m_slot;
-    RowChunks<CPL> rc[J];
+    RowData<CPL, GPC> rd[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-        load_row<BITS, CPL, LPR>(rc[j], w + row * wpr, lane_in_row);
+        load_row<BITS, CPL, LPR, GPC>(rd[j], w + row * wpr, s + row * gpr, b + row * gpr, p.group,
+                                      lane_in_row);
     }
+    XVec<BITS, BF16, CPL, GPC> xv[TT];
+#pragma unroll
+    for (int q = 0; q < TT; ++q) load_xvec_lds<BITS, BF16, CPL, LPR, GPC>(xv[q], xl[q], lane_in_row);
+    sched_fence();
+    const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
     float v[NV];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
         float pq[TT];
-        row_partial_multi<BITS, BF16, CPL, LPR, GPC, TT>(rc[j], xv, s + row * gpr, b + row * gpr,
-                                                         p.group, lane_in_row, pq);
+        row_partial_multi<BITS, BF16, CPL, LPR, GPC, TT>(rd[j], xv, pq, magic_v);
 #pragma unroll
         for (int q = 0; q < TT; ++q) v[j * TT + q] = pq[q];
     }
@@ -213,7 +229,7 @@ template <int BITS, bool BF16, int CPL, int LPR, int GPC>
 hipError_t launch_grouped_t(int which, const GroupedKernelLaunch &L, hipStream_t st) {
     constexpr int TT = kGroupedTileTokens;
     using G = Geom<BITS, CPL, LPR, GPC>;
-    constexpr int waves = 4;
+    constexpr int waves = kGroupedWaves;
     if (which == 0) {
         constexpr int J = (LPR >= 4 * TT) ? 2 : 1;
         const int rpb = waves * J * G::kRPL;

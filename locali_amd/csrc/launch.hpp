@@ -24,9 +24,19 @@ struct CombineArgs {
     int32_t mode;               // 0: products rounded (single tier), 1: fp32 products
 };
 
+// A batch of prepared vectors (see qgemv.hpp): vector v's pairs start at
+// pairs + v * pairs_stride and its partial sums at parts + v * parts_stride.
+struct PrepVec {
+    uint32_t *pairs;
+    float2 *parts;
+    int64_t pairs_stride, parts_stride;
+};
+
 // ---- decode path -----------------------------------------------------------
 struct DecodeLaunch {
     RouteArgs ra;
+    PrepVec xprep;              // prepared activations, one per token (gate/up geometry)
+    PrepVec hprep;              // prepared hidden vectors, one per route (down geometry)
     int32_t routes;             // tokens * top_k + n_shared * tokens
     bool bf16;
     QProj gate, up, down;       // routed arena
@@ -38,6 +48,9 @@ struct DecodeLaunch {
 };
 
 hipError_t launch_gateup_decode(const DecodeLaunch &L, hipStream_t st);
+// Prepare n_vec vectors of K values (rows of v) for a projection of `bits`-bit codes.
+hipError_t launch_prep_vectors(const uint16_t *v, int n_vec, int K, int bits, bool bf16,
+                               PrepVec out, hipStream_t st);
 hipError_t launch_down_combine_decode(const DecodeLaunch &L, hipStream_t st);
 int chunks_per_row(const QProj &p);
 int group_parts(const QProj &p);
@@ -64,6 +77,8 @@ struct RouterLaunch {
     float *logits;              // workspace [tokens, E]
     uint32_t *counter;          // workspace, zero between calls
     const float *logits_in;     // optional precomputed logits [tokens, E]
+    PrepVec xprep;              // optional: also prepare x for a projection of
+    int32_t prep_bits;          //   prep_bits-bit codes (pairs null = skip)
 };
 
 hipError_t launch_router(const RouterLaunch &L, hipStream_t st);

@@ -1,4 +1,4 @@
-// Wave-level affine-quantised GEMV core shared by the decode kernels.
+// Wave-level affine-quantised GEMV core shared by the expert kernels.
 //
 // Lane geometry for a projection with K inputs at BITS per code:
 //   VPC = 128 / BITS values per 16-byte chunk, CPR = K / VPC chunks per row.
@@ -6,8 +6,13 @@
 //   covered by one wave-wide 16-byte load; each lane streams CPL = CPR / LPR
 //   chunks of its row (chunk = lane_in_row + LPR * i), so a load instruction
 //   reads 1 KiB of contiguous weights when LPR = 64.
-// The activation slice a lane needs never changes across rows, so it is
-// loaded once, pre-scaled and packed into registers (XVec).
+//
+// The activation slice a lane needs never changes across rows. A workgroup
+// prepares it once in LDS (prep_vector: pre-scaled 16-bit pairs in the order
+// the weight pairs are expanded, plus per-word partial sums), then every
+// wave copies its lanes' slice into registers (XVec) and streams rows.
+// All of a wave's weight words and group metadata are requested before any
+// arithmetic, so the memory round trips of its rows overlap.
 #pragma once
 
 #include "common.hpp"
@@ -41,108 +46,236 @@ struct XVec {
     float xs[CPL][GPC];     // plain sum of values per group part
 };
 
-template <bool BF16>
-__device__ __forceinline__ uint16_t scale_pow2(uint16_t v, int e) {
-    if (e == 0) return v;
-    return from_float<BF16>(ldexpf(to_float<BF16>(v), e));
+// LDS image of one prepared vector, lane-minor so that lane reads are
+// conflict-free: pairs[i][wd][p][lane], part[i][wd][lane] = (corr, xs).
+template <int BITS, bool BF16, int CPL, int LPR>
+struct XLds {
+    using P = Pairs<BITS, BF16>;
+    uint32_t pairs[CPL][4][P::kCount][LPR];
+    float2 part[CPL][4][LPR];
+};
+
+// 16-bit value times 2^E, exact for the powers of two used here.
+template <bool BF16, int E>
+__device__ __forceinline__ uint16_t scale_pow2(uint16_t v) {
+    if constexpr (E == 0) return v;
+    else return from_float<BF16>(ldexpf(to_float<BF16>(v), E));
 }
 
-// Load the lane's slice of a 16-bit vector (K values) into an XVec.
-template <int BITS, bool BF16, int CPL, int LPR, int GPC>
-__device__ __forceinline__ void load_xvec(XVec<BITS, BF16, CPL, GPC> &xv,
-                                          const uint16_t *__restrict__ v,
-                                          int lane_in_row) {
-    using G = Geom<BITS, CPL, LPR, GPC>;
+// Prepare one word's worth of activations (VPW values at `src`).
+template <int BITS, bool BF16>
+__device__ __forceinline__ void prep_word(const uint16_t *__restrict__ src, uint32_t *pairs,
+                                          int pair_stride, float2 &part) {
     using P = Pairs<BITS, BF16>;
+    constexpr int VPW = 32 / BITS;
+    uint16_t vals[VPW];
+    if constexpr (VPW == 16) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(src);
+        const uint4 c = *reinterpret_cast<const uint4 *>(src + 8);
+        const uint32_t ww[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            vals[2 * q] = static_cast<uint16_t>(ww[q]);
+            vals[2 * q + 1] = static_cast<uint16_t>(ww[q] >> 16);
+        }
+    } else if constexpr (VPW == 8) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(src);
+        const uint32_t ww[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            vals[2 * q] = static_cast<uint16_t>(ww[q]);
+            vals[2 * q + 1] = static_cast<uint16_t>(ww[q] >> 16);
+        }
+    } else {
+        const uint2 a = *reinterpret_cast<const uint2 *>(src);
+        const uint32_t ww[2] = {a.x, a.y};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            vals[2 * q] = static_cast<uint16_t>(ww[q]);
+            vals[2 * q + 1] = static_cast<uint16_t>(ww[q] >> 16);
+        }
+    }
+    float xs = 0.f, corr = 0.f;
+#pragma unroll
+    for (int q = 0; q < VPW; ++q) xs += to_float<BF16>(vals[q]);
+    static_for<0, P::kCount>([&](auto pc) {
+        constexpr PairSpec ps = P::kSpec[decltype(pc)::value];
+        const uint16_t lo = scale_pow2<BF16, ps.lo_xexp>(vals[ps.lo_val]);
+        const uint16_t hi = scale_pow2<BF16, ps.hi_xexp>(vals[ps.hi_val]);
+        pairs[decltype(pc)::value * pair_stride] =
+            static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+        if constexpr (!P::kSubtract)
+            corr += P::kMagicValue * (to_float<BF16>(lo) + to_float<BF16>(hi));
+    });
+    part = make_float2(corr, xs);
+}
+
+// Cooperative prep of a K-vector into LDS by `nthreads` threads.
+template <int BITS, bool BF16, int CPL, int LPR>
+__device__ __forceinline__ void prep_vector(XLds<BITS, BF16, CPL, LPR> &lds,
+                                            const uint16_t *__restrict__ v, int tid, int nthreads) {
+    constexpr int VPC = 128 / BITS, VPW = 32 / BITS;
+    constexpr int units = LPR * CPL * 4;
+    for (int u = tid; u < units; u += nthreads) {
+        const int lane = u % LPR, wd = (u / LPR) % 4, i = u / (LPR * 4);
+        const int k0 = (lane + LPR * i) * VPC + wd * VPW;
+        prep_word<BITS, BF16>(v + k0, &lds.pairs[i][wd][0][lane], LPR, lds.part[i][wd][lane]);
+    }
+}
+
+template <int BITS, bool BF16, int CPL, int LPR, int GPC>
+__device__ __forceinline__ void load_xvec_lds(XVec<BITS, BF16, CPL, GPC> &xv,
+                                              const XLds<BITS, BF16, CPL, LPR> &lds,
+                                              int lane_in_row) {
+    using P = Pairs<BITS, BF16>;
+    constexpr int WPG = 4 / GPC;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-        const int k0 = (lane_in_row + LPR * i) * G::kVPC;
 #pragma unroll
-        for (int gp = 0; gp < GPC; ++gp) { xv.corr[i][gp] = 0.f; xv.xs[i][gp] = 0.f; }
+        for (int gp = 0; gp < GPC; ++gp) {
+            float c = 0.f, s = 0.f;
 #pragma unroll
-        for (int wd = 0; wd < 4; ++wd) {
-            uint16_t vals[G::kVPW];
-            const uint16_t *src = v + k0 + wd * G::kVPW;
-            if constexpr (G::kVPW == 16) {
-                const uint4 a = *reinterpret_cast<const uint4 *>(src);
-                const uint4 c = *reinterpret_cast<const uint4 *>(src + 8);
-                const uint32_t ww[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    vals[2 * q] = static_cast<uint16_t>(ww[q]);
-                    vals[2 * q + 1] = static_cast<uint16_t>(ww[q] >> 16);
-                }
-            } else if constexpr (G::kVPW == 8) {
-                const uint4 a = *reinterpret_cast<const uint4 *>(src);
-                const uint32_t ww[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    vals[2 * q] = static_cast<uint16_t>(ww[q]);
-                    vals[2 * q + 1] = static_cast<uint16_t>(ww[q] >> 16);
-                }
-            } else {
-                const uint2 a = *reinterpret_cast<const uint2 *>(src);
-                const uint32_t ww[2] = {a.x, a.y};
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    vals[2 * q] = static_cast<uint16_t>(ww[q]);
-                    vals[2 * q + 1] = static_cast<uint16_t>(ww[q] >> 16);
-                }
+            for (int wd = gp * WPG; wd < (gp + 1) * WPG; ++wd) {
+                const float2 pt = lds.part[i][wd][lane_in_row];
+                c += pt.x;
+                s += pt.y;
             }
-            const int gp = wd / G::kWPG;
-            float s = 0.f;
+            xv.corr[i][gp] = c;
+            xv.xs[i][gp] = s;
+        }
 #pragma unroll
-            for (int q = 0; q < G::kVPW; ++q) s += to_float<BF16>(vals[q]);
-            xv.xs[i][gp] += s;
+        for (int wd = 0; wd < 4; ++wd)
 #pragma unroll
-            for (int p = 0; p < P::kCount; ++p) {
-                const PairSpec ps = P::kSpec[p];
-                const uint16_t lo = scale_pow2<BF16>(vals[ps.lo_val], ps.lo_xexp);
-                const uint16_t hi = scale_pow2<BF16>(vals[ps.hi_val], ps.hi_xexp);
-                xv.xp[i][wd][p] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
-                xv.corr[i][gp] += P::kMagicValue * (to_float<BF16>(lo) + to_float<BF16>(hi));
+            for (int p = 0; p < P::kCount; ++p) xv.xp[i][wd][p] = lds.pairs[i][wd][p][lane_in_row];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Prepared vectors in global memory. A vector of K values for a projection
+// of BITS-bit codes is stored chunk-major: for chunk c (K range
+// [c*VPC, (c+1)*VPC)) and word wd < 4, pairs[(c*4 + wd)*kCount + p] and
+// part[c*4 + wd] = (corr, xs) -- the same per-word content XLds holds, laid
+// out so that a lane reads its chunk with 16-byte loads. Prepared once per
+// vector (by the router, a prep kernel, or the producing kernel's epilogue).
+// ---------------------------------------------------------------------------
+template <bool BF16>
+__device__ __forceinline__ int pairs_per_word(int bits) {
+    return bits == 2 ? Pairs<2, BF16>::kCount : bits == 4 ? Pairs<4, BF16>::kCount
+                                                          : Pairs<8, BF16>::kCount;
+}
+
+// Prepare one word (32 / bits values starting at src) into its pairs and
+// partial sums (runtime bit width). Word `unit` of a vector starts at value
+// unit * (32 / bits) and lands at pairs + unit * pairs_per_word, part + unit.
+template <bool BF16>
+__device__ __forceinline__ void prep_unit_at(int bits, const uint16_t *src,
+                                             uint32_t *__restrict__ pairs, float2 *__restrict__ part) {
+    switch (bits) {
+    case 2: prep_word<2, BF16>(src, pairs, 1, *part); break;
+    case 4: prep_word<4, BF16>(src, pairs, 1, *part); break;
+    default: prep_word<8, BF16>(src, pairs, 1, *part); break;
+    }
+}
+
+// u32 pairs and float2 parts per prepared vector of K values.
+__host__ __device__ inline int64_t prep_pairs_count(int K, int bits, bool bf16) {
+    const int per_word = bits == 2 ? 8 : bits == 4 ? 4 : (bf16 ? 4 : 2);
+    return static_cast<int64_t>(K) * bits / 32 * per_word;
+}
+__host__ __device__ inline int64_t prep_parts_count(int K, int bits) {
+    return static_cast<int64_t>(K) * bits / 32;
+}
+
+template <int BITS, bool BF16, int CPL, int LPR, int GPC>
+__device__ __forceinline__ void load_xvec_global(XVec<BITS, BF16, CPL, GPC> &xv,
+                                                 const uint32_t *__restrict__ pairs,
+                                                 const float2 *__restrict__ part, int lane_in_row) {
+    using P = Pairs<BITS, BF16>;
+    constexpr int WPG = 4 / GPC;
+    constexpr int N32 = 4 * P::kCount;         // u32 per chunk
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = lane_in_row + LPR * i;
+        const uint32_t *src = pairs + static_cast<int64_t>(c) * N32;
+        uint32_t buf[N32];
+        if constexpr (N32 % 4 == 0) {
+#pragma unroll
+            for (int q = 0; q < N32 / 4; ++q) {
+                const uint4 u = reinterpret_cast<const uint4 *>(src)[q];
+                buf[4 * q] = u.x; buf[4 * q + 1] = u.y; buf[4 * q + 2] = u.z; buf[4 * q + 3] = u.w;
             }
+        } else {
+#pragma unroll
+            for (int q = 0; q < N32; ++q) buf[q] = src[q];
+        }
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd)
+#pragma unroll
+            for (int p = 0; p < P::kCount; ++p) xv.xp[i][wd][p] = buf[wd * P::kCount + p];
+        const float4 pa = reinterpret_cast<const float4 *>(part + static_cast<int64_t>(c) * 4)[0];
+        const float4 pb = reinterpret_cast<const float4 *>(part + static_cast<int64_t>(c) * 4)[1];
+        const float2 pw[4] = {make_float2(pa.x, pa.y), make_float2(pa.z, pa.w),
+                              make_float2(pb.x, pb.y), make_float2(pb.z, pb.w)};
+#pragma unroll
+        for (int gp = 0; gp < GPC; ++gp) {
+            float cs = 0.f, xs = 0.f;
+#pragma unroll
+            for (int wd = gp * WPG; wd < (gp + 1) * WPG; ++wd) {
+                cs += pw[wd].x;
+                xs += pw[wd].y;
+            }
+            xv.corr[i][gp] = cs;
+            xv.xs[i][gp] = xs;
         }
     }
 }
 
-// Weights of one row for one lane: CPL chunks of 16 bytes.
-template <int CPL>
-struct RowChunks {
+// One row's weights and group metadata for one lane.
+template <int CPL, int GPC>
+struct RowData {
     u32x4 c[CPL];
+    uint16_t s[CPL][GPC];
+    uint16_t b[CPL][GPC];
 };
 
-template <int BITS, int CPL, int LPR>
-__device__ __forceinline__ void load_row(RowChunks<CPL> &rc, const uint32_t *__restrict__ wrow,
+template <int BITS, int CPL, int LPR, int GPC>
+__device__ __forceinline__ void load_row(RowData<CPL, GPC> &rd, const uint32_t *__restrict__ wrow,
+                                         const uint16_t *__restrict__ srow,
+                                         const uint16_t *__restrict__ brow, int group,
                                          int lane_in_row) {
+    using G = Geom<BITS, CPL, LPR, GPC>;
 #pragma unroll
-    for (int i = 0; i < CPL; ++i)
-        rc.c[i] = __builtin_nontemporal_load(
+    for (int i = 0; i < CPL; ++i) {
+        rd.c[i] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x4 *>(wrow) + lane_in_row + LPR * i);
+        const int k0 = (lane_in_row + LPR * i) * G::kVPC;
+#pragma unroll
+        for (int gp = 0; gp < GPC; ++gp) {
+            const int g = (k0 + gp * G::kWPG * G::kVPW) / group;
+            rd.s[i][gp] = srow[g];
+            rd.b[i][gp] = brow[g];
+        }
+    }
 }
 
 // Partial (this lane's chunks) of sum_k x_k w[row, k].
 template <int BITS, bool BF16, int CPL, int LPR, int GPC>
-__device__ __forceinline__ float row_partial(const RowChunks<CPL> &rc,
+__device__ __forceinline__ float row_partial(const RowData<CPL, GPC> &rd,
                                              const XVec<BITS, BF16, CPL, GPC> &xv,
-                                             const uint16_t *__restrict__ srow,
-                                             const uint16_t *__restrict__ brow,
-                                             int group, int lane_in_row) {
+                                             uint32_t magic_v) {
     using G = Geom<BITS, CPL, LPR, GPC>;
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-        const uint32_t words[4] = {rc.c[i][0], rc.c[i][1], rc.c[i][2], rc.c[i][3]};
-        const int k0 = (lane_in_row + LPR * i) * G::kVPC;
+        const uint32_t words[4] = {rd.c[i][0], rd.c[i][1], rd.c[i][2], rd.c[i][3]};
 #pragma unroll
         for (int gp = 0; gp < GPC; ++gp) {
             float d = 0.f;
 #pragma unroll
             for (int wd = gp * G::kWPG; wd < (gp + 1) * G::kWPG; ++wd)
-                d = word_dot<BITS, BF16>(words[wd], xv.xp[i][wd], d);
-            const int g = (k0 + gp * G::kWPG * G::kVPW) / group;
-            const float sc = to_float<BF16>(srow[g]);
-            const float bi = to_float<BF16>(brow[g]);
+                d = word_dot<BITS, BF16>(words[wd], xv.xp[i][wd], d, magic_v);
+            const float sc = to_float<BF16>(rd.s[i][gp]);
+            const float bi = to_float<BF16>(rd.b[i][gp]);
             acc = fmaf(sc, d - xv.corr[i][gp], fmaf(bi, xv.xs[i][gp], acc));
         }
     }

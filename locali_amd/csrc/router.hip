@@ -9,35 +9,33 @@
 // canonical: descending selection value, ties to the lower expert id.
 //
 // Kernels
-//   router_logits_gemv   one wave per expert, lanes split d; T tokens looped
-//                        (decode). The last workgroup to finish (device-scope
-//                        counter) runs the selection for every token, so
+//   router_gemv_kernel   one wave per expert (decode, few tokens): 16-byte
+//                        loads of the gate row and of x, v_dot2 when x and Wg
+//                        share a 16-bit type. The same launch prepares the
+//                        activations for the expert kernels (prepared-vector
+//                        form, see qgemv.hpp). The last wave to finish
+//                        (device-scope counter) selects for every token, so
 //                        decode routing is a single launch.
-//   router_logits_mfma   bf16/fp16 x and Wg: 32 tokens x 32 experts per wave
-//                        with v_mfma_f32_32x32x16, split over K into
-//                        kRouterSplits partial sums (summed in fixed order by
-//                        the selection, so logits are deterministic).
-//   router_select        one wave per token: scores, top-k, weights, slots.
+//   router_mfma_kernel   prefill: 32 tokens x 32 experts per wave with
+//                        v_mfma_f32_32x32x16, K split kRouterSplits ways into
+//                        partial sums that the selection adds in fixed order.
+//   router_select_kernel one wave per token: scores, top-k, weights, slots.
+//   prep_vectors_kernel  standalone activation prep for the expert kernels.
 #include "launch.hpp"
 
 namespace locali {
 
 constexpr int kRouterMaxExpertsPerLane = 8;   // E <= 512
 constexpr int kRouterSplits = 4;
-
-template <int GDT>
-__device__ __forceinline__ float gate_elem(const void *w, int64_t i) {
-    if constexpr (GDT == 0) return static_cast<const float *>(w)[i];
-    else if constexpr (GDT == 1) return f16_to_float(static_cast<const uint16_t *>(w)[i]);
-    else return bf16_to_float(static_cast<const uint16_t *>(w)[i]);
-}
+constexpr int kRouterTokensPerPass = 8;
 
 __device__ __forceinline__ float softplus_f(float l) {
     return l > 20.0f ? l : log1pf(expf(l));
 }
 
 // --------------------------------------------------------------------------
-// Selection for one token, executed by one full wave.
+// Selection for one token, executed by one full wave. Lane j < top_k ends up
+// owning the j-th choice.
 // --------------------------------------------------------------------------
 __device__ void select_token(const RouterLaunch &L, int t, const float *logit_row, int nsplit,
                              int64_t split_stride) {
@@ -49,9 +47,12 @@ __device__ void select_token(const RouterLaunch &L, int t, const float *logit_ro
         const int e = lane + 64 * i;
         float l = -INFINITY;
         if (e < L.E) {
-            l = 0.f;
-            for (int s = 0; s < nsplit; ++s) l += logit_row[s * split_stride + e];
-            if (L.logits_in) l = L.logits_in[static_cast<int64_t>(t) * L.E + e];
+            if (L.logits_in) {
+                l = L.logits_in[static_cast<int64_t>(t) * L.E + e];
+            } else {
+                l = 0.f;
+                for (int s = 0; s < nsplit; ++s) l += logit_row[s * split_stride + e];
+            }
         }
         sc[i] = l;
         lmax = fmaxf(lmax, l);
@@ -82,14 +83,14 @@ __device__ void select_token(const RouterLaunch &L, int t, const float *logit_ro
             sel[i] = -INFINITY;
         }
     }
-    // top-k (or hash lookup), weights in fixed j order.
-    float chosen_score[16];
-    int chosen[16];
+    int my_e = -1;
+    float my_s = 0.f;
     for (int j = 0; j < L.top_k; ++j) {
         int best_e;
         if (L.tid2eid) {
             const int id = L.input_ids[t];
             best_e = (id >= 0 && id < L.vocab) ? L.tid2eid[static_cast<int64_t>(id) * L.top_k + j] : -1;
+            if (best_e >= L.E) best_e = -1;
         } else {
             float bv = -INFINITY;
             int be = 0x7fffffff;
@@ -103,73 +104,131 @@ __device__ void select_token(const RouterLaunch &L, int t, const float *logit_ro
                 const int oe = __shfl_xor(be, m, 64);
                 if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
             }
-            best_e = be;
+            best_e = be < L.E ? be : -1;
 #pragma unroll
             for (int i = 0; i < kRouterMaxExpertsPerLane; ++i)
                 if (lane + 64 * i == best_e) sel[i] = -INFINITY;
         }
-        // broadcast the chosen expert's score from its owner lane
-        float s = 0.f;
-        if (best_e >= 0 && best_e < L.E) {
-            const int owner = best_e & 63, slot_i = best_e >> 6;
-            float mine = 0.f;
+        float mine = 0.f;
+        const int slot_i = best_e >= 0 ? (best_e >> 6) : 0;
 #pragma unroll
-            for (int i = 0; i < kRouterMaxExpertsPerLane; ++i)
-                if (i == slot_i) mine = sc[i];
-            s = __shfl(mine, owner, 64);
-        } else {
-            best_e = -1;
+        for (int i = 0; i < kRouterMaxExpertsPerLane; ++i)
+            if (i == slot_i) mine = sc[i];
+        const float s = best_e >= 0 ? __shfl(mine, best_e & 63, 64) : 0.f;
+        if (lane == j) {
+            my_e = best_e;
+            my_s = s;
         }
-        chosen[j] = best_e;
-        chosen_score[j] = s;
     }
-    float sum = 0.f;
-    for (int j = 0; j < L.top_k; ++j) sum += chosen_score[j];
-    if (lane == 0) {
-        for (int j = 0; j < L.top_k; ++j) {
-            float w = chosen_score[j];
-            if (L.norm_topk) w = w / (sum + 1e-20f);
-            const int64_t o = static_cast<int64_t>(t) * L.top_k + j;
-            L.idx[o] = chosen[j];
-            L.weights[o] = w * L.routed_scale;
-            if (L.route_slot) {
-                int slot = -1;
-                if (chosen[j] >= 0 && L.slot_of_expert) slot = L.slot_of_expert[chosen[j]];
-                if (slot >= L.n_slots) slot = -1;
-                L.route_slot[o] = slot;
-            }
+    float sum = lane < L.top_k ? my_s : 0.f;
+    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
+    if (lane < L.top_k) {
+        float w = my_s;
+        if (L.norm_topk) w = w / (sum + 1e-20f);
+        const int64_t o = static_cast<int64_t>(t) * L.top_k + lane;
+        L.idx[o] = my_e;
+        L.weights[o] = w * L.routed_scale;
+        if (L.route_slot) {
+            int slot = -1;
+            if (my_e >= 0 && L.slot_of_expert) slot = L.slot_of_expert[my_e];
+            if (slot >= L.n_slots) slot = -1;
+            L.route_slot[o] = slot;
         }
     }
 }
 
 // --------------------------------------------------------------------------
-// GEMV logits (decode) + fused last-workgroup selection.
+// Activation prep (prepared-vector form of qgemv.hpp) for n_vec rows of v.
+// --------------------------------------------------------------------------
+template <bool BF16>
+__device__ __forceinline__ void prep_units(const uint16_t *v, int n_vec, int K, int bits,
+                                           const PrepVec &out, int first, int count) {
+    const int vpw = 32 / bits;
+    const int per_vec = K / vpw;
+    const int ppw = pairs_per_word<BF16>(bits);
+    for (int u = first; u < first + count && u < n_vec * per_vec; u += 1) {
+        const int vec = u / per_vec, unit = u % per_vec;
+        prep_unit_at<BF16>(bits, v + static_cast<int64_t>(vec) * K + unit * vpw,
+                           out.pairs + vec * out.pairs_stride + unit * ppw,
+                           out.parts + vec * out.parts_stride + unit);
+    }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void prep_vectors_kernel(const uint16_t *v, int n_vec, int K,
+                                                           int bits, PrepVec out) {
+    const int u = blockIdx.x * blockDim.x + threadIdx.x;
+    prep_units<BF16>(v, n_vec, K, bits, out, u, 1);
+}
+
+hipError_t launch_prep_vectors(const uint16_t *v, int n_vec, int K, int bits, bool bf16, PrepVec out,
+                               hipStream_t st) {
+    const int units = n_vec * (K * bits / 32);
+    dim3 grid((units + 255) / 256);
+    if (bf16) hipLaunchKernelGGL(prep_vectors_kernel<true>, grid, dim3(256), 0, st, v, n_vec, K, bits, out);
+    else hipLaunchKernelGGL(prep_vectors_kernel<false>, grid, dim3(256), 0, st, v, n_vec, K, bits, out);
+    return hipGetLastError();
+}
+
+// --------------------------------------------------------------------------
+// GEMV logits (decode) + activation prep + fused last-wave selection.
 // --------------------------------------------------------------------------
 template <int GDT, bool XBF16>
-__global__ __launch_bounds__(256) void router_gemv_kernel(RouterLaunch L) {
-    constexpr int TB = 8;   // tokens per pass (register accumulators)
+__device__ __forceinline__ void gate_chunk(const void *w, int64_t off, uint32_t (&wp)[4], float (&wf)[8]) {
+    if constexpr (GDT == 0) {
+        const float4 a = *reinterpret_cast<const float4 *>(static_cast<const float *>(w) + off);
+        const float4 b = *reinterpret_cast<const float4 *>(static_cast<const float *>(w) + off + 4);
+        wf[0] = a.x; wf[1] = a.y; wf[2] = a.z; wf[3] = a.w;
+        wf[4] = b.x; wf[5] = b.y; wf[6] = b.z; wf[7] = b.w;
+    } else {
+        const uint4 a = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(w) + off);
+        wp[0] = a.x; wp[1] = a.y; wp[2] = a.z; wp[3] = a.w;
+        if constexpr ((GDT == 2) != XBF16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                wf[2 * q] = GDT == 2 ? bf16_to_float(wp[q] & 0xffff) : f16_to_float(wp[q] & 0xffff);
+                wf[2 * q + 1] = GDT == 2 ? bf16_to_float(wp[q] >> 16) : f16_to_float(wp[q] >> 16);
+            }
+        }
+    }
+}
+
+constexpr int kRouterWaves = 8;   // experts per workgroup (one per wave)
+
+template <int GDT, bool XBF16>
+__global__ __launch_bounds__(64 * kRouterWaves) void router_gemv_kernel(RouterLaunch L) {
+    constexpr int TB = kRouterTokensPerPass;
+    constexpr bool kDot = GDT != 0 && ((GDT == 2) == XBF16);
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int e = blockIdx.x * 4 + wave;
-    if (e < L.E && !L.logits_in) {
+    const int e = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+    if (L.xprep.pairs)
+        prep_units<XBF16>(L.x, L.tokens, L.d, L.prep_bits, L.xprep,
+                          blockIdx.x * blockDim.x + threadIdx.x, 1);
+    if (!L.logits_in && e < L.E) {
         for (int t0 = 0; t0 < L.tokens; t0 += TB) {
             float acc[TB];
 #pragma unroll
             for (int q = 0; q < TB; ++q) acc[q] = 0.f;
             for (int k = lane * 8; k < L.d; k += 64 * 8) {
-                float wv[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) wv[u] = gate_elem<GDT>(L.gate_w, static_cast<int64_t>(e) * L.d + k + u);
+                uint32_t wp[4];
+                float wf[8];
+                gate_chunk<GDT, XBF16>(L.gate_w, static_cast<int64_t>(e) * L.d + k, wp, wf);
 #pragma unroll
                 for (int q = 0; q < TB; ++q) {
                     if (t0 + q < L.tokens) {
                         const uint4 xv = *reinterpret_cast<const uint4 *>(
                             L.x + static_cast<int64_t>(t0 + q) * L.d + k);
                         const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+                        if constexpr (kDot) {
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            acc[q] = fmaf(to_float<XBF16>(static_cast<uint16_t>(xw[u])), wv[2 * u], acc[q]);
-                            acc[q] = fmaf(to_float<XBF16>(static_cast<uint16_t>(xw[u] >> 16)), wv[2 * u + 1], acc[q]);
+                            for (int u = 0; u < 4; ++u) acc[q] = dot2<XBF16>(xw[u], wp[u], acc[q]);
+                        } else {
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) {
+                                acc[q] = fmaf(to_float<XBF16>(static_cast<uint16_t>(xw[u])), wf[2 * u], acc[q]);
+                                acc[q] = fmaf(to_float<XBF16>(static_cast<uint16_t>(xw[u] >> 16)),
+                                              wf[2 * u + 1], acc[q]);
+                            }
                         }
                     }
                 }
@@ -180,19 +239,17 @@ __global__ __launch_bounds__(256) void router_gemv_kernel(RouterLaunch L) {
                 L.logits[static_cast<int64_t>(t0 + q) * L.E + e] = acc[0];
         }
     }
-    // Last workgroup to arrive selects. Release this block's logits, count,
-    // and let the final arrival acquire everyone's.
-    __shared__ int is_last;
+    // Last workgroup to arrive selects: release this workgroup's logits,
+    // count once per workgroup (device-scope atomics are costly, so only
+    // E / 8 of them), and let the final arrival acquire everyone's.
+    __shared__ unsigned last;
     __threadfence();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned prev = atomicAdd(L.counter, 1u);
-        is_last = prev == gridDim.x - 1;
-    }
+    if (threadIdx.x == 0) last = atomicAdd(L.counter, 1u) == gridDim.x - 1;
     __syncthreads();
-    if (!is_last) return;
+    if (!last) return;
     __threadfence();
-    for (int t = wave; t < L.tokens; t += 4)
+    for (int t = threadIdx.x >> 6; t < L.tokens; t += kRouterWaves)
         select_token(L, t, L.logits + static_cast<int64_t>(t) * L.E, 1, 0);
     if (threadIdx.x == 0) atomicExch(L.counter, 0u);
 }
@@ -233,7 +290,6 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(RouterLaunch L) {
     const int wt = (wave & 1) * 32, we = (wave >> 1) * 32;   // wave sub-tile
     f32x16_t acc = {};
     for (int k0 = kbeg; k0 < kend; k0 += KT) {
-        // stage 64 x 64 of x and of Wg: 256 threads x 2 x 16 bytes each
         for (int c = threadIdx.x; c < 64 * KT / 8; c += 256) {
             const int row = c / (KT / 8), col = (c % (KT / 8)) * 8;
             uint4 xv = make_uint4(0, 0, 0, 0), wv = make_uint4(0, 0, 0, 0);
@@ -277,9 +333,13 @@ __global__ __launch_bounds__(256) void router_select_kernel(RouterLaunch L, int 
 hipError_t launch_router(const RouterLaunch &L, hipStream_t st) {
     if (L.E > 64 * kRouterMaxExpertsPerLane || L.top_k > 16 || L.top_k < 1 || L.top_k > L.E)
         return hipErrorInvalidValue;
-    const bool mfma_ok = !L.logits_in && L.tokens > 8 && L.gate_dtype != 0 &&
+    const bool mfma_ok = !L.logits_in && L.tokens > kRouterTokensPerPass && L.gate_dtype != 0 &&
                          ((L.gate_dtype == 2) == L.x_bf16) && L.d % (64 * kRouterSplits) == 0;
     if (mfma_ok) {
+        if (L.xprep.pairs) {
+            hipError_t e = launch_prep_vectors(L.x, L.tokens, L.d, L.prep_bits, L.x_bf16, L.xprep, st);
+            if (e != hipSuccess) return e;
+        }
         dim3 grid((L.tokens + 63) / 64, (L.E + 63) / 64, kRouterSplits);
         if (L.x_bf16) hipLaunchKernelGGL(router_mfma_kernel<true>, grid, dim3(256), 0, st, L);
         else hipLaunchKernelGGL(router_mfma_kernel<false>, grid, dim3(256), 0, st, L);
@@ -290,10 +350,20 @@ hipError_t launch_router(const RouterLaunch &L, hipStream_t st) {
         return hipGetLastError();
     }
     if (L.d % 8 != 0) return hipErrorInvalidValue;
-    dim3 grid((L.E + 3) / 4);
+    // every wave must cover its share of the prep units
+    const int blocks = (L.E + kRouterWaves - 1) / kRouterWaves;
+    if (L.xprep.pairs && static_cast<int64_t>(blocks) * 64 * kRouterWaves <
+                             static_cast<int64_t>(L.tokens) * (L.d * L.prep_bits / 32)) {
+        hipError_t e = launch_prep_vectors(L.x, L.tokens, L.d, L.prep_bits, L.x_bf16, L.xprep, st);
+        if (e != hipSuccess) return e;
+        RouterLaunch L2 = L;
+        L2.xprep.pairs = nullptr;
+        return launch_router(L2, st);
+    }
+    dim3 grid(blocks), block(64 * kRouterWaves);
 #define LOCALI_ROUTER(GDT)                                                                  \
-    if (L.x_bf16) hipLaunchKernelGGL((router_gemv_kernel<GDT, true>), grid, dim3(256), 0, st, L); \
-    else hipLaunchKernelGGL((router_gemv_kernel<GDT, false>), grid, dim3(256), 0, st, L);
+    if (L.x_bf16) hipLaunchKernelGGL((router_gemv_kernel<GDT, true>), grid, block, 0, st, L); \
+    else hipLaunchKernelGGL((router_gemv_kernel<GDT, false>), grid, block, 0, st, L);
     switch (L.gate_dtype) {
     case 0: LOCALI_ROUTER(0); break;
     case 1: LOCALI_ROUTER(1); break;

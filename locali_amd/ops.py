@@ -19,7 +19,7 @@ from ._lib import (COMBINE_FP32, COMBINE_ROUNDED, DT_BF16, DT_F16, DT_F32, SCORE
 
 __all__ = [
     "ProjArena", "ExpertArenaT", "RouterSpec", "Workspace", "router", "dispatch",
-    "expert_decode", "expert_grouped", "combine", "forward", "arena_fill",
+    "expert_decode", "decode_gateup", "decode_down_combine", "expert_grouped", "combine", "forward", "arena_fill",
     "COMBINE_ROUNDED", "COMBINE_FP32",
 ]
 
@@ -195,9 +195,14 @@ def dispatch(route_slot: torch.Tensor, n_slots: int):
     return sorted_route, seg
 
 
+def _decode_ws(ws, arena, T, k, shared):
+    ws = ws if ws is not None else Workspace()
+    return ws.reserve(T, arena.d_model, arena.d_ff, 1, k, shared is not None)
+
+
 def expert_decode(arena: ExpertArenaT, shared: ExpertArenaT | None, x: torch.Tensor,
                   route_slot: torch.Tensor, weights: torch.Tensor, *, swiglu_limit=10.0,
-                  fp32_swiglu=False, combine_mode=COMBINE_ROUNDED, hidden=None):
+                  fp32_swiglu=False, combine_mode=COMBINE_ROUNDED, hidden=None, ws=None):
     x2 = _flat(x)
     T = x2.shape[0]
     k = route_slot.shape[-1]
@@ -205,15 +210,51 @@ def expert_decode(arena: ExpertArenaT, shared: ExpertArenaT | None, x: torch.Ten
     if hidden is None:
         hidden = torch.empty(routes, arena.d_ff, dtype=x2.dtype, device=x.device)
     out = torch.empty_like(x2)
+    buf = _decode_ws(ws, arena, T, k, shared)
     a = arena.struct()
     s = shared.struct() if shared is not None else None
     rc = lib().locali_moe_expert_decode(ctypes.byref(a), ctypes.byref(s) if s is not None else None,
                                         _ptr(x2), _dt(x2), T, k, _ptr(route_slot.contiguous()),
                                         _ptr(weights.contiguous()), float(swiglu_limit),
                                         int(fp32_swiglu), int(combine_mode), _ptr(hidden), _ptr(out),
-                                        _stream())
+                                        _ptr(buf), buf.numel(), _stream())
     check(rc, "locali_moe_expert_decode")
     return out.reshape(x.shape)
+
+
+def decode_gateup(arena: ExpertArenaT, shared: ExpertArenaT | None, x: torch.Tensor,
+                  route_slot: torch.Tensor, hidden: torch.Tensor, ws: "Workspace", *,
+                  swiglu_limit=10.0, fp32_swiglu=False):
+    """Stage 1 of expert_decode: hidden[r] = swiglu(gate_r(x), up_r(x)); the
+    down stage's prepared inputs stay in `ws`."""
+    x2 = _flat(x)
+    k = route_slot.shape[-1]
+    buf = _decode_ws(ws, arena, x2.shape[0], k, shared)
+    a = arena.struct()
+    s = shared.struct() if shared is not None else None
+    rc = lib().locali_moe_decode_gateup(ctypes.byref(a), ctypes.byref(s) if s is not None else None,
+                                        _ptr(x2), _dt(x2), x2.shape[0], k, _ptr(route_slot),
+                                        float(swiglu_limit), int(fp32_swiglu), _ptr(hidden),
+                                        _ptr(buf), buf.numel(), _stream())
+    check(rc, "locali_moe_decode_gateup")
+    return hidden
+
+
+def decode_down_combine(arena: ExpertArenaT, shared: ExpertArenaT | None, route_slot: torch.Tensor,
+                        weights: torch.Tensor, out: torch.Tensor, ws: "Workspace", *,
+                        combine_mode=COMBINE_ROUNDED):
+    """Stage 2 of expert_decode (same workspace as stage 1): down projection,
+    weighted combine, shared add."""
+    T, k = route_slot.shape
+    buf = _decode_ws(ws, arena, T, k, shared)
+    a = arena.struct()
+    s = shared.struct() if shared is not None else None
+    rc = lib().locali_moe_decode_down_combine(ctypes.byref(a), ctypes.byref(s) if s is not None else None,
+                                              _dt(out), T, k, _ptr(route_slot), _ptr(weights),
+                                              int(combine_mode), _ptr(out), _ptr(buf), buf.numel(),
+                                              _stream())
+    check(rc, "locali_moe_decode_down_combine")
+    return out
 
 
 def expert_grouped(arena: ExpertArenaT, shared: ExpertArenaT | None, x: torch.Tensor,

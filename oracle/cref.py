@@ -34,7 +34,7 @@ class CRef:
         P = ctypes.c_void_p
         self.lib.oracle_qmv.argtypes = [ctypes.POINTER(OProj), ctypes.c_int, P, P]
         self.lib.oracle_moe_layer.argtypes = [ctypes.POINTER(OProj)] * 6 + [
-            P, ctypes.c_int, ctypes.c_int, P, P, ctypes.c_int, ctypes.c_float, ctypes.c_int, P]
+            P, ctypes.c_int, ctypes.c_int, P, P, ctypes.c_int, ctypes.c_float, ctypes.c_int, P, P]
         self.lib.oracle_moe_layer.restype = ctypes.c_int
         self.lib.oracle_router.argtypes = [P, P, P] + [ctypes.c_int] * 6 + [ctypes.c_float, P, P]
         self.lib.oracle_round_array.argtypes = [P, P, ctypes.c_int, ctypes.c_int]
@@ -59,7 +59,7 @@ class CRef:
         return out
 
     def moe_layer(self, x, slots, weights, arena, dt, *, shared=None, limit=10.0,
-                  fp32_swiglu=False):
+                  fp32_swiglu=False, return_terms=False):
         """arena/shared: {"gate_proj"|"up_proj"|"down_proj": (w, s, b, bits, group)}."""
         x = _f32(x)
         T, d = x.shape
@@ -73,14 +73,15 @@ class CRef:
         else:
             sg = su = sd = None
         out = np.zeros((T, d), dtype=np.float32)
+        terms = np.zeros((T, d), dtype=np.float32)
         rc = self.lib.oracle_moe_layer(ctypes.byref(g), ctypes.byref(u), ctypes.byref(dn), sg, su,
                                        sd, x.ctypes.data, T, k, slots.ctypes.data,
                                        weights.ctypes.data, DT[dt], float(limit), int(fp32_swiglu),
-                                       out.ctypes.data)
+                                       out.ctypes.data, terms.ctypes.data)
         self._keep.clear()
         if rc:
             raise MemoryError("oracle_moe_layer")
-        return out
+        return (out, terms) if return_terms else out
 
     def router(self, x, wg, bias, k, score_func=0, norm=True, scale=1.0):
         x, wg = _f32(x), _f32(wg)

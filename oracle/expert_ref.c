@@ -156,13 +156,14 @@ void oracle_expert(const oracle_proj *gate, const oracle_proj *up,
 
 /* Full layer on T tokens. slots [T*k] (arena slot per route), weights [T*k]
  * fp32 router weights (cast to dt here), x [T*d] values in dt. shared_* may
- * be NULL. out [T*d] values rounded to dt. Returns 0. */
+ * be NULL. out [T*d] values rounded to dt; terms (optional, zero-filled by
+ * the caller) receives the sum of |rounded terms| added per element. */
 int oracle_moe_layer(const oracle_proj *gate, const oracle_proj *up,
                      const oracle_proj *down, const oracle_proj *sgate,
                      const oracle_proj *sup, const oracle_proj *sdown,
                      const float *x, int T, int k, const int32_t *slots,
                      const float *weights, int dt, float limit,
-                     int fp32_swiglu, float *out) {
+                     int fp32_swiglu, float *out, float *terms) {
     const int d = down->N, dff = gate->N;
     float *scratch = (float *)malloc(sizeof(float) * (3 * dff + 2 * d));
     if (!scratch) return -1;
@@ -174,13 +175,19 @@ int oracle_moe_layer(const oracle_proj *gate, const oracle_proj *up,
             oracle_expert(gate, up, down, slots[t * k + j], xt, dt, limit,
                           fp32_swiglu, scratch, y);
             float w = round_dt(weights[t * k + j], dt);
-            for (int n = 0; n < d; n++) acc[n] += round_dt(y[n] * w, dt);
+            for (int n = 0; n < d; n++) {
+                const float term = round_dt(y[n] * w, dt);
+                acc[n] += term;
+                if (terms) terms[(size_t)t * d + n] += fabsf(term);
+            }
         }
         for (int n = 0; n < d; n++) out[(size_t)t * d + n] = round_dt(acc[n], dt);
         if (sgate) {
             oracle_expert(sgate, sup, sdown, 0, xt, dt, limit, fp32_swiglu, scratch, y);
-            for (int n = 0; n < d; n++)
+            for (int n = 0; n < d; n++) {
                 out[(size_t)t * d + n] = round_dt(out[(size_t)t * d + n] + y[n], dt);
+                if (terms) terms[(size_t)t * d + n] += fabsf(y[n]);
+            }
         }
     }
     free(scratch);

@@ -140,11 +140,14 @@ def first_appearance(idx) -> list[int]:
 # -- whole layer ------------------------------------------------------------
 
 def moe_layer(x, idx, weights, arena, slot_of_expert, dtype, *, limit=10.0,
-              fp32_swiglu=False, shared=None, combine_mode="single"):
+              fp32_swiglu=False, shared=None, combine_mode="single", return_terms=False):
     """Routed MoE over an arena plus optional shared expert.
 
     arena: {proj: (w[S,...], scales[S,...], biases[S,...], bits, group)}
-    slot_of_expert: mapping expert -> slot. Returns out [T, d] rounded."""
+    slot_of_expert: mapping expert -> slot. Returns out [T, d] rounded, and
+    with return_terms the per-element sum of |rounded terms| that were added
+    (each term's rounding spacing bounds how far one last-place flip of that
+    term moves the output)."""
     x = np.asarray(x, dtype=np.float64)
     T, k = np.shape(idx)
     y = np.zeros((T, k, x.shape[-1]))
@@ -154,6 +157,10 @@ def moe_layer(x, idx, weights, arena, slot_of_expert, dtype, *, limit=10.0,
             proj = {p: (a[0][s], a[1][s], a[2][s], a[3], a[4]) for p, a in arena.items()}
             y[t, j] = expert(x[t:t + 1], proj, dtype, limit, fp32_swiglu)[0]
     out = combine(y, weights, dtype, combine_mode)
+    wq = affine.round_to(weights, dtype).astype(np.float64)
+    terms = np.abs(y * wq[..., None]).sum(axis=1)
     if shared is not None:
-        out = add_shared(out, expert(x, shared, dtype, limit, fp32_swiglu), dtype)
-    return out
+        ys = expert(x, shared, dtype, limit, fp32_swiglu)
+        out = add_shared(out, ys, dtype)
+        terms = terms + np.abs(ys)
+    return (out, terms) if return_terms else out

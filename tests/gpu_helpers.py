@@ -60,5 +60,21 @@ def assert_close(got, want, what, rtol=RTOL, atol=ATOL):
             f"got {got[tuple(i)]!r} want {want[tuple(i)]!r}")
 
 
+def assert_close_terms(got, want, terms, what, rtol=RTOL, atol=ATOL):
+    """Combined outputs are sums of terms each rounded to 16 bits; one
+    last-place flip of a term of magnitude m moves the result by up to
+    2^-7 m (bf16 spacing, a superset of fp16's). The bound adds that to the
+    north-star tolerance, with terms = sum of |rounded term| per element."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    tol = atol + rtol * np.abs(want) + 2.0 ** -7 * np.asarray(terms, dtype=np.float64)
+    bad = np.abs(got - want) > tol
+    if bad.any():
+        i = np.argwhere(bad)[0]
+        raise AssertionError(
+            f"{what}: {bad.sum()} / {bad.size} outside the term-rounding bound; first at {tuple(i)}: "
+            f"got {got[tuple(i)]!r} want {want[tuple(i)]!r} terms {np.asarray(terms)[tuple(i)]!r}")
+
+
 def exact_fraction(got, want) -> float:
     return float(np.mean(np.asarray(got) == np.asarray(want)))
