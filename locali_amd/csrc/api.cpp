@@ -45,7 +45,7 @@ bool dtype16(int32_t dt) { return dt == LOCALI_DT_F16 || dt == LOCALI_DT_BF16; }
 
 // Workspace layout for up to T tokens.
 struct Layout {
-    size_t counter, logits, route_slot, hidden, xprep, hprep, seg_start, sorted_route, route_pos,
+    size_t logits, route_slot, hidden, xprep, hprep, seg_start, sorted_route, route_pos,
         tiles, n_tiles, gh, gy, total;
     int max_tiles;
 };
@@ -65,7 +65,6 @@ Layout layout(int T, int d, int dff, int E, int k, int has_shared) {
     const int R = T * k;
     const int routes = R + (has_shared ? T : 0);
     L.max_tiles = grouped_max_tiles(T, k, has_shared ? 1 : 0, E, kGroupedTileTokens);
-    L.counter = take(kAlign);
     L.logits = take(sizeof(float) * kRouterSplitsHost * static_cast<size_t>(T) * E);
     L.route_slot = take(sizeof(int32_t) * R);
     L.hidden = take(sizeof(uint16_t) * static_cast<size_t>(routes) * dff);
@@ -326,7 +325,6 @@ int route(const locali_router *router, const void *x, int32_t x_dtype, int32_t t
     L.weights = weights;
     L.route_slot = route_slot;
     L.logits = at<float>(workspace, lay.logits);
-    L.counter = at<uint32_t>(workspace, lay.counter);
     L.logits_in = logits_in;
     L.xprep = xprep;
     L.prep_bits = prep_bits;

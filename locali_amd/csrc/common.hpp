@@ -176,14 +176,13 @@ template <> struct Pairs<8, false> {
                                           {8, 0x00FF00FFu, 1, 3, 0, 0}};
 };
 
-// (v & mask) | magic in one v_and_or_b32. GFX9 VOP3 encodings take no
-// literal constants and read at most one SGPR, so the compiler splits the
-// expression into v_and + v_or when both are immediates; here the mask rides
-// in an SGPR and the magic in a VGPR materialised once per kernel (magic_vgpr).
+// (v & mask) | magic in one gfx950 v_bitop3_b32 (truth table 0xEA for
+// (src0 & src1) | src2). GFX9 VOP3 encodings take no literal constants and
+// read at most one SGPR, so the mask rides in an SGPR and the magic in a VGPR
+// materialised once per kernel (opaque_vgpr). A builtin rather than inline
+// assembly lets the compiler track the result's hazards (no padding s_nop).
 __device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t magic_v) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(magic_v));
-    return r;
+    return __builtin_amdgcn_bitop3_b32(v, mask, magic_v, 0xEA);
 }
 
 // A VGPR holding `value` that the compiler cannot see through (so it is kept
@@ -260,6 +259,47 @@ __device__ __forceinline__ void reduce_transposed(float (&v)[NV], int lane) {
             v[0] += shfl_xor(v[0], m);
         }
     }
+}
+
+// ---- wave-wide arg-max over 64-bit keys -------------------------------------
+// Monotone map of a float onto uint32 (larger float -> larger key; -inf maps
+// above 0, so 0 can mark "no candidate").
+__device__ __forceinline__ uint32_t ordered_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return u ^ ((static_cast<uint32_t>(static_cast<int32_t>(u) >> 31)) | 0x80000000u);
+}
+
+template <int CTRL>
+__device__ __forceinline__ void key_max_dpp(uint32_t &hi, uint32_t &lo) {
+    const uint32_t h2 = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(hi), CTRL, 0xf, 0xf, false));
+    const uint32_t l2 = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(lo), CTRL, 0xf, 0xf, false));
+    const bool take = h2 > hi || (h2 == hi && l2 > lo);
+    hi = take ? h2 : hi;
+    lo = take ? l2 : lo;
+}
+
+// Maximum of the key (hi, lo) over the wave, returned wave-uniform. Within
+// each 16-lane row: quad swaps (xor 1, xor 2), then half-row and row
+// mirrors, all DPP; across the four rows: lane reads of 0, 16, 32, 48.
+__device__ __forceinline__ void wave_max_key(uint32_t &hi, uint32_t &lo) {
+    key_max_dpp<0xB1>(hi, lo);    // quad_perm [1,0,3,2]
+    key_max_dpp<0x4E>(hi, lo);    // quad_perm [2,3,0,1]
+    key_max_dpp<0x141>(hi, lo);   // row_half_mirror
+    key_max_dpp<0x140>(hi, lo);   // row_mirror
+    uint32_t bh = __builtin_amdgcn_readlane(static_cast<int>(hi), 0);
+    uint32_t bl = __builtin_amdgcn_readlane(static_cast<int>(lo), 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16) {
+        const uint32_t h = __builtin_amdgcn_readlane(static_cast<int>(hi), r);
+        const uint32_t l = __builtin_amdgcn_readlane(static_cast<int>(lo), r);
+        const bool take = h > bh || (h == bh && l > bl);
+        bh = take ? h : bh;
+        bl = take ? l : bl;
+    }
+    hi = bh;
+    lo = bl;
 }
 
 __device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + __expf(-g)); }

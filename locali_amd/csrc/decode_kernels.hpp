@@ -77,16 +77,26 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_route_kernel(
                                                     xin.parts + token * xin.parts_stride,
                                                     lane_in_row);
         sched_fence();
+        // Then every row's (small) metadata, then the weights in the order
+        // they are consumed, so row j's math waits only for row j's chunk.
         RowData<CPL, GPC> wg[J], wu[J];
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-            load_row<BITS, CPL, LPR, GPC>(wg[j], gw + row * wpr, gs + row * gpr, gb + row * gpr,
-                                          pg.group, lane_in_row);
-            load_row<BITS, CPL, LPR, GPC>(wu[j], uw + row * wpr, us + row * gpr, ub + row * gpr,
-                                          pu.group, lane_in_row);
+            load_row_meta<BITS, CPL, LPR, GPC>(wg[j], gs + row * gpr, gb + row * gpr, pg.group,
+                                               lane_in_row);
+            load_row_meta<BITS, CPL, LPR, GPC>(wu[j], us + row * gpr, ub + row * gpr, pu.group,
+                                               lane_in_row);
         }
         sched_fence();
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
+            load_row_weights<CPL, LPR, GPC>(wg[j], gw + row * wpr, lane_in_row);
+            load_row_weights<CPL, LPR, GPC>(wu[j], uw + row * wpr, lane_in_row);
+        }
+        sched_fence();
+        xvec_finish(xv);
         const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
         float v[2 * J];
 #pragma unroll
@@ -164,10 +174,17 @@ __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, 
 #pragma unroll
         for (int q = 0; q < J; ++q) {
             const int row = min(row0 + q * G::kRPL + row_sub, N - 1);
-            load_row<BITS, CPL, LPR, GPC>(rd[q], w + row * wpr, s + row * gpr, b + row * gpr, p.group,
-                                          lane_in_row);
+            load_row_meta<BITS, CPL, LPR, GPC>(rd[q], s + row * gpr, b + row * gpr, p.group,
+                                               lane_in_row);
         }
         sched_fence();
+#pragma unroll
+        for (int q = 0; q < J; ++q) {
+            const int row = min(row0 + q * G::kRPL + row_sub, N - 1);
+            load_row_weights<CPL, LPR, GPC>(rd[q], w + row * wpr, lane_in_row);
+        }
+        sched_fence();
+        xvec_finish(xv);
         const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
         float v[J];
 #pragma unroll

@@ -75,7 +75,6 @@ struct RouterLaunch {
     float *weights;             // [tokens, top_k]
     int32_t *route_slot;        // [tokens, top_k] or null
     float *logits;              // workspace [tokens, E]
-    uint32_t *counter;          // workspace, zero between calls
     const float *logits_in;     // optional precomputed logits [tokens, E]
     PrepVec xprep;              // optional: also prepare x for a projection of
     int32_t prep_bits;          //   prep_bits-bit codes (pairs null = skip)

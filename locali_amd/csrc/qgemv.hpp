@@ -44,6 +44,7 @@ struct XVec {
     uint32_t xp[CPL][4][P::kCount];
     float corr[CPL][GPC];   // magic * sum of pre-scaled values per group part
     float xs[CPL][GPC];     // plain sum of values per group part
+    float4 raw[CPL][2];     // per-word (corr, xs) as loaded, before xvec_finish
 };
 
 // LDS image of one prepared vector, lane-minor so that lane reads are
@@ -63,37 +64,18 @@ __device__ __forceinline__ uint16_t scale_pow2(uint16_t v) {
 }
 
 // Prepare one word's worth of activations (VPW values at `src`).
+// Prepare one word's worth of activations (32 / BITS values, given as 16-bit
+// pairs in ww) into its pairs and partial sums (corr, xs).
 template <int BITS, bool BF16>
-__device__ __forceinline__ void prep_word(const uint16_t *__restrict__ src, uint32_t *pairs,
+__device__ __forceinline__ void prep_vals(const uint32_t (&ww)[16 / BITS], uint32_t *pairs,
                                           int pair_stride, float2 &part) {
     using P = Pairs<BITS, BF16>;
     constexpr int VPW = 32 / BITS;
     uint16_t vals[VPW];
-    if constexpr (VPW == 16) {
-        const uint4 a = *reinterpret_cast<const uint4 *>(src);
-        const uint4 c = *reinterpret_cast<const uint4 *>(src + 8);
-        const uint32_t ww[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            vals[2 * q] = static_cast<uint16_t>(ww[q]);
-            vals[2 * q + 1] = static_cast<uint16_t>(ww[q] >> 16);
-        }
-    } else if constexpr (VPW == 8) {
-        const uint4 a = *reinterpret_cast<const uint4 *>(src);
-        const uint32_t ww[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            vals[2 * q] = static_cast<uint16_t>(ww[q]);
-            vals[2 * q + 1] = static_cast<uint16_t>(ww[q] >> 16);
-        }
-    } else {
-        const uint2 a = *reinterpret_cast<const uint2 *>(src);
-        const uint32_t ww[2] = {a.x, a.y};
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            vals[2 * q] = static_cast<uint16_t>(ww[q]);
-            vals[2 * q + 1] = static_cast<uint16_t>(ww[q] >> 16);
-        }
+    for (int q = 0; q < VPW / 2; ++q) {
+        vals[2 * q] = static_cast<uint16_t>(ww[q]);
+        vals[2 * q + 1] = static_cast<uint16_t>(ww[q] >> 16);
     }
     float xs = 0.f, corr = 0.f;
 #pragma unroll
@@ -108,6 +90,25 @@ __device__ __forceinline__ void prep_word(const uint16_t *__restrict__ src, uint
             corr += P::kMagicValue * (to_float<BF16>(lo) + to_float<BF16>(hi));
     });
     part = make_float2(corr, xs);
+}
+
+template <int BITS, bool BF16>
+__device__ __forceinline__ void prep_word(const uint16_t *__restrict__ src, uint32_t *pairs,
+                                          int pair_stride, float2 &part) {
+    uint32_t ww[16 / BITS];
+    if constexpr (BITS == 2) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(src);
+        const uint4 c = *reinterpret_cast<const uint4 *>(src + 8);
+        ww[0] = a.x; ww[1] = a.y; ww[2] = a.z; ww[3] = a.w;
+        ww[4] = c.x; ww[5] = c.y; ww[6] = c.z; ww[7] = c.w;
+    } else if constexpr (BITS == 4) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(src);
+        ww[0] = a.x; ww[1] = a.y; ww[2] = a.z; ww[3] = a.w;
+    } else {
+        const uint2 a = *reinterpret_cast<const uint2 *>(src);
+        ww[0] = a.x; ww[1] = a.y;
+    }
+    prep_vals<BITS, BF16>(ww, pairs, pair_stride, part);
 }
 
 // Cooperative prep of a K-vector into LDS by `nthreads` threads.
@@ -177,6 +178,39 @@ __device__ __forceinline__ void prep_unit_at(int bits, const uint16_t *src,
     }
 }
 
+// Split form of prep_unit_at for kernels that want the loads issued early:
+// prep_unit_load reads the unit's 32 / bits values as four 8-byte loads
+// (pieces past the unit re-read its first piece, so every address stays
+// inside the unit), prep_unit_store prepares and writes them.
+struct PrepRaw {
+    uint4 a, c;
+};
+__device__ __forceinline__ PrepRaw prep_unit_load(int bits, const uint16_t *src) {
+    const int pieces = 8 / bits;   // 4, 2 or 1 pieces of 4 values
+    uint2 p[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        p[k] = *reinterpret_cast<const uint2 *>(src + (k < pieces ? 4 * k : 0));
+    PrepRaw r;
+    r.a = make_uint4(p[0].x, p[0].y, p[1].x, p[1].y);
+    r.c = make_uint4(p[2].x, p[2].y, p[3].x, p[3].y);
+    return r;
+}
+template <bool BF16>
+__device__ __forceinline__ void prep_unit_store(int bits, const PrepRaw &r, uint32_t *__restrict__ pairs,
+                                                float2 *__restrict__ part) {
+    if (bits == 2) {
+        const uint32_t ww[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.c.x, r.c.y, r.c.z, r.c.w};
+        prep_vals<2, BF16>(ww, pairs, 1, *part);
+    } else if (bits == 4) {
+        const uint32_t ww[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+        prep_vals<4, BF16>(ww, pairs, 1, *part);
+    } else {
+        const uint32_t ww[2] = {r.a.x, r.a.y};
+        prep_vals<8, BF16>(ww, pairs, 1, *part);
+    }
+}
+
 // u32 pairs and float2 parts per prepared vector of K values.
 __host__ __device__ inline int64_t prep_pairs_count(int K, int bits, bool bf16) {
     const int per_word = bits == 2 ? 8 : bits == 4 ? 4 : (bf16 ? 4 : 2);
@@ -191,7 +225,6 @@ __device__ __forceinline__ void load_xvec_global(XVec<BITS, BF16, CPL, GPC> &xv,
                                                  const uint32_t *__restrict__ pairs,
                                                  const float2 *__restrict__ part, int lane_in_row) {
     using P = Pairs<BITS, BF16>;
-    constexpr int WPG = 4 / GPC;
     constexpr int N32 = 4 * P::kCount;         // u32 per chunk
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
@@ -212,8 +245,20 @@ __device__ __forceinline__ void load_xvec_global(XVec<BITS, BF16, CPL, GPC> &xv,
         for (int wd = 0; wd < 4; ++wd)
 #pragma unroll
             for (int p = 0; p < P::kCount; ++p) xv.xp[i][wd][p] = buf[wd * P::kCount + p];
-        const float4 pa = reinterpret_cast<const float4 *>(part + static_cast<int64_t>(c) * 4)[0];
-        const float4 pb = reinterpret_cast<const float4 *>(part + static_cast<int64_t>(c) * 4)[1];
+        xv.raw[i][0] = reinterpret_cast<const float4 *>(part + static_cast<int64_t>(c) * 4)[0];
+        xv.raw[i][1] = reinterpret_cast<const float4 *>(part + static_cast<int64_t>(c) * 4)[1];
+    }
+}
+
+// Folds the per-word sums loaded by load_xvec_global into per-group-part
+// sums. Kept separate so that a kernel can issue its weight loads before
+// anything waits on the activation loads.
+template <int BITS, bool BF16, int CPL, int GPC>
+__device__ __forceinline__ void xvec_finish(XVec<BITS, BF16, CPL, GPC> &xv) {
+    constexpr int WPG = 4 / GPC;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const float4 pa = xv.raw[i][0], pb = xv.raw[i][1];
         const float2 pw[4] = {make_float2(pa.x, pa.y), make_float2(pa.z, pa.w),
                               make_float2(pb.x, pb.y), make_float2(pb.z, pb.w)};
 #pragma unroll
@@ -238,16 +283,15 @@ struct RowData {
     uint16_t b[CPL][GPC];
 };
 
+// Group metadata of one row for one lane (scale and bias per group part).
 template <int BITS, int CPL, int LPR, int GPC>
-__device__ __forceinline__ void load_row(RowData<CPL, GPC> &rd, const uint32_t *__restrict__ wrow,
-                                         const uint16_t *__restrict__ srow,
-                                         const uint16_t *__restrict__ brow, int group,
-                                         int lane_in_row) {
+__device__ __forceinline__ void load_row_meta(RowData<CPL, GPC> &rd,
+                                              const uint16_t *__restrict__ srow,
+                                              const uint16_t *__restrict__ brow, int group,
+                                              int lane_in_row) {
     using G = Geom<BITS, CPL, LPR, GPC>;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-        rd.c[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4 *>(wrow) + lane_in_row + LPR * i);
         const int k0 = (lane_in_row + LPR * i) * G::kVPC;
 #pragma unroll
         for (int gp = 0; gp < GPC; ++gp) {
@@ -256,6 +300,26 @@ __device__ __forceinline__ void load_row(RowData<CPL, GPC> &rd, const uint32_t *
             rd.b[i][gp] = brow[g];
         }
     }
+}
+
+// Packed weights of one row for one lane: CPL 16-byte chunks, streamed once.
+template <int CPL, int LPR, int GPC>
+__device__ __forceinline__ void load_row_weights(RowData<CPL, GPC> &rd,
+                                                 const uint32_t *__restrict__ wrow,
+                                                 int lane_in_row) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+        rd.c[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(wrow) + lane_in_row + LPR * i);
+}
+
+template <int BITS, int CPL, int LPR, int GPC>
+__device__ __forceinline__ void load_row(RowData<CPL, GPC> &rd, const uint32_t *__restrict__ wrow,
+                                         const uint16_t *__restrict__ srow,
+                                         const uint16_t *__restrict__ brow, int group,
+                                         int lane_in_row) {
+    load_row_weights<CPL, LPR, GPC>(rd, wrow, lane_in_row);
+    load_row_meta<BITS, CPL, LPR, GPC>(rd, srow, brow, group, lane_in_row);
 }
 
 // Partial (this lane's chunks) of sum_k x_k w[row, k].

@@ -9,17 +9,18 @@
 // canonical: descending selection value, ties to the lower expert id.
 //
 // Kernels
-//   router_gemv_kernel   one wave per expert (decode, few tokens): 16-byte
-//                        loads of the gate row and of x, v_dot2 when x and Wg
-//                        share a 16-bit type. The same launch prepares the
+//   router_gemv_fast_kernel  decode (few tokens), gate and x of one 16-bit
+//                        type, d = 512 * NCH: one wave per expert, all of a
+//                        lane's 16-byte gate chunks and x chunks issued before
+//                        the first v_dot2. The same launch prepares the
 //                        activations for the expert kernels (prepared-vector
-//                        form, see qgemv.hpp). The last wave to finish
-//                        (device-scope counter) selects for every token, so
-//                        decode routing is a single launch.
+//                        form, see qgemv.hpp).
+//   router_gemv_kernel   the same for any gate dtype and d % 8 == 0.
 //   router_mfma_kernel   prefill: 32 tokens x 32 experts per wave with
 //                        v_mfma_f32_32x32x16, K split kRouterSplits ways into
 //                        partial sums that the selection adds in fixed order.
-//   router_select_kernel one wave per token: scores, top-k, weights, slots.
+//   router_select_kernel one wave per token: scores, top-k (DPP arg-max over
+//                        (value, ~expert) keys), weights, slots.
 //   prep_vectors_kernel  standalone activation prep for the expert kernels.
 #include "launch.hpp"
 
@@ -35,105 +36,128 @@ __device__ __forceinline__ float softplus_f(float l) {
 
 // --------------------------------------------------------------------------
 // Selection for one token, executed by one full wave. Lane j < top_k ends up
-// owning the j-th choice.
+// owning the j-th choice. Logits are the sum of NS partial rows (fixed order)
+// at logit_row + s * split_stride, or L.logits_in when given. Lane l holds
+// experts l + 64 i, i < M (M = ceil(E / 64)); SF is the score function.
+// A single wave has nothing to hide latency behind, so everything the
+// selection can need (logits, bias, the expert -> slot map, the hash row) is
+// loaded up front at clamped in-bounds addresses, and the code is kept small
+// and branch-free (one score function and M per instantiation): a lone wave
+// also pays for every instruction-cache miss.
 // --------------------------------------------------------------------------
-__device__ void select_token(const RouterLaunch &L, int t, const float *logit_row, int nsplit,
+template <int SF>
+__device__ __forceinline__ float score_of(float l, float lmax, float denom) {
+    if constexpr (SF == 0) return sqrtf(softplus_f(l));
+    else if constexpr (SF == 1) return 1.0f / (1.0f + expf(-l));
+    else return expf(l - lmax) / denom;
+}
+
+template <int NS, int SF, int M>
+__device__ void select_token(const RouterLaunch &L, int t, const float *logit_row,
                              int64_t split_stride) {
     const int lane = threadIdx.x & 63;
-    float sc[kRouterMaxExpertsPerLane], sel[kRouterMaxExpertsPerLane];
-    float lmax = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kRouterMaxExpertsPerLane; ++i) {
-        const int e = lane + 64 * i;
-        float l = -INFINITY;
-        if (e < L.E) {
-            if (L.logits_in) {
-                l = L.logits_in[static_cast<int64_t>(t) * L.E + e];
-            } else {
-                l = 0.f;
-                for (int s = 0; s < nsplit; ++s) l += logit_row[s * split_stride + e];
-            }
-        }
-        sc[i] = l;
-        lmax = fmaxf(lmax, l);
+    float part[NS][M], bias[M];
+    int slot_of[M];
+    int hash_e = -1;
+    if (L.tid2eid) {
+        const int id = L.input_ids[t];
+        if (id >= 0 && id < L.vocab && lane < L.top_k)
+            hash_e = L.tid2eid[static_cast<int64_t>(id) * L.top_k + lane];
     }
-    float denom = 1.f;
-    if (L.score_func == 2) {
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int e = min(lane + 64 * i, L.E - 1);
+        if (L.logits_in) {
+            part[0][i] = L.logits_in[static_cast<int64_t>(t) * L.E + e];
+#pragma unroll
+            for (int q = 1; q < NS; ++q) part[q][i] = 0.f;
+        } else {
+#pragma unroll
+            for (int q = 0; q < NS; ++q) part[q][i] = logit_row[q * split_stride + e];
+        }
+        bias[i] = L.bias ? L.bias[e] : 0.f;
+        slot_of[i] = L.slot_of_expert ? L.slot_of_expert[e] : -1;
+    }
+    float sc[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        float l = part[0][i];
+#pragma unroll
+        for (int q = 1; q < NS; ++q) l += part[q][i];
+        sc[i] = lane + 64 * i < L.E ? l : -INFINITY;
+    }
+    float denom = 1.f, lmax = -INFINITY;
+    if constexpr (SF == 2) {
+#pragma unroll
+        for (int i = 0; i < M; ++i) lmax = fmaxf(lmax, sc[i]);
         for (int m = 32; m >= 1; m >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, m, 64));
         float z = 0.f;
 #pragma unroll
-        for (int i = 0; i < kRouterMaxExpertsPerLane; ++i)
-            if (lane + 64 * i < L.E) z += expf(sc[i] - lmax);
+        for (int i = 0; i < M; ++i) z += lane + 64 * i < L.E ? expf(sc[i] - lmax) : 0.f;
         for (int m = 32; m >= 1; m >>= 1) z += __shfl_xor(z, m, 64);
         denom = z;
     }
+    // Keys: hi = ordered selection value, lo = ~expert (ties -> lower id);
+    // hi = 0 marks an invalid or already-taken candidate.
+    uint32_t khi[M];
 #pragma unroll
-    for (int i = 0; i < kRouterMaxExpertsPerLane; ++i) {
-        const int e = lane + 64 * i;
-        if (e < L.E) {
-            const float l = sc[i];
-            float s;
-            if (L.score_func == 0) s = sqrtf(softplus_f(l));
-            else if (L.score_func == 1) s = 1.0f / (1.0f + expf(-l));
-            else s = expf(l - lmax) / denom;
-            sc[i] = s;
-            sel[i] = s + (L.bias ? L.bias[e] : 0.f);
-        } else {
-            sc[i] = 0.f;
-            sel[i] = -INFINITY;
-        }
+    for (int i = 0; i < M; ++i) {
+        const bool valid = lane + 64 * i < L.E;
+        const float s = score_of<SF>(valid ? sc[i] : 0.f, lmax, denom);
+        sc[i] = valid ? s : 0.f;
+        khi[i] = valid ? ordered_bits(s + bias[i]) : 0u;
     }
-    int my_e = -1;
-    float my_s = 0.f;
+    int my_e = -1, my_slot = -1;
+    float my_s = 0.f, sum = 0.f;
     for (int j = 0; j < L.top_k; ++j) {
         int best_e;
         if (L.tid2eid) {
-            const int id = L.input_ids[t];
-            best_e = (id >= 0 && id < L.vocab) ? L.tid2eid[static_cast<int64_t>(id) * L.top_k + j] : -1;
-            if (best_e >= L.E) best_e = -1;
+            best_e = __builtin_amdgcn_readlane(hash_e, j);
+            if (best_e >= L.E || best_e < 0) best_e = -1;
         } else {
-            float bv = -INFINITY;
-            int be = 0x7fffffff;
+            uint32_t bh = 0, bl = 0;
 #pragma unroll
-            for (int i = 0; i < kRouterMaxExpertsPerLane; ++i) {
-                const int e = lane + 64 * i;
-                if (e < L.E && (sel[i] > bv || (sel[i] == bv && e < be))) { bv = sel[i]; be = e; }
+            for (int i = 0; i < M; ++i) {
+                const uint32_t h = khi[i], l = ~static_cast<uint32_t>(lane + 64 * i);
+                const bool take = h > bh || (h == bh && h != 0 && l > bl);
+                bh = take ? h : bh;
+                bl = take ? l : bl;
             }
-            for (int m = 32; m >= 1; m >>= 1) {
-                const float ov = __shfl_xor(bv, m, 64);
-                const int oe = __shfl_xor(be, m, 64);
-                if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
-            }
-            best_e = be < L.E ? be : -1;
+            wave_max_key(bh, bl);
+            best_e = bh == 0 ? -1 : static_cast<int>(~bl);
 #pragma unroll
-            for (int i = 0; i < kRouterMaxExpertsPerLane; ++i)
-                if (lane + 64 * i == best_e) sel[i] = -INFINITY;
+            for (int i = 0; i < M; ++i)
+                if (lane + 64 * i == best_e) khi[i] = 0u;
         }
-        float mine = 0.f;
-        const int slot_i = best_e >= 0 ? (best_e >> 6) : 0;
+        float s = 0.f;
+        int slot = -1;
+        if (best_e >= 0) {
+            float mine = sc[0];
+            int mslot = slot_of[0];
 #pragma unroll
-        for (int i = 0; i < kRouterMaxExpertsPerLane; ++i)
-            if (i == slot_i) mine = sc[i];
-        const float s = best_e >= 0 ? __shfl(mine, best_e & 63, 64) : 0.f;
+            for (int i = 1; i < M; ++i) {
+                if (i == (best_e >> 6)) {
+                    mine = sc[i];
+                    mslot = slot_of[i];
+                }
+            }
+            s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), best_e & 63));
+            slot = __builtin_amdgcn_readlane(mslot, best_e & 63);
+        }
+        sum += s;   // selection order, as the scores are gathered
         if (lane == j) {
             my_e = best_e;
             my_s = s;
+            my_slot = slot;
         }
     }
-    float sum = lane < L.top_k ? my_s : 0.f;
-    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m, 64);
     if (lane < L.top_k) {
         float w = my_s;
         if (L.norm_topk) w = w / (sum + 1e-20f);
         const int64_t o = static_cast<int64_t>(t) * L.top_k + lane;
         L.idx[o] = my_e;
         L.weights[o] = w * L.routed_scale;
-        if (L.route_slot) {
-            int slot = -1;
-            if (my_e >= 0 && L.slot_of_expert) slot = L.slot_of_expert[my_e];
-            if (slot >= L.n_slots) slot = -1;
-            L.route_slot[o] = slot;
-        }
+        if (L.route_slot) L.route_slot[o] = my_slot >= L.n_slots ? -1 : my_slot;
     }
 }
 
@@ -171,7 +195,7 @@ hipError_t launch_prep_vectors(const uint16_t *v, int n_vec, int K, int bits, bo
 }
 
 // --------------------------------------------------------------------------
-// GEMV logits (decode) + activation prep + fused last-wave selection.
+// GEMV logits (decode) + activation prep + fused last-workgroup selection.
 // --------------------------------------------------------------------------
 template <int GDT, bool XBF16>
 __device__ __forceinline__ void gate_chunk(const void *w, int64_t off, uint32_t (&wp)[4], float (&wf)[8]) {
@@ -193,18 +217,105 @@ __device__ __forceinline__ void gate_chunk(const void *w, int64_t off, uint32_t 
     }
 }
 
-constexpr int kRouterWaves = 8;   // experts per workgroup (one per wave)
+constexpr int kRouterWaves = 4;   // experts per workgroup (one per wave)
 
+// Prep units of the prepared activation vectors, one per thread over the
+// whole grid (the launcher checks that the grid covers them). Split in two so
+// that the loads go out with the gate loads: router_prep_load reads the
+// thread's unit (a clamped, in-bounds unit when it has none), and
+// router_prep_store writes it.
+__device__ __forceinline__ int router_prep_unit(const RouterLaunch &L, int &vec, int &unit) {
+    const int per_vec = L.d / (32 / L.prep_bits);
+    const int u = blockIdx.x * blockDim.x + threadIdx.x;
+    const int uc = min(u, L.tokens * per_vec - 1);
+    vec = uc / per_vec;
+    unit = uc % per_vec;
+    return u;
+}
+
+__device__ __forceinline__ PrepRaw router_prep_load(const RouterLaunch &L) {
+    int vec, unit;
+    router_prep_unit(L, vec, unit);
+    return prep_unit_load(L.prep_bits, L.x + static_cast<int64_t>(vec) * L.d + unit * (32 / L.prep_bits));
+}
+
+template <bool XBF16>
+__device__ __forceinline__ void router_prep_store(const RouterLaunch &L, const PrepRaw &raw) {
+    int vec, unit;
+    const int u = router_prep_unit(L, vec, unit);
+    if (u < L.tokens * (L.d / (32 / L.prep_bits)))
+        prep_unit_store<XBF16>(L.prep_bits, raw,
+                               L.xprep.pairs + vec * L.xprep.pairs_stride +
+                                   unit * pairs_per_word<XBF16>(L.prep_bits),
+                               L.xprep.parts + vec * L.xprep.parts_stride + unit);
+}
+
+template <bool XBF16>
+__device__ __forceinline__ void router_prep(const RouterLaunch &L) {
+    if (L.xprep.pairs) router_prep_store<XBF16>(L, router_prep_load(L));
+}
+
+// Fast path: gate and x share a 16-bit type (v_dot2), d = 512 * NCH, and TB
+// tokens per pass. Every lane issues all NCH gate chunks of its expert and
+// the TB tokens' x chunks before the first dot; tokens beyond L.tokens in
+// the last pass re-read the last token and are not stored.
+template <bool XBF16, int NCH, int TB>
+__global__ __launch_bounds__(64 * kRouterWaves) void router_gemv_fast_kernel(RouterLaunch L) {
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+    const bool have = e < L.E;
+    const uint16_t *gw = static_cast<const uint16_t *>(L.gate_w) +
+                         static_cast<int64_t>(min(e, L.E - 1)) * L.d;
+    u32x4 w[NCH];
+    if (have) {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i)
+            w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gw) + lane + 64 * i);
+    }
+    const bool prep = L.xprep.pairs != nullptr;
+    PrepRaw raw{};
+    if (prep) raw = router_prep_load(L);
+    if (have) {
+        for (int t0 = 0; t0 < L.tokens; t0 += TB) {
+            uint4 xv[TB][NCH];
+#pragma unroll
+            for (int q = 0; q < TB; ++q) {
+                const uint16_t *xr = L.x + static_cast<int64_t>(min(t0 + q, L.tokens - 1)) * L.d;
+#pragma unroll
+                for (int i = 0; i < NCH; ++i)
+                    xv[q][i] = reinterpret_cast<const uint4 *>(xr)[lane + 64 * i];
+            }
+            float acc[TB];
+#pragma unroll
+            for (int q = 0; q < TB; ++q) {
+                acc[q] = 0.f;
+#pragma unroll
+                for (int i = 0; i < NCH; ++i) {
+                    acc[q] = dot2<XBF16>(xv[q][i].x, w[i].x, acc[q]);
+                    acc[q] = dot2<XBF16>(xv[q][i].y, w[i].y, acc[q]);
+                    acc[q] = dot2<XBF16>(xv[q][i].z, w[i].z, acc[q]);
+                    acc[q] = dot2<XBF16>(xv[q][i].w, w[i].w, acc[q]);
+                }
+            }
+            reduce_transposed<TB, 64>(acc, lane);
+            const int q = lane / (64 / TB);
+            if ((lane % (64 / TB)) == 0 && t0 + q < L.tokens)
+                L.logits[static_cast<int64_t>(t0 + q) * L.E + e] = acc[0];
+        }
+    }
+    if (prep) router_prep_store<XBF16>(L, raw);
+}
+
+// General path: any gate dtype (fp32, or a 16-bit type other than x's) and
+// any d that is a multiple of 8.
 template <int GDT, bool XBF16>
 __global__ __launch_bounds__(64 * kRouterWaves) void router_gemv_kernel(RouterLaunch L) {
     constexpr int TB = kRouterTokensPerPass;
     constexpr bool kDot = GDT != 0 && ((GDT == 2) == XBF16);
     const int lane = threadIdx.x & 63;
     const int e = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
-    if (L.xprep.pairs)
-        prep_units<XBF16>(L.x, L.tokens, L.d, L.prep_bits, L.xprep,
-                          blockIdx.x * blockDim.x + threadIdx.x, 1);
-    if (!L.logits_in && e < L.E) {
+    router_prep<XBF16>(L);
+    if (e < L.E) {
         for (int t0 = 0; t0 < L.tokens; t0 += TB) {
             float acc[TB];
 #pragma unroll
@@ -215,20 +326,18 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_gemv_kernel(RouterLa
                 gate_chunk<GDT, XBF16>(L.gate_w, static_cast<int64_t>(e) * L.d + k, wp, wf);
 #pragma unroll
                 for (int q = 0; q < TB; ++q) {
-                    if (t0 + q < L.tokens) {
-                        const uint4 xv = *reinterpret_cast<const uint4 *>(
-                            L.x + static_cast<int64_t>(t0 + q) * L.d + k);
-                        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-                        if constexpr (kDot) {
+                    const uint4 xv = *reinterpret_cast<const uint4 *>(
+                        L.x + static_cast<int64_t>(min(t0 + q, L.tokens - 1)) * L.d + k);
+                    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+                    if constexpr (kDot) {
 #pragma unroll
-                            for (int u = 0; u < 4; ++u) acc[q] = dot2<XBF16>(xw[u], wp[u], acc[q]);
-                        } else {
+                        for (int u = 0; u < 4; ++u) acc[q] = dot2<XBF16>(xw[u], wp[u], acc[q]);
+                    } else {
 #pragma unroll
-                            for (int u = 0; u < 4; ++u) {
-                                acc[q] = fmaf(to_float<XBF16>(static_cast<uint16_t>(xw[u])), wf[2 * u], acc[q]);
-                                acc[q] = fmaf(to_float<XBF16>(static_cast<uint16_t>(xw[u] >> 16)),
-                                              wf[2 * u + 1], acc[q]);
-                            }
+                        for (int u = 0; u < 4; ++u) {
+                            acc[q] = fmaf(to_float<XBF16>(static_cast<uint16_t>(xw[u])), wf[2 * u], acc[q]);
+                            acc[q] = fmaf(to_float<XBF16>(static_cast<uint16_t>(xw[u] >> 16)),
+                                          wf[2 * u + 1], acc[q]);
                         }
                     }
                 }
@@ -239,19 +348,6 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_gemv_kernel(RouterLa
                 L.logits[static_cast<int64_t>(t0 + q) * L.E + e] = acc[0];
         }
     }
-    // Last workgroup to arrive selects: release this workgroup's logits,
-    // count once per workgroup (device-scope atomics are costly, so only
-    // E / 8 of them), and let the final arrival acquire everyone's.
-    __shared__ unsigned last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(L.counter, 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    for (int t = threadIdx.x >> 6; t < L.tokens; t += kRouterWaves)
-        select_token(L, t, L.logits + static_cast<int64_t>(t) * L.E, 1, 0);
-    if (threadIdx.x == 0) atomicExch(L.counter, 0u);
 }
 
 // --------------------------------------------------------------------------
@@ -321,12 +417,33 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(RouterLaunch L) {
     }
 }
 
-__global__ __launch_bounds__(256) void router_select_kernel(RouterLaunch L, int nsplit) {
+template <int NS, int SF, int M>
+__global__ __launch_bounds__(256) void router_select_kernel(RouterLaunch L) {
     const int wave = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wave;
     if (t >= L.tokens) return;
-    select_token(L, t, L.logits + static_cast<int64_t>(t) * L.E, nsplit,
-                 static_cast<int64_t>(L.tokens) * L.E);
+    select_token<NS, SF, M>(L, t, L.logits + static_cast<int64_t>(t) * L.E,
+                            static_cast<int64_t>(L.tokens) * L.E);
+}
+
+template <int NS, int SF>
+hipError_t launch_select_m(const RouterLaunch &L, hipStream_t st) {
+    const dim3 grid((L.tokens + 3) / 4), block(256);
+    if (L.E <= 64) hipLaunchKernelGGL((router_select_kernel<NS, SF, 1>), grid, block, 0, st, L);
+    else if (L.E <= 128) hipLaunchKernelGGL((router_select_kernel<NS, SF, 2>), grid, block, 0, st, L);
+    else if (L.E <= 256) hipLaunchKernelGGL((router_select_kernel<NS, SF, 4>), grid, block, 0, st, L);
+    else hipLaunchKernelGGL((router_select_kernel<NS, SF, 8>), grid, block, 0, st, L);
+    return hipGetLastError();
+}
+
+template <int NS>
+hipError_t launch_select(const RouterLaunch &L, hipStream_t st) {
+    switch (L.score_func) {
+    case 0: return launch_select_m<NS, 0>(L, st);
+    case 1: return launch_select_m<NS, 1>(L, st);
+    case 2: return launch_select_m<NS, 2>(L, st);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 // --------------------------------------------------------------------------
@@ -335,22 +452,21 @@ hipError_t launch_router(const RouterLaunch &L, hipStream_t st) {
         return hipErrorInvalidValue;
     const bool mfma_ok = !L.logits_in && L.tokens > kRouterTokensPerPass && L.gate_dtype != 0 &&
                          ((L.gate_dtype == 2) == L.x_bf16) && L.d % (64 * kRouterSplits) == 0;
-    if (mfma_ok) {
+    if (mfma_ok || L.logits_in) {
         if (L.xprep.pairs) {
             hipError_t e = launch_prep_vectors(L.x, L.tokens, L.d, L.prep_bits, L.x_bf16, L.xprep, st);
             if (e != hipSuccess) return e;
         }
+        if (L.logits_in) return launch_select<1>(L, st);
         dim3 grid((L.tokens + 63) / 64, (L.E + 63) / 64, kRouterSplits);
         if (L.x_bf16) hipLaunchKernelGGL(router_mfma_kernel<true>, grid, dim3(256), 0, st, L);
         else hipLaunchKernelGGL(router_mfma_kernel<false>, grid, dim3(256), 0, st, L);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(router_select_kernel, dim3((L.tokens + 3) / 4), dim3(256), 0, st, L,
-                           kRouterSplits);
-        return hipGetLastError();
+        return launch_select<kRouterSplits>(L, st);
     }
     if (L.d % 8 != 0) return hipErrorInvalidValue;
-    // every wave must cover its share of the prep units
+    // every thread of the grid prepares at most one unit
     const int blocks = (L.E + kRouterWaves - 1) / kRouterWaves;
     if (L.xprep.pairs && static_cast<int64_t>(blocks) * 64 * kRouterWaves <
                              static_cast<int64_t>(L.tokens) * (L.d * L.prep_bits / 32)) {
@@ -361,17 +477,35 @@ hipError_t launch_router(const RouterLaunch &L, hipStream_t st) {
         return launch_router(L2, st);
     }
     dim3 grid(blocks), block(64 * kRouterWaves);
+    const bool dot_ok = L.gate_dtype != 0 && ((L.gate_dtype == 2) == L.x_bf16);
+    const int nch = L.d % 512 == 0 ? L.d / 512 : 0;
+    if (dot_ok && (nch == 2 || nch == 4 || nch == 8 || nch == 16)) {
+        const int tb = L.tokens == 1 ? 1 : L.tokens == 2 ? 2 : 4;
+#define LOCALI_FAST(XB, N, T) hipLaunchKernelGGL((router_gemv_fast_kernel<XB, N, T>), grid, block, 0, st, L)
+#define LOCALI_FAST_TB(XB, N) \
+    if (tb == 1) LOCALI_FAST(XB, N, 1); else if (tb == 2) LOCALI_FAST(XB, N, 2); else LOCALI_FAST(XB, N, 4);
+#define LOCALI_FAST_N(XB) \
+    switch (nch) { case 2: LOCALI_FAST_TB(XB, 2) break; case 4: LOCALI_FAST_TB(XB, 4) break; \
+                   case 8: LOCALI_FAST_TB(XB, 8) break; default: LOCALI_FAST_TB(XB, 16) break; }
+        if (L.x_bf16) { LOCALI_FAST_N(true) } else { LOCALI_FAST_N(false) }
+#undef LOCALI_FAST_N
+#undef LOCALI_FAST_TB
+#undef LOCALI_FAST
+    } else {
 #define LOCALI_ROUTER(GDT)                                                                  \
     if (L.x_bf16) hipLaunchKernelGGL((router_gemv_kernel<GDT, true>), grid, block, 0, st, L); \
     else hipLaunchKernelGGL((router_gemv_kernel<GDT, false>), grid, block, 0, st, L);
-    switch (L.gate_dtype) {
-    case 0: LOCALI_ROUTER(0); break;
-    case 1: LOCALI_ROUTER(1); break;
-    case 2: LOCALI_ROUTER(2); break;
-    default: return hipErrorInvalidValue;
-    }
+        switch (L.gate_dtype) {
+        case 0: LOCALI_ROUTER(0); break;
+        case 1: LOCALI_ROUTER(1); break;
+        case 2: LOCALI_ROUTER(2); break;
+        default: return hipErrorInvalidValue;
+        }
 #undef LOCALI_ROUTER
-    return hipGetLastError();
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_select<1>(L, st);
 }
 
 }  // namespace locali
