@@ -10,8 +10,14 @@ expert. Steps are replayed from a captured HIP graph (inputs already in HBM).
 
 Also reported:
   roofline      the dominant kernel (decode gate/up + SwiGLU), its average
-                launch duration from HIP events recorded around it on its own
-                stream, and achieved algorithmic GB/s against the 8 TB/s peak
+                launch duration from HIP events around a graph of back-to-back
+                launches on the replay stream, achieved algorithmic GB/s
+                against the 8 TB/s peak, and `traffic`: HBM bytes per launch
+                measured by two rocprofv3 --pmc passes (FETCH_SIZE, then
+                WRITE_SIZE), each scaled by what the counter reads for a
+                reference kernel of known bytes -- a 256 MiB reduction and a
+                256 MiB fill (`--copy-calibration`) -- summarised by
+                `--summarize-pmc` into profiles/gateup_route_kernel_decode_traffic.json
   prefill64     64-token prefill on the same layer with Zipf(1.1) expert
                 popularity (grouped path), tokens/s and algorithmic GB/s
   cpu_baseline  the C oracle (oracle/expert_ref.c, OpenMP) on the host cores
@@ -40,6 +46,9 @@ from locali_amd import ops, synth  # noqa: E402
 
 METRIC = "MoE-layer tokens/s at 1 GPU (decode & 64-tok prefill); achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "gateup_route_kernel_decode_traffic.json"
+GATEUP_KERNEL = "gateup_route_kernel<2, true, 1, 64, 1, 8>"
+COPY_BYTES = 256 << 20
 D, E, DFF, K_TOP, GROUP, BITS = 4096, 256, 2048, 6, 64, 2
 
 
@@ -50,6 +59,8 @@ def proj_bytes(rows, cols, bits=BITS, group=GROUP):
 EXPERT_BYTES = 2 * proj_bytes(DFF, D) + proj_bytes(D, DFF)          # 7,864,320
 GATEUP_ROUTE_BYTES = 2 * proj_bytes(DFF, D)                           # 5,242,880
 ROUTER_BYTES = E * D * 2
+# per decode gate/up launch: 7 routes' gate+up slots, x read once, h written
+GATEUP_ALG_BYTES = (K_TOP + 1) * GATEUP_ROUTE_BYTES + D * 2 + (K_TOP + 1) * DFF * 2   # 36,737,024
 
 
 def layer(dev, seed=1):
@@ -107,35 +118,47 @@ def decode_graph_run(spec, arena, shared, slot_of, X, ws, steps, warmup, use_gra
     return e0.elapsed_time(e1) / 1e3, wall, idx
 
 
-def stage_timing(spec, arena, shared, slot_of, X, ws, reps):
-    """Average durations (s) of router / gate-up / down+combine launches, each
-    bracketed by HIP events on the stream the kernels are launched on."""
+def stage_timing(spec, arena, shared, slot_of, X, ws, m=40, replays=5):
+    """Average device time (s) of one router / gate-up / down+combine launch.
+
+    Each stage is captured m times back to back (inputs 0..m-1, so every
+    launch streams different experts) into its own HIP graph; HIP events on
+    the replay stream bracket `replays` replays, and the per-launch average
+    is elapsed / (replays * m) -- the same quantity rocprofv3 reports as a
+    kernel's average duration."""
     dev = X.device
+    n_in = X.shape[0]
+    xs = [X[i % n_in:i % n_in + 1] for i in range(m)]
     hidden = torch.empty(K_TOP + 1, DFF, dtype=torch.bfloat16, device=dev)
     out = torch.empty(1, D, dtype=torch.bfloat16, device=dev)
     dws = ops.Workspace(dev)
     dws.reserve(1, D, DFF, 1, K_TOP, True)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(reps)]
-    # Keep the GPU busy while the host enqueues every step, so that each event
-    # pair measures device time of its kernel rather than host launch latency.
-    torch.cuda._sleep(int(2e8))
-    for r in range(reps):
-        x = X[r % X.shape[0]:r % X.shape[0] + 1]
-        ev = evs[r]
-        ev[0].record()
-        _, w, rs = ops.router(spec, x, ws, slot_of_expert=slot_of, n_slots=E + 1)
-        ev[1].record()
-        ev[2].record()
-        ops.decode_gateup(arena, shared, x, rs, hidden, dws)
-        ev[3].record()
-        ev[4].record()
-        ops.decode_down_combine(arena, shared, rs, w, out, dws)
-        ev[5].record()
-    torch.cuda.synchronize()
-    skip = min(10, reps // 4)
-    def avg(a, b):
-        return sum(e[a].elapsed_time(e[b]) for e in evs[skip:]) / (reps - skip) / 1e3
-    return {"router": avg(0, 1), "gateup": avg(2, 3), "down_combine": avg(4, 5)}
+    routed = [ops.router(spec, x, ws, slot_of_expert=slot_of, n_slots=E + 1) for x in xs]
+    stages = {
+        "router": lambda i: ops.router(spec, xs[i], ws, slot_of_expert=slot_of, n_slots=E + 1),
+        "gateup": lambda i: ops.decode_gateup(arena, shared, xs[i], routed[i][2], hidden, dws),
+        "down_combine": lambda i: ops.decode_down_combine(arena, shared, routed[i][2], routed[i][1],
+                                                          out, dws),
+    }
+    res = {}
+    for name, fn in stages.items():
+        for i in range(2):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(m):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / 1e3 / (replays * m)
+    return res
 
 
 def prefill_run(arena, shared, slot_of, dev, tokens, calls, seed):
@@ -210,6 +233,58 @@ def cpu_baseline(arena, shared, spec, X, seconds):
                       "reference dsv4_arena path on MLX's CPU backend (not runnable here)"}
 
 
+def copy_calibration(dev):
+    """Reference kernels of known traffic for the FETCH_SIZE / WRITE_SIZE
+    counters: a reduction that reads COPY_BYTES (and writes one scalar) and a
+    fill that writes COPY_BYTES (and reads nothing). A plain copy is not used:
+    its stores allocate lines in L2 and read them first, so its FETCH_SIZE
+    counts the destination as well."""
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev)
+    for _ in range(3):
+        src.sum()
+        src.fill_(0.5)
+    torch.cuda.synchronize()
+
+
+def summarize_pmc(fetch_csv, write_csv, out_path=TRAFFIC_FILE):
+    """Turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE pass,
+    WRITE_SIZE pass) into HBM bytes per launch of the decode gate/up kernel,
+    each counter scaled by its reading for a reference kernel of known bytes
+    (reduction for FETCH_SIZE, fill for WRITE_SIZE)."""
+    import csv
+
+    def per_kernel(path, counter, ref_name):
+        rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+        refs = [float(r["Counter_Value"]) for r in rows
+                if ref_name in r["Kernel_Name"] and int(r["Grid_Size"]) >= 1 << 16]
+        target = [float(r["Counter_Value"]) for r in rows if GATEUP_KERNEL in r["Kernel_Name"]]
+        if not refs or not target:
+            raise SystemExit(f"{path}: no {counter} rows for {ref_name} and/or {GATEUP_KERNEL}")
+        ref_kib = sorted(refs)[len(refs) // 2]
+        scale = (COPY_BYTES / 1024) / ref_kib        # true KiB per counted KiB
+        kib = sum(target) / len(target)
+        return {"counter_kib_per_launch": kib, "reference_kernel": ref_name,
+                "reference_counter_kib": ref_kib, "reference_true_kib": COPY_BYTES / 1024,
+                "scale": scale, "bytes_per_launch": kib * 1024 * scale, "launches": len(target)}
+
+    fetch = per_kernel(fetch_csv, "FETCH_SIZE", "reduce_kernel")
+    write = per_kernel(write_csv, "WRITE_SIZE", "FillFunctor")
+    res = {"kernel": GATEUP_KERNEL, "fetch": fetch, "write": write,
+           "traffic_bytes_per_launch": fetch["bytes_per_launch"] + write["bytes_per_launch"],
+           "algorithmic_bytes_per_launch": GATEUP_ALG_BYTES}
+    Path(out_path).write_text(json.dumps(res, indent=1) + "\n")
+    print(json.dumps(res, indent=1))
+    return res
+
+
+def measured_traffic():
+    try:
+        t = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    return t.get("traffic_bytes_per_launch") if t.get("kernel") == GATEUP_KERNEL else None
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -221,16 +296,25 @@ def main(argv=None):
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run 256 MiB read and write reference kernels first (for --pmc byte counters)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two rocprofv3 --pmc runs into HBM bytes per gate/up launch")
     args = ap.parse_args(argv)
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures the streamed-MoE layer on one GPU only; multi-GPU runs are not "
-              "part of this build (see DESIGN.md on expert-parallel sharding).", file=sys.stderr)
+        print("bench.py measures the streamed-MoE layer on one GPU; expert-parallel runs over "
+              "several GPUs are not implemented.", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        copy_calibration(dev)
     print(f"[bench] building layer d={D} E={E} dff={DFF} {BITS}-bit g{GROUP}", file=sys.stderr, flush=True)
     arena, shared, slot_of = layer(dev, args.seed)
     w, _ = synth.uniform_router(E, D, torch.bfloat16, seed=args.seed + 2, device=dev)
@@ -247,8 +331,8 @@ def main(argv=None):
     layer_bytes = 7 * EXPERT_BYTES + ROUTER_BYTES
 
     print("[bench] stage timing", file=sys.stderr, flush=True)
-    st = stage_timing(spec, arena, shared, slot_of, X, ws, reps=200)
-    gate_bytes = (K_TOP + 1) * GATEUP_ROUTE_BYTES + D * 2 + (K_TOP + 1) * DFF * 2
+    st = stage_timing(spec, arena, shared, slot_of, X, ws)
+    gate_bytes = GATEUP_ALG_BYTES
     achieved = gate_bytes / st["gateup"] / 1e9
     result = {
         "metric": METRIC,
@@ -273,6 +357,7 @@ def main(argv=None):
             "wall_s": wall,
             "layer_bytes_per_token": layer_bytes,
             "layer_GBps": layer_bytes * value / 1e9,
+            "layer_frac_of_hbm_peak": layer_bytes * value / 1e9 / HBM_PEAK_GBS,
         },
         "roofline": {
             "bound": "hbm",
@@ -281,7 +366,7 @@ def main(argv=None):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(),
             "algorithmic_bytes_per_launch": gate_bytes,
             "avg_launch_us": st["gateup"] * 1e6,
             "stage_us": {k: v * 1e6 for k, v in st.items()},

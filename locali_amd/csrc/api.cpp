@@ -45,7 +45,7 @@ bool dtype16(int32_t dt) { return dt == LOCALI_DT_F16 || dt == LOCALI_DT_BF16; }
 
 // Workspace layout for up to T tokens.
 struct Layout {
-    size_t logits, route_slot, hidden, xprep, hprep, seg_start, sorted_route, route_pos,
+    size_t logits, route_slot, hidden, hprep, seg_start, sorted_route, route_pos,
         tiles, n_tiles, gh, gy, total;
     int max_tiles;
 };
@@ -68,7 +68,6 @@ Layout layout(int T, int d, int dff, int E, int k, int has_shared) {
     L.logits = take(sizeof(float) * kRouterSplitsHost * static_cast<size_t>(T) * E);
     L.route_slot = take(sizeof(int32_t) * R);
     L.hidden = take(sizeof(uint16_t) * static_cast<size_t>(routes) * dff);
-    L.xprep = take(prep_bytes(d) * T);
     L.hprep = take(prep_bytes(dff) * routes);
     L.seg_start = take(sizeof(int32_t) * (kMaxSlots + 1));
     L.sorted_route = take(sizeof(int32_t) * R);
@@ -177,13 +176,11 @@ PrepVec prep_batch(void *base, int n_vec, int K, int bits, bool bf16) {
     return v;
 }
 
-// stages: bit 0 = gate/up, bit 1 = down + combine. xprep_ready: the
-// activations were already prepared into x_prep_base by the router.
+// stages: bit 0 = gate/up, bit 1 = down + combine.
 int run_decode(const locali_expert_arena *routed, const locali_expert_arena *shared, const void *x,
                int32_t x_dtype, int32_t tokens, int32_t top_k, const int32_t *route_slot,
                const float *weights, float limit, int32_t fp32_swiglu, int32_t combine_mode,
-               void *hidden, void *out, hipStream_t st, int stages, void *x_prep_base,
-               bool xprep_ready, void *h_prep_base) {
+               void *hidden, void *out, hipStream_t st, int stages, void *h_prep_base) {
     DecodeLaunch L{};
     L.ra.x = static_cast<const uint16_t *>(x);
     L.ra.route_slot = route_slot;
@@ -206,14 +203,8 @@ int run_decode(const locali_expert_arena *routed, const locali_expert_arena *sha
     L.ca.out = static_cast<uint16_t *>(out);
     L.ca.mode = combine_mode;
     const bool bf16 = x_dtype == LOCALI_DT_BF16;
-    L.xprep = prep_batch(x_prep_base, tokens, routed->gate.cols, routed->gate.bits, bf16);
     L.hprep = prep_batch(h_prep_base, L.routes, routed->down.cols, routed->down.bits, bf16);
     hipError_t e;
-    if ((stages & 1) && !xprep_ready) {
-        e = launch_prep_vectors(static_cast<const uint16_t *>(x), tokens, routed->gate.cols,
-                                routed->gate.bits, bf16, L.xprep, st);
-        if (e != hipSuccess) return hip_fail(e, "activation prep launch");
-    }
     if ((stages & 1) && (e = launch_gateup_decode(L, st)) != hipSuccess)
         return hip_fail(e, "gate/up decode launch");
     if ((stages & 2) && (e = launch_down_combine_decode(L, st)) != hipSuccess)
@@ -299,7 +290,7 @@ int check_router(const locali_router *r, int d) {
 int route(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens, int32_t d_model,
           const int32_t *input_ids, const float *logits_in, const int32_t *slot_of_expert,
           int32_t n_slots, int32_t *idx, float *weights, int32_t *route_slot, void *workspace,
-          const Layout &lay, PrepVec xprep, int prep_bits, hipStream_t st) {
+          const Layout &lay, hipStream_t st) {
     if (router->tid2eid && !input_ids) return fail(LOCALI_E_ARG, "router: hash routing needs input_ids");
     if (route_slot && (!slot_of_expert || n_slots < 1))
         return fail(LOCALI_E_ARG, "router: route_slot needs slot_of_expert and n_slots");
@@ -326,8 +317,6 @@ int route(const locali_router *router, const void *x, int32_t x_dtype, int32_t t
     L.route_slot = route_slot;
     L.logits = at<float>(workspace, lay.logits);
     L.logits_in = logits_in;
-    L.xprep = xprep;
-    L.prep_bits = prep_bits;
     hipError_t e = launch_router(L, st);
     if (e != hipSuccess) return hip_fail(e, "router launch");
     return 0;
@@ -357,7 +346,7 @@ int locali_moe_router(const locali_router *router, const void *x, int32_t x_dtyp
     if (workspace_bytes < lay.route_slot)
         return fail(LOCALI_E_WORKSPACE, "router: workspace %zu < %zu bytes", workspace_bytes, lay.route_slot);
     return route(router, x, x_dtype, tokens, d_model, input_ids, logits_in, slot_of_expert, n_slots, idx,
-                 weights, route_slot, workspace, lay, PrepVec{}, 0, S(stream));
+                 weights, route_slot, workspace, lay, S(stream));
 }
 
 int locali_moe_dispatch(const int32_t *route_slot, int32_t tokens, int32_t top_k, int32_t n_slots,
@@ -392,8 +381,7 @@ int locali_moe_expert_decode(const locali_expert_arena *routed, const locali_exp
     Layout lay;
     if ((rc = decode_workspace(routed, shared, tokens, top_k, workspace_bytes, workspace, &lay))) return rc;
     return run_decode(routed, shared, x, x_dtype, tokens, top_k, route_slot, weights, swiglu_limit,
-                      fp32_swiglu, combine_mode, hidden, out, S(stream), 3, at<void>(workspace, lay.xprep),
-                      false, at<void>(workspace, lay.hprep));
+                      fp32_swiglu, combine_mode, hidden, out, S(stream), 3, at<void>(workspace, lay.hprep));
 }
 
 int locali_moe_decode_gateup(const locali_expert_arena *routed, const locali_expert_arena *shared,
@@ -408,7 +396,7 @@ int locali_moe_decode_gateup(const locali_expert_arena *routed, const locali_exp
     if ((rc = decode_workspace(routed, shared, tokens, top_k, workspace_bytes, workspace, &lay))) return rc;
     return run_decode(routed, shared, x, x_dtype, tokens, top_k, route_slot, nullptr, swiglu_limit,
                       fp32_swiglu, LOCALI_COMBINE_ROUNDED, hidden, nullptr, S(stream), 1,
-                      at<void>(workspace, lay.xprep), false, at<void>(workspace, lay.hprep));
+                      at<void>(workspace, lay.hprep));
 }
 
 int locali_moe_decode_down_combine(const locali_expert_arena *routed,
@@ -423,7 +411,7 @@ int locali_moe_decode_down_combine(const locali_expert_arena *routed,
     if ((rc = decode_workspace(routed, shared, tokens, top_k, workspace_bytes, workspace, &lay))) return rc;
     return run_decode(routed, shared, nullptr, x_dtype, tokens, top_k, route_slot, weights, 0.f, 0,
                       combine_mode, at<void>(workspace, lay.hidden), out, S(stream), 2,
-                      at<void>(workspace, lay.xprep), true, at<void>(workspace, lay.hprep));
+                      at<void>(workspace, lay.hprep));
 }
 
 int locali_moe_expert_grouped(const locali_expert_arena *routed, const locali_expert_arena *shared,
@@ -494,17 +482,13 @@ int locali_moe_forward(const locali_router *router, const locali_expert_arena *r
         return fail(LOCALI_E_WORKSPACE, "forward: workspace %zu < %zu bytes", workspace_bytes, lay.total);
     int32_t *route_slot = at<int32_t>(workspace, lay.route_slot);
     const bool decode = tokens <= kDecodeMaxTokens;
-    const bool bf16 = x_dtype == LOCALI_DT_BF16;
-    PrepVec xprep{};
-    if (decode) xprep = prep_batch(at<void>(workspace, lay.xprep), tokens, d, routed->gate.bits, bf16);
     rc = route(router, x, x_dtype, tokens, d, input_ids, nullptr, slot_of_expert, routed->gate.n_slots,
-               idx, weights, route_slot, workspace, lay, xprep, routed->gate.bits, S(stream));
+               idx, weights, route_slot, workspace, lay, S(stream));
     if (rc) return rc;
     if (decode)
         return run_decode(routed, shared, x, x_dtype, tokens, k, route_slot, weights, swiglu_limit,
                           fp32_swiglu, LOCALI_COMBINE_ROUNDED, at<void>(workspace, lay.hidden), out,
-                          S(stream), 3, at<void>(workspace, lay.xprep), true,
-                          at<void>(workspace, lay.hprep));
+                          S(stream), 3, at<void>(workspace, lay.hprep));
     return run_grouped(routed, shared, x, x_dtype, tokens, k, E, route_slot, weights, swiglu_limit,
                        fp32_swiglu, LOCALI_COMBINE_ROUNDED, out, workspace, lay, S(stream));
 }

@@ -3,12 +3,11 @@
 //   gateup_route_kernel   h[r, n] = swiglu(up_r(x_t)[n], gate_r(x_t)[n]) for
 //                         every route r (routed top-k entries, then one
 //                         shared-expert route per token). A workgroup of 8
-//                         waves covers RB consecutive rows of one route; each
-//                         lane loads its slice of the token's prepared
-//                         activations (written once per token by the router
-//                         or the prep kernel) and streams J rows of the
-//                         slot's gate and up matrices. The epilogue writes h
-//                         and, because the workgroup owns whole words of the
+//                         waves covers RB consecutive rows of one route: it
+//                         prepares the token's activations into LDS while the
+//                         slot's gate and up rows (J per wave) stream in, then
+//                         consumes the rows in load order. The epilogue writes
+//                         h and, because the workgroup owns whole words of the
 //                         down projection's input, also h's prepared form.
 //   down_combine_kernel   out[t, d] = round(sum_j round(round(y_j[d]) * w_j))
 //                         (+ shared, rounded) for RB output rows d: one wave
@@ -41,12 +40,16 @@ constexpr int gateup_rows_per_wave_load() { return LPR >= 16 ? 8 : LPR / 2; }
 // ---------------------------------------------------------------------------
 template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J>
 __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_route_kernel(
-    RouteArgs ra, QProj gate, QProj up, QProj sgate, QProj sup, PrepVec xin, uint16_t *__restrict__ h,
+    RouteArgs ra, QProj gate, QProj up, QProj sgate, QProj sup, uint16_t *__restrict__ h,
     PrepVec hout, int down_bits, float limit, int fp32_swiglu) {
     using G = Geom<BITS, CPL, LPR, GPC>;
     constexpr int RPW = J * G::kRPL;              // rows per wave
     constexpr int RB = kGateUpWaves * RPW;        // rows per workgroup
+    constexpr int kUnits = LPR * CPL * 4;         // words of one row slice = prep units of x
+    constexpr int kThreads = 64 * kGateUpWaves;
+    constexpr int UPT = (kUnits + kThreads - 1) / kThreads;
     __shared__ __align__(16) uint16_t hs[RB];
+    __shared__ XLds<BITS, BF16, CPL, LPR> xl;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int lane_in_row = lane % LPR;
@@ -66,37 +69,67 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_route_kernel(
     const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;   // words per row
     const int gpr = K / pg.group;                               // groups per row
 
+    // The token's activations first (loads retire in issue order, so rows
+    // can be consumed as they land only if x is already in): each thread
+    // reads the raw values of its prep unit(s) of the LDS prepared vector.
+    constexpr int VPW = 32 / BITS;
+    uint32_t xraw[UPT][VPW / 2];
+    const uint16_t *xt = ra.x + static_cast<int64_t>(token) * K;
+#pragma unroll
+    for (int q = 0; q < UPT; ++q) {
+        const int u = min(static_cast<int>(threadIdx.x) + q * kThreads, kUnits - 1);
+        const int ul = u % LPR, uwd = (u / LPR) % 4, ui = u / (LPR * 4);
+        const uint16_t *src = xt + (ul + LPR * ui) * G::kVPC + uwd * VPW;
+#pragma unroll
+        for (int c = 0; c < VPW / 8; ++c) {
+            const uint4 a = reinterpret_cast<const uint4 *>(src)[c];
+            xraw[q][4 * c] = a.x; xraw[q][4 * c + 1] = a.y; xraw[q][4 * c + 2] = a.z; xraw[q][4 * c + 3] = a.w;
+        }
+        if constexpr (VPW == 4) {
+            const uint2 a = *reinterpret_cast<const uint2 *>(src);
+            xraw[q][0] = a.x; xraw[q][1] = a.y;
+        }
+    }
+    sched_fence();
+    // Then every row's (small) metadata, then the weights in the order they
+    // are consumed, so row j's math waits only for row j's chunk. The loads
+    // are unconditional (rows clamped in range; a wave past the last row
+    // re-reads it and stores nothing) so that the wait for x above does not
+    // merge with a path on which no weight loads are outstanding.
+    RowData<CPL, GPC> wg[J], wu[J];
+    const uint32_t *gw = pg.w + sl * pg.w_slot, *uw = pu.w + sl * pu.w_slot;
+    const uint16_t *gs = pg.s + sl * pg.m_slot, *gb = pg.b + sl * pg.m_slot;
+    const uint16_t *us = pu.s + sl * pu.m_slot, *ub = pu.b + sl * pu.m_slot;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
+        load_row_meta<BITS, CPL, LPR, GPC>(wg[j], gs + row * gpr, gb + row * gpr, pg.group,
+                                           lane_in_row);
+        load_row_meta<BITS, CPL, LPR, GPC>(wu[j], us + row * gpr, ub + row * gpr, pu.group,
+                                           lane_in_row);
+    }
+    sched_fence();
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
+        load_row_weights<CPL, LPR, GPC>(wg[j], gw + row * wpr, lane_in_row);
+        load_row_weights<CPL, LPR, GPC>(wu[j], uw + row * wpr, lane_in_row);
+    }
+    sched_fence();
+    // Prepare x into LDS while the weights stream in (waits only for the x
+    // loads issued above).
+#pragma unroll
+    for (int q = 0; q < UPT; ++q) {
+        const int u = static_cast<int>(threadIdx.x) + q * kThreads;
+        if (u < kUnits) {
+            const int ul = u % LPR, uwd = (u / LPR) % 4, ui = u / (LPR * 4);
+            prep_vals<BITS, BF16>(xraw[q], &xl.pairs[ui][uwd][0][ul], LPR, xl.part[ui][uwd][ul]);
+        }
+    }
+    __syncthreads();
     if (active) {
-        const uint32_t *gw = pg.w + sl * pg.w_slot, *uw = pu.w + sl * pu.w_slot;
-        const uint16_t *gs = pg.s + sl * pg.m_slot, *gb = pg.b + sl * pg.m_slot;
-        const uint16_t *us = pu.s + sl * pu.m_slot, *ub = pu.b + sl * pu.m_slot;
-        // Activations first: loads retire in issue order, so rows can be
-        // consumed as they land only if the activations are already in.
         XVec<BITS, BF16, CPL, GPC> xv;
-        load_xvec_global<BITS, BF16, CPL, LPR, GPC>(xv, xin.pairs + token * xin.pairs_stride,
-                                                    xin.parts + token * xin.parts_stride,
-                                                    lane_in_row);
-        sched_fence();
-        // Then every row's (small) metadata, then the weights in the order
-        // they are consumed, so row j's math waits only for row j's chunk.
-        RowData<CPL, GPC> wg[J], wu[J];
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-            load_row_meta<BITS, CPL, LPR, GPC>(wg[j], gs + row * gpr, gb + row * gpr, pg.group,
-                                               lane_in_row);
-            load_row_meta<BITS, CPL, LPR, GPC>(wu[j], us + row * gpr, ub + row * gpr, pu.group,
-                                               lane_in_row);
-        }
-        sched_fence();
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-            load_row_weights<CPL, LPR, GPC>(wg[j], gw + row * wpr, lane_in_row);
-            load_row_weights<CPL, LPR, GPC>(wu[j], uw + row * wpr, lane_in_row);
-        }
-        sched_fence();
-        xvec_finish(xv);
+        load_xvec_lds<BITS, BF16, CPL, LPR, GPC>(xv, xl, lane_in_row);
         const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
         float v[2 * J];
 #pragma unroll
@@ -225,7 +258,7 @@ hipError_t launch_gateup_t(const DecodeLaunch &L, hipStream_t st) {
     if (L.hprep.pairs && rows_per_block % (32 / L.down.bits)) return hipErrorInvalidValue;
     dim3 grid((L.gate.rows + rows_per_block - 1) / rows_per_block, L.routes);
     hipLaunchKernelGGL((gateup_route_kernel<BITS, BF16, CPL, LPR, GPC, J>), grid,
-                       dim3(64 * kGateUpWaves), 0, st, L.ra, L.gate, L.up, L.sgate, L.sup, L.xprep,
+                       dim3(64 * kGateUpWaves), 0, st, L.ra, L.gate, L.up, L.sgate, L.sup,
                        L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu);
     return hipGetLastError();
 }

@@ -35,7 +35,6 @@ struct PrepVec {
 // ---- decode path -----------------------------------------------------------
 struct DecodeLaunch {
     RouteArgs ra;
-    PrepVec xprep;              // prepared activations, one per token (gate/up geometry)
     PrepVec hprep;              // prepared hidden vectors, one per route (down geometry)
     int32_t routes;             // tokens * top_k + n_shared * tokens
     bool bf16;
@@ -48,9 +47,6 @@ struct DecodeLaunch {
 };
 
 hipError_t launch_gateup_decode(const DecodeLaunch &L, hipStream_t st);
-// Prepare n_vec vectors of K values (rows of v) for a projection of `bits`-bit codes.
-hipError_t launch_prep_vectors(const uint16_t *v, int n_vec, int K, int bits, bool bf16,
-                               PrepVec out, hipStream_t st);
 hipError_t launch_down_combine_decode(const DecodeLaunch &L, hipStream_t st);
 int chunks_per_row(const QProj &p);
 int group_parts(const QProj &p);
@@ -76,8 +72,6 @@ struct RouterLaunch {
     int32_t *route_slot;        // [tokens, top_k] or null
     float *logits;              // workspace [tokens, E]
     const float *logits_in;     // optional precomputed logits [tokens, E]
-    PrepVec xprep;              // optional: also prepare x for a projection of
-    int32_t prep_bits;          //   prep_bits-bit codes (pairs null = skip)
 };
 
 hipError_t launch_router(const RouterLaunch &L, hipStream_t st);

@@ -178,39 +178,6 @@ __device__ __forceinline__ void prep_unit_at(int bits, const uint16_t *src,
     }
 }
 
-// Split form of prep_unit_at for kernels that want the loads issued early:
-// prep_unit_load reads the unit's 32 / bits values as four 8-byte loads
-// (pieces past the unit re-read its first piece, so every address stays
-// inside the unit), prep_unit_store prepares and writes them.
-struct PrepRaw {
-    uint4 a, c;
-};
-__device__ __forceinline__ PrepRaw prep_unit_load(int bits, const uint16_t *src) {
-    const int pieces = 8 / bits;   // 4, 2 or 1 pieces of 4 values
-    uint2 p[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        p[k] = *reinterpret_cast<const uint2 *>(src + (k < pieces ? 4 * k : 0));
-    PrepRaw r;
-    r.a = make_uint4(p[0].x, p[0].y, p[1].x, p[1].y);
-    r.c = make_uint4(p[2].x, p[2].y, p[3].x, p[3].y);
-    return r;
-}
-template <bool BF16>
-__device__ __forceinline__ void prep_unit_store(int bits, const PrepRaw &r, uint32_t *__restrict__ pairs,
-                                                float2 *__restrict__ part) {
-    if (bits == 2) {
-        const uint32_t ww[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.c.x, r.c.y, r.c.z, r.c.w};
-        prep_vals<2, BF16>(ww, pairs, 1, *part);
-    } else if (bits == 4) {
-        const uint32_t ww[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
-        prep_vals<4, BF16>(ww, pairs, 1, *part);
-    } else {
-        const uint32_t ww[2] = {r.a.x, r.a.y};
-        prep_vals<8, BF16>(ww, pairs, 1, *part);
-    }
-}
-
 // u32 pairs and float2 parts per prepared vector of K values.
 __host__ __device__ inline int64_t prep_pairs_count(int K, int bits, bool bf16) {
     const int per_word = bits == 2 ? 8 : bits == 4 ? 4 : (bf16 ? 4 : 2);

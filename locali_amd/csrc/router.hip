@@ -12,16 +12,13 @@
 //   router_gemv_fast_kernel  decode (few tokens), gate and x of one 16-bit
 //                        type, d = 512 * NCH: one wave per expert, all of a
 //                        lane's 16-byte gate chunks and x chunks issued before
-//                        the first v_dot2. The same launch prepares the
-//                        activations for the expert kernels (prepared-vector
-//                        form, see qgemv.hpp).
+//                        the first v_dot2.
 //   router_gemv_kernel   the same for any gate dtype and d % 8 == 0.
 //   router_mfma_kernel   prefill: 32 tokens x 32 experts per wave with
 //                        v_mfma_f32_32x32x16, K split kRouterSplits ways into
 //                        partial sums that the selection adds in fixed order.
 //   router_select_kernel one wave per token: scores, top-k (DPP arg-max over
 //                        (value, ~expert) keys), weights, slots.
-//   prep_vectors_kernel  standalone activation prep for the expert kernels.
 #include "launch.hpp"
 
 namespace locali {
@@ -30,31 +27,40 @@ constexpr int kRouterMaxExpertsPerLane = 8;   // E <= 512
 constexpr int kRouterSplits = 4;
 constexpr int kRouterTokensPerPass = 8;
 
-__device__ __forceinline__ float softplus_f(float l) {
-    return l > 20.0f ? l : log1pf(expf(l));
-}
-
 // --------------------------------------------------------------------------
 // Selection for one token, executed by one full wave. Lane j < top_k ends up
 // owning the j-th choice. Logits are the sum of NS partial rows (fixed order)
 // at logit_row + s * split_stride, or L.logits_in when given. Lane l holds
 // experts l + 64 i, i < M (M = ceil(E / 64)); SF is the score function.
-// A single wave has nothing to hide latency behind, so everything the
-// selection can need (logits, bias, the expert -> slot map, the hash row) is
-// loaded up front at clamped in-bounds addresses, and the code is kept small
-// and branch-free (one score function and M per instantiation): a lone wave
-// also pays for every instruction-cache miss.
+// A lone wave pays for every instruction and every memory round trip, so:
+// everything the selection can need (logits, bias, the expert -> slot map,
+// the hash row) is loaded up front at clamped in-bounds addresses; scores use
+// the hardware exp/log; each lane sorts its M keys once, after which a round
+// of top-k is one wave-wide arg-max of the lane heads plus a pop; scores and
+// slots of the chosen experts are fetched back from LDS (`stage`, 64 * M
+// float2 per wave) by the owning lanes.
 // --------------------------------------------------------------------------
 template <int SF>
 __device__ __forceinline__ float score_of(float l, float lmax, float denom) {
-    if constexpr (SF == 0) return sqrtf(softplus_f(l));
-    else if constexpr (SF == 1) return 1.0f / (1.0f + expf(-l));
-    else return expf(l - lmax) / denom;
+    if constexpr (SF == 0) {
+        // sqrt(softplus(l)); log1p(e) ~ e within 1.5e-7 relative below -15
+        const float e = __expf(l);
+        const float sp = l > 20.0f ? l : (l < -15.0f ? e : __logf(1.0f + e));
+        return sqrtf(sp);
+    } else if constexpr (SF == 1) {
+        return 1.0f / (1.0f + __expf(-l));
+    } else {
+        return __expf(l - lmax) / denom;
+    }
+}
+
+__device__ __forceinline__ bool key_gt(uint32_t ah, uint32_t al, uint32_t bh, uint32_t bl) {
+    return ah > bh || (ah == bh && al > bl);
 }
 
 template <int NS, int SF, int M>
 __device__ void select_token(const RouterLaunch &L, int t, const float *logit_row,
-                             int64_t split_stride) {
+                             int64_t split_stride, float2 *stage) {
     const int lane = threadIdx.x & 63;
     float part[NS][M], bias[M];
     int slot_of[M];
@@ -93,109 +99,80 @@ __device__ void select_token(const RouterLaunch &L, int t, const float *logit_ro
         for (int m = 32; m >= 1; m >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, m, 64));
         float z = 0.f;
 #pragma unroll
-        for (int i = 0; i < M; ++i) z += lane + 64 * i < L.E ? expf(sc[i] - lmax) : 0.f;
+        for (int i = 0; i < M; ++i) z += lane + 64 * i < L.E ? __expf(sc[i] - lmax) : 0.f;
         for (int m = 32; m >= 1; m >>= 1) z += __shfl_xor(z, m, 64);
         denom = z;
     }
     // Keys: hi = ordered selection value, lo = ~expert (ties -> lower id);
-    // hi = 0 marks an invalid or already-taken candidate.
-    uint32_t khi[M];
+    // (0, 0) marks an invalid candidate.
+    uint32_t kh[M], kl[M];
 #pragma unroll
     for (int i = 0; i < M; ++i) {
-        const bool valid = lane + 64 * i < L.E;
+        const int e = lane + 64 * i;
+        const bool valid = e < L.E;
         const float s = score_of<SF>(valid ? sc[i] : 0.f, lmax, denom);
-        sc[i] = valid ? s : 0.f;
-        khi[i] = valid ? ordered_bits(s + bias[i]) : 0u;
+        stage[e] = make_float2(s, __int_as_float(slot_of[i]));
+        kh[i] = valid ? ordered_bits(s + bias[i]) : 0u;
+        kl[i] = valid ? ~static_cast<uint32_t>(e) : 0u;
     }
-    int my_e = -1, my_slot = -1;
-    float my_s = 0.f, sum = 0.f;
+    // Sort the lane's keys descending (insertion network, M <= 8).
+#pragma unroll
+    for (int i = 1; i < M; ++i) {
+#pragma unroll
+        for (int j = i; j > 0; --j) {
+            const bool sw = key_gt(kh[j], kl[j], kh[j - 1], kl[j - 1]);
+            const uint32_t th = kh[j], tl = kl[j];
+            kh[j] = sw ? kh[j - 1] : th;
+            kl[j] = sw ? kl[j - 1] : tl;
+            kh[j - 1] = sw ? th : kh[j - 1];
+            kl[j - 1] = sw ? tl : kl[j - 1];
+        }
+    }
+    int my_e = -1;
     for (int j = 0; j < L.top_k; ++j) {
         int best_e;
         if (L.tid2eid) {
             best_e = __builtin_amdgcn_readlane(hash_e, j);
             if (best_e >= L.E || best_e < 0) best_e = -1;
         } else {
-            uint32_t bh = 0, bl = 0;
-#pragma unroll
-            for (int i = 0; i < M; ++i) {
-                const uint32_t h = khi[i], l = ~static_cast<uint32_t>(lane + 64 * i);
-                const bool take = h > bh || (h == bh && h != 0 && l > bl);
-                bh = take ? h : bh;
-                bl = take ? l : bl;
-            }
+            uint32_t bh = kh[0], bl = kl[0];
             wave_max_key(bh, bl);
-            best_e = bh == 0 ? -1 : static_cast<int>(~bl);
+            best_e = bh == 0 && bl == 0 ? -1 : static_cast<int>(~bl);
+            if (kh[0] == bh && kl[0] == bl && best_e >= 0) {   // the winner pops its head
 #pragma unroll
-            for (int i = 0; i < M; ++i)
-                if (lane + 64 * i == best_e) khi[i] = 0u;
-        }
-        float s = 0.f;
-        int slot = -1;
-        if (best_e >= 0) {
-            float mine = sc[0];
-            int mslot = slot_of[0];
-#pragma unroll
-            for (int i = 1; i < M; ++i) {
-                if (i == (best_e >> 6)) {
-                    mine = sc[i];
-                    mslot = slot_of[i];
+                for (int i = 0; i + 1 < M; ++i) {
+                    kh[i] = kh[i + 1];
+                    kl[i] = kl[i + 1];
                 }
+                kh[M - 1] = 0u;
+                kl[M - 1] = 0u;
             }
-            s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), best_e & 63));
-            slot = __builtin_amdgcn_readlane(mslot, best_e & 63);
         }
-        sum += s;   // selection order, as the scores are gathered
-        if (lane == j) {
-            my_e = best_e;
-            my_s = s;
-            my_slot = slot;
-        }
+        if (lane == j) my_e = best_e;
     }
+    __builtin_amdgcn_wave_barrier();
+    float my_s = 0.f;
+    int my_slot = -1;
+    if (lane < L.top_k && my_e >= 0) {
+        const float2 v = stage[my_e];
+        my_s = v.x;
+        my_slot = __float_as_int(v.y);
+    }
+    float sum = 0.f;   // selection order, as the scores are gathered
+    for (int j = 0; j < L.top_k; ++j)
+        sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_s), j));
     if (lane < L.top_k) {
         float w = my_s;
         if (L.norm_topk) w = w / (sum + 1e-20f);
         const int64_t o = static_cast<int64_t>(t) * L.top_k + lane;
         L.idx[o] = my_e;
         L.weights[o] = w * L.routed_scale;
-        if (L.route_slot) L.route_slot[o] = my_slot >= L.n_slots ? -1 : my_slot;
+        if (L.route_slot) L.route_slot[o] = my_e < 0 || my_slot >= L.n_slots ? -1 : my_slot;
     }
 }
 
 // --------------------------------------------------------------------------
-// Activation prep (prepared-vector form of qgemv.hpp) for n_vec rows of v.
-// --------------------------------------------------------------------------
-template <bool BF16>
-__device__ __forceinline__ void prep_units(const uint16_t *v, int n_vec, int K, int bits,
-                                           const PrepVec &out, int first, int count) {
-    const int vpw = 32 / bits;
-    const int per_vec = K / vpw;
-    const int ppw = pairs_per_word<BF16>(bits);
-    for (int u = first; u < first + count && u < n_vec * per_vec; u += 1) {
-        const int vec = u / per_vec, unit = u % per_vec;
-        prep_unit_at<BF16>(bits, v + static_cast<int64_t>(vec) * K + unit * vpw,
-                           out.pairs + vec * out.pairs_stride + unit * ppw,
-                           out.parts + vec * out.parts_stride + unit);
-    }
-}
-
-template <bool BF16>
-__global__ __launch_bounds__(256) void prep_vectors_kernel(const uint16_t *v, int n_vec, int K,
-                                                           int bits, PrepVec out) {
-    const int u = blockIdx.x * blockDim.x + threadIdx.x;
-    prep_units<BF16>(v, n_vec, K, bits, out, u, 1);
-}
-
-hipError_t launch_prep_vectors(const uint16_t *v, int n_vec, int K, int bits, bool bf16, PrepVec out,
-                               hipStream_t st) {
-    const int units = n_vec * (K * bits / 32);
-    dim3 grid((units + 255) / 256);
-    if (bf16) hipLaunchKernelGGL(prep_vectors_kernel<true>, grid, dim3(256), 0, st, v, n_vec, K, bits, out);
-    else hipLaunchKernelGGL(prep_vectors_kernel<false>, grid, dim3(256), 0, st, v, n_vec, K, bits, out);
-    return hipGetLastError();
-}
-
-// --------------------------------------------------------------------------
-// GEMV logits (decode) + activation prep + fused last-workgroup selection.
+// GEMV logits (decode).
 // --------------------------------------------------------------------------
 template <int GDT, bool XBF16>
 __device__ __forceinline__ void gate_chunk(const void *w, int64_t off, uint32_t (&wp)[4], float (&wf)[8]) {
@@ -219,42 +196,6 @@ __device__ __forceinline__ void gate_chunk(const void *w, int64_t off, uint32_t 
 
 constexpr int kRouterWaves = 4;   // experts per workgroup (one per wave)
 
-// Prep units of the prepared activation vectors, one per thread over the
-// whole grid (the launcher checks that the grid covers them). Split in two so
-// that the loads go out with the gate loads: router_prep_load reads the
-// thread's unit (a clamped, in-bounds unit when it has none), and
-// router_prep_store writes it.
-__device__ __forceinline__ int router_prep_unit(const RouterLaunch &L, int &vec, int &unit) {
-    const int per_vec = L.d / (32 / L.prep_bits);
-    const int u = blockIdx.x * blockDim.x + threadIdx.x;
-    const int uc = min(u, L.tokens * per_vec - 1);
-    vec = uc / per_vec;
-    unit = uc % per_vec;
-    return u;
-}
-
-__device__ __forceinline__ PrepRaw router_prep_load(const RouterLaunch &L) {
-    int vec, unit;
-    router_prep_unit(L, vec, unit);
-    return prep_unit_load(L.prep_bits, L.x + static_cast<int64_t>(vec) * L.d + unit * (32 / L.prep_bits));
-}
-
-template <bool XBF16>
-__device__ __forceinline__ void router_prep_store(const RouterLaunch &L, const PrepRaw &raw) {
-    int vec, unit;
-    const int u = router_prep_unit(L, vec, unit);
-    if (u < L.tokens * (L.d / (32 / L.prep_bits)))
-        prep_unit_store<XBF16>(L.prep_bits, raw,
-                               L.xprep.pairs + vec * L.xprep.pairs_stride +
-                                   unit * pairs_per_word<XBF16>(L.prep_bits),
-                               L.xprep.parts + vec * L.xprep.parts_stride + unit);
-}
-
-template <bool XBF16>
-__device__ __forceinline__ void router_prep(const RouterLaunch &L) {
-    if (L.xprep.pairs) router_prep_store<XBF16>(L, router_prep_load(L));
-}
-
 // Fast path: gate and x share a 16-bit type (v_dot2), d = 512 * NCH, and TB
 // tokens per pass. Every lane issues all NCH gate chunks of its expert and
 // the TB tokens' x chunks before the first dot; tokens beyond L.tokens in
@@ -272,9 +213,6 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_gemv_fast_kernel(Rou
         for (int i = 0; i < NCH; ++i)
             w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gw) + lane + 64 * i);
     }
-    const bool prep = L.xprep.pairs != nullptr;
-    PrepRaw raw{};
-    if (prep) raw = router_prep_load(L);
     if (have) {
         for (int t0 = 0; t0 < L.tokens; t0 += TB) {
             uint4 xv[TB][NCH];
@@ -303,7 +241,6 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_gemv_fast_kernel(Rou
                 L.logits[static_cast<int64_t>(t0 + q) * L.E + e] = acc[0];
         }
     }
-    if (prep) router_prep_store<XBF16>(L, raw);
 }
 
 // General path: any gate dtype (fp32, or a 16-bit type other than x's) and
@@ -314,7 +251,6 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_gemv_kernel(RouterLa
     constexpr bool kDot = GDT != 0 && ((GDT == 2) == XBF16);
     const int lane = threadIdx.x & 63;
     const int e = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
-    router_prep<XBF16>(L);
     if (e < L.E) {
         for (int t0 = 0; t0 < L.tokens; t0 += TB) {
             float acc[TB];
@@ -419,11 +355,12 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(RouterLaunch L) {
 
 template <int NS, int SF, int M>
 __global__ __launch_bounds__(256) void router_select_kernel(RouterLaunch L) {
+    __shared__ float2 stage[4][64 * M];
     const int wave = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wave;
     if (t >= L.tokens) return;
     select_token<NS, SF, M>(L, t, L.logits + static_cast<int64_t>(t) * L.E,
-                            static_cast<int64_t>(L.tokens) * L.E);
+                            static_cast<int64_t>(L.tokens) * L.E, stage[wave]);
 }
 
 template <int NS, int SF>
@@ -453,10 +390,6 @@ hipError_t launch_router(const RouterLaunch &L, hipStream_t st) {
     const bool mfma_ok = !L.logits_in && L.tokens > kRouterTokensPerPass && L.gate_dtype != 0 &&
                          ((L.gate_dtype == 2) == L.x_bf16) && L.d % (64 * kRouterSplits) == 0;
     if (mfma_ok || L.logits_in) {
-        if (L.xprep.pairs) {
-            hipError_t e = launch_prep_vectors(L.x, L.tokens, L.d, L.prep_bits, L.x_bf16, L.xprep, st);
-            if (e != hipSuccess) return e;
-        }
         if (L.logits_in) return launch_select<1>(L, st);
         dim3 grid((L.tokens + 63) / 64, (L.E + 63) / 64, kRouterSplits);
         if (L.x_bf16) hipLaunchKernelGGL(router_mfma_kernel<true>, grid, dim3(256), 0, st, L);
@@ -466,16 +399,7 @@ hipError_t launch_router(const RouterLaunch &L, hipStream_t st) {
         return launch_select<kRouterSplits>(L, st);
     }
     if (L.d % 8 != 0) return hipErrorInvalidValue;
-    // every thread of the grid prepares at most one unit
     const int blocks = (L.E + kRouterWaves - 1) / kRouterWaves;
-    if (L.xprep.pairs && static_cast<int64_t>(blocks) * 64 * kRouterWaves <
-                             static_cast<int64_t>(L.tokens) * (L.d * L.prep_bits / 32)) {
-        hipError_t e = launch_prep_vectors(L.x, L.tokens, L.d, L.prep_bits, L.x_bf16, L.xprep, st);
-        if (e != hipSuccess) return e;
-        RouterLaunch L2 = L;
-        L2.xprep.pairs = nullptr;
-        return launch_router(L2, st);
-    }
     dim3 grid(blocks), block(64 * kRouterWaves);
     const bool dot_ok = L.gate_dtype != 0 && ((L.gate_dtype == 2) == L.x_bf16);
     const int nch = L.d % 512 == 0 ? L.d / 512 : 0;

@@ -64,7 +64,7 @@ def assert_close_terms(got, want, terms, what, rtol=RTOL, atol=ATOL):
     """Combined outputs are sums of terms each rounded to 16 bits; one
     last-place flip of a term of magnitude m moves the result by up to
     2^-7 m (bf16 spacing, a superset of fp16's). The bound adds that to the
-    north-star tolerance, with terms = sum of |rounded term| per element."""
+    stated tolerance (1e-2 rel, 2e-3 abs), with terms = sum of |rounded term| per element."""
     got = np.asarray(got, dtype=np.float64)
     want = np.asarray(want, dtype=np.float64)
     tol = atol + rtol * np.abs(want) + 2.0 ** -7 * np.asarray(terms, dtype=np.float64)

@@ -1,7 +1,7 @@
 """GPU parity: the HIP kernels (through the liblocali_amd.so C ABI) against the
 CPU oracle on identical seeded inputs.
 
-Bars (north star): router indices bit-exact as sets wherever the oracle's
+Bars: router indices bit-exact as sets wherever the oracle's
 selection margin exceeds the fp32 accumulation-order noise (1e-4); weights
 within 1e-5 relative; slot assignment exact; expert outputs within 1e-2
 relative / 2e-3 absolute of the oracle.
@@ -143,7 +143,7 @@ def test_expert_decode_matches_oracle(case, T):
     # fp16 keeps 3 more mantissa bits than bf16, so fp32-vs-fp64 accumulation
     # order flips its last place more often
     assert exact_fraction(got, want) > (0.8 if dtype == torch.bfloat16 else 0.7)
-    # Pure expert outputs (one route, weight 1, no shared): the north-star bar.
+    # Pure expert outputs (one route, weight 1, no shared): 1e-2 rel / 2e-3 abs.
     one = ops.expert_decode(_dev(arena), None, x.to(DEV), slots[:, :1].contiguous().to(DEV),
                             torch.ones(T, 1, device=DEV))
     want1 = _oracle_layer(x, slots[:, :1].numpy(), np.ones((T, 1)), arena, slot_of, dtype)
