@@ -1,0 +1,518 @@
+"""The HBM expert arena: slot pools per tier, a slot planner, and bounded
+asynchronous fills from the checkpoint files.
+
+Mirrors the reference's ArenaStore / ArenaMoE (arena.py:64-681) for a GPU
+with its own memory: the arena is a set of slot-major device tensors
+[n_slots, *shape] per (tier, projection, array) -- exactly the layout the
+expert kernels index by slot -- and a miss is a preadv of the expert's nine
+records into pinned host staging followed by an asynchronous host -> HBM copy
+on a dedicated fill stream (locali_moe_arena_fill). Slot 0 of every tier is
+reserved and all-zero: a masked-out route reads it and contributes exactly 0.
+
+Slots are claimed synchronously by the planner (so a later submit cannot
+steal a slot an earlier one is still filling); only the reads and copies are
+deferred to a thread pool, and a fill's future completes once its copy has
+landed in HBM. `pinned` keeps the slots of the layer being computed out of the
+victim search while a cross-layer prefetch claims slots; `inflight` maps a
+resident key to the fills still writing it.
+
+The planner is the compiled one (locali_amd.native, the reference C ABI) in
+V4ArenaStore; this base class also carries the reference's Python SLRU
+(arena.py:212-354) for native_scheduler=False.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import threading
+import time
+from collections import OrderedDict
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+import numpy as np
+import torch
+
+PROJS = ("gate_proj", "up_proj", "down_proj")
+ARRS = ("weight", "scales", "biases")
+TORCH_DT = {"U32": torch.int32, "I32": torch.int32, "F16": torch.float16, "BF16": torch.bfloat16,
+            "F32": torch.float32, "U8": torch.uint8}
+POLICIES = ("lru", "slru-cold", "slru-all", "lfu-decay")
+
+
+class ReadPlan(dict):
+    """Per-tier futures plus the experts whose slots are not filled yet
+    (reference arena.py:55-61)."""
+
+    def __init__(self, *args, pending_experts=(), **kwargs):
+        super().__init__(*args, **kwargs)
+        self.pending_experts = frozenset(pending_experts)
+
+
+class _Staging:
+    """A small pool of pinned host buffers, one expert each."""
+
+    def __init__(self, nbytes: int, count: int, pinned: bool):
+        self.free = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=pinned) for _ in range(count)]
+        self.cv = threading.Condition()
+
+    def take(self) -> torch.Tensor:
+        with self.cv:
+            while not self.free:
+                self.cv.wait()
+            return self.free.pop()
+
+    def give(self, buf: torch.Tensor) -> None:
+        with self.cv:
+            self.free.append(buf)
+            self.cv.notify()
+
+
+class ArenaStore:
+    def __init__(self, index_path, ceiling_gb=8.0, hot_share=0.33, threads=8, nocache=True,
+                 cache_policy="lru", device=None):
+        idx = json.loads(Path(index_path).read_text())
+        if cache_policy not in POLICIES:
+            raise ValueError(f"cache_policy must be one of {POLICIES}")
+        self.meta = idx["experts"]
+        self.layers, self.E = int(idx["layers"]), int(idx["num_experts"])
+        self.top_k = int(idx["top_k"])
+        self.cache_policy = cache_policy
+        self.ceiling = int(ceiling_gb * 1e9)
+        self.tier_overlap = bool(idx.get("pack"))
+        self.device = torch.device(device) if device is not None else torch.device("cuda")
+        self._nocache = nocache
+        self.fds: dict = {}
+        self._fd_lock = threading.Lock()
+        self.pool = ThreadPoolExecutor(max_workers=threads)
+        self.hits = self.misses = self.evictions = self.bytes_read = 0
+        self.t_stall = 0.0
+        self.pinned: dict = {}
+        self.inflight: dict = {}
+        self.pf_keys: set = set()
+        self.prefetched = self.prefetch_used = self.prefetch_wasted = 0
+
+        sample = {}
+        for m in self.meta.values():
+            sample.setdefault(m["tier"], m)
+            if len(sample) == 2:
+                break
+        self.tiers = sorted(sample)
+        share = ({self.tiers[0]: 1.0} if len(self.tiers) == 1
+                 else {"hot": hot_share, "cold": 1.0 - hot_share})
+        self.arena, self.item, self.slots = {}, {}, {}
+        self.lru, self.protected, self.protected_cap, self.free = {}, {}, {}, {}
+        self.layout = {}   # (tier, proj, array) -> (nbytes per slot, shape, dtype name)
+        for t in self.tiers:
+            m = sample[t]
+            per = sum(m[p][k][3] for p in PROJS for k in ARRS)
+            self.item[t] = per
+            n = int(self.ceiling * share.get(t, 0.5) / per)
+            if n < 2:
+                raise ValueError(f"{ceiling_gb:.3f} GB gives tier {t} no usable expert slot after "
+                                 "its reserved zero slot; raise ceiling_gb or adjust hot_share")
+            self.slots[t] = n
+            self.lru[t] = OrderedDict()
+            self.protected[t] = OrderedDict()
+            slru = cache_policy == "slru-all" or (cache_policy == "slru-cold" and t == "cold")
+            self.protected_cap[t] = (n - 1) // 2 if slru else 0
+            self.free[t] = list(range(1, n))
+            for p in PROJS:
+                for k in ARRS:
+                    _, _, _, nb, shape, dt = m[p][k]
+                    if dt not in TORCH_DT:
+                        raise ValueError(f"tier {t} {p}.{k}: unsupported dtype {dt}")
+                    self.layout[(t, p, k)] = (nb, tuple(shape), dt)
+                    # zero-filled: slot 0 stays the all-zero expert
+                    self.arena[(t, p, k)] = torch.zeros((n, *shape), dtype=TORCH_DT[dt],
+                                                        device=self.device)
+        self.resident = sum(self.slots[t] * self.item[t] for t in self.tiers)
+        if self.resident > self.ceiling:
+            raise AssertionError(f"arena allocated {self.resident} bytes against {self.ceiling}")
+        gpu = self.device.type == "cuda"
+        self.fill_stream = torch.cuda.Stream(device=self.device) if gpu else None
+        self.staging = _Staging(max(self.item.values()), max(2, threads), pinned=gpu)
+
+    # ---- kernel views ----------------------------------------------------
+    def group_size(self, t) -> int:
+        """Quantisation group of tier t (the index's, else the reference
+        arena's fixed 64, arena.py:51)."""
+        return 64
+
+    def expert_arena(self, t):
+        """The tier's slot arrays as the expert kernels take them; bits per
+        projection follow from the packed and metadata widths."""
+        from .ops import ExpertArenaT, ProjArena
+        cache = self.__dict__.setdefault("_expert_arena", {})
+        if t not in cache:
+            g = self.group_size(t)
+            projs = []
+            for p in PROJS:
+                w = self.arena[(t, p, "weight")]
+                sc = self.arena[(t, p, "scales")]
+                cols = sc.shape[-1] * g
+                if (w.shape[-1] * 32) % cols:
+                    raise ValueError(f"tier {t} {p}: packed width {w.shape[-1]} does not fit "
+                                     f"{cols} inputs")
+                projs.append(ProjArena(w, sc, self.arena[(t, p, "biases")],
+                                       w.shape[-1] * 32 // cols, g))
+            cache[t] = ExpertArenaT(*projs)
+        return cache[t]
+
+    def use_f16(self, t) -> bool:
+        """Tier t keeps fp16 scales/biases: bf16 activations are cast to fp16
+        before its experts (reference dsv4_arena.py:30-40, 172-173)."""
+        return all(self.layout[(t, p, k)][2] == "F16" for p in PROJS for k in ("scales", "biases"))
+
+    def slot_identity(self, t) -> torch.Tensor:
+        cache = self.__dict__.setdefault("_slot_ident", {})
+        if t not in cache:
+            cache[t] = torch.arange(self.slots[t], dtype=torch.int32, device=self.device)
+        return cache[t]
+
+    # ---- files ---------------------------------------------------------
+    def _fd(self, root, shard):
+        key = (root, shard)
+        with self._fd_lock:
+            if key not in self.fds:
+                self.fds[key] = os.open(os.path.join(root, shard), os.O_RDONLY)
+            return self.fds[key]
+
+    def tier(self, layer, expert):
+        return self.meta[f"L{layer}.E{expert}"]["tier"]
+
+    def _records(self, layer, expert, t):
+        m = self.meta[f"L{layer}.E{expert}"]
+        recs = [m[p][k] for p in PROJS for k in ARRS]
+        for (p, k), rec in zip(((p, k) for p in PROJS for k in ARRS), recs):
+            if rec[3] != self.layout[(t, p, k)][0]:
+                raise ValueError(f"L{layer}.E{expert} {p}.{k}: {rec[3]} bytes, slot holds "
+                                 f"{self.layout[(t, p, k)][0]}")
+        return recs
+
+    @staticmethod
+    def _contiguous(recs):
+        root, shard, end = recs[0][0], recs[0][1], recs[0][2]
+        for r in recs:
+            if (r[0], r[1], r[2]) != (root, shard, end):
+                return False
+            end += r[3]
+        return True
+
+    def _read(self, recs, host: np.ndarray) -> None:
+        """preadv the nine records into consecutive ranges of `host`: one call
+        for an expert-major packed expert, one per record otherwise."""
+        views, off = [], 0
+        for r in recs:
+            views.append(memoryview(host[off:off + r[3]]))
+            off += r[3]
+        groups = [list(range(len(recs)))] if self._contiguous(recs) else [[i] for i in range(len(recs))]
+        for g in groups:
+            r0 = recs[g[0]]
+            fd = self._fd(r0[0], r0[1])
+            want = sum(recs[i][3] for i in g)
+            got = os.preadv(fd, [views[i] for i in g], r0[2])
+            if got != want:
+                raise IOError(f"short read {got}/{want} at {r0[1]}+{r0[2]}")
+            if self._nocache and hasattr(os, "posix_fadvise"):
+                os.posix_fadvise(fd, r0[2], want, os.POSIX_FADV_DONTNEED)
+
+    def _fill(self, t, slot, recs) -> None:
+        """Worker: file -> pinned staging -> HBM slot; returns once the bytes
+        are in device memory."""
+        buf = self.staging.take()
+        try:
+            host = buf.numpy()
+            self._read(recs, host)
+            off = 0
+            if self.fill_stream is not None:
+                from .ops import arena_fill
+                with torch.cuda.device(self.device):
+                    for (p, k), r in zip(((p, k) for p in PROJS for k in ARRS), recs):
+                        dst = self.arena[(t, p, k)][slot].view(torch.uint8).reshape(-1)
+                        arena_fill(dst, buf[off:off + r[3]], stream=self.fill_stream)
+                        off += r[3]
+                    ev = torch.cuda.Event()
+                    ev.record(self.fill_stream)
+                ev.synchronize()
+            else:
+                for (p, k), r in zip(((p, k) for p in PROJS for k in ARRS), recs):
+                    dst = self.arena[(t, p, k)][slot].view(torch.uint8).reshape(-1)
+                    dst.copy_(buf[off:off + r[3]])
+                    off += r[3]
+        finally:
+            self.staging.give(buf)
+
+    # ---- Python planner (reference arena.py:212-289) ---------------------
+    def _claim(self, t, key, also_pinned=()):
+        """A slot for `key`: a free slot while probation has room, else the
+        least recently used unpinned probation entry, else the least recently
+        used unpinned protected entry; None when every candidate is pinned.
+        Pinned: the previous demand call's slots and `also_pinned` (the slots
+        the current call resolved already)."""
+        pin = set(self.pinned.get(t, ())) | set(also_pinned)
+        probation_cap = self.slots[t] - 1 - self.protected_cap[t]
+        probation_full = len(self.lru[t]) >= probation_cap
+        victim = segment = None
+        if probation_full or not self.free[t]:
+            victim = next((k for k, v in self.lru[t].items() if v not in pin), None)
+            if victim is not None:
+                segment = self.lru[t]
+        if victim is None and not probation_full and self.free[t]:
+            s = self.free[t].pop()
+        else:
+            if victim is None:
+                victim = next((k for k, v in self.protected[t].items() if v not in pin), None)
+                if victim is not None:
+                    segment = self.protected[t]
+            if victim is None:
+                return None
+            s = segment.pop(victim)
+            self._evicted(victim)
+        self.lru[t][key] = s
+        return s
+
+    def _evicted(self, victim):
+        self.inflight.pop(victim, None)
+        if victim in self.pf_keys:
+            self.pf_keys.discard(victim)
+            self.prefetch_wasted += 1
+        self.evictions += 1
+
+    def _slot(self, t, key):
+        return self.protected[t][key] if key in self.protected[t] else self.lru[t][key]
+
+    def _resident(self, t, key):
+        return key in self.lru[t] or key in self.protected[t]
+
+    def _protected_size(self, t):
+        return len(self.protected[t])
+
+    def _touch(self, t, key):
+        """Refresh a hit: move to the fresh end, or promote a probation hit
+        (demoting the oldest protected entry when over capacity)."""
+        if key in self.protected[t]:
+            self.protected[t].move_to_end(key)
+            return
+        if self.protected_cap[t] == 0:
+            self.lru[t].move_to_end(key)
+            return
+        slot = self.lru[t].pop(key)
+        self.protected[t][key] = slot
+        if len(self.protected[t]) > self.protected_cap[t]:
+            old, old_slot = self.protected[t].popitem(last=False)
+            self.lru[t][old] = old_slot
+
+    def _hit(self, key, t, prefetch, waits):
+        if not prefetch:
+            self.hits += 1
+            if key in self.pf_keys:
+                self.pf_keys.discard(key)
+                self.prefetch_used += 1
+        futs = self.inflight.get(key)
+        if futs:
+            if all(f.done() for f in futs):
+                del self.inflight[key]
+            elif not prefetch:
+                waits[t].extend(futs)
+
+    def _place_keys(self, layer, want, prefetch):
+        """Resolve a layer's unique experts to slots (hits first, then misses
+        in order), returning (placed, issued fills, fills to wait for)."""
+        out, miss = {}, []
+        waits = {t: [] for t in self.tiers}
+        for e in want:
+            key, t = (layer, e), self.tier(layer, e)
+            if self._resident(t, key):
+                out[e] = (t, self._slot(t, key))
+                if not prefetch:
+                    self._touch(t, key)
+                self._hit(key, t, prefetch, waits)
+            else:
+                if not prefetch:
+                    self.misses += 1
+                miss.append((e, t))
+        if not prefetch:
+            need: dict = {}
+            for _, t in miss:
+                need[t] = need.get(t, 0) + 1
+            for t, n in need.items():
+                if n > self.slots[t] - 1:
+                    raise ValueError(f"layer {layer} needs {n} {t} experts but the arena has "
+                                     f"{self.slots[t] - 1}; raise ceiling_gb or hot_share")
+        issued = []
+        taken = {t: {s for tt, s in out.values() if tt == t} for t in self.tiers}
+        for e, t in miss:
+            s = self._claim(t, (layer, e), taken[t])
+            if s is None:
+                continue
+            out[e] = (t, s)
+            taken[t].add(s)
+            issued.append((e, t, s))
+        if not prefetch:
+            pin = {t: set() for t in self.tiers}
+            for t, s in out.values():
+                pin[t].add(s)
+            self.pinned = pin
+        return out, issued, waits
+
+    # ---- public surface (reference arena.py:291-457) ---------------------
+    def submit(self, layer, experts, prefetch=False):
+        """Claim slots now; queue the fills; return ({expert: (tier, slot)},
+        ReadPlan). prefetch=True is best effort: it never evicts a pinned slot,
+        never raises on a full arena and leaves hit/miss accounting alone."""
+        want = list(dict.fromkeys(int(e) for e in experts))
+        out, issued, waits = self._place_keys(layer, want, prefetch)
+        # A later miss of the same call may have taken an earlier one's slot
+        # (only when the tier is nearly all pinned): that earlier claim is
+        # stale and must not be filled or used.
+        owner = {}
+        for e, t, s in issued:
+            owner[(t, s)] = e
+        stale = [e for e, t, s in issued if owner[(t, s)] != e]
+        if stale:
+            if not prefetch:
+                raise RuntimeError(f"layer {layer}: the arena cannot hold this call's experts "
+                                   "next to the previous call's pinned slots; raise ceiling_gb")
+            issued = [(e, t, s) for e, t, s in issued if owner[(t, s)] == e]
+            for e in stale:
+                out.pop(e, None)
+        plan = ReadPlan()
+        jobs = {t: [] for t in self.tiers}
+        for e, t, s in issued:
+            jobs[t].append(((layer, e), t, s, self._records(layer, e, t)))
+            self.bytes_read += self.item[t]
+        for t in self.tiers:   # a whole tier before the next
+            futs = []
+            for key, tt, s, recs in jobs[t]:
+                f = self.pool.submit(self._fill, tt, s, recs)
+                self.inflight.setdefault(key, []).append(f)
+                futs.append(f)
+            plan[t] = futs + waits[t]
+        plan.pending_experts = frozenset(
+            e for e in want if any(not f.done() for f in self.inflight.get((layer, e), ())))
+        if prefetch:
+            self.prefetched += len(issued)
+            self.pf_keys.update((layer, e) for e, _, _ in issued)
+        return out, plan
+
+    def slots_for(self, layer, experts):
+        """{expert: (tier, slot)}, every one resident in HBM on return."""
+        placed, plan = self.submit(layer, experts)
+        self.wait([f for futs in plan.values() for f in futs])
+        return placed
+
+    def wait(self, futs):
+        if not futs:
+            return
+        t0 = time.perf_counter()
+        for f in futs:
+            f.result()
+        self.t_stall += time.perf_counter() - t0
+
+    def stats(self):
+        n = self.hits + self.misses
+        return {"hits": self.hits, "misses": self.misses, "hit_rate": self.hits / n if n else 0.0,
+                "evictions": self.evictions, "bytes_read": self.bytes_read,
+                "resident": self.resident, "peak": self.resident,
+                "slots": {t: self.slots[t] for t in self.tiers},
+                "t_stall": self.t_stall, "t_convert": 0.0, "t_eval": 0.0,
+                "prefetched": self.prefetched, "prefetch_used": self.prefetch_used,
+                "prefetch_wasted": self.prefetch_wasted, "cache_policy": self.cache_policy,
+                "protected": {t: self._protected_size(t) for t in self.tiers}}
+
+    def close(self):
+        """Drain the fills, close the files and release the arena's memory."""
+        self.pool.shutdown(wait=True)
+        for fd in self.fds.values():
+            os.close(fd)
+        self.fds.clear()
+        self.arena.clear()
+        self.__dict__.pop("_expert_arena", None)
+        self.staging.free.clear()
+
+
+class ArenaMoE:
+    """Locali's own MoE module over the arena (reference arena.py:460-547):
+    sigmoid router with a selection-only bias, top-k renormalised, weights in
+    x.dtype. Subclasses replace route() (the V4 gate) and keep __call__."""
+
+    def __init__(self, store: ArenaStore, layer: int, gate, bias, top_k: int):
+        self.store, self.layer, self.gate, self.bias, self.top_k = store, layer, gate, bias, top_k
+        self.scores_follow_output = False
+        self.nxt = None          # next layer's module, for cross-layer prefetch
+        self.nxt2 = None         # depth-2 lookahead
+        self.prefetch_k = None   # prefetch only the highest-gate candidates
+        self.prefetch_k2 = None
+        self.overlap_hits = False
+        self.swiglu_limit = 0.0
+        self.fp32_swiglu = False
+        self._spec = None
+
+    def route(self, x, input_ids=None):
+        """(indices int32 [T, k], scores fp32 [T, k]) from the sigmoid router."""
+        from . import ops
+        if self._spec is None:
+            w = self.gate.weight if hasattr(self.gate, "weight") else self.gate
+            bias = None if self.bias is None else self.bias.to(device=w.device, dtype=torch.float32)
+            self._spec = ops.RouterSpec(w, self.top_k, score_func="sigmoid", norm_topk=True,
+                                        routed_scale=1.0, score_bias=bias)
+        idx, w, _ = ops.router(self._spec, x.reshape(-1, x.shape[-1]), self._workspace())
+        return idx, w
+
+    def _workspace(self):
+        from . import ops
+        ws = getattr(self.store, "workspace", None)
+        if ws is None:
+            ws = self.store.workspace = ops.Workspace(self.store.device)
+        return ws
+
+    def __call__(self, x, input_ids=None):
+        shape = x.shape
+        flat = x.reshape(-1, shape[-1])
+        inds, gates = self.route(x, input_ids)
+        ii = inds.reshape(-1, self.top_k).tolist()          # host sync, as the reference
+        experts = [e for row in ii for e in row]
+        if self.store.tier_overlap:
+            placed, reads = self.store.submit(self.layer, experts)
+        else:
+            placed, reads = self.store.slots_for(self.layer, experts), None
+        for blk, k in ((self.nxt, self.prefetch_k), (self.nxt2, self.prefetch_k2)):
+            if blk is None:
+                continue
+            pi, pg = blk.route(x, input_ids)
+            pi = pi.reshape(-1, self.top_k)
+            if k and k < self.top_k:
+                order = torch.argsort(-pg.reshape(-1, self.top_k).float(), dim=-1, stable=True)
+                pi = torch.gather(pi, 1, order[:, :k])
+            self.store.submit(blk.layer, [e for row in pi.tolist() for e in row], prefetch=True)
+        out = self._apply(flat, ii, placed, gates.reshape(-1, self.top_k), x.dtype, reads)
+        return out.reshape(shape).to(x.dtype)
+
+    def _apply(self, flat, ii, placed, gates, dtype, reads=None):
+        from . import ops
+        T = len(ii)
+        tiers = {placed[e][0] for row in ii for e in row}
+        if len(tiers) != 1:
+            raise NotImplementedError("routes spanning two tiers in one call are not supported")
+        t = tiers.pop()
+        if reads is not None:
+            self.store.wait(reads[t])
+        slots = torch.tensor([[placed[e][1] for e in row] for row in ii], dtype=torch.int32,
+                             device=flat.device)
+        arena = self.store.expert_arena(t)
+        x_in = flat.contiguous()
+        if self.store.use_f16(t) and x_in.dtype == torch.bfloat16:
+            x_in = x_in.to(torch.float16)
+        w = gates.to(torch.float32).contiguous()
+        ws = self._workspace()
+        if T <= 2:
+            y = ops.expert_decode(arena, None, x_in, slots, w, swiglu_limit=self.swiglu_limit,
+                                  fp32_swiglu=self.fp32_swiglu, ws=ws)
+        else:
+            n = arena.n_slots
+            ident = self.store.slot_identity(t)
+            y = ops.expert_grouped(arena, None, x_in, slots, ident, w, ws, n_experts=n,
+                                   swiglu_limit=self.swiglu_limit, fp32_swiglu=self.fp32_swiglu)
+        return y.to(dtype)

@@ -1,0 +1,198 @@
+"""DeepSeek-V4 routed experts over the HBM expert arena: the drop-in for the
+reference's V4ArenaStore / V4ArenaMoE (dsv4_arena.py:17-235).
+
+The engine seam is unchanged (reference dsv4_engine.py:188-210, 253-261):
+
+    store = V4ArenaStore(index_path, ceiling_gb=..., hot_share=..., threads=...,
+                         nocache=..., cache_policy=..., native_scheduler=True)
+    moe = V4ArenaMoE(store, layer, gate, top_k, swiglu_limit,
+                     fused_decode=..., overlap_hits=...)
+    routed = moe(x, input_ids)            # x's shape and dtype
+    out = routed + shared_expert(x)       # the caller adds the shared expert
+
+`gate(x, input_ids) -> (indices [..., k], scores [..., k])` is the gate
+protocol; V4Gate implements it on the router kernel from the gate's own
+tensors (weight, e_score_correction_bias, tid2eid). Expert arithmetic is the
+HIP expert kernels (decode GEMV path up to two tokens, slot-grouped path
+beyond), with the reference's contract: fp32 accumulation, projections
+rounded to the activation dtype, up clipped to +-limit and gate capped at
+limit, SiLU(gate) * up op by op in the activation dtype (fp32 with one final
+rounding when fp32_swiglu), weights cast to the expert output dtype, terms
+rounded, summed in fp32 and rounded.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import torch
+
+from . import ops
+from .arena import PROJS, ArenaMoE, ArenaStore
+from .native import NativeCache
+
+
+class V4ArenaStore(ArenaStore):
+    """The arena with V4 affine quantisation metadata validated and the
+    compiled planner per tier over layers * E keys (key = layer * E + e)."""
+
+    def __init__(self, index_path, native_scheduler=True, **kwargs):
+        config = json.loads(Path(index_path).read_text())
+        self.expert_quant = config.get("quantization", {})
+        for tier, q in self.expert_quant.items():
+            if q.get("mode", "affine") != "affine":
+                raise ValueError(f"DeepSeek V4 streaming requires affine MLX weights, got "
+                                 f"{q.get('mode')!r} for tier {tier}")
+        super().__init__(index_path, **kwargs)
+        self.use_f16_moe = {t: self.use_f16(t) for t in self.tiers}
+        self.native_caches = {}
+        if native_scheduler:
+            policy = "lfu-decay" if self.cache_policy == "lfu-decay" else "slru"
+            for t in self.tiers:
+                self.native_caches[t] = NativeCache(self.layers * self.E, self.slots[t],
+                                                    self.protected_cap[t], policy=policy)
+        elif self.cache_policy == "lfu-decay":
+            raise RuntimeError("lfu-decay requires the compiled planner")
+
+    def _key_id(self, key):
+        layer, expert = key
+        return layer * self.E + expert
+
+    def _decode_key(self, key_id):
+        return divmod(key_id, self.E)
+
+    def quant(self, tier, field):
+        defaults = {"bits": 2, "group_size": 128, "mode": "affine"}
+        return self.expert_quant.get(tier, {}).get(field, defaults[field])
+
+    def group_size(self, t) -> int:
+        return int(self.quant(t, "group_size"))
+
+    def _place_keys(self, layer, want, prefetch):
+        """Planner calls for one layer (reference dsv4_arena.py:68-127): the
+        previous demand call's slots are pinned, hits are touched only on
+        demand, and the per-token LFU tick happens on layer 0 decode calls."""
+        if not self.native_caches:
+            return super()._place_keys(layer, want, prefetch)
+        if not want:
+            return {}, [], {t: [] for t in self.tiers}
+        tiers = {self.tier(layer, e) for e in want}
+        if len(tiers) != 1:
+            raise ValueError(f"layer {layer} spans multiple expert tiers: {tiers}")
+        t = tiers.pop()
+        cache = self.native_caches[t]
+        if layer == 0 and not prefetch and len(want) <= self.top_k:
+            for c in self.native_caches.values():
+                c.note_token()
+        if not prefetch and len(want) > self.slots[t] - 1:
+            raise ValueError(f"layer {layer} needs {len(want)} {t} experts but the arena has "
+                             f"{self.slots[t] - 1}; raise ceiling_gb")
+        # One planner call per key, each pinning the previous demand call's
+        # slots plus every slot this call has resolved so far: a multi-key
+        # call could hand a slot claimed (or hit) earlier in the same call to
+        # a later miss when the tier is nearly full, leaving two experts on
+        # one slot. Whenever that cannot happen the assignments equal one
+        # multi-key call's (same operations in the same order).
+        pins = set(self.pinned.get(t, ()))
+        results = []
+        for e in want:
+            (r,) = cache.plan([layer * self.E + e], pinned_slots=tuple(pins),
+                              touch_hits=not prefetch)
+            results.append(r)
+            if r.placed:
+                pins.add(r.slot)
+        out, issued = {}, []
+        waits = {name: [] for name in self.tiers}
+        for e, r in zip(want, results):
+            key = (layer, e)
+            if r.hit:
+                self._hit(key, t, prefetch, waits)
+            else:
+                if not prefetch:
+                    self.misses += 1
+                if r.evicted_key >= 0:
+                    self._evicted(self._decode_key(r.evicted_key))
+                if r.placed:
+                    issued.append((e, t, r.slot))
+            if r.placed:
+                out[e] = (t, r.slot)
+            elif not prefetch:
+                raise RuntimeError(f"native scheduler could not place demanded L{layer}.E{e}")
+        if not prefetch:
+            self.pinned = {t: {s for _, s in out.values()}}
+        return out, issued, waits
+
+    def _protected_size(self, t):
+        if t in self.native_caches:
+            return self.native_caches[t].protected_size
+        return super()._protected_size(t)
+
+    def stats(self):
+        st = super().stats()
+        st["scheduler"] = "c" if self.native_caches else "python"
+        return st
+
+    def close(self):
+        for c in self.native_caches.values():
+            c.close()
+        self.native_caches = {}
+        super().close()
+
+
+class V4Gate:
+    """The V4 MoEGate on the router kernel: logits = x . W^T in fp32;
+    sqrt(softplus) (or sigmoid / softmax) scores; top-k on score + the
+    selection-only bias; weights = score / (sum + 1e-20) * routed_scaling;
+    hash layers take idx = tid2eid[input_id] (reference dsv4_arena.py:147-153,
+    165-166; restated formula tf:models/deepseek_v4/modeling_deepseek_v4.py:
+    1024-1073). Returns (indices int32 [..., k], scores fp32 [..., k])."""
+
+    def __init__(self, weight, top_k=6, e_score_correction_bias=None, tid2eid=None,
+                 score_func="sqrtsoftplus", routed_scaling_factor=1.5, norm_topk_prob=True):
+        bias = (None if e_score_correction_bias is None
+                else e_score_correction_bias.to(device=weight.device, dtype=torch.float32).contiguous())
+        t2e = None if tid2eid is None else tid2eid.to(device=weight.device, dtype=torch.int32).contiguous()
+        self.spec = ops.RouterSpec(weight.contiguous(), top_k, score_func=score_func,
+                                   norm_topk=norm_topk_prob, routed_scale=routed_scaling_factor,
+                                   score_bias=bias, tid2eid=t2e)
+        self.top_k = top_k
+        self.ws = ops.Workspace(weight.device)
+
+    @property
+    def weight(self):
+        return self.spec.weight
+
+    def __call__(self, x, input_ids=None):
+        lead = x.shape[:-1]
+        if self.spec.tid2eid is not None and input_ids is None:
+            raise ValueError("hash-routed gate needs input_ids")
+        idx, w, _ = ops.router(self.spec, x.reshape(-1, x.shape[-1]), self.ws, input_ids=input_ids)
+        return idx.reshape(*lead, self.top_k), w.reshape(*lead, self.top_k)
+
+
+class V4ArenaMoE(ArenaMoE):
+    """V4 top-k routing and clamped SwiGLU over the arena's affine experts.
+    Routing is the gate's (hash routing in the first layers, selection-only
+    bias elsewhere); only the routed experts are replaced -- the shared
+    expert is added by the model block."""
+
+    def __init__(self, store: V4ArenaStore, layer: int, gate, top_k: int,
+                 swiglu_limit: float = 10.0, fused_decode: bool = False,
+                 overlap_hits: bool = False, fp32_swiglu: bool = False):
+        super().__init__(store, layer, gate, bias=None, top_k=top_k)
+        self.swiglu_limit = swiglu_limit
+        self.scores_follow_output = True
+        # The decode path always fuses gate/up + SwiGLU; the flag is accepted
+        # for interface parity.
+        self.fused_decode = fused_decode
+        # Results do not depend on it: hit and miss routes are computed by the
+        # same kernels once every fill has landed.
+        self.overlap_hits = overlap_hits
+        self.fp32_swiglu = fp32_swiglu
+
+    def route(self, x, input_ids=None):
+        return self.gate(x, input_ids)
+
+
+__all__ = ["V4ArenaStore", "V4ArenaMoE", "V4Gate", "PROJS"]

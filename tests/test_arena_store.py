@@ -1,0 +1,208 @@
+"""The arena store (locali_amd.arena / dsv4_arena) on the CPU: slot geometry
+and the zero slot, fills that land the exact expert bytes from either file
+layout, the planner driven the way the reference drives it
+(dsv4_arena.py:68-127; arena.py:212-354) against the oracle planner,
+prefetch and capacity semantics, and the stats surface (arena.py:437-451)."""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+
+from checkpoint_fixture import expert_bytes, make_index, make_snapshot
+from locali_amd.arena import ArenaStore
+from locali_amd.dsv4_arena import PROJS, V4ArenaStore
+from oracle.scheduler import LFU_DECAY, SLRU, OraclePlanner
+
+LAYERS, EXPERTS, TOP_K = 3, 8, 2
+
+
+@pytest.fixture(scope="module")
+def ckpt(tmp_path_factory):
+    root = tmp_path_factory.mktemp("ckpt")
+    truth = make_snapshot(root, layers=LAYERS, experts=EXPERTS, top_k=TOP_K, d=128, dff=64)
+    return root, truth, make_index(root), make_index(root, packed=True)
+
+
+def _store(index, slots, cls=V4ArenaStore, **kw):
+    per = ArenaStore.__new__(ArenaStore)  # item size from the index, without allocating
+    import json
+    meta = next(iter(json.loads(open(index).read())["experts"].values()))
+    per = sum(meta[p][k][3] for p in PROJS for k in ("weight", "scales", "biases"))
+    return cls(index, ceiling_gb=(slots * per + 1) / 1e9, threads=2, device="cpu", **kw)
+
+
+def _slot_bytes(store, t, slot) -> bytes:
+    out = b""
+    for p in PROJS:
+        for k in ("weight", "scales", "biases"):
+            out += store.arena[(t, p, k)][slot].contiguous().view(torch.uint8).numpy().tobytes()
+    return out
+
+
+def test_geometry_zero_slot_and_ceiling(ckpt):
+    _, _, index, _ = ckpt
+    st = _store(index, 5)
+    try:
+        assert st.tiers == ["cold"] and st.slots["cold"] == 5
+        assert st.resident == 5 * st.item["cold"] <= st.ceiling
+        assert st.arena[("cold", "gate_proj", "weight")].shape[0] == 5
+        assert not any(_slot_bytes(st, "cold", 0))
+        assert st.quant("cold", "bits") == 2 and st.quant("cold", "group_size") == 64
+        assert st.use_f16_moe == {"cold": False}
+    finally:
+        st.close()
+    with pytest.raises(ValueError, match="no usable expert slot"):
+        _store(index, 1)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_fills_land_the_experts_bytes(ckpt, packed):
+    _, truth, index, pindex = ckpt
+    st = _store(pindex if packed else index, 6)
+    try:
+        assert st.tier_overlap == packed
+        placed = st.slots_for(1, [3, 5, 3])
+        assert set(placed) == {3, 5}
+        for e, (t, s) in placed.items():
+            assert _slot_bytes(st, t, s) == expert_bytes(truth, 1, e)
+        assert not any(_slot_bytes(st, "cold", 0))
+        assert st.bytes_read == 2 * st.item["cold"]
+        ea = st.expert_arena("cold")
+        assert (ea.gate.bits, ea.down.bits, ea.gate.group_size) == (2, 2, 64)
+        assert (ea.d_model, ea.d_ff, ea.n_slots) == (128, 64, 6)
+    finally:
+        st.close()
+
+
+@pytest.mark.parametrize("policy,slots", [("lru", 5), ("lru", 9), ("slru-all", 9), ("slru-all", 13),
+                                          ("lfu-decay", 5), ("lfu-decay", 8)])
+def test_native_planner_matches_the_oracle_driven_the_same_way(ckpt, policy, slots):
+    _, _, index, _ = ckpt
+    st = _store(index, slots, cache_policy=policy)
+    prot = (slots - 1) // 2 if policy == "slru-all" else 0
+    ref = OraclePlanner(LAYERS * EXPERTS, slots, prot, LFU_DECAY if policy == "lfu-decay" else SLRU)
+    rng = random.Random(5)
+    pinned: dict = {}
+    hits = misses = evictions = 0
+    try:
+        for tok in range(12):
+            for layer in range(LAYERS):
+                want = list(dict.fromkeys(rng.randrange(EXPERTS) for _ in range(TOP_K)))
+                if layer == 0 and len(want) <= TOP_K:
+                    ref.note_token()
+                res, pins = [], set(pinned)
+                for e in want:                        # one key at a time, growing pins
+                    rc, (r,) = ref.plan([layer * EXPERTS + e], pinned_slots=pins, touch_hits=True)
+                    assert rc == 0
+                    res.append(r)
+                    pins.add(r.slot)
+                want_slots = {e: r.slot for e, r in zip(want, res)}
+                hits += sum(r.hit for r in res)
+                misses += sum(not r.hit for r in res)
+                evictions += sum(r.evicted_key >= 0 for r in res)
+                pinned = set(want_slots.values())
+                placed = st.slots_for(layer, want)
+                assert {e: s for e, (_, s) in placed.items()} == want_slots
+        s = st.stats()
+        assert (s["hits"], s["misses"], s["evictions"]) == (hits, misses, evictions)
+        assert s["protected"]["cold"] == ref.protected_size
+        assert s["scheduler"] == "c"
+    finally:
+        st.close()
+
+
+def test_one_multi_key_call_could_put_two_experts_on_one_slot():
+    """Why the store plans key by key: with the previous call's two slots
+    pinned and three usable slots, a single two-key call evicts its own first
+    claim for its second miss."""
+    ref = OraclePlanner(16, 4, 0, SLRU)
+    _, first = ref.plan([0, 1], pinned_slots=(), touch_hits=True)
+    _, res = ref.plan([2, 3], pinned_slots={r.slot for r in first}, touch_hits=True)
+    assert res[0].slot == res[1].slot and res[1].evicted_key == 2
+
+
+def test_python_planner_is_lru_with_pins(ckpt):
+    _, truth, index, _ = ckpt
+    st = _store(index, 3, native_scheduler=False, cache_policy="lru")
+    try:
+        a = st.slots_for(0, [1, 2])
+        assert sorted(s for _, s in a.values()) == [1, 2]
+        st.slots_for(0, [1])                          # 1 becomes most recent
+        b = st.slots_for(0, [4])                      # evicts 2 (least recent, not pinned)
+        assert b[4][1] == a[2][1]
+        assert _slot_bytes(st, "cold", b[4][1]) == expert_bytes(truth, 0, 4)
+        s = st.stats()
+        assert (s["hits"], s["misses"], s["evictions"]) == (1, 3, 1)
+        assert s["scheduler"] == "python"
+    finally:
+        st.close()
+    with pytest.raises(RuntimeError, match="lfu-decay"):
+        _store(index, 3, native_scheduler=False, cache_policy="lfu-decay")
+
+
+def test_prefetch_is_best_effort_and_accounted(ckpt):
+    _, truth, index, _ = ckpt
+    st = _store(index, 5)
+    try:
+        st.slots_for(0, [0, 1])
+        out, plan = st.submit(1, [2, 6], prefetch=True)
+        st.wait([f for fs in plan.values() for f in fs])
+        s = st.stats()
+        assert (s["hits"], s["misses"], s["prefetched"]) == (0, 2, 2)
+        placed = st.slots_for(1, [6])                 # a demand hit on a prefetched expert
+        assert placed[6] == out[6]
+        assert _slot_bytes(st, "cold", out[6][1]) == expert_bytes(truth, 1, 6)
+        s = st.stats()
+        assert (s["hits"], s["prefetch_used"]) == (1, 1)
+        st.slots_for(2, [3, 4])                       # evicts L0.E0 and L0.E1
+        st.slots_for(2, [5, 7])                       # evicts the never-used prefetch L1.E2
+        s = st.stats()
+        assert s["prefetch_wasted"] == 1 and s["evictions"] == 4
+    finally:
+        st.close()
+
+
+def test_a_prefetch_never_fills_a_slot_it_gave_away(ckpt):
+    _, truth, index, _ = ckpt
+    st = _store(index, 4)                              # three usable slots
+    try:
+        st.slots_for(0, [0, 1])                       # pins two of them
+        out, plan = st.submit(1, [2, 6], prefetch=True)
+        st.wait([f for fs in plan.values() for f in fs])
+        slots = [s for _, s in out.values()]
+        assert len(slots) == len(set(slots))          # no expert shares a slot
+        for e, (t, s) in out.items():
+            assert _slot_bytes(st, t, s) == expert_bytes(truth, 1, e)
+    finally:
+        st.close()
+
+
+def test_capacity_is_enforced_for_demand_only(ckpt):
+    _, _, index, _ = ckpt
+    st = _store(index, 3)
+    try:
+        with pytest.raises(ValueError, match="arena has 2"):
+            st.slots_for(0, [0, 1, 2])
+        out, _ = st.submit(1, [0, 1, 2, 3], prefetch=True)   # best effort, no raise
+        assert len(out) <= 2
+    finally:
+        st.close()
+
+
+def test_stats_surface(ckpt):
+    _, _, index, _ = ckpt
+    st = _store(index, 3)
+    try:
+        keys = {"hits", "misses", "hit_rate", "evictions", "bytes_read", "resident", "peak", "slots",
+                "t_stall", "t_convert", "t_eval", "prefetched", "prefetch_used",
+                "prefetch_wasted", "cache_policy", "protected", "scheduler"}
+        assert set(st.stats()) == keys
+        st.slots_for(0, [1])
+        st.slots_for(0, [1])
+        assert st.stats()["hit_rate"] == 0.5
+    finally:
+        st.close()
+    assert not st.arena and not st.fds
