@@ -15,5 +15,4 @@ Modules:
   cref        ctypes wrapper of expert_ref.c, an independent C restatement of
               the expert arithmetic (OpenMP) used for large sizes and as the
               CPU baseline
-  synth       seeded synthetic inputs for the five benchmark workloads
 """
