@@ -28,8 +28,9 @@ ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"-I{INCLUDE}", f"-I{CSRC}"]
+# MFMA results go straight to VGPRs (no accumulator-register round trips).
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
-          "-packed-fp32-ops", "-munsafe-fp-atomics"]
+          "-packed-fp32-ops", "-munsafe-fp-atomics", "-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def sources() -> list[Path]:

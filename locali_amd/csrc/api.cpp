@@ -9,7 +9,7 @@
 #include <cstring>
 #include <string>
 
-#include "grouped_kernels.hpp"
+#include "mfma_grouped.hpp"
 #include "launch.hpp"
 
 using namespace locali;
@@ -46,13 +46,30 @@ bool dtype16(int32_t dt) { return dt == LOCALI_DT_F16 || dt == LOCALI_DT_BF16; }
 // Workspace layout for up to T tokens.
 struct Layout {
     size_t logits, route_slot, hidden, hprep, seg_start, sorted_route, route_pos,
-        tiles, n_tiles, gh, gy, total;
+        tiles, n_tiles, gh, gy, mx, mh, total;
     int max_tiles;
 };
 
 // Bytes of one prepared vector of K values, for any bit width (pairs take at
 // most K u32, partial sums at most K / 4 float2).
 size_t prep_bytes(int K) { return align_up(4 * static_cast<size_t>(K)) + align_up(2 * static_cast<size_t>(K)); }
+
+// Prepared inputs of the MFMA grouped kernels for n vectors of K values:
+// pairs (K / 2 u32 each: at most 8 pairs per 16 values) then per-64 sums.
+size_t mfma_batch_bytes(int n, int K) {
+    return align_up(sizeof(uint32_t) * static_cast<size_t>(n) * (K / 2)) +
+           align_up(sizeof(float2) * static_cast<size_t>(n) * (K / 64 + 1));
+}
+
+MfmaVec mfma_batch(void *base, int n, int K) {
+    MfmaVec v{};
+    v.pairs = static_cast<uint32_t *>(base);
+    v.pairs_stride = K / 2;
+    v.gsum = reinterpret_cast<float2 *>(static_cast<char *>(base) +
+                                        align_up(sizeof(uint32_t) * static_cast<size_t>(n) * (K / 2)));
+    v.gsum_stride = K / 64;
+    return v;
+}
 
 Layout layout(int T, int d, int dff, int E, int k, int has_shared) {
     Layout L{};
@@ -76,6 +93,8 @@ Layout layout(int T, int d, int dff, int E, int k, int has_shared) {
     L.n_tiles = take(sizeof(int32_t));
     L.gh = take(sizeof(uint16_t) * static_cast<size_t>(routes) * dff);
     L.gy = take(sizeof(uint16_t) * static_cast<size_t>(routes) * d);
+    L.mx = take(mfma_batch_bytes(T, d));
+    L.mh = take(mfma_batch_bytes(routes, dff));
     L.total = off;
     return L;
 }
@@ -227,10 +246,85 @@ int check_decode_args(const locali_expert_arena *routed, const locali_expert_are
     return 0;
 }
 
+// The matrix-core grouped path needs 2- or 4-bit codes (gate and up alike),
+// groups of a multiple of 64, rows in multiples of 64, columns in multiples
+// of 2 * 64 * kMfmaDepth holding a multiple of 8 groups, and its staged inputs
+// within 64 KiB of LDS; the
+// shared expert must match the routed one (they share prepared inputs).
+bool mfma_eligible(const locali_expert_arena *routed, const locali_expert_arena *shared) {
+    auto ok = [](const locali_qproj &p) {
+        const int gpr = p.cols / p.group_size;
+        const size_t lds = sizeof(float2) * (p.cols / 64) * kMfmaTileTokens +
+                           sizeof(uint16_t) * 4 * kMfmaRows * (p.cols / 64);
+        return (p.bits == 2 || p.bits == 4) && p.group_size % 64 == 0 && p.rows % kMfmaRows == 0 &&
+               p.cols % (128 * kMfmaDepth) == 0 && gpr % 8 == 0 && lds <= 64 * 1024;
+    };
+    if (!ok(routed->gate) || !ok(routed->up) || !ok(routed->down)) return false;
+    if (routed->gate.bits != routed->up.bits) return false;
+    if (shared && (shared->gate.bits != routed->gate.bits || shared->up.bits != routed->up.bits ||
+                   shared->down.bits != routed->down.bits || !ok(shared->gate) || !ok(shared->up) ||
+                   !ok(shared->down)))
+        return false;
+    return true;
+}
+
+int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_arena *shared,
+                     const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k, int32_t n_experts,
+                     const int32_t *route_slot, const float *weights, float limit,
+                     int32_t fp32_swiglu, int32_t combine_mode, void *out, void *ws,
+                     const Layout &lay, hipStream_t st) {
+    const int R = tokens * top_k;
+    const int n_slots = routed->gate.n_slots;
+    const int routes = R + (shared ? tokens : 0);
+    int32_t *route_pos = at<int32_t>(ws, lay.route_pos);
+    int32_t *tiles = at<int32_t>(ws, lay.tiles);
+    int32_t *n_tiles = at<int32_t>(ws, lay.n_tiles);
+    uint16_t *gy = at<uint16_t>(ws, lay.gy);
+    const int max_tiles = grouped_max_tiles(tokens, top_k, shared ? 1 : 0, n_experts, kMfmaTileTokens);
+    if (max_tiles > lay.max_tiles) return fail(LOCALI_E_WORKSPACE, "grouped: tile list too small");
+    hipError_t e = launch_dispatch(route_slot, R, n_slots, shared ? tokens : 0, kMfmaTileTokens,
+                                   at<int32_t>(ws, lay.seg_start), at<int32_t>(ws, lay.sorted_route),
+                                   route_pos, tiles, n_tiles, max_tiles, st);
+    if (e != hipSuccess) return hip_fail(e, "dispatch launch");
+    MfmaLaunch L{};
+    L.ta.x = static_cast<const uint16_t *>(x);
+    L.ta.tiles = tiles;
+    L.ta.n_tiles = n_tiles;
+    L.ta.sorted_route = at<int32_t>(ws, lay.sorted_route);
+    L.ta.R = R;
+    L.ta.top_k = top_k;
+    L.gate = to_dev(routed->gate);
+    L.up = to_dev(routed->up);
+    L.down = to_dev(routed->down);
+    const locali_expert_arena *sh = shared ? shared : routed;
+    L.sgate = to_dev(sh->gate);
+    L.sup = to_dev(sh->up);
+    L.sdown = to_dev(sh->down);
+    L.xin = mfma_batch(at<void>(ws, lay.mx), tokens, routed->gate.cols);
+    L.hmid = mfma_batch(at<void>(ws, lay.mh), routes, routed->down.cols);
+    L.y = gy;
+    L.limit = limit;
+    L.fp32_swiglu = fp32_swiglu;
+    L.max_tiles = max_tiles;
+    L.tokens = tokens;
+    L.routes = routes;
+    const bool bf16 = x_dtype == LOCALI_DT_BF16;
+    for (int which = 0; which < 3; ++which)
+        if ((e = launch_mfma(which, bf16, L, st)) != hipSuccess) return hip_fail(e, "grouped MFMA launch");
+    const int d = routed->down.rows;
+    e = launch_combine(gy, route_pos, shared ? gy + static_cast<int64_t>(R) * d : nullptr, weights, tokens,
+                       top_k, d, combine_mode, bf16, static_cast<uint16_t *>(out), st);
+    if (e != hipSuccess) return hip_fail(e, "combine launch");
+    return 0;
+}
+
 int run_grouped(const locali_expert_arena *routed, const locali_expert_arena *shared, const void *x,
                 int32_t x_dtype, int32_t tokens, int32_t top_k, int32_t n_experts,
                 const int32_t *route_slot, const float *weights, float limit, int32_t fp32_swiglu,
                 int32_t combine_mode, void *out, void *ws, const Layout &lay, hipStream_t st) {
+    if (mfma_eligible(routed, shared))
+        return run_grouped_mfma(routed, shared, x, x_dtype, tokens, top_k, n_experts, route_slot, weights, limit,
+                                fp32_swiglu, combine_mode, out, ws, lay, st);
     const int R = tokens * top_k;
     const int n_slots = routed->gate.n_slots;
     int32_t *seg_start = at<int32_t>(ws, lay.seg_start);

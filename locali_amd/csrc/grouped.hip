@@ -13,7 +13,7 @@
 //                           with a ballot and writes sorted_route / route_pos
 //                           in route order (stable)
 //   combine_kernel          out[t] = round(sum_j round(y[pos(t,j)] * w)) (+ shared)
-#include "grouped_kernels.hpp"
+#include "mfma_grouped.hpp"
 
 namespace locali {
 
@@ -186,6 +186,20 @@ hipError_t launch_grouped_kernels(int which, const GroupedKernelLaunch &L, hipSt
     case 2: return L.bf16 ? grouped_b2_bf16(which, gpc, cpr, L, st) : grouped_b2_f16(which, gpc, cpr, L, st);
     case 4: return L.bf16 ? grouped_b4_bf16(which, gpc, cpr, L, st) : grouped_b4_f16(which, gpc, cpr, L, st);
     case 8: return L.bf16 ? grouped_b8_bf16(which, gpc, cpr, L, st) : grouped_b8_f16(which, gpc, cpr, L, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t mfma_b2(int which, bool bf16, const MfmaLaunch &L, hipStream_t st);
+hipError_t mfma_b4(int which, bool bf16, const MfmaLaunch &L, hipStream_t st);
+
+// which: 0 = prepare x, 1 = gate/up + SwiGLU (+ prepared h), 2 = down.
+// Gate and up share the prepared x, so they must share a bit width.
+hipError_t launch_mfma(int which, bool bf16, const MfmaLaunch &L, hipStream_t st) {
+    const int bits = which == 2 ? L.down.bits : L.gate.bits;
+    switch (bits) {
+    case 2: return mfma_b2(which, bf16, L, st);
+    case 4: return mfma_b4(which, bf16, L, st);
     default: return hipErrorInvalidValue;
     }
 }

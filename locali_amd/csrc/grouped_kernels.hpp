@@ -20,6 +20,7 @@ struct TileArgs {
     const int32_t *n_tiles;       // [1]
     const int32_t *sorted_route;  // [R]
     int32_t R, top_k;
+    int32_t n_vec;                // vectors in the MFMA kernels' input array (bounds of its loads)
 };
 
 __device__ __forceinline__ int tile_token(const TileArgs &ta, bool shared, int pos) {

@@ -104,5 +104,7 @@ struct GroupedLaunch {
 
 hipError_t launch_grouped(const GroupedLaunch &L, hipStream_t st);
 int grouped_max_tiles(int tokens, int top_k, int n_shared, int E, int tile_tokens);
+struct MfmaLaunch;
+hipError_t launch_mfma(int which, bool bf16, const MfmaLaunch &L, hipStream_t st);
 
 }  // namespace locali

@@ -1,0 +1,10 @@
+// MFMA grouped kernels instantiated for 2-bit codes (bf16 and fp16 activations).
+#include "mfma_grouped.hpp"
+
+namespace locali {
+
+hipError_t mfma_b2(int which, bool bf16, const MfmaLaunch &L, hipStream_t st) {
+    return bf16 ? launch_mfma_stage<2, true>(which, L, st) : launch_mfma_stage<2, false>(which, L, st);
+}
+
+}  // namespace locali

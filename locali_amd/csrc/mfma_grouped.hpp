@@ -1,0 +1,436 @@
+// Grouped expert kernels on the matrix cores (prefill, batched decode).
+//
+// A tile is (slot, first sorted position, up to 16 tokens) of the dispatch's
+// slot-sorted route order. A workgroup of 4 waves covers 64 output rows of
+// one tile; each wave owns 16 rows and computes the 16x16 (token x row) block
+// with v_mfma_f32_16x16x32_{bf16,f16}:
+//
+//   B operand (weights): lane (row n = lane % 16, k-lane kb = lane / 16) owns
+//     WPL whole 32-bit words of every 64-value block of row n and expands them
+//     with one v_bitop3_b32 per pair into 16-bit floats magic + q * 4^j (fp16:
+//     the magic removed exactly by one packed add) -- 8 values per MFMA step.
+//   A operand (activations): the same lane reads the matching prepared pairs
+//     (x pre-scaled by 4^-j, see qgemv.hpp) of token m = lane % 16, so A and B
+//     agree on every k slot whatever order the words put the codes in.
+//   Per 64-value block the two MFMA steps start from zero and the affine
+//     group terms are applied in fp32:  acc += s * (D - magic*sum x') + b * sum x
+//     (the factorised affine GEMV of dsv4_kernels.py:75-79), with the per-block
+//     sums of the tile's tokens staged in LDS.
+//
+//   mfma_prep_kernel     prepared pairs + per-64 sums of the tokens' x
+//   mfma_gateup_kernel   h = swiglu(up, gate) rounded as the decode path; the
+//                        epilogue prepares h for the down projection (the
+//                        workgroup owns whole 64-value blocks of h)
+//   mfma_down_kernel     y[pos] = round(down(h[pos]))
+// Weights of a slot are streamed once per tile of 16 tokens; each wave keeps
+// the next chunk of kMfmaDepth blocks (words and activations) in flight while
+// it works on the current one.
+#pragma once
+
+#include "grouped_kernels.hpp"
+
+namespace locali {
+
+constexpr int kMfmaTileTokens = 16;
+constexpr int kMfmaWaves = 4;
+constexpr int kMfmaRows = 16 * kMfmaWaves;
+constexpr int kMfmaDepth = 4;   // 64-value blocks in flight per wave
+
+typedef float mf32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 mbf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 mf16x8_t __attribute__((ext_vector_type(8)));
+
+template <bool BF16>
+__device__ __forceinline__ mf32x4_t mfma_16x16x32(u32x4 a, u32x4 b, mf32x4_t c) {
+    if constexpr (BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mbf16x8_t, a),
+                                                        __builtin_bit_cast(mbf16x8_t, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf16x8_t, a),
+                                                       __builtin_bit_cast(mf16x8_t, b), c, 0, 0, 0);
+}
+
+// Prepared inputs of the MFMA kernels, one vector per token or position:
+// pairs [words * P] u32 (P pairs per word, as the decode layout) and
+// gsum [K / 64] float2 = (magic * sum of pre-scaled values, sum of values).
+struct MfmaVec {
+    uint32_t *pairs;
+    float2 *gsum;
+    int64_t pairs_stride, gsum_stride;
+};
+
+template <int BITS, bool BF16>
+struct MfmaGeom {
+    using P = Pairs<BITS, BF16>;
+    static constexpr int kNP = P::kCount;        // pairs per word
+    static constexpr int kVPW = 32 / BITS;       // values per word
+    static constexpr int kW64 = 64 / kVPW;       // words per 64-value block
+    static constexpr int kWPL = kW64 / 4;        // words per lane per block
+    static_assert(kWPL * kNP == 8, "one block = two MFMA steps of 4 pairs per lane");
+};
+
+// One thread per (vector, word); the W64 words of a 64-block are consecutive
+// lanes, so their sums meet by butterfly.
+template <int BITS, bool BF16>
+__global__ __launch_bounds__(256) void mfma_prep_kernel(const uint16_t *__restrict__ v, int n_vec, int K,
+                                                        MfmaVec out) {
+    using G = MfmaGeom<BITS, BF16>;
+    const int words = K / G::kVPW;
+    const int u = blockIdx.x * blockDim.x + threadIdx.x;
+    const int vec = u / words, w = u % words;
+    float2 part = make_float2(0.f, 0.f);
+    if (vec < n_vec)
+        prep_word<BITS, BF16>(v + static_cast<int64_t>(vec) * K + w * G::kVPW,
+                              out.pairs + vec * out.pairs_stride + w * G::kNP, 1, part);
+#pragma unroll
+    for (int m = 1; m < G::kW64; m <<= 1) {
+        part.x += __shfl_xor(part.x, m, 64);
+        part.y += __shfl_xor(part.y, m, 64);
+    }
+    if (vec < n_vec && w % G::kW64 == 0) out.gsum[vec * out.gsum_stride + w / G::kW64] = part;
+}
+
+// Buffer resources: one 128-bit descriptor per array, held in SGPRs, so a
+// load is "descriptor + per-lane 32-bit offset + per-block scalar offset"
+// with no 64-bit address arithmetic per load, and out-of-range offsets read
+// zero instead of faulting. (Descriptor word 3 for GFX9-family parts.)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+constexpr int kAuxStream = 2;   // non-temporal: weights are read once
+
+// The lane's words of one 64-value block of one projection.
+template <int WPL>
+struct BlockW {
+    uint32_t w[WPL];
+};
+
+template <int WPL>
+__device__ __forceinline__ void load_block_w(BlockW<WPL> &o, __amdgpu_buffer_rsrc_t rsrc, uint32_t voff,
+                                             int blk) {
+#pragma unroll
+    for (int i = 0; i < WPL; ++i)
+        o.w[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff + 4u * i, blk * 16 * WPL, kAuxStream);
+}
+
+__device__ __forceinline__ void load_block_a(u32x4 (&a)[2], __amdgpu_buffer_rsrc_t rsrc, uint32_t voff,
+                                             int blk) {
+    a[0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, blk * 128, 0);
+    a[1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff + 16u, blk * 128, 0);
+}
+
+// Group scales and biases of the workgroup's 64 rows, staged once into LDS as
+// meta[g][r] = {scale, bias} of each projection (16-bit each): in the loop a
+// lane then reads its row's pair with one LDS load instead of issuing small
+// global loads that the compiler would schedule next to their use. Staged
+// with 16-byte global loads (8 groups of one row per array).
+template <int NPROJ>
+__device__ __forceinline__ void stage_meta(uint16_t *meta, const uint16_t *const (&arr)[2 * NPROJ],
+                                           int gpr, int bpg) {
+    const int chunks = kMfmaRows * (gpr / 8);
+    for (int e = threadIdx.x; e < chunks; e += blockDim.x) {
+        const int r = e % kMfmaRows, c = e / kMfmaRows;
+        uint4 v[2 * NPROJ];
+#pragma unroll
+        for (int a = 0; a < 2 * NPROJ; ++a)
+            v[a] = reinterpret_cast<const uint4 *>(arr[a] + static_cast<int64_t>(r) * gpr)[c];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int g = c * 8 + q;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {   // one entry per 64-value block (bpg is 1 or 2)
+                if (t >= bpg) break;
+                uint16_t *dst = meta + (static_cast<int64_t>(g * bpg + t) * kMfmaRows + r) * (2 * NPROJ);
+#pragma unroll
+                for (int a = 0; a < 2 * NPROJ; ++a) {
+                    const uint32_t wv = q < 2 ? (q == 0 ? v[a].x : v[a].x >> 16)
+                                      : q < 4 ? (q == 2 ? v[a].y : v[a].y >> 16)
+                                      : q < 6 ? (q == 4 ? v[a].z : v[a].z >> 16)
+                                              : (q == 6 ? v[a].w : v[a].w >> 16);
+                    dst[a] = static_cast<uint16_t>(wv);
+                }
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void load_block_a(u32x4 (&a)[2], const uint32_t *__restrict__ ap, int blk) {
+    const u32x4 *p = reinterpret_cast<const u32x4 *>(ap + blk * 32);
+    a[0] = p[0];
+    a[1] = p[1];
+}
+
+// Two MFMA steps of one block for one projection, from zero.
+template <int BITS, bool BF16>
+__device__ __forceinline__ mf32x4_t block_mfma(const BlockW<MfmaGeom<BITS, BF16>::kWPL> &bw,
+                                               const u32x4 (&a)[2], uint32_t magic_v) {
+    using G = MfmaGeom<BITS, BF16>;
+    uint32_t e[8];
+#pragma unroll
+    for (int i = 0; i < G::kWPL; ++i)
+        static_for<0, G::kNP>([&](auto pc) {
+            constexpr int p = decltype(pc)::value;
+            e[i * G::kNP + p] = expand_pair<BITS, BF16, p>(bw.w[i], magic_v);
+        });
+    const u32x4 b0 = {e[0], e[1], e[2], e[3]}, b1 = {e[4], e[5], e[6], e[7]};
+    mf32x4_t d = {0.f, 0.f, 0.f, 0.f};
+    d = mfma_16x16x32<BF16>(a[0], b0, d);
+    d = mfma_16x16x32<BF16>(a[1], b1, d);
+    return d;
+}
+
+__device__ __forceinline__ void stage_gsum(float2 *gsl, const MfmaVec &in, int nblk, int count,
+                                           const TileArgs &ta, bool shared, int first, bool by_token) {
+    for (int e = threadIdx.x; e < nblk * kMfmaTileTokens; e += blockDim.x) {
+        const int q = e % kMfmaTileTokens, blk = e / kMfmaTileTokens;
+        const int pos = first + min(q, count - 1);
+        const int vec = by_token ? tile_token(ta, shared, pos) : pos;
+        gsl[e] = in.gsum[vec * in.gsum_stride + blk];
+    }
+}
+
+__device__ __forceinline__ void apply_block(mf32x4_t &acc, const mf32x4_t &d, float s, float b,
+                                            const float2 *gsl_blk, int kb) {
+    const float4 c01 = reinterpret_cast<const float4 *>(gsl_blk + 4 * kb)[0];
+    const float4 c23 = reinterpret_cast<const float4 *>(gsl_blk + 4 * kb)[1];
+    const float cx[4] = {c01.x, c01.z, c23.x, c23.z}, cy[4] = {c01.y, c01.w, c23.y, c23.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = fmaf(s, d[i] - cx[i], fmaf(b, cy[i], acc[i]));
+}
+
+template <int BITS, bool BF16>
+__global__ __launch_bounds__(64 * kMfmaWaves) void mfma_gateup_kernel(
+    TileArgs ta, QProj gate, QProj up, QProj sgate, QProj sup, MfmaVec xin, MfmaVec hout,
+    int down_bits, float limit, int fp32_swiglu) {
+    using G = MfmaGeom<BITS, BF16>;
+    constexpr int WPL = G::kWPL;
+    extern __shared__ __align__(16) float2 gsl[];                 // [nblk][16], then meta
+    __shared__ __align__(16) uint16_t hs[kMfmaTileTokens][kMfmaRows];
+    const int tile = blockIdx.y;
+    if (tile >= *ta.n_tiles) return;
+    const int slot = ta.tiles[4 * tile], first = ta.tiles[4 * tile + 1];
+    const int count = ta.tiles[4 * tile + 2];
+    const bool shared = slot == -2;
+    const QProj &pg = shared ? sgate : gate;
+    const QProj &pu = shared ? sup : up;
+    if (count <= 0 || count > kMfmaTileTokens ||
+        (!shared && (slot < 0 || slot >= pg.n_slots || first < 0 || first + count > ta.R)))
+        return;
+    const int N = pg.rows, K = pg.cols, nblk = K / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nl = lane & 15, kb = lane >> 4;
+    const int n0 = blockIdx.x * kMfmaRows;
+    const int n = n0 + wave * 16 + nl;
+    stage_gsum(gsl, xin, nblk, count, ta, shared, first, true);
+    const int sl = shared ? 0 : slot;
+    const int wpr = K / G::kVPW;
+    const int gpr = K / pg.group, bpg = pg.group / 64;
+    // x pairs of token m = nl; the workgroup's 64 rows of gate and up
+    const int tok_a = tile_token(ta, shared, first + min(nl, count - 1));
+    const __amdgpu_buffer_rsrc_t ra_rs = make_rsrc(xin.pairs, static_cast<uint32_t>(4 * xin.pairs_stride * ta.n_vec));
+    const uint32_t a_off = 4u * static_cast<uint32_t>(tok_a * xin.pairs_stride + kb * WPL * G::kNP);
+    const uint32_t wbytes = 4u * kMfmaRows * wpr;
+    const __amdgpu_buffer_rsrc_t gw_rs = make_rsrc(pg.w + sl * pg.w_slot + static_cast<int64_t>(n0) * wpr, wbytes);
+    const __amdgpu_buffer_rsrc_t uw_rs = make_rsrc(pu.w + sl * pu.w_slot + static_cast<int64_t>(n0) * wpr, wbytes);
+    const uint32_t w_off = 4u * static_cast<uint32_t>((wave * 16 + nl) * wpr + kb * WPL);
+    uint16_t *meta = reinterpret_cast<uint16_t *>(gsl + nblk * kMfmaTileTokens);   // [blk][64][4]
+    {
+        const int64_t r0 = static_cast<int64_t>(n0) * gpr;
+        const uint16_t *const arr[4] = {pg.s + sl * pg.m_slot + r0, pg.b + sl * pg.m_slot + r0,
+                                        pu.s + sl * pu.m_slot + r0, pu.b + sl * pu.m_slot + r0};
+        stage_meta<2>(meta, arr, gpr, bpg);
+    }
+    const uint2 *lmeta = reinterpret_cast<const uint2 *>(meta) + wave * 16 + nl;   // + blk * 64
+    __syncthreads();
+    const uint32_t magic_v = opaque_vgpr(G::P::kMagic);
+    mf32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+    // Two chunks of kMfmaDepth blocks alternate: the loads of chunk c + 1 are
+    // issued before the math of chunk c, and scheduling barriers keep the
+    // compiler from sinking them behind it (nblk is a multiple of 2 chunks).
+    BlockW<WPL> g0[kMfmaDepth], u0[kMfmaDepth], g1[kMfmaDepth], u1[kMfmaDepth];
+    u32x4 a0[kMfmaDepth][2], a1[kMfmaDepth][2];
+    auto load_chunk = [&](BlockW<WPL>(&g)[kMfmaDepth], BlockW<WPL>(&u)[kMfmaDepth],
+                          u32x4(&a)[kMfmaDepth][2], int c) {
+        const int b0 = min(c, nblk / kMfmaDepth - 1) * kMfmaDepth;
+#pragma unroll
+        for (int j = 0; j < kMfmaDepth; ++j) {
+            load_block_w<WPL>(g[j], gw_rs, w_off, b0 + j);
+            load_block_w<WPL>(u[j], uw_rs, w_off, b0 + j);
+            load_block_a(a[j], ra_rs, a_off, b0 + j);
+        }
+    };
+    auto math_chunk = [&](const BlockW<WPL>(&g)[kMfmaDepth], const BlockW<WPL>(&u)[kMfmaDepth],
+                          const u32x4(&a)[kMfmaDepth][2], int c) {
+#pragma unroll
+        for (int j = 0; j < kMfmaDepth; ++j) {
+            const int blk = c * kMfmaDepth + j;
+            const uint2 m = lmeta[blk * kMfmaRows];
+            const mf32x4_t dg = block_mfma<BITS, BF16>(g[j], a[j], magic_v);
+            const mf32x4_t du = block_mfma<BITS, BF16>(u[j], a[j], magic_v);
+            const float2 *gb_lds = gsl + blk * kMfmaTileTokens;
+            apply_block(accg, dg, to_float<BF16>(static_cast<uint16_t>(m.x)),
+                        to_float<BF16>(static_cast<uint16_t>(m.x >> 16)), gb_lds, kb);
+            apply_block(accu, du, to_float<BF16>(static_cast<uint16_t>(m.y)),
+                        to_float<BF16>(static_cast<uint16_t>(m.y >> 16)), gb_lds, kb);
+        }
+    };
+    const int nchunks = nblk / kMfmaDepth;
+    load_chunk(g0, u0, a0, 0);
+    for (int c = 0; c < nchunks; c += 2) {
+        load_chunk(g1, u1, a1, c + 1);
+        sched_fence();
+        math_chunk(g0, u0, a0, c);
+        sched_fence();
+        load_chunk(g0, u0, a0, c + 2);
+        sched_fence();
+        math_chunk(g1, u1, a1, c + 1);
+        sched_fence();
+    }
+    // lane holds tokens q = 4 kb + i of row n
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = 4 * kb + i;
+        hs[q][wave * 16 + nl] = q < count ? swiglu16<BF16>(round16<BF16>(accg[i]), round16<BF16>(accu[i]),
+                                                           limit, fp32_swiglu != 0)
+                                          : static_cast<uint16_t>(0);
+    }
+    __syncthreads();
+    // Prepared h for the down projection: rows [n0, n0 + 64) are whole words
+    // and one whole 64-block of every position's h.
+    const int vpw_d = 32 / down_bits, wpw = kMfmaRows / vpw_d;
+    const int u = threadIdx.x, q = u / wpw, wd = u % wpw;
+    float2 part = make_float2(0.f, 0.f);
+    const bool mine = u < kMfmaTileTokens * wpw && q < count;
+    if (mine)
+        prep_unit_at<BF16>(down_bits, &hs[q][wd * vpw_d],
+                           hout.pairs + (first + q) * hout.pairs_stride +
+                               (n0 / vpw_d + wd) * pairs_per_word<BF16>(down_bits),
+                           &part);
+    for (int m = 1; m < wpw; m <<= 1) {
+        part.x += __shfl_xor(part.x, m, 64);
+        part.y += __shfl_xor(part.y, m, 64);
+    }
+    if (mine && wd == 0) hout.gsum[(first + q) * hout.gsum_stride + n0 / 64] = part;
+}
+
+template <int BITS, bool BF16>
+__global__ __launch_bounds__(64 * kMfmaWaves) void mfma_down_kernel(TileArgs ta, QProj down, QProj sdown,
+                                                                    MfmaVec hin, uint16_t *__restrict__ y) {
+    using G = MfmaGeom<BITS, BF16>;
+    constexpr int WPL = G::kWPL;
+    extern __shared__ __align__(16) float2 gsl[];
+    const int tile = blockIdx.y;
+    if (tile >= *ta.n_tiles) return;
+    const int slot = ta.tiles[4 * tile], first = ta.tiles[4 * tile + 1];
+    const int count = ta.tiles[4 * tile + 2];
+    const bool shared = slot == -2;
+    const QProj &p = shared ? sdown : down;
+    if (count <= 0 || count > kMfmaTileTokens ||
+        (!shared && (slot < 0 || slot >= p.n_slots || first < 0 || first + count > ta.R)))
+        return;
+    const int N = p.rows, K = p.cols, nblk = K / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nl = lane & 15, kb = lane >> 4;
+    const int n = blockIdx.x * kMfmaRows + wave * 16 + nl;
+    stage_gsum(gsl, hin, nblk, count, ta, shared, first, false);
+    const int sl = shared ? 0 : slot;
+    const int wpr = K / G::kVPW;
+    const int gpr = K / p.group, bpg = p.group / 64;
+    const int n0 = blockIdx.x * kMfmaRows;
+    const __amdgpu_buffer_rsrc_t ra_rs = make_rsrc(hin.pairs, static_cast<uint32_t>(4 * hin.pairs_stride * ta.n_vec));
+    const uint32_t a_off =
+        4u * static_cast<uint32_t>((first + min(nl, count - 1)) * hin.pairs_stride + kb * WPL * G::kNP);
+    const __amdgpu_buffer_rsrc_t w_rs =
+        make_rsrc(p.w + sl * p.w_slot + static_cast<int64_t>(n0) * wpr, 4u * kMfmaRows * wpr);
+    const uint32_t w_off = 4u * static_cast<uint32_t>((wave * 16 + nl) * wpr + kb * WPL);
+    uint16_t *meta = reinterpret_cast<uint16_t *>(gsl + nblk * kMfmaTileTokens);   // [blk][64][2]
+    {
+        const int64_t r0 = static_cast<int64_t>(n0) * gpr;
+        const uint16_t *const arr[2] = {p.s + sl * p.m_slot + r0, p.b + sl * p.m_slot + r0};
+        stage_meta<1>(meta, arr, gpr, bpg);
+    }
+    const uint32_t *lmeta = reinterpret_cast<const uint32_t *>(meta) + wave * 16 + nl;
+    __syncthreads();
+    const uint32_t magic_v = opaque_vgpr(G::P::kMagic);
+    mf32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    BlockW<WPL> w0[kMfmaDepth], w1[kMfmaDepth];
+    u32x4 a0[kMfmaDepth][2], a1[kMfmaDepth][2];
+    auto load_chunk = [&](BlockW<WPL>(&w)[kMfmaDepth], u32x4(&a)[kMfmaDepth][2], int c) {
+        const int b0 = min(c, nblk / kMfmaDepth - 1) * kMfmaDepth;
+#pragma unroll
+        for (int j = 0; j < kMfmaDepth; ++j) {
+            load_block_w<WPL>(w[j], w_rs, w_off, b0 + j);
+            load_block_a(a[j], ra_rs, a_off, b0 + j);
+        }
+    };
+    auto math_chunk = [&](const BlockW<WPL>(&w)[kMfmaDepth], const u32x4(&a)[kMfmaDepth][2], int c) {
+#pragma unroll
+        for (int j = 0; j < kMfmaDepth; ++j) {
+            const int blk = c * kMfmaDepth + j;
+            const uint32_t m = lmeta[blk * kMfmaRows];
+            const mf32x4_t d = block_mfma<BITS, BF16>(w[j], a[j], magic_v);
+            apply_block(acc, d, to_float<BF16>(static_cast<uint16_t>(m)),
+                        to_float<BF16>(static_cast<uint16_t>(m >> 16)), gsl + blk * kMfmaTileTokens, kb);
+        }
+    };
+    const int nchunks = nblk / kMfmaDepth;
+    load_chunk(w0, a0, 0);
+    for (int c = 0; c < nchunks; c += 2) {
+        load_chunk(w1, a1, c + 1);
+        sched_fence();
+        math_chunk(w0, a0, c);
+        sched_fence();
+        load_chunk(w0, a0, c + 2);
+        sched_fence();
+        math_chunk(w1, a1, c + 1);
+        sched_fence();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = 4 * kb + i;
+        if (q < count) y[static_cast<int64_t>(first + q) * N + n] = from_float<BF16>(acc[i]);
+    }
+}
+
+struct MfmaLaunch {
+    TileArgs ta;
+    QProj gate, up, down, sgate, sup, sdown;
+    MfmaVec xin, hmid;
+    uint16_t *y;
+    float limit;
+    int32_t fp32_swiglu;
+    int32_t max_tiles;
+    int32_t tokens, routes;
+};
+
+template <int BITS, bool BF16>
+hipError_t launch_mfma_stage(int which, const MfmaLaunch &L, hipStream_t st) {
+    if (which == 0) {   // prepare x for gate/up
+        const int words = L.gate.cols / MfmaGeom<BITS, BF16>::kVPW;
+        const int64_t threads = static_cast<int64_t>(L.tokens) * words;
+        hipLaunchKernelGGL((mfma_prep_kernel<BITS, BF16>), dim3((threads + 255) / 256), dim3(256), 0, st,
+                           L.ta.x, L.tokens, L.gate.cols, L.xin);
+    } else if (which == 1) {
+        TileArgs ta = L.ta;
+        ta.n_vec = L.tokens;
+        const size_t lds = sizeof(float2) * (L.gate.cols / 64) * kMfmaTileTokens +
+                           sizeof(uint16_t) * 4 * kMfmaRows * (L.gate.cols / 64);
+        dim3 grid(L.gate.rows / kMfmaRows, L.max_tiles);
+        hipLaunchKernelGGL((mfma_gateup_kernel<BITS, BF16>), grid, dim3(64 * kMfmaWaves), lds, st, ta,
+                           L.gate, L.up, L.sgate, L.sup, L.xin, L.hmid, L.down.bits, L.limit,
+                           L.fp32_swiglu);
+    } else {
+        TileArgs ta = L.ta;
+        ta.n_vec = L.routes;
+        const size_t lds = sizeof(float2) * (L.down.cols / 64) * kMfmaTileTokens +
+                           sizeof(uint16_t) * 2 * kMfmaRows * (L.down.cols / 64);
+        dim3 grid(L.down.rows / kMfmaRows, L.max_tiles);
+        hipLaunchKernelGGL((mfma_down_kernel<BITS, BF16>), grid, dim3(64 * kMfmaWaves), lds, st, ta,
+                           L.down, L.sdown, L.hmid, L.y);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace locali
