@@ -248,16 +248,21 @@ int check_decode_args(const locali_expert_arena *routed, const locali_expert_are
 
 // The matrix-core grouped path needs 2- or 4-bit codes (gate and up alike),
 // groups of a multiple of 64, rows in multiples of 64, columns in multiples
-// of 2 * 64 * kMfmaDepth holding a multiple of 8 groups, and its staged inputs
-// within 64 KiB of LDS; the
-// shared expert must match the routed one (they share prepared inputs).
-bool mfma_eligible(const locali_expert_arena *routed, const locali_expert_arena *shared) {
+// of kMfmaColsAlign holding a multiple of 8 groups, its staged inputs within
+// 64 KiB of LDS, and prepared inputs (2 bytes per value) below 2 GiB so that
+// its buffer offsets stay 31-bit; the shared expert must match the routed one
+// (they share prepared inputs).
+bool mfma_eligible(const locali_expert_arena *routed, const locali_expert_arena *shared, int64_t tokens,
+                   int64_t routes) {
+    if (2 * tokens * routed->gate.cols >= (int64_t{1} << 31) ||
+        2 * routes * routed->down.cols >= (int64_t{1} << 31))
+        return false;
     auto ok = [](const locali_qproj &p) {
         const int gpr = p.cols / p.group_size;
         const size_t lds = sizeof(float2) * (p.cols / 64) * kMfmaTileTokens +
                            sizeof(uint16_t) * 4 * kMfmaRows * (p.cols / 64);
         return (p.bits == 2 || p.bits == 4) && p.group_size % 64 == 0 && p.rows % kMfmaRows == 0 &&
-               p.cols % (128 * kMfmaDepth) == 0 && gpr % 8 == 0 && lds <= 64 * 1024;
+               p.cols % kMfmaColsAlign == 0 && gpr % 8 == 0 && lds <= 64 * 1024;
     };
     if (!ok(routed->gate) || !ok(routed->up) || !ok(routed->down)) return false;
     if (routed->gate.bits != routed->up.bits) return false;
@@ -322,7 +327,7 @@ int run_grouped(const locali_expert_arena *routed, const locali_expert_arena *sh
                 int32_t x_dtype, int32_t tokens, int32_t top_k, int32_t n_experts,
                 const int32_t *route_slot, const float *weights, float limit, int32_t fp32_swiglu,
                 int32_t combine_mode, void *out, void *ws, const Layout &lay, hipStream_t st) {
-    if (mfma_eligible(routed, shared))
+    if (mfma_eligible(routed, shared, tokens, static_cast<int64_t>(tokens) * (top_k + (shared ? 1 : 0))))
         return run_grouped_mfma(routed, shared, x, x_dtype, tokens, top_k, n_experts, route_slot, weights, limit,
                                 fp32_swiglu, combine_mode, out, ws, lay, st);
     const int R = tokens * top_k;

@@ -9,6 +9,10 @@
 //     WPL whole 32-bit words of every 64-value block of row n and expands them
 //     with one v_bitop3_b32 per pair into 16-bit floats magic + q * 4^j (fp16:
 //     the magic removed exactly by one packed add) -- 8 values per MFMA step.
+//     The words arrive by one 16-byte load per lane and projection (the four
+//     k-lanes of a row read 64 contiguous bytes = 4 / WPL blocks) and are
+//     transposed across the k-lanes with v_permlane16/32_swap so that each
+//     lane again holds its WPL words of every block of the chunk.
 //   A operand (activations): the same lane reads the matching prepared pairs
 //     (x pre-scaled by 4^-j, see qgemv.hpp) of token m = lane % 16, so A and B
 //     agree on every k slot whatever order the words put the codes in.
@@ -23,8 +27,8 @@
 //                        workgroup owns whole 64-value blocks of h)
 //   mfma_down_kernel     y[pos] = round(down(h[pos]))
 // Weights of a slot are streamed once per tile of 16 tokens; each wave keeps
-// the next chunk of kMfmaDepth blocks (words and activations) in flight while
-// it works on the current one.
+// the next chunk (one 16-byte weight load per projection and the matching
+// activations) in flight while it works on the current one.
 #pragma once
 
 #include "grouped_kernels.hpp"
@@ -34,7 +38,7 @@ namespace locali {
 constexpr int kMfmaTileTokens = 16;
 constexpr int kMfmaWaves = 4;
 constexpr int kMfmaRows = 16 * kMfmaWaves;
-constexpr int kMfmaDepth = 4;   // 64-value blocks in flight per wave
+constexpr int kMfmaColsAlign = 512;   // cols: a whole number of chunk pairs at 2 and 4 bits
 
 typedef float mf32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 mbf16x8_t __attribute__((ext_vector_type(8)));
@@ -66,6 +70,7 @@ struct MfmaGeom {
     static constexpr int kVPW = 32 / BITS;       // values per word
     static constexpr int kW64 = 64 / kVPW;       // words per 64-value block
     static constexpr int kWPL = kW64 / 4;        // words per lane per block
+    static constexpr int kCB = 4 / kWPL;         // blocks per 16-byte load (a chunk)
     static_assert(kWPL * kNP == 8, "one block = two MFMA steps of 4 pairs per lane");
 };
 
@@ -107,13 +112,44 @@ struct BlockW {
     uint32_t w[WPL];
 };
 
+// A 16-byte load gives k-lane kb the words [4 kb, 4 kb + 4) of the row's 64
+// bytes; after the transpose k-lane kb holds words [kb * WPL, (kb + 1) * WPL)
+// of each of the 4 / WPL blocks, block j in x[j * WPL + i]. v_permlane32_swap
+// exchanges k-lanes {2, 3} of its first operand with k-lanes {0, 1} of its
+// second, v_permlane16_swap k-lanes {1, 3} of the first with {0, 2} of the
+// second: for one word per block the 4 x 4 transpose is the 32-swap of the
+// register pairs (0, 2), (1, 3) and then the 16-swap of (0, 1), (2, 3); for
+// two words per block the 2 x 2 transpose of word pairs is the 16-swap of
+// (0, 2), (1, 3) and then the 32-swap of the same pairs.
 template <int WPL>
-__device__ __forceinline__ void load_block_w(BlockW<WPL> &o, __amdgpu_buffer_rsrc_t rsrc, uint32_t voff,
-                                             int blk) {
-#pragma unroll
-    for (int i = 0; i < WPL; ++i)
-        o.w[i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff + 4u * i, blk * 16 * WPL, kAuxStream);
+__device__ __forceinline__ void transpose_words(u32x4 &x) {
+    if constexpr (WPL == 1) {
+        const auto a = __builtin_amdgcn_permlane32_swap(x[0], x[2], false, false);
+        const auto b = __builtin_amdgcn_permlane32_swap(x[1], x[3], false, false);
+        const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+        const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+        x = u32x4{c[0], c[1], d[0], d[1]};
+    } else {
+        static_assert(WPL == 2, "2- and 4-bit words");
+        const auto a = __builtin_amdgcn_permlane16_swap(x[0], x[2], false, false);
+        const auto b = __builtin_amdgcn_permlane16_swap(x[1], x[3], false, false);
+        const auto c = __builtin_amdgcn_permlane32_swap(a[0], a[1], false, false);
+        const auto d = __builtin_amdgcn_permlane32_swap(b[0], b[1], false, false);
+        x = u32x4{c[0], d[0], c[1], d[1]};
+    }
 }
+
+template <int WPL>
+__device__ __forceinline__ BlockW<WPL> block_words(const u32x4 &x, int j) {
+    BlockW<WPL> o;
+#pragma unroll
+    for (int i = 0; i < WPL; ++i) o.w[i] = x[j * WPL + i];
+    return o;
+}
+
+// Offsets at or above 2^31 are outside every buffer here: such a load reads
+// zero without touching memory (the pipeline's loads past the last chunk).
+constexpr uint32_t kPastEnd = 0x80000000u;
 
 __device__ __forceinline__ void load_block_a(u32x4 (&a)[2], __amdgpu_buffer_rsrc_t rsrc, uint32_t voff,
                                              int blk) {
@@ -154,12 +190,6 @@ __device__ __forceinline__ void stage_meta(uint16_t *meta, const uint16_t *const
             }
         }
     }
-}
-
-__device__ __forceinline__ void load_block_a(u32x4 (&a)[2], const uint32_t *__restrict__ ap, int blk) {
-    const u32x4 *p = reinterpret_cast<const u32x4 *>(ap + blk * 32);
-    a[0] = p[0];
-    a[1] = p[1];
 }
 
 // Two MFMA steps of one block for one projection, from zero.
@@ -218,12 +248,10 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void mfma_gateup_kernel(
     if (count <= 0 || count > kMfmaTileTokens ||
         (!shared && (slot < 0 || slot >= pg.n_slots || first < 0 || first + count > ta.R)))
         return;
-    const int N = pg.rows, K = pg.cols, nblk = K / 64;
+    const int K = pg.cols, nblk = K / 64;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nl = lane & 15, kb = lane >> 4;
     const int n0 = blockIdx.x * kMfmaRows;
-    const int n = n0 + wave * 16 + nl;
-    stage_gsum(gsl, xin, nblk, count, ta, shared, first, true);
     const int sl = shared ? 0 : slot;
     const int wpr = K / G::kVPW;
     const int gpr = K / pg.group, bpg = pg.group / 64;
@@ -234,7 +262,24 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void mfma_gateup_kernel(
     const uint32_t wbytes = 4u * kMfmaRows * wpr;
     const __amdgpu_buffer_rsrc_t gw_rs = make_rsrc(pg.w + sl * pg.w_slot + static_cast<int64_t>(n0) * wpr, wbytes);
     const __amdgpu_buffer_rsrc_t uw_rs = make_rsrc(pu.w + sl * pu.w_slot + static_cast<int64_t>(n0) * wpr, wbytes);
-    const uint32_t w_off = 4u * static_cast<uint32_t>((wave * 16 + nl) * wpr + kb * WPL);
+    const uint32_t w_off = 4u * static_cast<uint32_t>((wave * 16 + nl) * wpr) + 16u * kb;
+    // Two chunks alternate: the loads of chunk c + 1 are issued before the
+    // math of chunk c, and scheduling barriers keep the compiler from sinking
+    // them behind it. Chunk 0 is issued before the staging below.
+    constexpr int CB = G::kCB;
+    const int nchunks = nblk / CB;   // even
+    u32x4 g0, u0, g1, u1;
+    u32x4 a0[CB][2], a1[CB][2];
+    auto load_chunk = [&](u32x4 &g, u32x4 &u, u32x4(&a)[CB][2], int c) {
+        const uint32_t past = c < nchunks ? 0u : kPastEnd;
+        g = __builtin_amdgcn_raw_buffer_load_b128(gw_rs, w_off | past, c * 64, kAuxStream);
+        u = __builtin_amdgcn_raw_buffer_load_b128(uw_rs, w_off | past, c * 64, kAuxStream);
+#pragma unroll
+        for (int j = 0; j < CB; ++j) load_block_a(a[j], ra_rs, a_off | past, c * CB + j);
+    };
+    load_chunk(g0, u0, a0, 0);
+    sched_fence();
+    stage_gsum(gsl, xin, nblk, count, ta, shared, first, true);
     uint16_t *meta = reinterpret_cast<uint16_t *>(gsl + nblk * kMfmaTileTokens);   // [blk][64][4]
     {
         const int64_t r0 = static_cast<int64_t>(n0) * gpr;
@@ -246,29 +291,15 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void mfma_gateup_kernel(
     __syncthreads();
     const uint32_t magic_v = opaque_vgpr(G::P::kMagic);
     mf32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
-    // Two chunks of kMfmaDepth blocks alternate: the loads of chunk c + 1 are
-    // issued before the math of chunk c, and scheduling barriers keep the
-    // compiler from sinking them behind it (nblk is a multiple of 2 chunks).
-    BlockW<WPL> g0[kMfmaDepth], u0[kMfmaDepth], g1[kMfmaDepth], u1[kMfmaDepth];
-    u32x4 a0[kMfmaDepth][2], a1[kMfmaDepth][2];
-    auto load_chunk = [&](BlockW<WPL>(&g)[kMfmaDepth], BlockW<WPL>(&u)[kMfmaDepth],
-                          u32x4(&a)[kMfmaDepth][2], int c) {
-        const int b0 = min(c, nblk / kMfmaDepth - 1) * kMfmaDepth;
+    auto math_chunk = [&](u32x4 g, u32x4 u, const u32x4(&a)[CB][2], int c) {
+        transpose_words<WPL>(g);
+        transpose_words<WPL>(u);
 #pragma unroll
-        for (int j = 0; j < kMfmaDepth; ++j) {
-            load_block_w<WPL>(g[j], gw_rs, w_off, b0 + j);
-            load_block_w<WPL>(u[j], uw_rs, w_off, b0 + j);
-            load_block_a(a[j], ra_rs, a_off, b0 + j);
-        }
-    };
-    auto math_chunk = [&](const BlockW<WPL>(&g)[kMfmaDepth], const BlockW<WPL>(&u)[kMfmaDepth],
-                          const u32x4(&a)[kMfmaDepth][2], int c) {
-#pragma unroll
-        for (int j = 0; j < kMfmaDepth; ++j) {
-            const int blk = c * kMfmaDepth + j;
+        for (int j = 0; j < CB; ++j) {
+            const int blk = c * CB + j;
             const uint2 m = lmeta[blk * kMfmaRows];
-            const mf32x4_t dg = block_mfma<BITS, BF16>(g[j], a[j], magic_v);
-            const mf32x4_t du = block_mfma<BITS, BF16>(u[j], a[j], magic_v);
+            const mf32x4_t dg = block_mfma<BITS, BF16>(block_words<WPL>(g, j), a[j], magic_v);
+            const mf32x4_t du = block_mfma<BITS, BF16>(block_words<WPL>(u, j), a[j], magic_v);
             const float2 *gb_lds = gsl + blk * kMfmaTileTokens;
             apply_block(accg, dg, to_float<BF16>(static_cast<uint16_t>(m.x)),
                         to_float<BF16>(static_cast<uint16_t>(m.x >> 16)), gb_lds, kb);
@@ -276,8 +307,6 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void mfma_gateup_kernel(
                         to_float<BF16>(static_cast<uint16_t>(m.y >> 16)), gb_lds, kb);
         }
     };
-    const int nchunks = nblk / kMfmaDepth;
-    load_chunk(g0, u0, a0, 0);
     for (int c = 0; c < nchunks; c += 2) {
         load_chunk(g1, u1, a1, c + 1);
         sched_fence();
@@ -334,7 +363,6 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void mfma_down_kernel(TileArgs ta,
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nl = lane & 15, kb = lane >> 4;
     const int n = blockIdx.x * kMfmaRows + wave * 16 + nl;
-    stage_gsum(gsl, hin, nblk, count, ta, shared, first, false);
     const int sl = shared ? 0 : slot;
     const int wpr = K / G::kVPW;
     const int gpr = K / p.group, bpg = p.group / 64;
@@ -344,7 +372,20 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void mfma_down_kernel(TileArgs ta,
         4u * static_cast<uint32_t>((first + min(nl, count - 1)) * hin.pairs_stride + kb * WPL * G::kNP);
     const __amdgpu_buffer_rsrc_t w_rs =
         make_rsrc(p.w + sl * p.w_slot + static_cast<int64_t>(n0) * wpr, 4u * kMfmaRows * wpr);
-    const uint32_t w_off = 4u * static_cast<uint32_t>((wave * 16 + nl) * wpr + kb * WPL);
+    const uint32_t w_off = 4u * static_cast<uint32_t>((wave * 16 + nl) * wpr) + 16u * kb;
+    constexpr int CB = G::kCB;
+    const int nchunks = nblk / CB;   // even
+    u32x4 w0, w1;
+    u32x4 a0[CB][2], a1[CB][2];
+    auto load_chunk = [&](u32x4 &w, u32x4(&a)[CB][2], int c) {
+        const uint32_t past = c < nchunks ? 0u : kPastEnd;
+        w = __builtin_amdgcn_raw_buffer_load_b128(w_rs, w_off | past, c * 64, kAuxStream);
+#pragma unroll
+        for (int j = 0; j < CB; ++j) load_block_a(a[j], ra_rs, a_off | past, c * CB + j);
+    };
+    load_chunk(w0, a0, 0);
+    sched_fence();
+    stage_gsum(gsl, hin, nblk, count, ta, shared, first, false);
     uint16_t *meta = reinterpret_cast<uint16_t *>(gsl + nblk * kMfmaTileTokens);   // [blk][64][2]
     {
         const int64_t r0 = static_cast<int64_t>(n0) * gpr;
@@ -355,28 +396,17 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void mfma_down_kernel(TileArgs ta,
     __syncthreads();
     const uint32_t magic_v = opaque_vgpr(G::P::kMagic);
     mf32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    BlockW<WPL> w0[kMfmaDepth], w1[kMfmaDepth];
-    u32x4 a0[kMfmaDepth][2], a1[kMfmaDepth][2];
-    auto load_chunk = [&](BlockW<WPL>(&w)[kMfmaDepth], u32x4(&a)[kMfmaDepth][2], int c) {
-        const int b0 = min(c, nblk / kMfmaDepth - 1) * kMfmaDepth;
+    auto math_chunk = [&](u32x4 w, const u32x4(&a)[CB][2], int c) {
+        transpose_words<WPL>(w);
 #pragma unroll
-        for (int j = 0; j < kMfmaDepth; ++j) {
-            load_block_w<WPL>(w[j], w_rs, w_off, b0 + j);
-            load_block_a(a[j], ra_rs, a_off, b0 + j);
-        }
-    };
-    auto math_chunk = [&](const BlockW<WPL>(&w)[kMfmaDepth], const u32x4(&a)[kMfmaDepth][2], int c) {
-#pragma unroll
-        for (int j = 0; j < kMfmaDepth; ++j) {
-            const int blk = c * kMfmaDepth + j;
+        for (int j = 0; j < CB; ++j) {
+            const int blk = c * CB + j;
             const uint32_t m = lmeta[blk * kMfmaRows];
-            const mf32x4_t d = block_mfma<BITS, BF16>(w[j], a[j], magic_v);
+            const mf32x4_t d = block_mfma<BITS, BF16>(block_words<WPL>(w, j), a[j], magic_v);
             apply_block(acc, d, to_float<BF16>(static_cast<uint16_t>(m)),
                         to_float<BF16>(static_cast<uint16_t>(m >> 16)), gsl + blk * kMfmaTileTokens, kb);
         }
     };
-    const int nchunks = nblk / kMfmaDepth;
-    load_chunk(w0, a0, 0);
     for (int c = 0; c < nchunks; c += 2) {
         load_chunk(w1, a1, c + 1);
         sched_fence();
