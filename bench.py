@@ -17,7 +17,7 @@ Also reported:
                 WRITE_SIZE), each scaled by what the counter reads for a
                 reference kernel of known bytes -- a 256 MiB reduction and a
                 256 MiB fill (`--copy-calibration`) -- summarised by
-                `--summarize-pmc` into profiles/gateup_route_kernel_decode_traffic.json
+                `--summarize-pmc` into profiles/gateup_diag_kernel_decode_traffic.json
   prefill64     64-token prefill on the same layer with Zipf(1.1) expert
                 popularity (grouped path), tokens/s and algorithmic GB/s
   cpu_baseline  the C oracle (oracle/expert_ref.c, OpenMP) on the host cores
@@ -46,8 +46,8 @@ from locali_amd import ops, synth  # noqa: E402
 
 METRIC = "MoE-layer tokens/s at 1 GPU (decode & 64-tok prefill); achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = ROOT / "profiles" / "gateup_route_kernel_decode_traffic.json"
-GATEUP_KERNEL = "gateup_route_kernel<2, true, 1, 64, 1, 8>"
+TRAFFIC_FILE = ROOT / "profiles" / "gateup_diag_kernel_decode_traffic.json"
+GATEUP_KERNEL = "gateup_diag_kernel<2, true>"
 COPY_BYTES = 256 << 20
 D, E, DFF, K_TOP, GROUP, BITS = 4096, 256, 2048, 6, 64, 2
 
@@ -361,7 +361,7 @@ def main(argv=None):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gateup_route_kernel (decode gate/up + clamped SwiGLU, 7 routes)",
+            "kernel": "gateup_diag_kernel (decode gate/up + clamped SwiGLU on the matrix cores, 7 routes)",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

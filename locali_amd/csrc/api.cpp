@@ -199,7 +199,7 @@ PrepVec prep_batch(void *base, int n_vec, int K, int bits, bool bf16) {
 int run_decode(const locali_expert_arena *routed, const locali_expert_arena *shared, const void *x,
                int32_t x_dtype, int32_t tokens, int32_t top_k, const int32_t *route_slot,
                const float *weights, float limit, int32_t fp32_swiglu, int32_t combine_mode,
-               void *hidden, void *out, hipStream_t st, int stages, void *h_prep_base) {
+               void *hidden, void *out, hipStream_t st, int stages, void *ws, const Layout &lay) {
     DecodeLaunch L{};
     L.ra.x = static_cast<const uint16_t *>(x);
     L.ra.route_slot = route_slot;
@@ -222,7 +222,7 @@ int run_decode(const locali_expert_arena *routed, const locali_expert_arena *sha
     L.ca.out = static_cast<uint16_t *>(out);
     L.ca.mode = combine_mode;
     const bool bf16 = x_dtype == LOCALI_DT_BF16;
-    L.hprep = prep_batch(h_prep_base, L.routes, routed->down.cols, routed->down.bits, bf16);
+    L.hprep = prep_batch(at<void>(ws, lay.hprep), L.routes, routed->down.cols, routed->down.bits, bf16);
     hipError_t e;
     if ((stages & 1) && (e = launch_gateup_decode(L, st)) != hipSuccess)
         return hip_fail(e, "gate/up decode launch");
@@ -480,7 +480,7 @@ int locali_moe_expert_decode(const locali_expert_arena *routed, const locali_exp
     Layout lay;
     if ((rc = decode_workspace(routed, shared, tokens, top_k, workspace_bytes, workspace, &lay))) return rc;
     return run_decode(routed, shared, x, x_dtype, tokens, top_k, route_slot, weights, swiglu_limit,
-                      fp32_swiglu, combine_mode, hidden, out, S(stream), 3, at<void>(workspace, lay.hprep));
+                      fp32_swiglu, combine_mode, hidden, out, S(stream), 3, workspace, lay);
 }
 
 int locali_moe_decode_gateup(const locali_expert_arena *routed, const locali_expert_arena *shared,
@@ -495,7 +495,7 @@ int locali_moe_decode_gateup(const locali_expert_arena *routed, const locali_exp
     if ((rc = decode_workspace(routed, shared, tokens, top_k, workspace_bytes, workspace, &lay))) return rc;
     return run_decode(routed, shared, x, x_dtype, tokens, top_k, route_slot, nullptr, swiglu_limit,
                       fp32_swiglu, LOCALI_COMBINE_ROUNDED, hidden, nullptr, S(stream), 1,
-                      at<void>(workspace, lay.hprep));
+                      workspace, lay);
 }
 
 int locali_moe_decode_down_combine(const locali_expert_arena *routed,
@@ -510,7 +510,7 @@ int locali_moe_decode_down_combine(const locali_expert_arena *routed,
     if ((rc = decode_workspace(routed, shared, tokens, top_k, workspace_bytes, workspace, &lay))) return rc;
     return run_decode(routed, shared, nullptr, x_dtype, tokens, top_k, route_slot, weights, 0.f, 0,
                       combine_mode, at<void>(workspace, lay.hidden), out, S(stream), 2,
-                      at<void>(workspace, lay.hprep));
+                      workspace, lay);
 }
 
 int locali_moe_expert_grouped(const locali_expert_arena *routed, const locali_expert_arena *shared,
@@ -587,7 +587,7 @@ int locali_moe_forward(const locali_router *router, const locali_expert_arena *r
     if (decode)
         return run_decode(routed, shared, x, x_dtype, tokens, k, route_slot, weights, swiglu_limit,
                           fp32_swiglu, LOCALI_COMBINE_ROUNDED, at<void>(workspace, lay.hidden), out,
-                          S(stream), 3, at<void>(workspace, lay.hprep));
+                          S(stream), 3, workspace, lay);
     return run_grouped(routed, shared, x, x_dtype, tokens, k, E, route_slot, weights, swiglu_limit,
                        fp32_swiglu, LOCALI_COMBINE_ROUNDED, out, workspace, lay, S(stream));
 }

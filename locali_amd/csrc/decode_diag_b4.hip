@@ -1,0 +1,11 @@
+// Matrix-core decode gate/up kernel instantiated for 4-bit codes (bf16 and
+// fp16 activations).
+#include "mfma_decode.hpp"
+
+namespace locali {
+
+hipError_t decode_diag_b4(const DecodeLaunch &L, hipStream_t st) {
+    return L.bf16 ? launch_gateup_diag<4, true>(L, st) : launch_gateup_diag<4, false>(L, st);
+}
+
+}  // namespace locali

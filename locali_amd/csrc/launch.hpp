@@ -32,6 +32,16 @@ struct PrepVec {
     int64_t pairs_stride, parts_stride;
 };
 
+// Prepared inputs of the matrix-core kernels, one vector per token or
+// position: pairs [words * P] u32 (P pairs per word, as the decode layout) and
+// gsum [K / span] float2 = (magic * sum of pre-scaled values, sum of values)
+// per span of 64 values (32 for the decode path's hidden vectors).
+struct MfmaVec {
+    uint32_t *pairs;
+    float2 *gsum;
+    int64_t pairs_stride, gsum_stride;
+};
+
 // ---- decode path -----------------------------------------------------------
 struct DecodeLaunch {
     RouteArgs ra;
@@ -50,6 +60,27 @@ hipError_t launch_gateup_decode(const DecodeLaunch &L, hipStream_t st);
 hipError_t launch_down_combine_decode(const DecodeLaunch &L, hipStream_t st);
 int chunks_per_row(const QProj &p);
 int group_parts(const QProj &p);
+
+// Matrix-core decode gate/up kernel (mfma_decode.hpp): one wave per
+// 512-value window of K and 16-row tile, workgroups of 2 tiles and K / 512
+// waves. It takes 2- or 4-bit codes (gate and up alike) with groups of 64, K
+// a multiple of 512 and at most 4096, d_ff a multiple of 32, and a down
+// projection of 2 or 4 bits (its epilogue prepares whole words of the down
+// input, the decode layout the down kernel reads). The shared expert has the
+// routed experts' shapes and quantisation.
+constexpr int kDiagWindow = 512;
+constexpr int kDiagGateUpTiles = 2;
+constexpr int kDiagGateUpMaxWaves = 8;
+
+inline bool gateup_diag_eligible(const DecodeLaunch &L) {
+    auto ok = [](const QProj &p) {
+        return (p.bits == 2 || p.bits == 4) && p.group == 64 && p.cols % kDiagWindow == 0;
+    };
+    return ok(L.gate) && ok(L.up) && L.gate.bits == L.up.bits && (L.down.bits == 2 || L.down.bits == 4) &&
+           L.gate.cols / kDiagWindow <= kDiagGateUpMaxWaves && L.gate.rows % (16 * kDiagGateUpTiles) == 0;
+}
+hipError_t decode_diag_b2(const DecodeLaunch &L, hipStream_t st);
+hipError_t decode_diag_b4(const DecodeLaunch &L, hipStream_t st);
 
 // ---- router ------------------------------------------------------------------
 struct RouterLaunch {

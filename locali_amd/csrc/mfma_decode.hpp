@@ -1,0 +1,307 @@
+// Decode-path gate/up kernel on the matrix cores (one token per route).
+//
+// A wave owns 16 output rows (a row tile) and a 512-value window of K. Its
+// weight loads cover whole 128-byte lines: in one 16-byte load, lane (n =
+// lane % 16, kb = lane / 16) reads "unit" 4 h + kb (h = n / 8) of the line of
+// row 8 i + n % 8, so 8 lanes read a row's line and one load covers 8 rows.
+// A unit is 16 bytes of codes: one 64-value block at 2 bits, half a block at
+// 4 bits. Every MFMA step (v_mfma_f32_16x16x32) takes 8 values of the lane's
+// unit from each k-lane; the A operand is "diagonal": A[m][k] holds x' of
+// k-lane kb(k)'s unit 4 h + kb only in rows m with m / 4 == kb and
+// (m / 2) % 2 == h, zero elsewhere, so D[4 kb + 2 h][n] is exactly the dot of
+// lane (n, kb)'s unit with x -- the product keeps the units apart and every
+// lane receives its own unit's dot. The per-unit affine terms
+//   acc += s * (D - magic * sum x') + b * sum x        (dsv4_kernels.py:75-79)
+// are one instruction each for 64 (row, unit) pairs, and the units of a row
+// meet by three cross-lane adds. The zero rows of A come from a zeroed LDS
+// slot read by the off-diagonal lanes, so building A costs LDS reads, not
+// VALU; the VALU is left with the dequant (one v_bitop3_b32 per value pair)
+// and the matrix core does every product.
+//
+//   gateup_diag_kernel  h[r, n] = swiglu(up_r(x_t)[n], gate_r(x_t)[n]): a
+//                       workgroup is 32 rows of one route, one wave per
+//                       window of K (K / 512 waves). Each wave prepares its
+//                       window of x into its own LDS slice while the weights
+//                       stream in; the workgroup's scales and biases arrive
+//                       by whole lines into LDS; the windows meet in LDS in
+//                       window order. The epilogue writes h and its prepared
+//                       form (pairs and per-word sums, the decode layout: the
+//                       workgroup owns whole words of the down input).
+// The down projection and combine of the decode path stay on the VALU
+// kernel (decode_kernels.hpp), which reads the same hidden layout.
+// Reference arithmetic: dsv4_arena.py:168-235 (expert).
+#pragma once
+
+#include "decode_kernels.hpp"
+#include "mfma_grouped.hpp"
+
+namespace locali {
+
+template <int BITS>
+struct DiagGeom {
+    static constexpr int kUnitVals = 128 / BITS;            // values per 16-byte unit
+    static constexpr int kUnits = kDiagWindow / kUnitVals;  // units per window row (8 or 16)
+    static constexpr int kLines = kUnits / 8;               // 128-byte lines per window row
+    static constexpr int kSteps = kUnitVals / 8;            // MFMA steps per unit
+    static constexpr int kUnitPairs = kUnitVals / 2;        // prepared pairs per unit
+    static constexpr int kStride = 4 * kUnitPairs + 16;     // LDS bytes per unit (padded)
+    static constexpr int kUnitsPerGroup = 64 / kUnitVals;   // group 64
+    static_assert(BITS == 2 || BITS == 4, "2- and 4-bit codes");
+};
+
+// One window of a prepared vector in LDS: unit u's pairs at u * kStride
+// (padding spreads the eight units one step reads over distinct banks), then
+// a zeroed slot for the off-diagonal lanes, then the per-unit sums
+// (magic * sum x', sum x).
+template <int BITS>
+struct DiagSlice {
+    using G = DiagGeom<BITS>;
+    uint8_t pairs[G::kUnits * G::kStride];
+    uint32_t zero[4 * G::kSteps];
+    float2 usum[G::kUnits];
+};
+
+// Raw values of the lane's word of a window (lanes past the window's words
+// read the last word again; their values are not used).
+template <int BITS>
+__device__ __forceinline__ void diag_prep_load(uint32_t (&ww)[16 / BITS], const uint16_t *win_src, int lane) {
+    constexpr int VPW = 32 / BITS, WORDS = kDiagWindow / VPW;
+    const uint4 *p = reinterpret_cast<const uint4 *>(win_src + min(lane, WORDS - 1) * VPW);
+    if constexpr (BITS == 2) {
+        const uint4 a = p[0], c = p[1];
+        ww[0] = a.x; ww[1] = a.y; ww[2] = a.z; ww[3] = a.w;
+        ww[4] = c.x; ww[5] = c.y; ww[6] = c.z; ww[7] = c.w;
+    } else {
+        const uint4 a = p[0];
+        ww[0] = a.x; ww[1] = a.y; ww[2] = a.z; ww[3] = a.w;
+    }
+}
+
+// Prepares the wave's window (a word per lane; 2-bit: lanes 0-31) into its
+// slice; the words of a unit are consecutive lanes, so the unit sums meet by
+// butterfly. The slice is the wave's own: its LDS writes are ordered before
+// its later reads without a workgroup barrier.
+template <int BITS, bool BF16>
+__device__ __forceinline__ void diag_prep_store(DiagSlice<BITS> &sl, const uint32_t (&ww)[16 / BITS], int lane) {
+    using G = DiagGeom<BITS>;
+    using P = Pairs<BITS, BF16>;
+    constexpr int VPW = 32 / BITS, WORDS = kDiagWindow / VPW, WPU = G::kUnitVals / VPW;
+    float2 part = make_float2(0.f, 0.f);
+    const int u = lane / WPU, wu = lane % WPU;
+    if (lane < WORDS)
+        prep_vals<BITS, BF16>(ww, reinterpret_cast<uint32_t *>(sl.pairs + u * G::kStride) + wu * P::kCount, 1,
+                              part);
+#pragma unroll
+    for (int m = 1; m < WPU; m <<= 1) {
+        part.x += __shfl_xor(part.x, m, 64);
+        part.y += __shfl_xor(part.y, m, 64);
+    }
+    if (lane < WORDS && wu == 0) sl.usum[u] = part;
+    if (lane < 4 * G::kSteps) sl.zero[lane] = 0u;
+}
+
+// B operand of step t of the lane's unit (8 values: pairs 4 t .. 4 t + 3).
+template <int BITS, bool BF16, int T>
+__device__ __forceinline__ u32x4 diag_b(const u32x4 &unit, uint32_t magic_v) {
+    using P = Pairs<BITS, BF16>;
+    constexpr int word = (4 * T) / P::kCount, pb = (4 * T) % P::kCount;
+    const uint32_t w = unit[word];
+    return u32x4{expand_pair<BITS, BF16, pb>(w, magic_v), expand_pair<BITS, BF16, pb + 1>(w, magic_v),
+                 expand_pair<BITS, BF16, pb + 2>(w, magic_v), expand_pair<BITS, BF16, pb + 3>(w, magic_v)};
+}
+
+// Sum over the 8 lanes sharing a row: the k-lanes (lanes 16 apart) and the
+// two halves h of the row's line (lanes 8 apart). Every lane gets the same
+// bits.
+__device__ __forceinline__ float diag_row_sum(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+    // row_ror:8 -- lane n of each 16-lane row reads lane n +- 8
+    const float o = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+    return (threadIdx.x & 8) ? o + v : v + o;
+}
+
+// s * (d - cx) + b * xs with 16-bit s, b.
+template <bool BF16>
+__device__ __forceinline__ float diag_fix(float d, uint16_t s, uint16_t b, float2 g) {
+    return fmaf(to_float<BF16>(s), d - g.x, to_float<BF16>(b) * g.y);
+}
+
+// ---------------------------------------------------------------------------
+template <int BITS, bool BF16>
+__global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
+    RouteArgs ra, QProj gate, QProj up, QProj sgate, QProj sup, uint16_t *__restrict__ h,
+    PrepVec hout, int down_bits, float limit, int fp32_swiglu) {
+    using G = DiagGeom<BITS>;
+    constexpr int RT = kDiagGateUpTiles;
+    constexpr int NI = 2 * G::kLines;   // loads per (tile, projection): row halves x lines
+    __shared__ __align__(16) DiagSlice<BITS> win[kDiagGateUpMaxWaves];
+    __shared__ float red[kDiagGateUpMaxWaves][RT][2][16];
+    __shared__ __align__(16) uint16_t hs[16 * RT];
+    // scales and biases of the workgroup's rows: [gs, gb, us, ub][row][K / 64]
+    // u16, rows padded by 16 bytes
+    __shared__ __align__(16) uint8_t mlds[4 * 16 * RT * (2 * (4096 / 64) + 16)];
+    // wave index in an SGPR: it feeds the loads' scalar offsets
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nl = lane & 15, kb = lane >> 4, hh = nl >> 3, r8 = nl & 7;
+    const int r = blockIdx.y;
+    int token, slot;
+    bool shared;
+    route_of(ra, r, token, slot, shared);
+    // the route's projections, field by field (selecting whole parameter
+    // structs by reference would put them in scratch memory)
+    const int N = gate.rows, K = gate.cols;
+    const int n_slots = shared ? sgate.n_slots : gate.n_slots;
+    const uint32_t *gwp = shared ? sgate.w : gate.w, *uwp = shared ? sup.w : up.w;
+    const int64_t gw_slot = shared ? sgate.w_slot : gate.w_slot, uw_slot = shared ? sup.w_slot : up.w_slot;
+    const int64_t gm_slot = shared ? sgate.m_slot : gate.m_slot, um_slot = shared ? sup.m_slot : up.m_slot;
+    const int n0 = blockIdx.x * 16 * RT;
+    const bool valid_slot = slot >= 0 && slot < n_slots;
+    const int sl = valid_slot ? slot : 0;
+    const int wpr = K * BITS / 32, gpr = K / 64;
+    const int waves = blockDim.x >> 6;   // = K / 512
+
+    // Raw x of the window first (the prep waits only for it), then the
+    // workgroup's scales and biases by whole lines (thread i loads 16-byte
+    // pieces i and i + 64 * waves of the four arrays' rows), then the weights
+    // in consumption order.
+    uint32_t xw[16 / BITS];
+    diag_prep_load<BITS>(xw, ra.x + static_cast<int64_t>(token) * K + wave * kDiagWindow, lane);
+    sched_fence();
+    const int mrs = 2 * gpr + 16;   // LDS bytes per metadata row
+    const int64_t mrow0 = static_cast<int64_t>(n0) * gpr;
+    const uint16_t *m_gs = (shared ? sgate.s : gate.s) + sl * gm_slot + mrow0;
+    const uint16_t *m_gb = (shared ? sgate.b : gate.b) + sl * gm_slot + mrow0;
+    const uint16_t *m_us = (shared ? sup.s : up.s) + sl * um_slot + mrow0;
+    const uint16_t *m_ub = (shared ? sup.b : up.b) + sl * um_slot + mrow0;
+    u32x4 mv0, mv1;
+    int md0, md1;
+    auto meta_piece = [&](int c, u32x4 &v, int &dst) {
+        const int a = c / (16 * RT * waves), row = (c / waves) % (16 * RT), pc = c % waves;
+        const uint16_t *arr = a == 0 ? m_gs : a == 1 ? m_gb : a == 2 ? m_us : m_ub;
+        v = reinterpret_cast<const u32x4 *>(arr + static_cast<int64_t>(row) * gpr)[pc];
+        dst = (a * 16 * RT + row) * mrs + 16 * pc;
+    };
+    meta_piece(static_cast<int>(threadIdx.x), mv0, md0);
+    meta_piece(static_cast<int>(threadIdx.x) + 64 * waves, mv1, md1);
+    sched_fence();
+    const uint32_t wbytes = 4u * 16 * RT * wpr;
+    const int64_t wrow0 = static_cast<int64_t>(n0) * wpr;
+    const __amdgpu_buffer_rsrc_t gw_rs = make_rsrc(gwp + sl * gw_slot + wrow0, wbytes);
+    const __amdgpu_buffer_rsrc_t uw_rs = make_rsrc(uwp + sl * uw_slot + wrow0, wbytes);
+    // load q = 2 * line + i: row 8 i + n % 8 of the tile, unit 4 h + kb of the line
+    u32x4 wg[RT][NI], wu[RT][NI];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int q = 0; q < NI; ++q) {
+            const int i = q & 1, line = q >> 1;
+            const uint32_t wo = 4u * static_cast<uint32_t>((16 * rt + 8 * i + r8) * wpr) + 128u * line +
+                                16u * (4 * hh + kb);
+            wg[rt][q] = __builtin_amdgcn_raw_buffer_load_b128(gw_rs, wo, 128 * G::kLines * wave, kAuxStream);
+            wu[rt][q] = __builtin_amdgcn_raw_buffer_load_b128(uw_rs, wo, 128 * G::kLines * wave, kAuxStream);
+        }
+    sched_fence();
+    DiagSlice<BITS> &mw = win[wave];
+    diag_prep_store<BITS, BF16>(mw, xw, lane);
+    *reinterpret_cast<u32x4 *>(mlds + md0) = mv0;
+    *reinterpret_cast<u32x4 *>(mlds + md1) = mv1;
+    __syncthreads();
+    const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
+    // diagonal A: lane (m, kb) feeds unit 8 line + 4 ((m / 2) % 2) + kb when m / 4 == kb
+    const bool diag = (nl >> 2) == kb;
+    const int ah = (nl >> 1) & 1;
+    const int as = 16 * RT * mrs / 2;   // u16 between metadata arrays
+    float accg[RT][2], accu[RT][2];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) accg[rt][i] = accu[rt][i] = 0.f;
+#pragma unroll
+    for (int line = 0; line < G::kLines; ++line) {
+        const int uA = 8 * line + 4 * ah + kb;
+        const uint8_t *abase =
+            diag ? mw.pairs + uA * G::kStride : reinterpret_cast<const uint8_t *>(mw.zero);
+        mf32x4_t dg[RT][2], du[RT][2];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                dg[rt][i] = mf32x4_t{0.f, 0.f, 0.f, 0.f};
+                du[rt][i] = dg[rt][i];
+            }
+        static_for<0, G::kSteps>([&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            const u32x4 a = reinterpret_cast<const u32x4 *>(abase)[t];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    dg[rt][i] = mfma_16x16x32<BF16>(a, diag_b<BITS, BF16, t>(wg[rt][2 * line + i], magic_v),
+                                                    dg[rt][i]);
+                    du[rt][i] = mfma_16x16x32<BF16>(a, diag_b<BITS, BF16, t>(wu[rt][2 * line + i], magic_v),
+                                                    du[rt][i]);
+                }
+        });
+        // the lane's unit 4 h + kb of this line, rows 8 i + n % 8 of each tile
+        const int uB = 8 * line + 4 * hh + kb;
+        const float2 us = mw.usum[uB];
+        const int grp = (G::kUnits * wave + uB) / G::kUnitsPerGroup;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint16_t *m0 = reinterpret_cast<const uint16_t *>(mlds + (16 * rt + 8 * i + r8) * mrs) + grp;
+                accg[rt][i] += diag_fix<BF16>(hh ? dg[rt][i][2] : dg[rt][i][0], m0[0], m0[as], us);
+                accu[rt][i] += diag_fix<BF16>(hh ? du[rt][i][2] : du[rt][i][0], m0[2 * as], m0[3 * as], us);
+            }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float g = diag_row_sum(accg[rt][i]);
+            const float u = diag_row_sum(accu[rt][i]);
+            if (lane < 8) {
+                red[wave][rt][0][8 * i + lane] = g;
+                red[wave][rt][1][8 * i + lane] = u;
+            }
+        }
+    __syncthreads();
+    if (wave != 0) return;
+    // Wave 0: the 32 rows' h in window order, then h's prepared form (the
+    // rows are whole words of the down input and one half of a 64-block).
+    if (lane < 16 * RT) {
+        const int rt = lane >> 4, n = lane & 15;
+        float g = 0.f, u = 0.f;
+        for (int w = 0; w < waves; ++w) {
+            g += red[w][rt][0][n];
+            u += red[w][rt][1][n];
+        }
+        uint16_t out = 0;
+        if (valid_slot) out = swiglu16<BF16>(round16<BF16>(g), round16<BF16>(u), limit, fp32_swiglu != 0);
+        h[static_cast<int64_t>(r) * N + n0 + lane] = out;
+        hs[lane] = out;
+    }
+    const int vpw = 32 / down_bits, words = 16 * RT / vpw;
+    if (lane < words) {
+        const int unit = n0 / vpw + lane;
+        prep_unit_at<BF16>(down_bits, &hs[lane * vpw],
+                           hout.pairs + r * hout.pairs_stride + unit * pairs_per_word<BF16>(down_bits),
+                           hout.parts + r * hout.parts_stride + unit);
+    }
+}
+
+// Launch shape: one workgroup per (32 rows, route) with K / 512 waves.
+template <int BITS, bool BF16>
+hipError_t launch_gateup_diag(const DecodeLaunch &L, hipStream_t st) {
+    const int waves = L.gate.cols / kDiagWindow;
+    dim3 grid(L.gate.rows / (16 * kDiagGateUpTiles), L.routes);
+    hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16>), grid, dim3(64 * waves), 0, st, L.ra, L.gate, L.up,
+                       L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu);
+    return hipGetLastError();
+}
+
+}  // namespace locali

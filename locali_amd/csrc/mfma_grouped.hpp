@@ -54,15 +54,6 @@ __device__ __forceinline__ mf32x4_t mfma_16x16x32(u32x4 a, u32x4 b, mf32x4_t c) 
                                                        __builtin_bit_cast(mf16x8_t, b), c, 0, 0, 0);
 }
 
-// Prepared inputs of the MFMA kernels, one vector per token or position:
-// pairs [words * P] u32 (P pairs per word, as the decode layout) and
-// gsum [K / 64] float2 = (magic * sum of pre-scaled values, sum of values).
-struct MfmaVec {
-    uint32_t *pairs;
-    float2 *gsum;
-    int64_t pairs_stride, gsum_stride;
-};
-
 template <int BITS, bool BF16>
 struct MfmaGeom {
     using P = Pairs<BITS, BF16>;
