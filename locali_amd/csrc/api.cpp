@@ -195,11 +195,10 @@ PrepVec prep_batch(void *base, int n_vec, int K, int bits, bool bf16) {
     return v;
 }
 
-// stages: bit 0 = gate/up, bit 1 = down + combine.
-int run_decode(const locali_expert_arena *routed, const locali_expert_arena *shared, const void *x,
-               int32_t x_dtype, int32_t tokens, int32_t top_k, const int32_t *route_slot,
-               const float *weights, float limit, int32_t fp32_swiglu, int32_t combine_mode,
-               void *hidden, void *out, hipStream_t st, int stages, void *ws, const Layout &lay) {
+DecodeLaunch decode_launch(const locali_expert_arena *routed, const locali_expert_arena *shared, const void *x,
+                           int32_t x_dtype, int32_t tokens, int32_t top_k, const int32_t *route_slot,
+                           const float *weights, float limit, int32_t fp32_swiglu, int32_t combine_mode,
+                           void *hidden, void *out, void *ws, const Layout &lay) {
     DecodeLaunch L{};
     L.ra.x = static_cast<const uint16_t *>(x);
     L.ra.route_slot = route_slot;
@@ -223,6 +222,19 @@ int run_decode(const locali_expert_arena *routed, const locali_expert_arena *sha
     L.ca.mode = combine_mode;
     const bool bf16 = x_dtype == LOCALI_DT_BF16;
     L.hprep = prep_batch(at<void>(ws, lay.hprep), L.routes, routed->down.cols, routed->down.bits, bf16);
+    return L;
+}
+
+// stages: bit 0 = gate/up, bit 1 = down + combine. sel: the gate/up kernel
+// selects the routes itself (forward with a deferred selection).
+int run_decode(const locali_expert_arena *routed, const locali_expert_arena *shared, const void *x,
+               int32_t x_dtype, int32_t tokens, int32_t top_k, const int32_t *route_slot,
+               const float *weights, float limit, int32_t fp32_swiglu, int32_t combine_mode,
+               void *hidden, void *out, hipStream_t st, int stages, void *ws, const Layout &lay,
+               const RouterLaunch *sel = nullptr) {
+    DecodeLaunch L = decode_launch(routed, shared, x, x_dtype, tokens, top_k, route_slot, weights, limit,
+                                   fp32_swiglu, combine_mode, hidden, out, ws, lay);
+    L.sel = sel;
     hipError_t e;
     if ((stages & 1) && (e = launch_gateup_decode(L, st)) != hipSuccess)
         return hip_fail(e, "gate/up decode launch");
@@ -386,10 +398,13 @@ int check_router(const locali_router *r, int d) {
     return 0;
 }
 
+// Builds the router launch; with logits_only (and a decode-sized call whose
+// gate/up kernel selects on its own, router_select_fusable) only the logits
+// kernel is launched and `*launch` carries what that kernel needs.
 int route(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens, int32_t d_model,
           const int32_t *input_ids, const float *logits_in, const int32_t *slot_of_expert,
           int32_t n_slots, int32_t *idx, float *weights, int32_t *route_slot, void *workspace,
-          const Layout &lay, hipStream_t st) {
+          const Layout &lay, hipStream_t st, bool logits_only = false, RouterLaunch *launch = nullptr) {
     if (router->tid2eid && !input_ids) return fail(LOCALI_E_ARG, "router: hash routing needs input_ids");
     if (route_slot && (!slot_of_expert || n_slots < 1))
         return fail(LOCALI_E_ARG, "router: route_slot needs slot_of_expert and n_slots");
@@ -416,7 +431,9 @@ int route(const locali_router *router, const void *x, int32_t x_dtype, int32_t t
     L.route_slot = route_slot;
     L.logits = at<float>(workspace, lay.logits);
     L.logits_in = logits_in;
-    hipError_t e = launch_router(L, st);
+    if (launch) *launch = L;
+    if (logits_only && !router_select_fusable(L)) return fail(LOCALI_E_ARG, "router: selection cannot be deferred");
+    hipError_t e = launch_router(L, st, logits_only);
     if (e != hipSuccess) return hip_fail(e, "router launch");
     return 0;
 }
@@ -581,13 +598,27 @@ int locali_moe_forward(const locali_router *router, const locali_expert_arena *r
         return fail(LOCALI_E_WORKSPACE, "forward: workspace %zu < %zu bytes", workspace_bytes, lay.total);
     int32_t *route_slot = at<int32_t>(workspace, lay.route_slot);
     const bool decode = tokens <= kDecodeMaxTokens;
+    // Decode: the gate/up kernel selects each token's routes itself when it
+    // can, which saves the select kernel between the logits and the experts.
+    bool defer = false;
+    if (decode) {
+        RouterLaunch probe{};
+        probe.tokens = tokens;
+        probe.E = E;
+        probe.top_k = k;
+        const DecodeLaunch DL = decode_launch(routed, shared, x, x_dtype, tokens, k, route_slot, weights,
+                                              swiglu_limit, fp32_swiglu, LOCALI_COMBINE_ROUNDED,
+                                              at<void>(workspace, lay.hidden), out, workspace, lay);
+        defer = router_select_fusable(probe) && gateup_diag_eligible(DL);
+    }
+    RouterLaunch RL{};
     rc = route(router, x, x_dtype, tokens, d, input_ids, nullptr, slot_of_expert, routed->gate.n_slots,
-               idx, weights, route_slot, workspace, lay, S(stream));
+               idx, weights, route_slot, workspace, lay, S(stream), defer, &RL);
     if (rc) return rc;
     if (decode)
         return run_decode(routed, shared, x, x_dtype, tokens, k, route_slot, weights, swiglu_limit,
                           fp32_swiglu, LOCALI_COMBINE_ROUNDED, at<void>(workspace, lay.hidden), out,
-                          S(stream), 3, workspace, lay);
+                          S(stream), 3, workspace, lay, defer ? &RL : nullptr);
     return run_grouped(routed, shared, x, x_dtype, tokens, k, E, route_slot, weights, swiglu_limit,
                        fp32_swiglu, LOCALI_COMBINE_ROUNDED, out, workspace, lay, S(stream));
 }

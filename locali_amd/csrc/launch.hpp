@@ -42,6 +42,8 @@ struct MfmaVec {
     int64_t pairs_stride, gsum_stride;
 };
 
+struct RouterLaunch;
+
 // ---- decode path -----------------------------------------------------------
 struct DecodeLaunch {
     RouteArgs ra;
@@ -54,6 +56,10 @@ struct DecodeLaunch {
     float limit;
     int32_t fp32_swiglu;
     CombineArgs ca;
+    // non-null: the routes' slots and weights are not chosen yet; the gate/up
+    // kernel selects for its token from these logits and writes idx, weights
+    // and route_slot (ra.route_slot, ca.weights point at the latter two)
+    const RouterLaunch *sel;
 };
 
 hipError_t launch_gateup_decode(const DecodeLaunch &L, hipStream_t st);
@@ -105,7 +111,17 @@ struct RouterLaunch {
     const float *logits_in;     // optional precomputed logits [tokens, E]
 };
 
-hipError_t launch_router(const RouterLaunch &L, hipStream_t st);
+// logits_only: launch only the logits kernel of the decode (gemv) path and
+// leave the selection to the caller's kernel (router_select_fusable).
+hipError_t launch_router(const RouterLaunch &L, hipStream_t st, bool logits_only = false);
+
+// The decode gate/up kernel can select for its own token when the logits come
+// from the gemv path (few tokens, no precomputed logits) into one partial row
+// per token, and E <= 256.
+constexpr int kFusedSelectMaxTokens = 8;
+inline bool router_select_fusable(const RouterLaunch &L) {
+    return !L.logits_in && L.tokens <= kFusedSelectMaxTokens && L.E <= 256 && L.top_k <= 16;
+}
 
 // ---- grouped (prefill) path --------------------------------------------------
 struct GroupedLaunch {

@@ -34,6 +34,7 @@
 
 #include "decode_kernels.hpp"
 #include "mfma_grouped.hpp"
+#include "router_select.hpp"
 
 namespace locali {
 
@@ -130,10 +131,15 @@ __device__ __forceinline__ float diag_fix(float d, uint16_t s, uint16_t b, float
 }
 
 // ---------------------------------------------------------------------------
-template <int BITS, bool BF16>
+// SELECT: the routes' slots are not chosen yet -- wave 0 of each routed
+// workgroup runs the top-k selection of its token on `sel`'s logits (one
+// partial row per token, E <= 256) while the other waves prepare x, and the
+// workgroup (blockIdx.x 0, first route of the token) stores the token's
+// choices for the down kernel and the caller.
+template <int BITS, bool BF16, bool SELECT>
 __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     RouteArgs ra, QProj gate, QProj up, QProj sgate, QProj sup, uint16_t *__restrict__ h,
-    PrepVec hout, int down_bits, float limit, int fp32_swiglu) {
+    PrepVec hout, int down_bits, float limit, int fp32_swiglu, RouterLaunch sel) {
     using G = DiagGeom<BITS>;
     constexpr int RT = kDiagGateUpTiles;
     constexpr int NI = 2 * G::kLines;   // loads per (tile, projection): row halves x lines
@@ -149,7 +155,14 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     const int r = blockIdx.y;
     int token, slot;
     bool shared;
-    route_of(ra, r, token, slot, shared);
+    if constexpr (SELECT) {
+        const int routed = ra.tokens * ra.top_k;
+        shared = r >= routed;
+        token = shared ? r - routed : r / ra.top_k;
+        slot = 0;
+    } else {
+        route_of(ra, r, token, slot, shared);
+    }
     // the route's projections, field by field (selecting whole parameter
     // structs by reference would put them in scratch memory)
     const int N = gate.rows, K = gate.cols;
@@ -158,10 +171,9 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     const int64_t gw_slot = shared ? sgate.w_slot : gate.w_slot, uw_slot = shared ? sup.w_slot : up.w_slot;
     const int64_t gm_slot = shared ? sgate.m_slot : gate.m_slot, um_slot = shared ? sup.m_slot : up.m_slot;
     const int n0 = blockIdx.x * 16 * RT;
-    const bool valid_slot = slot >= 0 && slot < n_slots;
-    const int sl = valid_slot ? slot : 0;
     const int wpr = K * BITS / 32, gpr = K / 64;
     const int waves = blockDim.x >> 6;   // = K / 512
+    DiagSlice<BITS> &mw = win[wave];
 
     // Raw x of the window first (the prep waits only for it), then the
     // workgroup's scales and biases by whole lines (thread i loads 16-byte
@@ -170,6 +182,27 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     uint32_t xw[16 / BITS];
     diag_prep_load<BITS>(xw, ra.x + static_cast<int64_t>(token) * K + wave * kDiagWindow, lane);
     sched_fence();
+    if constexpr (SELECT) {
+        __shared__ float2 stage[256];
+        __shared__ int s_slot;
+        if (!shared) {   // uniform across the workgroup
+            if (wave == 0) {
+                const SelectOut o = select_token_any<1, 4>(sel, token, sel.logits + static_cast<int64_t>(token) * sel.E,
+                                                           0, stage);
+                const int j = r - token * ra.top_k;
+                const int sj = __builtin_amdgcn_readlane(o.slot, j);
+                if (lane == 0) s_slot = sj;
+                if (blockIdx.x == 0 && j == 0) select_store(sel, token, o);
+            }
+            diag_prep_store<BITS, BF16>(mw, xw, lane);
+            __syncthreads();
+            slot = s_slot;
+        } else {
+            diag_prep_store<BITS, BF16>(mw, xw, lane);
+        }
+    }
+    const bool valid_slot = slot >= 0 && slot < n_slots;
+    const int sl = valid_slot ? slot : 0;
     const int mrs = 2 * gpr + 16;   // LDS bytes per metadata row
     const int64_t mrow0 = static_cast<int64_t>(n0) * gpr;
     const uint16_t *m_gs = (shared ? sgate.s : gate.s) + sl * gm_slot + mrow0;
@@ -204,8 +237,7 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
             wu[rt][q] = __builtin_amdgcn_raw_buffer_load_b128(uw_rs, wo, 128 * G::kLines * wave, kAuxStream);
         }
     sched_fence();
-    DiagSlice<BITS> &mw = win[wave];
-    diag_prep_store<BITS, BF16>(mw, xw, lane);
+    if constexpr (!SELECT) diag_prep_store<BITS, BF16>(mw, xw, lane);
     *reinterpret_cast<u32x4 *>(mlds + md0) = mv0;
     *reinterpret_cast<u32x4 *>(mlds + md1) = mv1;
     __syncthreads();
@@ -299,8 +331,13 @@ template <int BITS, bool BF16>
 hipError_t launch_gateup_diag(const DecodeLaunch &L, hipStream_t st) {
     const int waves = L.gate.cols / kDiagWindow;
     dim3 grid(L.gate.rows / (16 * kDiagGateUpTiles), L.routes);
-    hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16>), grid, dim3(64 * waves), 0, st, L.ra, L.gate, L.up,
-                       L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu);
+    if (L.sel)
+        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, true>), grid, dim3(64 * waves), 0, st, L.ra, L.gate,
+                           L.up, L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu, *L.sel);
+    else
+        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, false>), grid, dim3(64 * waves), 0, st, L.ra, L.gate,
+                           L.up, L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu,
+                           RouterLaunch{});
     return hipGetLastError();
 }
 

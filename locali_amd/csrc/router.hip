@@ -19,157 +19,13 @@
 //                        partial sums that the selection adds in fixed order.
 //   router_select_kernel one wave per token: scores, top-k (DPP arg-max over
 //                        (value, ~expert) keys), weights, slots.
-#include "launch.hpp"
+#include "router_select.hpp"
 
 namespace locali {
 
-constexpr int kRouterMaxExpertsPerLane = 8;   // E <= 512
 constexpr int kRouterSplits = 4;
 constexpr int kRouterTokensPerPass = 8;
-
-// --------------------------------------------------------------------------
-// Selection for one token, executed by one full wave. Lane j < top_k ends up
-// owning the j-th choice. Logits are the sum of NS partial rows (fixed order)
-// at logit_row + s * split_stride, or L.logits_in when given. Lane l holds
-// experts l + 64 i, i < M (M = ceil(E / 64)); SF is the score function.
-// A lone wave pays for every instruction and every memory round trip, so:
-// everything the selection can need (logits, bias, the expert -> slot map,
-// the hash row) is loaded up front at clamped in-bounds addresses; scores use
-// the hardware exp/log; each lane sorts its M keys once, after which a round
-// of top-k is one wave-wide arg-max of the lane heads plus a pop; scores and
-// slots of the chosen experts are fetched back from LDS (`stage`, 64 * M
-// float2 per wave) by the owning lanes.
-// --------------------------------------------------------------------------
-template <int SF>
-__device__ __forceinline__ float score_of(float l, float lmax, float denom) {
-    if constexpr (SF == 0) {
-        // sqrt(softplus(l)); log1p(e) ~ e within 1.5e-7 relative below -15
-        const float e = __expf(l);
-        const float sp = l > 20.0f ? l : (l < -15.0f ? e : __logf(1.0f + e));
-        return sqrtf(sp);
-    } else if constexpr (SF == 1) {
-        return 1.0f / (1.0f + __expf(-l));
-    } else {
-        return __expf(l - lmax) / denom;
-    }
-}
-
-__device__ __forceinline__ bool key_gt(uint32_t ah, uint32_t al, uint32_t bh, uint32_t bl) {
-    return ah > bh || (ah == bh && al > bl);
-}
-
-template <int NS, int SF, int M>
-__device__ void select_token(const RouterLaunch &L, int t, const float *logit_row,
-                             int64_t split_stride, float2 *stage) {
-    const int lane = threadIdx.x & 63;
-    float part[NS][M], bias[M];
-    int slot_of[M];
-    int hash_e = -1;
-    if (L.tid2eid) {
-        const int id = L.input_ids[t];
-        if (id >= 0 && id < L.vocab && lane < L.top_k)
-            hash_e = L.tid2eid[static_cast<int64_t>(id) * L.top_k + lane];
-    }
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-        const int e = min(lane + 64 * i, L.E - 1);
-        if (L.logits_in) {
-            part[0][i] = L.logits_in[static_cast<int64_t>(t) * L.E + e];
-#pragma unroll
-            for (int q = 1; q < NS; ++q) part[q][i] = 0.f;
-        } else {
-#pragma unroll
-            for (int q = 0; q < NS; ++q) part[q][i] = logit_row[q * split_stride + e];
-        }
-        bias[i] = L.bias ? L.bias[e] : 0.f;
-        slot_of[i] = L.slot_of_expert ? L.slot_of_expert[e] : -1;
-    }
-    float sc[M];
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-        float l = part[0][i];
-#pragma unroll
-        for (int q = 1; q < NS; ++q) l += part[q][i];
-        sc[i] = lane + 64 * i < L.E ? l : -INFINITY;
-    }
-    float denom = 1.f, lmax = -INFINITY;
-    if constexpr (SF == 2) {
-#pragma unroll
-        for (int i = 0; i < M; ++i) lmax = fmaxf(lmax, sc[i]);
-        for (int m = 32; m >= 1; m >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, m, 64));
-        float z = 0.f;
-#pragma unroll
-        for (int i = 0; i < M; ++i) z += lane + 64 * i < L.E ? __expf(sc[i] - lmax) : 0.f;
-        for (int m = 32; m >= 1; m >>= 1) z += __shfl_xor(z, m, 64);
-        denom = z;
-    }
-    // Keys: hi = ordered selection value, lo = ~expert (ties -> lower id);
-    // (0, 0) marks an invalid candidate.
-    uint32_t kh[M], kl[M];
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-        const int e = lane + 64 * i;
-        const bool valid = e < L.E;
-        const float s = score_of<SF>(valid ? sc[i] : 0.f, lmax, denom);
-        stage[e] = make_float2(s, __int_as_float(slot_of[i]));
-        kh[i] = valid ? ordered_bits(s + bias[i]) : 0u;
-        kl[i] = valid ? ~static_cast<uint32_t>(e) : 0u;
-    }
-    // Sort the lane's keys descending (insertion network, M <= 8).
-#pragma unroll
-    for (int i = 1; i < M; ++i) {
-#pragma unroll
-        for (int j = i; j > 0; --j) {
-            const bool sw = key_gt(kh[j], kl[j], kh[j - 1], kl[j - 1]);
-            const uint32_t th = kh[j], tl = kl[j];
-            kh[j] = sw ? kh[j - 1] : th;
-            kl[j] = sw ? kl[j - 1] : tl;
-            kh[j - 1] = sw ? th : kh[j - 1];
-            kl[j - 1] = sw ? tl : kl[j - 1];
-        }
-    }
-    int my_e = -1;
-    for (int j = 0; j < L.top_k; ++j) {
-        int best_e;
-        if (L.tid2eid) {
-            best_e = __builtin_amdgcn_readlane(hash_e, j);
-            if (best_e >= L.E || best_e < 0) best_e = -1;
-        } else {
-            uint32_t bh = kh[0], bl = kl[0];
-            wave_max_key(bh, bl);
-            best_e = bh == 0 && bl == 0 ? -1 : static_cast<int>(~bl);
-            if (kh[0] == bh && kl[0] == bl && best_e >= 0) {   // the winner pops its head
-#pragma unroll
-                for (int i = 0; i + 1 < M; ++i) {
-                    kh[i] = kh[i + 1];
-                    kl[i] = kl[i + 1];
-                }
-                kh[M - 1] = 0u;
-                kl[M - 1] = 0u;
-            }
-        }
-        if (lane == j) my_e = best_e;
-    }
-    __builtin_amdgcn_wave_barrier();
-    float my_s = 0.f;
-    int my_slot = -1;
-    if (lane < L.top_k && my_e >= 0) {
-        const float2 v = stage[my_e];
-        my_s = v.x;
-        my_slot = __float_as_int(v.y);
-    }
-    float sum = 0.f;   // selection order, as the scores are gathered
-    for (int j = 0; j < L.top_k; ++j)
-        sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_s), j));
-    if (lane < L.top_k) {
-        float w = my_s;
-        if (L.norm_topk) w = w / (sum + 1e-20f);
-        const int64_t o = static_cast<int64_t>(t) * L.top_k + lane;
-        L.idx[o] = my_e;
-        L.weights[o] = w * L.routed_scale;
-        if (L.route_slot) L.route_slot[o] = my_e < 0 || my_slot >= L.n_slots ? -1 : my_slot;
-    }
-}
+static_assert(kFusedSelectMaxTokens <= kRouterTokensPerPass, "fused selection needs the gemv path");
 
 // --------------------------------------------------------------------------
 // GEMV logits (decode).
@@ -359,8 +215,9 @@ __global__ __launch_bounds__(256) void router_select_kernel(RouterLaunch L) {
     const int wave = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wave;
     if (t >= L.tokens) return;
-    select_token<NS, SF, M>(L, t, L.logits + static_cast<int64_t>(t) * L.E,
-                            static_cast<int64_t>(L.tokens) * L.E, stage[wave]);
+    const SelectOut o = select_token<NS, SF, M>(L, t, L.logits + static_cast<int64_t>(t) * L.E,
+                                                static_cast<int64_t>(L.tokens) * L.E, stage[wave]);
+    select_store(L, t, o);
 }
 
 template <int NS, int SF>
@@ -384,7 +241,7 @@ hipError_t launch_select(const RouterLaunch &L, hipStream_t st) {
 }
 
 // --------------------------------------------------------------------------
-hipError_t launch_router(const RouterLaunch &L, hipStream_t st) {
+hipError_t launch_router(const RouterLaunch &L, hipStream_t st, bool logits_only) {
     if (L.E > 64 * kRouterMaxExpertsPerLane || L.top_k > 16 || L.top_k < 1 || L.top_k > L.E)
         return hipErrorInvalidValue;
     const bool mfma_ok = !L.logits_in && L.tokens > kRouterTokensPerPass && L.gate_dtype != 0 &&
@@ -428,7 +285,7 @@ hipError_t launch_router(const RouterLaunch &L, hipStream_t st) {
 #undef LOCALI_ROUTER
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || logits_only) return e;
     return launch_select<1>(L, st);
 }
 

@@ -1,0 +1,189 @@
+// Top-k selection of one token by one wave: scores, selection-only bias,
+// top-k, renormalisation and routed scaling, slot lookup. Shared by the router
+// select kernel and the decode gate/up kernel that selects for its own token.
+// Semantics follow the DeepSeek-V4 gate the reference module delegates to
+// (dsv4_arena.py:147-153, 165-166) and Locali's sigmoid router
+// (arena.py:501-506); in-row order is canonical (descending selection value,
+// ties to the lower expert id).
+#pragma once
+
+#include "launch.hpp"
+
+namespace locali {
+
+constexpr int kRouterMaxExpertsPerLane = 8;   // E <= 512
+
+// --------------------------------------------------------------------------
+// Selection for one token, executed by one full wave. Lane j < top_k ends up
+// owning the j-th choice. Logits are the sum of NS partial rows (fixed order)
+// at logit_row + s * split_stride, or L.logits_in when given. Lane l holds
+// experts l + 64 i, i < M (M = ceil(E / 64)); SF is the score function.
+// A lone wave pays for every instruction and every memory round trip, so:
+// everything the selection can need (logits, bias, the expert -> slot map,
+// the hash row) is loaded up front at clamped in-bounds addresses; scores use
+// the hardware exp/log; each lane sorts its M keys once, after which a round
+// of top-k is one wave-wide arg-max of the lane heads plus a pop; scores and
+// slots of the chosen experts are fetched back from LDS (`stage`, 64 * M
+// float2 per wave) by the owning lanes.
+// --------------------------------------------------------------------------
+template <int SF>
+__device__ __forceinline__ float score_of(float l, float lmax, float denom) {
+    if constexpr (SF == 0) {
+        // sqrt(softplus(l)); log1p(e) ~ e within 1.5e-7 relative below -15
+        const float e = __expf(l);
+        const float sp = l > 20.0f ? l : (l < -15.0f ? e : __logf(1.0f + e));
+        return sqrtf(sp);
+    } else if constexpr (SF == 1) {
+        return 1.0f / (1.0f + __expf(-l));
+    } else {
+        return __expf(l - lmax) / denom;
+    }
+}
+
+__device__ __forceinline__ bool key_gt(uint32_t ah, uint32_t al, uint32_t bh, uint32_t bl) {
+    return ah > bh || (ah == bh && al > bl);
+}
+
+// The choice owned by lane j < top_k: expert (-1: none), its slot (-1: no
+// slot) and its weight.
+struct SelectOut {
+    int e, slot;
+    float w;
+};
+
+template <int NS, int SF, int M>
+__device__ SelectOut select_token(const RouterLaunch &L, int t, const float *logit_row, int64_t split_stride,
+                                  float2 *stage) {
+    const int lane = threadIdx.x & 63;
+    float part[NS][M], bias[M];
+    int slot_of[M];
+    int hash_e = -1;
+    if (L.tid2eid) {
+        const int id = L.input_ids[t];
+        if (id >= 0 && id < L.vocab && lane < L.top_k)
+            hash_e = L.tid2eid[static_cast<int64_t>(id) * L.top_k + lane];
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int e = min(lane + 64 * i, L.E - 1);
+        if (L.logits_in) {
+            part[0][i] = L.logits_in[static_cast<int64_t>(t) * L.E + e];
+#pragma unroll
+            for (int q = 1; q < NS; ++q) part[q][i] = 0.f;
+        } else {
+#pragma unroll
+            for (int q = 0; q < NS; ++q) part[q][i] = logit_row[q * split_stride + e];
+        }
+        bias[i] = L.bias ? L.bias[e] : 0.f;
+        slot_of[i] = L.slot_of_expert ? L.slot_of_expert[e] : -1;
+    }
+    float sc[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        float l = part[0][i];
+#pragma unroll
+        for (int q = 1; q < NS; ++q) l += part[q][i];
+        sc[i] = lane + 64 * i < L.E ? l : -INFINITY;
+    }
+    float denom = 1.f, lmax = -INFINITY;
+    if constexpr (SF == 2) {
+#pragma unroll
+        for (int i = 0; i < M; ++i) lmax = fmaxf(lmax, sc[i]);
+        for (int m = 32; m >= 1; m >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, m, 64));
+        float z = 0.f;
+#pragma unroll
+        for (int i = 0; i < M; ++i) z += lane + 64 * i < L.E ? __expf(sc[i] - lmax) : 0.f;
+        for (int m = 32; m >= 1; m >>= 1) z += __shfl_xor(z, m, 64);
+        denom = z;
+    }
+    // Keys: hi = ordered selection value, lo = ~expert (ties -> lower id);
+    // (0, 0) marks an invalid candidate.
+    uint32_t kh[M], kl[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int e = lane + 64 * i;
+        const bool valid = e < L.E;
+        const float s = score_of<SF>(valid ? sc[i] : 0.f, lmax, denom);
+        stage[e] = make_float2(s, __int_as_float(slot_of[i]));
+        kh[i] = valid ? ordered_bits(s + bias[i]) : 0u;
+        kl[i] = valid ? ~static_cast<uint32_t>(e) : 0u;
+    }
+    // Sort the lane's keys descending (insertion network, M <= 8).
+#pragma unroll
+    for (int i = 1; i < M; ++i) {
+#pragma unroll
+        for (int j = i; j > 0; --j) {
+            const bool sw = key_gt(kh[j], kl[j], kh[j - 1], kl[j - 1]);
+            const uint32_t th = kh[j], tl = kl[j];
+            kh[j] = sw ? kh[j - 1] : th;
+            kl[j] = sw ? kl[j - 1] : tl;
+            kh[j - 1] = sw ? th : kh[j - 1];
+            kl[j - 1] = sw ? tl : kl[j - 1];
+        }
+    }
+    int my_e = -1;
+    for (int j = 0; j < L.top_k; ++j) {
+        int best_e;
+        if (L.tid2eid) {
+            best_e = __builtin_amdgcn_readlane(hash_e, j);
+            if (best_e >= L.E || best_e < 0) best_e = -1;
+        } else {
+            uint32_t bh = kh[0], bl = kl[0];
+            wave_max_key(bh, bl);
+            best_e = bh == 0 && bl == 0 ? -1 : static_cast<int>(~bl);
+            if (kh[0] == bh && kl[0] == bl && best_e >= 0) {   // the winner pops its head
+#pragma unroll
+                for (int i = 0; i + 1 < M; ++i) {
+                    kh[i] = kh[i + 1];
+                    kl[i] = kl[i + 1];
+                }
+                kh[M - 1] = 0u;
+                kl[M - 1] = 0u;
+            }
+        }
+        if (lane == j) my_e = best_e;
+    }
+    __builtin_amdgcn_wave_barrier();
+    float my_s = 0.f;
+    int my_slot = -1;
+    if (lane < L.top_k && my_e >= 0) {
+        const float2 v = stage[my_e];
+        my_s = v.x;
+        my_slot = __float_as_int(v.y);
+    }
+    float sum = 0.f;   // selection order, as the scores are gathered
+    for (int j = 0; j < L.top_k; ++j)
+        sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_s), j));
+    SelectOut o;
+    o.e = my_e;
+    o.slot = my_e < 0 || my_slot >= L.n_slots ? -1 : my_slot;
+    float w = my_s;
+    if (L.norm_topk) w = w / (sum + 1e-20f);
+    o.w = w * L.routed_scale;
+    return o;
+}
+
+// Stores token t's choices (lanes < top_k).
+__device__ __forceinline__ void select_store(const RouterLaunch &L, int t, const SelectOut &o) {
+    const int lane = threadIdx.x & 63;
+    if (lane < L.top_k) {
+        const int64_t i = static_cast<int64_t>(t) * L.top_k + lane;
+        L.idx[i] = o.e;
+        L.weights[i] = o.w;
+        if (L.route_slot) L.route_slot[i] = o.slot;
+    }
+}
+
+// Score function chosen at run time (for kernels that select on the side).
+template <int NS, int M>
+__device__ SelectOut select_token_any(const RouterLaunch &L, int t, const float *logit_row,
+                                      int64_t split_stride, float2 *stage) {
+    switch (L.score_func) {
+    case 0: return select_token<NS, 0, M>(L, t, logit_row, split_stride, stage);
+    case 1: return select_token<NS, 1, M>(L, t, logit_row, split_stride, stage);
+    default: return select_token<NS, 2, M>(L, t, logit_row, split_stride, stage);
+    }
+}
+
+
+}  // namespace locali
