@@ -278,6 +278,49 @@ def test_forward_small_cpu_config_fp16():
         assert_close_terms(values(out), want, terms, f"forward C1 T={T}")
 
 
+@pytest.mark.parametrize("mode", ["hash", "sigmoid_bias", "softmax"])
+def test_forward_decode_selects_in_gateup(mode):
+    """Decode forward selects each token's routes inside the gate/up kernel;
+    the result must equal router + expert_decode run separately (same kernels
+    and arithmetic: bit-exact), for hash routing, sigmoid scores with a
+    selection bias, and softmax scores; and the routes must match the oracle."""
+    banner(f"forward decode fused select {mode}")
+    d, E, dff, k, T, V = 1024, 64, 512, 6, 2, 40
+    arena = synth.expert_arena(E + 1, d, dff, dtype=torch.bfloat16, seed=31, device=DEV)
+    shared = synth.expert_arena(1, d, dff, dtype=torch.bfloat16, seed=32, device=DEV, zero_slot=False)
+    w, bias = synth.uniform_router(E, d, torch.bfloat16, seed=33, device=DEV, bias_std=0.05)
+    kw = dict(routed_scale=1.5)
+    ids = None
+    if mode == "hash":
+        table = torch.stack([torch.randperm(E, generator=torch.Generator().manual_seed(i))[:k]
+                             for i in range(V)]).to(torch.int32)
+        kw["tid2eid"] = table.to(DEV)
+        ids = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(3)).to(DEV)
+    elif mode == "sigmoid_bias":
+        kw.update(score_func="sigmoid", score_bias=bias)
+    else:
+        kw.update(score_func="softmax")
+    spec = ops.RouterSpec(w, k, **kw)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    x = synth.activations(T, d, torch.bfloat16, seed=34, device=DEV)
+    out, idx, wts = ops.forward(spec, arena, shared, slot_of, x, ops.Workspace(), input_ids=ids)
+    ridx, rw, rs = ops.router(spec, x, ops.Workspace(), input_ids=ids, slot_of_expert=slot_of,
+                              n_slots=E + 1)
+    sep = ops.expert_decode(arena, shared, x, rs, rw)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, ridx) and torch.equal(wts, rw)
+    assert torch.equal(out, sep)
+    score = {"hash": "sqrtsoftplus", "sigmoid_bias": "sigmoid", "softmax": "softmax"}[mode]
+    oi, ow, margin, _ = moe.route(values(x), values(w), k, routed_scale=1.5, score_func=score,
+                                  bias=values(bias) if mode == "sigmoid_bias" else None,
+                                  tid2eid=table.numpy() if mode == "hash" else None,
+                                  input_ids=ids.cpu().numpy() if mode == "hash" else None)
+    for t in range(T):
+        if mode == "hash" or margin[t] > 1e-4:
+            assert list(idx[t].cpu().numpy()) == list(oi[t])
+            np.testing.assert_allclose(wts[t].cpu().numpy(), ow[t], rtol=1e-5)
+
+
 def test_forward_full_width_decode(oracle_lib):
     """d 4096, 256 experts + shared, d_ff 2048, 2-bit g64 bf16, 1 token; checked
     against the C oracle (fp32) on the GPU's own routing."""
