@@ -152,31 +152,48 @@ __device__ __forceinline__ void load_block_a(u32x4 (&a)[2], __amdgpu_buffer_rsrc
 // meta[g][r] = {scale, bias} of each projection (16-bit each): in the loop a
 // lane then reads its row's pair with one LDS load instead of issuing small
 // global loads that the compiler would schedule next to their use. Staged
-// with 16-byte global loads (8 groups of one row per array).
+// with 16-byte global loads (8 groups of one row per array), all of a batch
+// of two per thread issued before the first LDS store, so the prologue costs
+// one memory round trip per batch (one batch up to K = 4096 at group 64).
 template <int NPROJ>
 __device__ __forceinline__ void stage_meta(uint16_t *meta, const uint16_t *const (&arr)[2 * NPROJ],
                                            int gpr, int bpg) {
     const int chunks = kMfmaRows * (gpr / 8);
-    for (int e = threadIdx.x; e < chunks; e += blockDim.x) {
-        const int r = e % kMfmaRows, c = e / kMfmaRows;
-        uint4 v[2 * NPROJ];
+    for (int e0 = threadIdx.x; e0 < chunks; e0 += 2 * blockDim.x) {
+        uint4 v[2][2 * NPROJ];
 #pragma unroll
-        for (int a = 0; a < 2 * NPROJ; ++a)
-            v[a] = reinterpret_cast<const uint4 *>(arr[a] + static_cast<int64_t>(r) * gpr)[c];
+        for (int it = 0; it < 2; ++it) {
+            const int e = e0 + it * blockDim.x;
+            if (e < chunks) {
+                const int r = e % kMfmaRows, c = e / kMfmaRows;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int g = c * 8 + q;
+                for (int a = 0; a < 2 * NPROJ; ++a)
+                    v[it][a] = reinterpret_cast<const uint4 *>(arr[a] + static_cast<int64_t>(r) * gpr)[c];
+            }
+        }
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {   // one entry per 64-value block (bpg is 1 or 2)
-                if (t >= bpg) break;
-                uint16_t *dst = meta + (static_cast<int64_t>(g * bpg + t) * kMfmaRows + r) * (2 * NPROJ);
+        for (int it = 0; it < 2; ++it) {
+            const int e = e0 + it * blockDim.x;
+            if (e >= chunks) break;
+            const int r = e % kMfmaRows, c = e / kMfmaRows;
 #pragma unroll
-                for (int a = 0; a < 2 * NPROJ; ++a) {
-                    const uint32_t wv = q < 2 ? (q == 0 ? v[a].x : v[a].x >> 16)
-                                      : q < 4 ? (q == 2 ? v[a].y : v[a].y >> 16)
-                                      : q < 6 ? (q == 4 ? v[a].z : v[a].z >> 16)
-                                              : (q == 6 ? v[a].w : v[a].w >> 16);
-                    dst[a] = static_cast<uint16_t>(wv);
+            for (int q = 0; q < 8; ++q) {
+                const int g = c * 8 + q;
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {   // one entry per 64-value block (bpg is 1 or 2)
+                    if (t >= bpg) break;
+                    uint16_t *dst = meta + (static_cast<int64_t>(g * bpg + t) * kMfmaRows + r) * (2 * NPROJ);
+                    if constexpr (NPROJ == 2) {
+                        uint2 pk;
+                        pk.x = ((v[it][0][q / 2] >> (16 * (q % 2))) & 0xffffu) |
+                               (((v[it][1][q / 2] >> (16 * (q % 2))) & 0xffffu) << 16);
+                        pk.y = ((v[it][2][q / 2] >> (16 * (q % 2))) & 0xffffu) |
+                               (((v[it][3][q / 2] >> (16 * (q % 2))) & 0xffffu) << 16);
+                        *reinterpret_cast<uint2 *>(dst) = pk;
+                    } else {
+                        *reinterpret_cast<uint32_t *>(dst) = ((v[it][0][q / 2] >> (16 * (q % 2))) & 0xffffu) |
+                                                             (((v[it][1][q / 2] >> (16 * (q % 2))) & 0xffffu) << 16);
+                    }
                 }
             }
         }
@@ -202,13 +219,29 @@ __device__ __forceinline__ mf32x4_t block_mfma(const BlockW<MfmaGeom<BITS, BF16>
     return d;
 }
 
+// Per-64 sums of the tile's 16 positions for every block, [blk][16] float2.
+// The position of thread i is i % 16 for every entry it stages (blockDim is a
+// multiple of 16), so its vector index is loaded once and every sum load is
+// issued before the first LDS store.
 __device__ __forceinline__ void stage_gsum(float2 *gsl, const MfmaVec &in, int nblk, int count,
                                            const TileArgs &ta, bool shared, int first, bool by_token) {
-    for (int e = threadIdx.x; e < nblk * kMfmaTileTokens; e += blockDim.x) {
-        const int q = e % kMfmaTileTokens, blk = e / kMfmaTileTokens;
-        const int pos = first + min(q, count - 1);
-        const int vec = by_token ? tile_token(ta, shared, pos) : pos;
-        gsl[e] = in.gsum[vec * in.gsum_stride + blk];
+    const int q = threadIdx.x % kMfmaTileTokens;
+    const int pos = first + min(q, count - 1);
+    const int vec = by_token ? tile_token(ta, shared, pos) : pos;
+    const float2 *src = in.gsum + vec * in.gsum_stride;
+    const int per = nblk * kMfmaTileTokens;
+    for (int e0 = threadIdx.x; e0 < per; e0 += 8 * blockDim.x) {
+        float2 v[8];
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int e = e0 + it * blockDim.x;
+            if (e < per) v[it] = src[e / kMfmaTileTokens];
+        }
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int e = e0 + it * blockDim.x;
+            if (e < per) gsl[e] = v[it];
+        }
     }
 }
 
