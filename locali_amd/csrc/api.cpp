@@ -285,6 +285,17 @@ bool mfma_eligible(const locali_expert_arena *routed, const locali_expert_arena 
     return true;
 }
 
+// Small-tile kernels (mfma_small.hpp): groups of exactly 64, K of both
+// stages a multiple of 512 and at most 4096, rows multiples of 32.
+constexpr int kSmallTileHost = 2;
+bool small_tiles_eligible(const locali_expert_arena *routed) {
+    auto ok = [](const locali_qproj &p) {
+        return (p.bits == 2 || p.bits == 4) && p.group_size == 64 && p.cols % 512 == 0 && p.cols <= 4096 &&
+               p.rows % 32 == 0;
+    };
+    return ok(routed->gate) && ok(routed->up) && ok(routed->down);
+}
+
 int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_arena *shared,
                      const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k, int32_t n_experts,
                      const int32_t *route_slot, const float *weights, float limit,
@@ -319,6 +330,7 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     L.sdown = to_dev(sh->down);
     L.xin = mfma_batch(at<void>(ws, lay.mx), tokens, routed->gate.cols);
     L.hmid = mfma_batch(at<void>(ws, lay.mh), routes, routed->down.cols);
+    L.hsum32 = at<float2>(ws, lay.gh);   // the VALU path's h buffer is free here
     L.y = gy;
     L.limit = limit;
     L.fp32_swiglu = fp32_swiglu;
@@ -326,8 +338,15 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     L.tokens = tokens;
     L.routes = routes;
     const bool bf16 = x_dtype == LOCALI_DT_BF16;
-    for (int which = 0; which < 3; ++which)
+    // Tiles of one or two positions go to the small-tile kernels when the
+    // shapes allow; the 16-position kernels skip them.
+    const bool small = small_tiles_eligible(routed);
+    L.ta.min_count = small ? kSmallTileHost + 1 : 0;
+    const int order[5] = {0, 1, 3, 2, 4};
+    for (int which : order) {
+        if (which >= 3 && !small) continue;
         if ((e = launch_mfma(which, bf16, L, st)) != hipSuccess) return hip_fail(e, "grouped MFMA launch");
+    }
     const int d = routed->down.rows;
     e = launch_combine(gy, route_pos, shared ? gy + static_cast<int64_t>(R) * d : nullptr, weights, tokens,
                        top_k, d, combine_mode, bf16, static_cast<uint16_t *>(out), st);

@@ -193,10 +193,11 @@ hipError_t launch_grouped_kernels(int which, const GroupedKernelLaunch &L, hipSt
 hipError_t mfma_b2(int which, bool bf16, const MfmaLaunch &L, hipStream_t st);
 hipError_t mfma_b4(int which, bool bf16, const MfmaLaunch &L, hipStream_t st);
 
-// which: 0 = prepare x, 1 = gate/up + SwiGLU (+ prepared h), 2 = down.
-// Gate and up share the prepared x, so they must share a bit width.
+// which: 0 = prepare x, 1 = gate/up + SwiGLU (+ prepared h), 2 = down,
+// 3 / 4 = gate/up / down of the small tiles. Gate and up share the prepared
+// x, so they must share a bit width.
 hipError_t launch_mfma(int which, bool bf16, const MfmaLaunch &L, hipStream_t st) {
-    const int bits = which == 2 ? L.down.bits : L.gate.bits;
+    const int bits = which == 2 || which == 4 ? L.down.bits : L.gate.bits;
     switch (bits) {
     case 2: return mfma_b2(which, bf16, L, st);
     case 4: return mfma_b4(which, bf16, L, st);

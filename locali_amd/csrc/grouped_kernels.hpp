@@ -21,6 +21,7 @@ struct TileArgs {
     const int32_t *sorted_route;  // [R]
     int32_t R, top_k;
     int32_t n_vec;                // vectors in the MFMA kernels' input array (bounds of its loads)
+    int32_t min_count;            // MFMA kernels: skip tiles of fewer positions (the small-tile kernels' share)
 };
 
 __device__ __forceinline__ int tile_token(const TileArgs &ta, bool shared, int pos) {

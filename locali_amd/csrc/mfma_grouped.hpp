@@ -269,7 +269,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void mfma_gateup_kernel(
     const bool shared = slot == -2;
     const QProj &pg = shared ? sgate : gate;
     const QProj &pu = shared ? sup : up;
-    if (count <= 0 || count > kMfmaTileTokens ||
+    if (count <= 0 || count > kMfmaTileTokens || count < ta.min_count ||
         (!shared && (slot < 0 || slot >= pg.n_slots || first < 0 || first + count > ta.R)))
         return;
     const int K = pg.cols, nblk = K / 64;
@@ -380,7 +380,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void mfma_down_kernel(TileArgs ta,
     const int count = ta.tiles[4 * tile + 2];
     const bool shared = slot == -2;
     const QProj &p = shared ? sdown : down;
-    if (count <= 0 || count > kMfmaTileTokens ||
+    if (count <= 0 || count > kMfmaTileTokens || count < ta.min_count ||
         (!shared && (slot < 0 || slot >= p.n_slots || first < 0 || first + count > ta.R)))
         return;
     const int N = p.rows, K = p.cols, nblk = K / 64;
@@ -452,6 +452,7 @@ struct MfmaLaunch {
     TileArgs ta;
     QProj gate, up, down, sgate, sup, sdown;
     MfmaVec xin, hmid;
+    float2 *hsum32;               // small tiles: sums of h per 32 values [routes][d_ff / 32]
     uint16_t *y;
     float limit;
     int32_t fp32_swiglu;
