@@ -18,11 +18,23 @@ Also reported:
                 reference kernel of known bytes -- a 256 MiB reduction and a
                 256 MiB fill (`--copy-calibration`) -- summarised by
                 `--summarize-pmc` into profiles/gateup_diag_kernel_decode_traffic.json
-  prefill64     64-token prefill on the same layer with Zipf(1.1) expert
-                popularity (grouped path), tokens/s and algorithmic GB/s
+  prefill64, prefill512
+                64- and 512-token prefill on the same layer with Zipf(1.1)
+                expert popularity (grouped path): tokens/s, algorithmic GB/s
+                against 8 TB/s, and matrix-core utilisation (flops against
+                the 2.5 PFLOP/s dense bf16 peak)
+  mixed32       batched decode of 32 tokens on a layer with 2-bit gate/up
+                and 4-bit down projections, uniform routing: tokens/s and GB/s
+  stack43       a 43-layer stack of full-width layers decoding through one
+                bounded arena (96 usable slots per layer, 4129 slots, 32.5 GB):
+                the compiled SLRU planner (and LFU-decay) picks evictions,
+                misses are copied from pinned host memory on the fill stream;
+                Zipf(1.1) routing with AR(1) cross-layer noise (rho 0.6);
+                hit rate, bytes moved, tokens/s and host -> HBM GB/s
   cpu_baseline  the C oracle (oracle/expert_ref.c, OpenMP) on the host cores
-                over a bounded sample of the same decode workload; a stand-in
-                for the reference's MLX-CPU path, which cannot run here
+                over a bounded sample of the same decode workload, on every
+                core and on one; a stand-in for the reference's MLX-CPU path,
+                which cannot run here
 
 `python bench.py --gpus N` with N > 1 exits: this path is measured on one GPU.
 """
@@ -46,8 +58,9 @@ from locali_amd import ops, synth  # noqa: E402
 
 METRIC = "MoE-layer tokens/s at 1 GPU (decode & 64-tok prefill); achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0          # dense bf16
 TRAFFIC_FILE = ROOT / "profiles" / "gateup_diag_kernel_decode_traffic.json"
-GATEUP_KERNEL = "gateup_diag_kernel<2, true>"
+GATEUP_KERNEL = "gateup_diag_kernel<2, true, false>"
 COPY_BYTES = 256 << 20
 D, E, DFF, K_TOP, GROUP, BITS = 4096, 256, 2048, 6, 64, 2
 
@@ -57,10 +70,16 @@ def proj_bytes(rows, cols, bits=BITS, group=GROUP):
 
 
 EXPERT_BYTES = 2 * proj_bytes(DFF, D) + proj_bytes(D, DFF)          # 7,864,320
+MIXED_EXPERT_BYTES = 2 * proj_bytes(DFF, D) + proj_bytes(D, DFF, bits=4)   # 9,961,472
 GATEUP_ROUTE_BYTES = 2 * proj_bytes(DFF, D)                           # 5,242,880
 ROUTER_BYTES = E * D * 2
 # per decode gate/up launch: 7 routes' gate+up slots, x read once, h written
 GATEUP_ALG_BYTES = (K_TOP + 1) * GATEUP_ROUTE_BYTES + D * 2 + (K_TOP + 1) * DFF * 2   # 36,737,024
+
+
+def layer_flops(tokens):
+    """Multiply-adds x 2 of the routed and shared experts for `tokens` tokens."""
+    return 2 * tokens * (K_TOP + 1) * 3 * D * DFF
 
 
 def layer(dev, seed=1):
@@ -189,14 +208,126 @@ def prefill_run(arena, shared, slot_of, dev, tokens, calls, seed):
     u = sum(distinct) / len(distinct)
     algo = (u + 1) * EXPERT_BYTES + ROUTER_BYTES + tokens * D * 2 * 2
     per_call = secs / calls
+    flops = layer_flops(tokens)
+    t_roof = max(algo / (HBM_PEAK_GBS * 1e9), flops / (MFMA_PEAK_TFLOPS * 1e12))
     return {"tokens": tokens, "calls": calls, "value": tokens * calls / secs, "unit": "tokens/s",
             "ms_per_call": per_call * 1e3, "distinct_experts": u,
             "algorithmic_bytes_per_call": int(algo),
-            "achieved_GBps": algo / per_call / 1e9, "frac_of_hbm_peak": algo / per_call / 1e9 / HBM_PEAK_GBS}
+            "achieved_GBps": algo / per_call / 1e9, "frac_of_hbm_peak": algo / per_call / 1e9 / HBM_PEAK_GBS,
+            "flops_per_call": flops, "achieved_TFLOPs": flops / per_call / 1e12,
+            "mfma_utilisation": flops / per_call / 1e12 / MFMA_PEAK_TFLOPS,
+            "roofline_frac": t_roof / per_call}
+
+
+def mixed_run(dev, tokens, calls, seed):
+    """Batched decode on a 2-bit gate/up, 4-bit down layer, uniform routing."""
+    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=2, bits_down=4, group=GROUP,
+                               dtype=torch.bfloat16, seed=seed, device=dev)
+    shared = synth.expert_arena(1, D, DFF, bits_gate_up=2, bits_down=4, group=GROUP,
+                                dtype=torch.bfloat16, seed=seed + 1, device=dev, zero_slot=False)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=dev)
+    w, _ = synth.uniform_router(E, D, torch.bfloat16, seed=seed + 2, device=dev)
+    spec = ops.RouterSpec(w, K_TOP, routed_scale=1.5)
+    ws = ops.Workspace(dev)
+    xs = [synth.activations(tokens, D, torch.bfloat16, seed=seed + 10 + c, device=dev)
+          for c in range(calls)]
+    out = torch.empty(tokens, D, dtype=torch.bfloat16, device=dev)
+    idx = torch.empty(tokens, K_TOP, dtype=torch.int32, device=dev)
+    wts = torch.empty(tokens, K_TOP, dtype=torch.float32, device=dev)
+    for x in xs[:2]:
+        ops.forward(spec, arena, shared, slot_of, x, ws, out=out, idx=idx, weights=wts)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for x in xs:
+        ops.forward(spec, arena, shared, slot_of, x, ws, out=out, idx=idx, weights=wts)
+    e1.record()
+    torch.cuda.synchronize()
+    secs = e0.elapsed_time(e1) / 1e3
+    distinct = [int(torch.unique(ops.router(spec, x, ws)[0]).numel()) for x in xs]
+    u = sum(distinct) / len(distinct)
+    per_call = secs / calls
+    algo = (u + 1) * MIXED_EXPERT_BYTES + ROUTER_BYTES + tokens * D * 2 * 2
+    del arena, shared
+    torch.cuda.empty_cache()
+    return {"tokens": tokens, "calls": calls, "value": tokens * calls / secs, "unit": "tokens/s",
+            "ms_per_call": per_call * 1e3, "distinct_experts": u,
+            "expert_bytes": MIXED_EXPERT_BYTES, "algorithmic_bytes_per_call": int(algo),
+            "achieved_GBps": algo / per_call / 1e9, "frac_of_hbm_peak": algo / per_call / 1e9 / HBM_PEAK_GBS,
+            "workload": "d_model 4096, 256 experts top-6 + shared, d_ff 2048, gate/up 2-bit + "
+                        "down 4-bit affine g64 bf16, 32 tokens per call, uniform routing"}
+
+
+def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96):
+    """Decode through a stack of full-width layers sharing one bounded arena,
+    misses copied from pinned host memory (V4ArenaStore host_source)."""
+    import tempfile
+    from locali_amd.dsv4_arena import V4ArenaMoE, V4ArenaStore, V4Gate
+    tmp = tempfile.TemporaryDirectory()
+    index = Path(tmp.name) / "stack.idx"
+    index.write_text(json.dumps(synth.stack_index(layers, E, K_TOP, D, DFF, bits=BITS, group=GROUP)))
+    payload = synth.expert_arena(E, D, DFF, bits_gate_up=BITS, group=GROUP, dtype=torch.bfloat16,
+                                 seed=seed, device=dev, zero_slot=False)
+    host = synth.host_payloads(payload)          # 256 distinct experts, pinned
+    del payload
+    n_slots = layers * per_layer + 1
+    store = V4ArenaStore(index, ceiling_gb=n_slots * EXPERT_BYTES / 1e9 + 1e-6, threads=1,
+                         cache_policy=policy, device=dev,
+                         host_source=lambda layer, e: host[e])
+    shared = synth.expert_arena(layers, D, DFF, bits_gate_up=BITS, group=GROUP, dtype=torch.bfloat16,
+                                seed=seed + 1, device=dev, zero_slot=False)
+
+    def shared_of(layer):
+        return ops.ExpertArenaT(*(ops.ProjArena(p.weight[layer:layer + 1], p.scales[layer:layer + 1],
+                                                p.biases[layer:layer + 1], p.bits, p.group_size)
+                                  for p in (shared.gate, shared.up, shared.down)))
+
+    gate = V4Gate(synth.identity_router(E, D, torch.bfloat16, dev), top_k=K_TOP,
+                  routed_scaling_factor=1.5)
+    mods = [V4ArenaMoE(store, layer, gate, K_TOP, shared_expert=shared_of(layer))
+            for layer in range(layers)]
+    n_tok = warmup + steps
+    X = synth.activations(n_tok * layers, D, torch.bfloat16, seed=seed + 2, device=dev).view(n_tok, layers, D)
+    X[:, :, :E] = synth.layered_zipf_logits(n_tok, layers, E, 1.1, 0.6, seed=seed + 3).to(dev, torch.bfloat16)
+    for t in range(warmup):
+        for layer in range(layers):
+            mods[layer](X[t, layer:layer + 1])
+    torch.cuda.synchronize()
+    store.hits = store.misses = store.evictions = store.bytes_read = 0
+    store.t_stall = 0.0
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for t in range(warmup, n_tok):
+        for layer in range(layers):
+            mods[layer](X[t, layer:layer + 1])
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    secs = e0.elapsed_time(e1) / 1e3
+    st = store.stats()
+    store.close()
+    del store, shared, host, mods
+    tmp.cleanup()
+    torch.cuda.empty_cache()
+    moved = st["bytes_read"]
+    return {"layers": layers, "slots": n_slots, "usable_slots_per_layer": per_layer,
+            "arena_GB": n_slots * EXPERT_BYTES / 1e9, "cache_policy": policy,
+            "steps": steps, "warmup_tokens": warmup, "value": steps / secs, "unit": "tokens/s",
+            "ms_per_token": secs / steps * 1e3, "wall_s": wall, "hit_rate": st["hit_rate"],
+            "hits": st["hits"], "misses": st["misses"], "evictions": st["evictions"],
+            "h2d_bytes": moved, "h2d_bytes_per_token": moved / steps,
+            "h2d_GBps": moved / secs / 1e9, "host_stall_s": st["t_stall"],
+            "hbm_expert_bytes_per_token": layers * (K_TOP + 1) * EXPERT_BYTES + layers * ROUTER_BYTES,
+            "workload": "43 full-width layers (d 4096, 256 experts top-6 + shared, d_ff 2048, 2-bit "
+                        "g64), one arena of 43 x 96 + 1 slots, Zipf(1.1) routing with AR(1) "
+                        "cross-layer noise rho 0.6, misses from pinned host memory (256 distinct "
+                        "expert payloads; expert e of every layer copies payload e)"}
 
 
 def cpu_baseline(arena, shared, spec, X, seconds):
-    """C oracle on the host cores, decode tokens until `seconds` elapse."""
+    """C oracle on the host cores, decode tokens until `seconds` elapse on
+    every core, then for half as long on one core."""
     import numpy as np
     from oracle import cref
     lib_path = ROOT / "oracle" / "liboracle.so"
@@ -215,22 +346,32 @@ def cpu_baseline(arena, shared, spec, X, seconds):
     hs = {n: host(p) for n, p in zip(names, (shared.gate, shared.up, shared.down))}
     wg = spec.weight.float().cpu().numpy()
     xs = X.float().cpu().numpy()
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        x = xs[n % xs.shape[0]:n % xs.shape[0] + 1]
-        idx, w = ref.router(x, wg, None, K_TOP, 0, True, spec.routed_scale)
-        ref.moe_layer(x, idx + 1, w, ha, "bf16", shared=hs)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= 2:
-            break
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
-    return {"value": n / el, "unit": "tokens/s", "cores": min(threads, len(os.sched_getaffinity(0))),
-            "kind": "port",
+
+    def timed(threads, budget):
+        ref.set_threads(threads)
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            x = xs[n % xs.shape[0]:n % xs.shape[0] + 1]
+            idx, w = ref.router(x, wg, None, K_TOP, 0, True, spec.routed_scale)
+            ref.moe_layer(x, idx + 1, w, ha, "bf16", shared=hs)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget and n >= 2:
+                return n, el
+
+    cores = len(os.sched_getaffinity(0))
+    threads = min(int(os.environ.get("OMP_NUM_THREADS", "0")) or cores, cores)
+    n, el = timed(threads, seconds)
+    n1, el1 = timed(1, seconds / 2)
+    ref.set_threads(0)
+    return {"value": n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "one_core": {"value": n1 / el1, "unit": "tokens/s", "cores": 1,
+                         "sample": f"{n1} decode tokens, {el1:.1f} s"},
             "sample": f"{n} decode tokens of the same layer (router + 6 routed + shared experts), "
-                      f"{el:.1f} s, C oracle oracle/expert_ref.c with OpenMP; stand-in for the "
-                      "reference dsv4_arena path on MLX's CPU backend (not runnable here)"}
+                      f"{el:.1f} s on {threads} threads, C oracle oracle/expert_ref.c with OpenMP; "
+                      "stand-in for the reference dsv4_arena path on MLX's CPU backend (not "
+                      "runnable here)"}
 
 
 def copy_calibration(dev):
@@ -293,6 +434,12 @@ def main(argv=None):
     ap.add_argument("--no-graph", action="store_true", help="launch steps eagerly")
     ap.add_argument("--prefill-calls", type=int, default=20)
     ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--skip-mixed", action="store_true")
+    ap.add_argument("--skip-stack", action="store_true")
+    ap.add_argument("--stack-steps", type=int, default=128)
+    ap.add_argument("--stack-warmup", type=int, default=16)
+    ap.add_argument("--stack-policies", default="slru-all,lfu-decay",
+                    help="comma-separated arena cache policies for the 43-layer stack")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=1)
@@ -361,7 +508,9 @@ def main(argv=None):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gateup_diag_kernel (decode gate/up + clamped SwiGLU on the matrix cores, 7 routes)",
+            "kernel": "gateup_diag_kernel<2, true, false> (decode gate/up + clamped SwiGLU on the "
+                      "matrix cores, 7 routes); the decode step runs its <2, true, true> "
+                      "instantiation, which also selects the token's top-6 in wave 0",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -373,9 +522,19 @@ def main(argv=None):
         },
     }
     if not args.skip_prefill:
-        print("[bench] prefill 64", file=sys.stderr, flush=True)
-        result["prefill64"] = prefill_run(arena, shared, slot_of, dev, 64, args.prefill_calls,
-                                          args.seed + 100)
+        for tokens in (64, 512):
+            print(f"[bench] prefill {tokens}", file=sys.stderr, flush=True)
+            result[f"prefill{tokens}"] = prefill_run(arena, shared, slot_of, dev, tokens,
+                                                     args.prefill_calls, args.seed + 100)
+    if not args.skip_mixed:
+        print("[bench] mixed 2/4-bit, 32 tokens", file=sys.stderr, flush=True)
+        result["mixed32"] = mixed_run(dev, 32, args.prefill_calls, args.seed + 200)
+    if not args.skip_stack:
+        result["stack43"] = []
+        for policy in args.stack_policies.split(","):
+            print(f"[bench] 43-layer bounded arena, {policy}", file=sys.stderr, flush=True)
+            result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, policy,
+                                               args.seed + 300))
     if not args.skip_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(arena, shared, spec, X, args.cpu_seconds)

@@ -50,6 +50,20 @@ class ReadPlan(dict):
         self.pending_experts = frozenset(pending_experts)
 
 
+class _Landed:
+    """Future of a fill copied from pinned host memory: an event recorded on
+    the fill stream after the expert's copies."""
+
+    def __init__(self, event):
+        self.event = event
+
+    def done(self) -> bool:
+        return self.event.query()
+
+    def result(self, timeout=None):
+        self.event.synchronize()
+
+
 class _Staging:
     """A small pool of pinned host buffers, one expert each."""
 
@@ -71,8 +85,14 @@ class _Staging:
 
 class ArenaStore:
     def __init__(self, index_path, ceiling_gb=8.0, hot_share=0.33, threads=8, nocache=True,
-                 cache_policy="lru", device=None):
+                 cache_policy="lru", device=None, host_source=None):
         idx = json.loads(Path(index_path).read_text())
+        # host_source(layer, expert) -> pinned uint8 host tensor holding the
+        # expert's nine records back to back in (gate, up, down) x (weight,
+        # scales, biases) order: misses then copy straight from host memory
+        # (a host tier for hosts whose RAM holds the experts) instead of
+        # reading the checkpoint files.
+        self.host_source = host_source
         if cache_policy not in POLICIES:
             raise ValueError(f"cache_policy must be one of {POLICIES}")
         self.meta = idx["experts"]
@@ -218,9 +238,15 @@ class ArenaStore:
             if self._nocache and hasattr(os, "posix_fadvise"):
                 os.posix_fadvise(fd, r0[2], want, os.POSIX_FADV_DONTNEED)
 
-    def _fill(self, t, slot, recs) -> None:
+    def _fill(self, t, slot, recs, key=None) -> None:
         """Worker: file -> pinned staging -> HBM slot; returns once the bytes
-        are in device memory."""
+        are in device memory. A host-memory arena copies from host_source."""
+        if self.host_source is not None:
+            src, off = self._host_bytes(key, t), 0
+            for (p, k), r in zip(((p, k) for p in PROJS for k in ARRS), recs):
+                self.arena[(t, p, k)][slot].view(torch.uint8).reshape(-1).copy_(src[off:off + r[3]])
+                off += r[3]
+            return
         buf = self.staging.take()
         try:
             host = buf.numpy()
@@ -243,6 +269,29 @@ class ArenaStore:
                     off += r[3]
         finally:
             self.staging.give(buf)
+
+    def _host_bytes(self, key, t) -> torch.Tensor:
+        src = self.host_source(*key)
+        if src.is_cuda or src.dtype != torch.uint8 or src.numel() != self.item[t]:
+            raise ValueError(f"host_source{key}: expected {self.item[t]} host bytes (uint8)")
+        return src
+
+    def _fill_from_host(self, key, t, slot, recs) -> _Landed:
+        """Queue the nine host -> HBM copies of one expert from host_source on
+        the fill stream, behind the work already queued on the compute stream
+        (a refilled slot may still be read there), and return their event."""
+        from .ops import arena_fill
+        src = self._host_bytes(key, t)
+        with torch.cuda.device(self.device):
+            self.fill_stream.wait_stream(torch.cuda.current_stream(self.device))
+            off = 0
+            for (p, k), r in zip(((p, k) for p in PROJS for k in ARRS), recs):
+                dst = self.arena[(t, p, k)][slot].view(torch.uint8).reshape(-1)
+                arena_fill(dst, src[off:off + r[3]], stream=self.fill_stream)
+                off += r[3]
+            ev = torch.cuda.Event()
+            ev.record(self.fill_stream)
+        return _Landed(ev)
 
     # ---- Python planner (reference arena.py:212-289) ---------------------
     def _claim(self, t, key, also_pinned=()):
@@ -386,7 +435,10 @@ class ArenaStore:
         for t in self.tiers:   # a whole tier before the next
             futs = []
             for key, tt, s, recs in jobs[t]:
-                f = self.pool.submit(self._fill, tt, s, recs)
+                if self.host_source is not None and self.fill_stream is not None:
+                    f = self._fill_from_host(key, tt, s, recs)
+                else:
+                    f = self.pool.submit(self._fill, tt, s, recs, key)
                 self.inflight.setdefault(key, []).append(f)
                 futs.append(f)
             plan[t] = futs + waits[t]
@@ -448,6 +500,7 @@ class ArenaMoE:
         self.overlap_hits = False
         self.swiglu_limit = 0.0
         self.fp32_swiglu = False
+        self.shared_expert = None
         self._spec = None
 
     def route(self, x, input_ids=None):
@@ -508,11 +561,11 @@ class ArenaMoE:
         w = gates.to(torch.float32).contiguous()
         ws = self._workspace()
         if T <= 2:
-            y = ops.expert_decode(arena, None, x_in, slots, w, swiglu_limit=self.swiglu_limit,
+            y = ops.expert_decode(arena, self.shared_expert, x_in, slots, w, swiglu_limit=self.swiglu_limit,
                                   fp32_swiglu=self.fp32_swiglu, ws=ws)
         else:
             n = arena.n_slots
             ident = self.store.slot_identity(t)
-            y = ops.expert_grouped(arena, None, x_in, slots, ident, w, ws, n_experts=n,
+            y = ops.expert_grouped(arena, self.shared_expert, x_in, slots, ident, w, ws, n_experts=n,
                                    swiglu_limit=self.swiglu_limit, fp32_swiglu=self.fp32_swiglu)
         return y.to(dtype)

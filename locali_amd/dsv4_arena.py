@@ -175,12 +175,19 @@ class V4ArenaMoE(ArenaMoE):
     """V4 top-k routing and clamped SwiGLU over the arena's affine experts.
     Routing is the gate's (hash routing in the first layers, selection-only
     bias elsewhere); only the routed experts are replaced -- the shared
-    expert is added by the model block."""
+    expert is added by the model block (dsv4_engine.py:255-259:
+    routed + shared_experts(x)).
+
+    shared_expert (optional, an ops.ExpertArenaT whose slot 0 holds the
+    block's shared expert, same quantisation as the routed tier) folds that
+    addition into the same launches: the call then returns
+    routed + shared_expert(x), each rounded to x's dtype before the sum."""
 
     def __init__(self, store: V4ArenaStore, layer: int, gate, top_k: int,
                  swiglu_limit: float = 10.0, fused_decode: bool = False,
-                 overlap_hits: bool = False, fp32_swiglu: bool = False):
+                 overlap_hits: bool = False, fp32_swiglu: bool = False, shared_expert=None):
         super().__init__(store, layer, gate, bias=None, top_k=top_k)
+        self.shared_expert = shared_expert
         self.swiglu_limit = swiglu_limit
         self.scores_follow_output = True
         # The decode path always fuses gate/up + SwiGLU; the flag is accepted

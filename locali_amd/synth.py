@@ -101,3 +101,77 @@ def zipf_router_inputs(tokens: int, n_experts: int, d_model: int, s: float = 1.1
     w = torch.zeros(n_experts, d_model, dtype=dtype, device=device)
     w[:, :n_experts] = torch.eye(n_experts, dtype=dtype, device=device)
     return x, w
+
+
+def layered_zipf_logits(tokens: int, layers: int, n_experts: int, s: float = 1.1, rho: float = 0.6,
+                        *, seed: int, device="cpu"):
+    """Router logits [tokens, layers, E] for a decode loop over a layer stack:
+    layer l ranks the experts by its own seeded permutation with
+    p(rank) ~ rank^-s, and adds Gumbel noise whose Gaussian copula is AR(1)
+    across layers with coefficient rho (z_l = rho z_{l-1} + sqrt(1-rho^2) n_l,
+    g = -log(-log Phi(z))). Each layer's marginal is therefore exactly the
+    Zipf sample without replacement of zipf_logits, and a token's noise at
+    consecutive layers is correlated."""
+    g = _gen(seed, device)
+    logp = -s * torch.log(torch.arange(1, n_experts + 1, device=device, dtype=torch.float64))
+    base = torch.empty(layers, n_experts, dtype=torch.float64, device=device)
+    for layer in range(layers):
+        base[layer, torch.randperm(n_experts, generator=g, device=device)] = logp
+    z = torch.randn(tokens, n_experts, generator=g, device=device, dtype=torch.float64)
+    out = torch.empty(tokens, layers, n_experts, dtype=torch.float32, device=device)
+    c = math.sqrt(1.0 - rho * rho)
+    for layer in range(layers):
+        if layer:
+            z = rho * z + c * torch.randn(tokens, n_experts, generator=g, device=device,
+                                          dtype=torch.float64)
+        u = (0.5 * torch.erfc(-z / math.sqrt(2.0))).clamp(1e-12, 1.0 - 1e-12)
+        out[:, layer] = (base[layer] - torch.log(-torch.log(u))).float()
+    return out
+
+
+def identity_router(n_experts: int, d_model: int, dtype=torch.bfloat16, device="cpu"):
+    """Wg = [I_E | 0]: x . Wg^T is x[:, :E], so router inputs carry the logits."""
+    if d_model < n_experts:
+        raise ValueError("identity routing needs d_model >= n_experts")
+    w = torch.zeros(n_experts, d_model, dtype=dtype, device=device)
+    w[:, :n_experts] = torch.eye(n_experts, dtype=dtype, device=device)
+    return w
+
+
+def stack_index(layers: int, n_experts: int, top_k: int, d_model: int, d_ff: int, *, bits: int = 2,
+                bits_down: int | None = None, group: int = 64, meta: str = "BF16") -> dict:
+    """Expert index (locali_amd.index schema) of a synthetic layer stack whose
+    bytes live in host memory, not in files: records name a shard that is
+    never opened, so the store must be given a host_source."""
+    bits_down = bits if bits_down is None else bits_down
+    msz = 2
+    shapes = {"gate_proj": (d_ff, d_model, bits), "up_proj": (d_ff, d_model, bits),
+              "down_proj": (d_model, d_ff, bits_down)}
+    entry = {"tier": "cold"}
+    for proj, (rows, cols, b) in shapes.items():
+        words = cols * b // 32
+        entry[proj] = {"weight": ["", "host", 0, rows * words * 4, [rows, words], "U32"],
+                       "scales": ["", "host", 0, rows * (cols // group) * msz, [rows, cols // group], meta],
+                       "biases": ["", "host", 0, rows * (cols // group) * msz, [rows, cols // group], meta]}
+    experts = {f"L{layer}.E{e}": entry for layer in range(layers) for e in range(n_experts)}
+    total = sum(entry[p][a][3] for p in shapes for a in ("weight", "scales", "biases"))
+    return {"format": 1, "model": "synthetic", "snapshot": "", "layers": layers,
+            "num_experts": n_experts, "top_k": top_k,
+            "quantization": {"cold": {"bits": bits, "group_size": group, "mode": "affine"}},
+            "expert_bytes": total * layers * n_experts, "experts": experts}
+
+
+def host_payloads(arena: ExpertArenaT) -> torch.Tensor:
+    """[n_slots, expert bytes] uint8 on the host (pinned when a GPU is present):
+    every slot's nine records back to back in (gate, up, down) x (weight,
+    scales, biases) order, the host_source layout."""
+    projs = (arena.gate, arena.up, arena.down)
+    parts = [t.reshape(t.shape[0], -1).view(torch.uint8) for p in projs
+             for t in (p.weight, p.scales, p.biases)]
+    n, per = parts[0].shape[0], sum(t.shape[1] for t in parts)
+    out = torch.empty(n, per, dtype=torch.uint8, pin_memory=torch.cuda.is_available())
+    off = 0
+    for t in parts:
+        out[:, off:off + t.shape[1]].copy_(t)
+        off += t.shape[1]
+    return out

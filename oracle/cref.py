@@ -38,7 +38,12 @@ class CRef:
         self.lib.oracle_moe_layer.restype = ctypes.c_int
         self.lib.oracle_router.argtypes = [P, P, P] + [ctypes.c_int] * 6 + [ctypes.c_float, P, P]
         self.lib.oracle_round_array.argtypes = [P, P, ctypes.c_int, ctypes.c_int]
+        self.lib.oracle_set_threads.argtypes = [ctypes.c_int]
         self._keep = []
+
+    def set_threads(self, n: int) -> None:
+        """OpenMP threads of the moe_layer / qmv loops (0: all processors)."""
+        self.lib.oracle_set_threads(int(n))
 
     def proj(self, arr, dt: str) -> OProj:
         """arr = (w uint32 [S,N,W], s uint16 [S,N,G], b uint16 [S,N,G], bits, group)."""

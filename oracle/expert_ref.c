@@ -16,6 +16,7 @@
  * T is bf16 (dt = 2) or fp16 (dt = 1); values travel as uint16 bit patterns.
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -244,3 +245,7 @@ void oracle_router(const float *x, const float *wg, const float *bias, int T,
 void oracle_round_array(const float *in, float *out, int n, int dt) {
     for (int i = 0; i < n; i++) out[i] = round_dt(in[i], dt);
 }
+
+/* Threads of the parallel loops above (n <= 0: every processor), so the CPU
+ * baseline can be timed on one core and on all of them in one process. */
+void oracle_set_threads(int n) { omp_set_num_threads(n > 0 ? n : omp_get_num_procs()); }

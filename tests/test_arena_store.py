@@ -77,6 +77,37 @@ def test_fills_land_the_experts_bytes(ckpt, packed):
         st.close()
 
 
+def test_host_source_fills_land_the_experts_bytes(ckpt, tmp_path):
+    """A host-memory arena copies misses from host_source, never the files:
+    the index's files are gone and the slots still hold the exact bytes."""
+    import numpy as np
+    _, truth, index, _ = ckpt
+    moved = tmp_path / "v4.idx"
+    moved.write_text(index.read_text().replace(str(index.parent), str(tmp_path / "absent")))
+    calls = []
+
+    def src(layer, expert):
+        calls.append((layer, expert))
+        return torch.from_numpy(np.frombuffer(expert_bytes(truth, layer, expert), np.uint8).copy())
+
+    st = _store(moved, 5, host_source=src)
+    try:
+        for layer, experts in ((0, [1, 2]), (2, [7, 1]), (0, [2, 4])):
+            placed = st.slots_for(layer, experts)
+            for e, (t, s) in placed.items():
+                assert _slot_bytes(st, t, s) == expert_bytes(truth, layer, e)
+        assert calls == [(0, 1), (0, 2), (2, 7), (2, 1), (0, 4)]
+        assert st.bytes_read == 5 * st.item["cold"] and st.stats()["evictions"] == 1
+    finally:
+        st.close()
+    bad = _store(moved, 4, host_source=lambda layer, e: torch.zeros(3, dtype=torch.uint8))
+    try:
+        with pytest.raises(ValueError, match="host bytes"):
+            bad.slots_for(0, [1])
+    finally:
+        bad.close()
+
+
 @pytest.mark.parametrize("policy,slots", [("lru", 5), ("lru", 9), ("slru-all", 9), ("slru-all", 13),
                                           ("lfu-decay", 5), ("lfu-decay", 8)])
 def test_native_planner_matches_the_oracle_driven_the_same_way(ckpt, policy, slots):

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from checkpoint_fixture import make_index, make_snapshot
+from checkpoint_fixture import expert_bytes, make_index, make_snapshot
 from gpu_helpers import arena_numpy, assert_close_terms, banner
 from locali_amd import ops, synth
 from locali_amd.dsv4_arena import V4ArenaMoE, V4ArenaStore, V4Gate
@@ -161,5 +161,93 @@ def test_v4_gate_protocol_and_oracle_parity(ckpt, oracle_lib):
                                             arena_numpy(truth[1], float_meta=False), "bf16",
                                             return_terms=True)
         assert_close_terms(got.float().cpu().numpy(), want, terms, "v4 arena vs oracle")
+    finally:
+        store.close()
+
+
+def _host_source(truth):
+    """Pinned host copies of every expert, nine records back to back."""
+    cache = {}
+
+    def src(layer, expert):
+        if (layer, expert) not in cache:
+            raw = np.frombuffer(expert_bytes(truth, layer, expert), dtype=np.uint8)
+            cache[(layer, expert)] = torch.from_numpy(raw.copy()).pin_memory()
+        return cache[(layer, expert)]
+    return src
+
+
+@pytest.mark.parametrize("policy", ["lru", "lfu-decay"])
+def test_host_source_fills_evict_and_stay_exact(ckpt, policy):
+    """Misses copied from pinned host memory on the fill stream (no file
+    reads) through evictions in a 6-slot arena: every call equals the
+    resident kernels bit for bit, and prefill-sized calls too."""
+    truth, index, _ = ckpt
+    banner(f"v4 arena host source: 6 usable slots, policy {policy}")
+    store = V4ArenaStore(index, ceiling_gb=7 * _item(index) / 1e9 + 1e-6, threads=2,
+                         cache_policy=policy, host_source=_host_source(truth))
+    rng = np.random.default_rng(5)
+    try:
+        resident = [_gpu(t) for t in truth]
+        gates = [FixedGate(None, None) for _ in range(LAYERS)]
+        mods = [V4ArenaMoE(store, L, gates[L], K) for L in range(LAYERS)]
+        for step in range(8):
+            T = 1 if step % 3 else 3
+            x = torch.from_numpy(rng.standard_normal((T, D)).astype(np.float32)).to(torch.bfloat16).cuda()
+            for L in range(LAYERS):
+                # 3 experts per call: this call's and the previous call's (pinned) fit 6 slots
+                pool = rng.choice(E, size=3, replace=False)
+                ids = np.stack([rng.choice(pool, size=K, replace=False) for _ in range(T)])
+                w = rng.random((T, K)).astype(np.float32)
+                gates[L].indices = torch.tensor(ids, dtype=torch.int32, device="cuda")
+                gates[L].scores = torch.tensor(w / w.sum(1, keepdims=True), device="cuda")
+                got = mods[L](x)
+                assert torch.equal(got, _direct(resident[L], x, gates[L].indices, gates[L].scores)), \
+                    f"step {step} layer {L}"
+                x = got
+        st = store.stats()
+        assert st["evictions"] > 0 and st["misses"] > 0
+        assert st["bytes_read"] == st["misses"] * store.item["cold"]
+    finally:
+        store.close()
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_shared_expert_folds_into_the_call(ckpt, oracle_lib, T):
+    """V4ArenaMoE(shared_expert=...) returns routed + shared_experts(x) as
+    the engine block forms it (dsv4_engine.py:259): bit-exact against the
+    expert kernels called with the same shared expert on resident weights,
+    within tolerance of the oracle's routed-then-shared rounding, and for a
+    decode call exactly the routed call's output plus the shared expert
+    alone, summed in bf16."""
+    from oracle import cref
+    truth, index, _ = ckpt
+    banner(f"v4 arena shared expert folded T={T}")
+    shared_cpu = synth.expert_arena(1, D, DFF, bits_gate_up=2, group=64, dtype=torch.bfloat16,
+                                    seed=41, zero_slot=False)
+    shared = _gpu(shared_cpu)
+    store = V4ArenaStore(index, ceiling_gb=(E + 1) * _item(index) / 1e9 + 1e-6, threads=2)
+    try:
+        g = torch.Generator().manual_seed(9)
+        x = (torch.randn(T, D, generator=g) * 0.5).to(torch.bfloat16).cuda()
+        ind = torch.tensor([[1, 4], [4, 5], [0, 1]][:T], dtype=torch.int32, device="cuda")
+        sc = torch.tensor([[0.6, 0.4], [0.3, 0.7], [0.5, 0.5]][:T], device="cuda")
+        folded = V4ArenaMoE(store, 0, FixedGate(ind, sc), K, shared_expert=shared)(x)
+        resident = _gpu(truth[0])
+        if T <= 2:
+            direct = ops.expert_decode(resident, shared, x, ind, sc)
+            routed = V4ArenaMoE(store, 0, FixedGate(ind, sc), K)(x)
+            alone = ops.expert_decode(shared, None, x, torch.zeros(T, 1, dtype=torch.int32, device="cuda"),
+                                      torch.ones(T, 1, device="cuda"))
+            assert torch.equal(folded, routed + alone)
+        else:
+            soe = torch.arange(E, dtype=torch.int32, device="cuda")
+            direct = ops.expert_grouped(resident, shared, x, ind, soe, sc, ops.Workspace(), n_experts=E)
+        assert torch.equal(folded, direct)
+        want, terms = cref.load().moe_layer(x.float().cpu().numpy(), ind.cpu().numpy(),
+                                            sc.cpu().numpy(), arena_numpy(truth[0], float_meta=False),
+                                            "bf16", shared=arena_numpy(shared_cpu, float_meta=False),
+                                            return_terms=True)
+        assert_close_terms(folded.float().cpu().numpy(), want, terms, "folded shared vs oracle")
     finally:
         store.close()
