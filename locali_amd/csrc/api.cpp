@@ -9,7 +9,7 @@
 #include <cstring>
 #include <string>
 
-#include "mfma_grouped.hpp"
+#include "mfma_wide.hpp"
 #include "launch.hpp"
 
 using namespace locali;
@@ -259,24 +259,23 @@ int check_decode_args(const locali_expert_arena *routed, const locali_expert_are
 }
 
 // The matrix-core grouped path needs 2- or 4-bit codes (gate and up alike),
-// groups of a multiple of 64, rows in multiples of 64, columns in multiples
-// of kMfmaColsAlign holding a multiple of 8 groups, its staged inputs within
-// 64 KiB of LDS, and prepared inputs (2 bytes per value) below 2 GiB so that
-// its buffer offsets stay 31-bit; the shared expert must match the routed one
-// (they share prepared inputs).
+// groups of a multiple of 64 with a multiple of 8 per row, rows in multiples
+// of 128, columns in multiples of kMfmaColsAlign, its staged scales, biases
+// and sums within the LDS of a workgroup, and prepared inputs (2 bytes per value) below 2 GiB so
+// that its buffer offsets stay 31-bit; the shared expert must match the
+// routed one (they share prepared inputs).
 bool mfma_eligible(const locali_expert_arena *routed, const locali_expert_arena *shared, int64_t tokens,
                    int64_t routes) {
     if (2 * tokens * routed->gate.cols >= (int64_t{1} << 31) ||
         2 * routes * routed->down.cols >= (int64_t{1} << 31))
         return false;
     auto ok = [](const locali_qproj &p) {
-        const int gpr = p.cols / p.group_size;
-        const size_t lds = sizeof(float2) * (p.cols / 64) * kMfmaTileTokens +
-                           sizeof(uint16_t) * 4 * kMfmaRows * (p.cols / 64);
-        return (p.bits == 2 || p.bits == 4) && p.group_size % 64 == 0 && p.rows % kMfmaRows == 0 &&
-               p.cols % kMfmaColsAlign == 0 && gpr % 8 == 0 && lds <= 64 * 1024;
+        return (p.bits == 2 || p.bits == 4) && p.group_size % 64 == 0 && p.rows % kWideRows == 0 &&
+               p.cols % kMfmaColsAlign == 0 && (p.cols / p.group_size) % 8 == 0;
     };
     if (!ok(routed->gate) || !ok(routed->up) || !ok(routed->down)) return false;
+    if (wide_lds_bytes(routed->gate.cols, 2) > kWideMaxLds || wide_lds_bytes(routed->down.cols, 1) > kWideMaxLds)
+        return false;
     if (routed->gate.bits != routed->up.bits) return false;
     if (shared && (shared->gate.bits != routed->gate.bits || shared->up.bits != routed->up.bits ||
                    shared->down.bits != routed->down.bits || !ok(shared->gate) || !ok(shared->up) ||
@@ -308,9 +307,9 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     int32_t *tiles = at<int32_t>(ws, lay.tiles);
     int32_t *n_tiles = at<int32_t>(ws, lay.n_tiles);
     uint16_t *gy = at<uint16_t>(ws, lay.gy);
-    const int max_tiles = grouped_max_tiles(tokens, top_k, shared ? 1 : 0, n_experts, kMfmaTileTokens);
+    const int max_tiles = grouped_max_tiles(tokens, top_k, shared ? 1 : 0, n_experts, kWideTokens);
     if (max_tiles > lay.max_tiles) return fail(LOCALI_E_WORKSPACE, "grouped: tile list too small");
-    hipError_t e = launch_dispatch(route_slot, R, n_slots, shared ? tokens : 0, kMfmaTileTokens,
+    hipError_t e = launch_dispatch(route_slot, R, n_slots, shared ? tokens : 0, kWideTokens,
                                    at<int32_t>(ws, lay.seg_start), at<int32_t>(ws, lay.sorted_route),
                                    route_pos, tiles, n_tiles, max_tiles, st);
     if (e != hipSuccess) return hip_fail(e, "dispatch launch");
@@ -339,7 +338,7 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     L.routes = routes;
     const bool bf16 = x_dtype == LOCALI_DT_BF16;
     // Tiles of one or two positions go to the small-tile kernels when the
-    // shapes allow; the 16-position kernels skip them.
+    // shapes allow; the 64-position kernels skip them.
     const bool small = small_tiles_eligible(routed);
     L.ta.min_count = small ? kSmallTileHost + 1 : 0;
     const int order[5] = {0, 1, 3, 2, 4};
