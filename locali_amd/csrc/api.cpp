@@ -55,19 +55,20 @@ struct Layout {
 size_t prep_bytes(int K) { return align_up(4 * static_cast<size_t>(K)) + align_up(2 * static_cast<size_t>(K)); }
 
 // Prepared inputs of the MFMA grouped kernels for n vectors of K values:
-// pairs (K / 2 u32 each: at most 8 pairs per 16 values) then per-64 sums.
+// pairs (K / 2 u32 each: at most 8 pairs per 16 values) then the per-64
+// fixup operands (16 bytes each).
 size_t mfma_batch_bytes(int n, int K) {
     return align_up(sizeof(uint32_t) * static_cast<size_t>(n) * (K / 2)) +
-           align_up(sizeof(float2) * static_cast<size_t>(n) * (K / 64 + 1));
+           align_up(sizeof(uint4) * static_cast<size_t>(n) * (K / 64 + 1));
 }
 
 MfmaVec mfma_batch(void *base, int n, int K) {
     MfmaVec v{};
     v.pairs = static_cast<uint32_t *>(base);
     v.pairs_stride = K / 2;
-    v.gsum = reinterpret_cast<float2 *>(static_cast<char *>(base) +
-                                        align_up(sizeof(uint32_t) * static_cast<size_t>(n) * (K / 2)));
-    v.gsum_stride = K / 64;
+    v.fix = reinterpret_cast<uint4 *>(static_cast<char *>(base) +
+                                      align_up(sizeof(uint32_t) * static_cast<size_t>(n) * (K / 2)));
+    v.fix_stride = K / 64;
     return v;
 }
 

@@ -32,14 +32,16 @@ struct PrepVec {
     int64_t pairs_stride, parts_stride;
 };
 
-// Prepared inputs of the matrix-core kernels, one vector per token or
-// position: pairs [words * P] u32 (P pairs per word, as the decode layout) and
-// gsum [K / span] float2 = (magic * sum of pre-scaled values, sum of values)
-// per span of 64 values (32 for the decode path's hidden vectors).
+// Prepared inputs of the matrix-core grouped kernels, one vector per token
+// or position: pairs [words * P] u32 (P pairs per word, as the decode
+// layout) and fix [K / 64] of 8 16-bit values per 64-value block, the block's
+// sums corr = magic * (sum of pre-scaled values) and xs = (sum of values)
+// each split into three 16-bit parts: [xs_hi, xs_mid, xs_lo, corr_hi,
+// corr_mid, corr_lo, 0, 0] (make_fix).
 struct MfmaVec {
     uint32_t *pairs;
-    float2 *gsum;
-    int64_t pairs_stride, gsum_stride;
+    uint4 *fix;
+    int64_t pairs_stride, fix_stride;
 };
 
 struct RouterLaunch;

@@ -13,11 +13,13 @@
 //   A operand (activations): the same lane supplies the matching prepared
 //     pairs (x pre-scaled by 4^-j, see qgemv.hpp) of position m = lane % 16, so
 //     A and B agree on every k slot whatever order the words put the codes in.
-//   Per 64-value block the two MFMA steps start from zero and the affine
-//     group terms are applied in fp32:  acc += s * (D - magic*sum x') + b * sum x
-//     (the factorised affine GEMV of dsv4_kernels.py:75-79).
+//   The affine group terms of the factorised affine GEMV (dsv4_kernels.py:
+//     75-79), acc = sum_g s_g * (D_g - magic*sum x') + b_g * sum x, are split:
+//     the kernels scale each block's two MFMA steps by its scale in fp32 and
+//     add sum_g (b_g * xs_g - s_g * corr_g) with one more MFMA k-group per
+//     block from the fixup operands (make_fix, fix_b).
 //
-//   mfma_prep_kernel     prepared pairs + per-64 sums of the tokens' x
+//   mfma_prep_kernel     prepared pairs + per-64 fixup operands of the tokens' x
 #pragma once
 
 #include "grouped_kernels.hpp"
@@ -53,6 +55,32 @@ struct MfmaGeom {
     static_assert(kWPL * kNP == 8, "one block = two MFMA steps of 4 pairs per lane");
 };
 
+// Fixup operand of one 64-value block from its sums part = (corr, xs): each
+// split into three 16-bit parts (hi + mid + lo hold about 24 significant
+// bits, as fp32), [xs_hi, xs_mid, xs_lo, corr_hi, corr_mid, corr_lo, 0, 0].
+// Against a row's fix_b operand [b, b, b, -s, -s, -s, 0, 0] one k-group of an
+// MFMA adds b * xs - s * corr, the block's affine terms.
+template <bool BF16>
+__device__ __forceinline__ uint4 make_fix(float2 part) {
+    uint16_t x[3], c[3];
+    float vx = part.y, vc = part.x;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        x[i] = from_float<BF16>(vx);
+        vx -= to_float<BF16>(x[i]);
+        c[i] = from_float<BF16>(vc);
+        vc -= to_float<BF16>(c[i]);
+    }
+    return make_uint4(x[0] | (static_cast<uint32_t>(x[1]) << 16), x[2] | (static_cast<uint32_t>(c[0]) << 16),
+                      c[1] | (static_cast<uint32_t>(c[2]) << 16), 0u);
+}
+
+// The row's half of that product from its packed (scale | bias << 16).
+__device__ __forceinline__ u32x4 fix_b(uint32_t sb) {
+    const uint32_t sc = sb & 0xffffu, b = sb >> 16, ns = sc ^ 0x8000u;
+    return u32x4{b | (b << 16), b | (ns << 16), ns | (ns << 16), 0u};
+}
+
 // One thread per (vector, word); the W64 words of a 64-block are consecutive
 // lanes, so their sums meet by butterfly.
 template <int BITS, bool BF16>
@@ -71,7 +99,7 @@ __global__ __launch_bounds__(256) void mfma_prep_kernel(const uint16_t *__restri
         part.x += __shfl_xor(part.x, m, 64);
         part.y += __shfl_xor(part.y, m, 64);
     }
-    if (vec < n_vec && w % G::kW64 == 0) out.gsum[vec * out.gsum_stride + w / G::kW64] = part;
+    if (vec < n_vec && w % G::kW64 == 0) out.fix[vec * out.fix_stride + w / G::kW64] = make_fix<BF16>(part);
 }
 
 // Buffer resources: one 128-bit descriptor per array, held in SGPRs, so a

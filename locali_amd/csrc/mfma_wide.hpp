@@ -10,9 +10,11 @@
 //     v_bitop3_b32 per pair, magic + q * 4^j, see mfma_grouped.hpp) and runs
 //     the two MFMA steps of the block for every active 16-position block of
 //     the tile, the A operand being the positions' prepared activations read
-//     from LDS; the affine group terms are applied per block and position in
-//     fp32, acc += s * (D - magic * sum x') + b * sum x (the factorised affine
-//     GEMV of dsv4_kernels.py:75-79). Its weight words arrive by one 16-byte
+//     from LDS; each block's result is scaled by the row's group scale in
+//     fp32, and every four blocks one more MFMA k-group against the positions'
+//     fixup operands adds the blocks' b * sum x - s * magic * sum x' (the
+//     factorised affine GEMV of dsv4_kernels.py:75-79, see make_fix). Its
+//     weight words arrive by one 16-byte
 //     load per lane, chunk and projection, several chunks ahead in registers
 //     (WideDepth); every load is issued unconditionally (past the end it
 //     reads zero through an out-of-range offset), so the in-order
@@ -24,8 +26,8 @@
 //     loads in flight per lane; the 16-byte parts are XOR-swizzled by
 //     position so that the 16 positions an MFMA step reads hit distinct
 //     banks. Two LDS stages alternate, one workgroup barrier per stage.
-//     The positions' per-64 sums travel with their stage (one 16-byte load
-//     per position).
+//     The positions' fixup operands travel with their stage (one 16-byte
+//     load per position and block) into a ring of three stages.
 //   before the loop every wave helps to stage the rows' scales and biases of
 //     the whole K range with 16-byte loads (whole runs of a row), overlapped
 //     with the first weight chunks and the positions' vectors.
@@ -63,14 +65,15 @@ constexpr int kWideStageBytes = kWideTokens * 256;
 // Dynamic LDS of a wide kernel with NPROJ projections over K columns (the
 // kernels have no static LDS, so all of kWideMaxLds is theirs): two
 // activation stages, then scales / biases [block][row][2 NPROJ] (16-bit) of
-// the whole K range, then the two stages' per-64 sums [stage][block of the
-// stage][position], then the positions' vectors.
+// the whole K range, then three stages of the positions' fixup operands
+// [stage % 3][block of the stage][position], then the positions' vectors.
+constexpr int kWideFixStages = 3;
 __host__ __device__ constexpr size_t wide_meta_offset() { return 2 * kWideStageBytes; }
 __host__ __device__ constexpr size_t wide_gs_offset(int K, int nproj) {
     return wide_meta_offset() + static_cast<size_t>(K / 64) * kWideRows * 2 * nproj * sizeof(uint16_t);
 }
 __host__ __device__ constexpr size_t wide_tok_offset(int K, int nproj) {
-    return wide_gs_offset(K, nproj) + 2 * 2 * kWideTokens * sizeof(float2);
+    return wide_gs_offset(K, nproj) + kWideFixStages * 2 * kWideTokens * sizeof(uint4);
 }
 __host__ __device__ constexpr size_t wide_lds_bytes(int K, int nproj) {
     return wide_tok_offset(K, nproj) + kWideTokens * sizeof(int);
@@ -81,12 +84,12 @@ template <int NPROJ>
 struct WideLds {
     u32x4 (*a)[kWideTokens][16];   // [stage][position][swizzled 16-byte part]
     uint16_t *meta;
-    float2 *gs;
+    u32x4 (*fix)[2][kWideTokens];  // [stage % 3][block of the stage][position]
 
     __device__ __forceinline__ WideLds(unsigned char *base, int K)
         : a(reinterpret_cast<u32x4(*)[kWideTokens][16]>(base)),
           meta(reinterpret_cast<uint16_t *>(base + wide_meta_offset())),
-          gs(reinterpret_cast<float2 *>(base + wide_gs_offset(K, NPROJ))) {}
+          fix(reinterpret_cast<u32x4(*)[2][kWideTokens]>(base + wide_gs_offset(K, NPROJ))) {}
 };
 
 // Scales and biases of the workgroup's rows for every block. Item (row r,
@@ -138,39 +141,37 @@ struct WideMetaStage {
 };
 
 // Loader lane lt (0 .. 255): part lt % 16 of positions lt / 16 + 16 i,
-// i < NACT (one 16-position block each), and the stage's two per-64 sums of
-// position min(lt, 16 NACT - 1) (one 16-byte load; stored by lanes below
-// 16 NACT). Every load is issued: a stage past the last reads zero through an
-// out-of-range offset.
+// i < NACT (one 16-position block each), and the fixup operand of block
+// lt % 2 of the stage of position min(lt / 2, 16 NACT - 1) (stored by lanes
+// below 32 NACT). Every load is issued: a stage past the last reads zero
+// through an out-of-range offset.
 template <int NACT>
 struct WideLoad {
     u32x4 a[NACT];
-    u32x4 g;
+    u32x4 f;
 };
 
 template <int NACT>
 struct WideLoader {
-    __amdgpu_buffer_rsrc_t rs, grs;
-    uint32_t off[NACT], goff;
-    int part, p0, gp;
+    __amdgpu_buffer_rsrc_t rs, frs;
+    uint32_t off[NACT], foff;
+    int part, p0, fp, fb;
 
     __device__ __forceinline__ void load(WideLoad<NACT> &r, int s, int nsteps) const {
         const uint32_t past = s < nsteps ? 0u : kPastEnd;
 #pragma unroll
         for (int i = 0; i < NACT; ++i) r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[i] | past, s * 256, 0);
-        r.g = __builtin_amdgcn_raw_buffer_load_b128(grs, goff | past, s * 16, 0);
+        r.f = __builtin_amdgcn_raw_buffer_load_b128(frs, foff | past, s * 32, 0);
     }
 
-    __device__ __forceinline__ void store(const WideLoad<NACT> &r, u32x4 (*st)[16], float2 *gs, int lt) const {
+    __device__ __forceinline__ void store(const WideLoad<NACT> &r, u32x4 (*st)[16], u32x4 (*fx)[kWideTokens],
+                                          int lt) const {
 #pragma unroll
         for (int i = 0; i < NACT; ++i) {
             const int pos = p0 + 16 * i;
             st[pos][part ^ (pos & 15)] = r.a[i];
         }
-        if (lt < 16 * NACT) {
-            gs[gp] = make_float2(__uint_as_float(r.g[0]), __uint_as_float(r.g[1]));
-            gs[kWideTokens + gp] = make_float2(__uint_as_float(r.g[2]), __uint_as_float(r.g[3]));
-        }
+        if (lt < 32 * NACT) fx[fb][fp] = r.f;
     }
 };
 
@@ -228,7 +229,6 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
             ms.store(L.meta, bpg, base);
         }
     };
-    float2 *const gs0 = L.gs, *const gs1 = L.gs + 2 * kWideTokens;
 
     if (wave >= kWideCompute) {
         const int lt = threadIdx.x - 64 * kWideCompute;
@@ -239,20 +239,21 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
         __syncthreads();
         WideLoader<NACT> ld;
         ld.rs = make_rsrc(in.pairs, static_cast<uint32_t>(4 * in.pairs_stride * n_vec));
-        ld.grs = make_rsrc(in.gsum, static_cast<uint32_t>(sizeof(float2) * in.gsum_stride * n_vec));
+        ld.frs = make_rsrc(in.fix, static_cast<uint32_t>(sizeof(uint4) * in.fix_stride * n_vec));
         ld.part = lt & 15;
         ld.p0 = lt >> 4;
-        ld.gp = min(lt, 16 * NACT - 1);
+        ld.fp = min(lt >> 1, 16 * NACT - 1);
+        ld.fb = lt & 1;
 #pragma unroll
         for (int i = 0; i < NACT; ++i)
             ld.off[i] = 4u * static_cast<uint32_t>(tok[ld.p0 + 16 * i] * in.pairs_stride) + 16u * ld.part;
-        ld.goff = static_cast<uint32_t>(sizeof(float2) * tok[ld.gp] * in.gsum_stride);
+        ld.foff = static_cast<uint32_t>(sizeof(uint4) * (tok[ld.fp] * in.fix_stride + ld.fb));
         constexpr int SETS = WideDepth<NACT>::kSets;
         WideLoad<NACT> r[SETS];
 #pragma unroll
         for (int q = 0; q < SETS; ++q) ld.load(r[q], q, nsteps);
         stage_meta();
-        ld.store(r[0], L.a[0], gs0, lt);
+        ld.store(r[0], L.a[0], L.fix[0], lt);
         __syncthreads();
         for (int s0 = 0; s0 < nsteps; s0 += SETS) {
 #pragma unroll
@@ -260,7 +261,7 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
                 const int s = s0 + q;
                 ld.load(r[q], s + SETS, nsteps);   // r[q] held stage s, stored during step s - 1
                 if (s < nsteps) {
-                    if (s + 1 < nsteps) ld.store(r[(q + 1) % SETS], L.a[(s + 1) & 1], (s + 1) & 1 ? gs1 : gs0, lt);
+                    if (s + 1 < nsteps) ld.store(r[(q + 1) % SETS], L.a[(s + 1) & 1], L.fix[(s + 1) % kWideFixStages], lt);
                     __syncthreads();
                 }
             }
@@ -313,7 +314,6 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
                         } else {
                             m[0] = *reinterpret_cast<const uint32_t *>(mrow);
                         }
-                        const float2 *gsb = L.gs + ((s & 1) * 2 + jb) * kWideTokens;
                         u32x4 a0[NACT], a1[NACT];
 #pragma unroll
                         for (int tb = 0; tb < NACT; ++tb) {
@@ -326,14 +326,35 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
                             u32x4 b0, b1;
                             wide_b<BITS, BF16>(block_words<WPL>(wt[j], 2 * sp + jb), magic_v, b0, b1);
                             const float sc = to_float<BF16>(static_cast<uint16_t>(m[j]));
-                            const float bi = to_float<BF16>(static_cast<uint16_t>(m[j] >> 16));
 #pragma unroll
                             for (int tb = 0; tb < NACT; ++tb) {
                                 mf32x4_t d = {0.f, 0.f, 0.f, 0.f};
                                 d = mfma_16x16x32<BF16>(a0[tb], b0, d);
                                 d = mfma_16x16x32<BF16>(a1[tb], b1, d);
-                                apply_block(acc[j][tb], d, sc, bi, gsb + 16 * tb, kb);
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) acc[j][tb][i] = fmaf(sc, d[i], acc[j][tb][i]);
                             }
+                        }
+                    }
+                    if (s & 1) {
+                        // affine terms of blocks 2s - 2 .. 2s + 1: k-lane kb takes block
+                        // 2s - 2 + kb (stages s - 1 and s of the fixup ring)
+                        const int blk = 2 * s - 2 + kb;
+                        const u32x4(*fx)[kWideTokens] = L.fix[(kb < 2 ? s - 1 : s) % kWideFixStages];
+                        const uint16_t *mrow = L.meta + (static_cast<int64_t>(blk) * kWideRows + row) * (2 * NPROJ);
+                        u32x4 fb[NPROJ];
+                        if constexpr (NPROJ == 2) {
+                            const uint2 mm = *reinterpret_cast<const uint2 *>(mrow);
+                            fb[0] = fix_b(mm.x);
+                            fb[1] = fix_b(mm.y);
+                        } else {
+                            fb[0] = fix_b(*reinterpret_cast<const uint32_t *>(mrow));
+                        }
+#pragma unroll
+                        for (int tb = 0; tb < NACT; ++tb) {
+                            const u32x4 fa = fx[kb & 1][16 * tb + nl];
+#pragma unroll
+                            for (int j = 0; j < NPROJ; ++j) acc[j][tb] = mfma_16x16x32<BF16>(fa, fb[j], acc[j][tb]);
                         }
                     }
                     __syncthreads();
@@ -410,7 +431,7 @@ __device__ __forceinline__ void wide_gateup_tile(const TileArgs &ta, const QProj
             part.x += __shfl_xor(part.x, m, 64);
             part.y += __shfl_xor(part.y, m, 64);
         }
-        if (mine && wd % wpb == 0) hout.gsum[(first + q) * hout.gsum_stride + n0 / 64 + wd / wpb] = part;
+        if (mine && wd % wpb == 0) hout.fix[(first + q) * hout.fix_stride + n0 / 64 + wd / wpb] = make_fix<BF16>(part);
     }
 }
 
