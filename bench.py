@@ -418,6 +418,44 @@ def summarize_pmc(fetch_csv, write_csv, out_path=TRAFFIC_FILE):
     return res
 
 
+def summarize_trace(trace_csv, phases_json):
+    """Per-phase kernel table (markdown) from a rocprofv3 --kernel-trace CSV of
+    a run made with --phase-log: kernels are assigned to the bench phase
+    whose [start, next start) window holds their start timestamp (both
+    clocks are CLOCK_MONOTONIC nanoseconds)."""
+    import csv
+    marks = json.loads(Path(phases_json).read_text())["phases"]
+    bounds = [(name, t0, marks[i + 1][1] if i + 1 < len(marks) else float("inf"))
+              for i, (name, t0) in enumerate(marks)]
+    per = {name: {} for name, _, _ in bounds}
+    unassigned = 0
+    for r in csv.DictReader(open(trace_csv)):
+        t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        name = r["Kernel_Name"].split("(")[0].replace("void ", "")
+        for ph, a, b in bounds:
+            if a <= t0 < b:
+                per[ph].setdefault(name, []).append((t1 - t0) / 1e3)
+                break
+        else:
+            unassigned += 1
+    out = []
+    for ph, _, _ in bounds:
+        ks = per[ph]
+        if not ks:
+            continue
+        total = sum(sum(v) for v in ks.values())
+        out += [f"### {ph}", "", "| kernel | calls | avg us | min us | max us | share of phase kernel time |",
+                "|---|---:|---:|---:|---:|---:|"]
+        for name, v in sorted(ks.items(), key=lambda kv: -sum(kv[1])):
+            if "locali" not in name and sum(v) < 0.01 * total:
+                continue
+            out.append(f"| `{name[:90]}` | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} | "
+                       f"{100 * sum(v) / total:.1f}% |")
+        out.append("")
+    out.append(f"({unassigned} dispatches outside the logged phases)")
+    print("\n".join(out))
+
+
 def measured_traffic():
     try:
         t = json.loads(TRAFFIC_FILE.read_text())
@@ -447,9 +485,16 @@ def main(argv=None):
                     help="run 256 MiB read and write reference kernels first (for --pmc byte counters)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc runs into HBM bytes per gate/up launch")
+    ap.add_argument("--phase-log", metavar="JSON",
+                    help="write the start time (CLOCK_MONOTONIC ns) of every bench phase")
+    ap.add_argument("--summarize-trace", nargs=2, metavar=("TRACE_CSV", "PHASES_JSON"),
+                    help="per-phase kernel table of a rocprofv3 kernel trace of a --phase-log run")
     args = ap.parse_args(argv)
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc)
+        return 0
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures the streamed-MoE layer on one GPU; expert-parallel runs over "
@@ -460,9 +505,16 @@ def main(argv=None):
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    marks = []
+
+    def phase(name):
+        torch.cuda.synchronize()
+        marks.append((name, time.monotonic_ns()))
+        print(f"[bench] {name}", file=sys.stderr, flush=True)
+
+    phase("setup")
     if args.copy_calibration:
         copy_calibration(dev)
-    print(f"[bench] building layer d={D} E={E} dff={DFF} {BITS}-bit g{GROUP}", file=sys.stderr, flush=True)
     arena, shared, slot_of = layer(dev, args.seed)
     w, _ = synth.uniform_router(E, D, torch.bfloat16, seed=args.seed + 2, device=dev)
     spec = ops.RouterSpec(w, K_TOP, routed_scale=1.5)
@@ -471,13 +523,13 @@ def main(argv=None):
     ws = ops.Workspace(dev)
     ws.reserve(1, D, DFF, E, K_TOP, True)
 
-    print("[bench] decode", file=sys.stderr, flush=True)
+    phase("decode (graph replay)")
     secs, wall, idx = decode_graph_run(spec, arena, shared, slot_of, X, ws, args.steps, args.warmup,
                                        not args.no_graph)
     value = args.steps / secs
     layer_bytes = 7 * EXPERT_BYTES + ROUTER_BYTES
 
-    print("[bench] stage timing", file=sys.stderr, flush=True)
+    phase("stage timing (router, gate/up, down+combine graphs)")
     st = stage_timing(spec, arena, shared, slot_of, X, ws)
     gate_bytes = GATEUP_ALG_BYTES
     achieved = gate_bytes / st["gateup"] / 1e9
@@ -523,23 +575,26 @@ def main(argv=None):
     }
     if not args.skip_prefill:
         for tokens in (64, 512):
-            print(f"[bench] prefill {tokens}", file=sys.stderr, flush=True)
+            phase(f"prefill {tokens} tokens")
             result[f"prefill{tokens}"] = prefill_run(arena, shared, slot_of, dev, tokens,
                                                      args.prefill_calls, args.seed + 100)
     if not args.skip_mixed:
-        print("[bench] mixed 2/4-bit, 32 tokens", file=sys.stderr, flush=True)
+        phase("mixed 2/4-bit, 32 tokens")
         result["mixed32"] = mixed_run(dev, 32, args.prefill_calls, args.seed + 200)
     if not args.skip_stack:
         result["stack43"] = []
         for policy in args.stack_policies.split(","):
-            print(f"[bench] 43-layer bounded arena, {policy}", file=sys.stderr, flush=True)
+            phase(f"43-layer bounded arena, {policy}")
             result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, policy,
                                                args.seed + 300))
     if not args.skip_cpu:
-        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        phase("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(arena, shared, spec, X, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
+    phase("end")
+    if args.phase_log:
+        Path(args.phase_log).write_text(json.dumps({"phases": marks}) + "\n")
     print(json.dumps(result), flush=True)
     return 0
 
