@@ -36,7 +36,7 @@ int hip_fail(hipError_t e, const char *where) {
 constexpr size_t kAlign = 256;
 constexpr int kMaxSlots = 16000;
 constexpr int kMaxExperts = 512;
-constexpr int kRouterSplitsHost = 4;
+constexpr int kRouterSplitsHost = 16;
 constexpr int kDecodeMaxTokens = 2;   // above this the grouped path is used
 
 size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }

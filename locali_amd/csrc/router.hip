@@ -16,14 +16,17 @@
 //   router_gemv_kernel   the same for any gate dtype and d % 8 == 0.
 //   router_mfma_kernel   prefill: 32 tokens x 32 experts per wave with
 //                        v_mfma_f32_32x32x16, K split kRouterSplits ways into
-//                        partial sums that the selection adds in fixed order.
+//                        partial sums that the selection adds in fixed order
+//                        (enough workgroups to stream the 2 MiB gate at 64
+//                        tokens); each stage's loads overlap the previous
+//                        stage's MFMAs.
 //   router_select_kernel one wave per token: scores, top-k (DPP arg-max over
 //                        (value, ~expert) keys), weights, slots.
 #include "router_select.hpp"
 
 namespace locali {
 
-constexpr int kRouterSplits = 4;
+constexpr int kRouterSplits = 16;
 constexpr int kRouterTokensPerPass = 8;
 static_assert(kFusedSelectMaxTokens <= kRouterTokensPerPass, "fused selection needs the gemv path");
 
@@ -177,18 +180,31 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(RouterLaunch L) {
     const uint16_t *gw = static_cast<const uint16_t *>(L.gate_w);
     const int wt = (wave & 1) * 32, we = (wave >> 1) * 32;   // wave sub-tile
     f32x16_t acc = {};
+    // Stage k0 + KT is loaded into registers while stage k0 is multiplied:
+    // a thread moves pieces c = threadIdx.x + 256 i (i < kPer) of x and of W.
+    constexpr int kPer = 64 * KT / 8 / 256;
+    uint4 xv[kPer], wv[kPer];
+    auto load_stage = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = threadIdx.x + 256 * i, row = c / (KT / 8), col = (c % (KT / 8)) * 8;
+            const int tr = min(t0 + row, L.tokens - 1), er = min(e0 + row, L.E - 1);
+            xv[i] = *reinterpret_cast<const uint4 *>(L.x + static_cast<int64_t>(tr) * L.d + k0 + col);
+            wv[i] = *reinterpret_cast<const uint4 *>(gw + static_cast<int64_t>(er) * L.d + k0 + col);
+        }
+    };
+    load_stage(kbeg);
     for (int k0 = kbeg; k0 < kend; k0 += KT) {
-        for (int c = threadIdx.x; c < 64 * KT / 8; c += 256) {
-            const int row = c / (KT / 8), col = (c % (KT / 8)) * 8;
-            uint4 xv = make_uint4(0, 0, 0, 0), wv = make_uint4(0, 0, 0, 0);
-            if (t0 + row < L.tokens)
-                xv = *reinterpret_cast<const uint4 *>(L.x + static_cast<int64_t>(t0 + row) * L.d + k0 + col);
-            if (e0 + row < L.E)
-                wv = *reinterpret_cast<const uint4 *>(gw + static_cast<int64_t>(e0 + row) * L.d + k0 + col);
-            *reinterpret_cast<uint4 *>(&xs[row][col]) = xv;
-            *reinterpret_cast<uint4 *>(&ws[row][col]) = wv;
+        // rows past the tokens / experts repeat the last one; their results
+        // are not stored
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = threadIdx.x + 256 * i, row = c / (KT / 8), col = (c % (KT / 8)) * 8;
+            *reinterpret_cast<uint4 *>(&xs[row][col]) = xv[i];
+            *reinterpret_cast<uint4 *>(&ws[row][col]) = wv[i];
         }
         __syncthreads();
+        load_stage(min(k0 + KT, kend - KT));
 #pragma unroll
         for (int kk = 0; kk < KT; kk += 16) {
             const int kofs = kk + (lane >> 5) * 8;
