@@ -31,6 +31,8 @@
  *                              (arena.py:623-624) or fp32 (arena.py:661-672)
  *   locali_moe_arena_fill      the slot fill ArenaStore._read_into/_read_many
  *                              (arena.py:179-200), as a host->HBM copy
+ *   locali_moe_arena_fill_batch the fills of several slots in one kernel that
+ *                              reads pinned host memory (same source lines)
  *   locali_moe_forward         ArenaMoE.__call__ (arena.py:508-547) for an
  *                              all-resident arena, plus the shared expert
  */
@@ -188,6 +190,23 @@ int locali_moe_combine(const void *y, const void *shared_y, const float *weights
 /* Asynchronous host -> device copy of `bytes` into an arena slot region
  * (src should be pinned host memory for a truly asynchronous copy). */
 int locali_moe_arena_fill(void *dst, const void *src_host, size_t bytes, void *stream);
+
+/* One piece of a batched fill: `bytes` from host memory at src_host to device
+ * memory at dst. */
+typedef struct {
+    void *dst;
+    const void *src_host;
+    size_t bytes;
+} locali_fill_piece;
+
+/* The records of several slot fills at once (ArenaStore._fill of several
+ * experts, arena.py:179-200): pieces whose source is pinned host memory
+ * visible to the device and whose addresses and sizes are multiples of 16
+ * bytes are copied by one kernel that reads the host memory over PCIe (64
+ * pieces per launch); any other piece by an asynchronous copy. The piece
+ * table is read before the call returns; the host memory must stay until the
+ * stream has passed the copy. */
+int locali_moe_arena_fill_batch(const locali_fill_piece *pieces, int32_t n, void *stream);
 
 /* Whole layer on an all-resident arena: router, dispatch (decode or grouped
  * by token count), experts, combine, shared expert. out [tokens, d_model]. */

@@ -45,6 +45,10 @@ class QProj(ctypes.Structure):
     ]
 
 
+class FillPiece(ctypes.Structure):
+    _fields_ = [("dst", ctypes.c_void_p), ("src_host", ctypes.c_void_p), ("bytes", ctypes.c_size_t)]
+
+
 class ExpertArena(ctypes.Structure):
     _fields_ = [("gate", QProj), ("up", QProj), ("down", QProj)]
 
@@ -95,6 +99,7 @@ _SIGNATURES = {
                                    _I, _I, _I, _P, _P, _P, _F, _I, _I, _P, _P, _SZ, _P], ctypes.c_int),
     "locali_moe_combine": ([_P, _P, _P, _I, _I, _I, _I, _I, _P, _P], ctypes.c_int),
     "locali_moe_arena_fill": ([_P, _P, _SZ, _P], ctypes.c_int),
+    "locali_moe_arena_fill_batch": ([ctypes.POINTER(FillPiece), ctypes.c_int32, _P], ctypes.c_int),
     "locali_moe_forward": ([ctypes.POINTER(Router), ctypes.POINTER(ExpertArena),
                             ctypes.POINTER(ExpertArena), _P, _P, _I, _I, _P, _F, _I, _P, _P, _P, _P,
                             _SZ, _P], ctypes.c_int),

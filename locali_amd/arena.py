@@ -91,7 +91,8 @@ class ArenaStore:
         # expert's nine records back to back in (gate, up, down) x (weight,
         # scales, biases) order: misses then copy straight from host memory
         # (a host tier for hosts whose RAM holds the experts) instead of
-        # reading the checkpoint files.
+        # reading the checkpoint files. The tensor must stay alive until the
+        # fill's future is done (the copy reads it asynchronously).
         self.host_source = host_source
         if cache_policy not in POLICIES:
             raise ValueError(f"cache_policy must be one of {POLICIES}")
@@ -276,19 +277,24 @@ class ArenaStore:
             raise ValueError(f"host_source{key}: expected {self.item[t]} host bytes (uint8)")
         return src
 
-    def _fill_from_host(self, key, t, slot, recs) -> _Landed:
-        """Queue the nine host -> HBM copies of one expert from host_source on
-        the fill stream, behind the work already queued on the compute stream
-        (a refilled slot may still be read there), and return their event."""
-        from .ops import arena_fill
-        src = self._host_bytes(key, t)
+    def _fill_from_host(self, jobs) -> _Landed:
+        """Queue the host -> HBM copies of several experts' records from
+        host_source on the fill stream as one batch, behind the work already
+        queued on the compute stream (a refilled slot may still be read there),
+        and return the event that follows them. jobs: (key, tier, slot, recs)."""
+        from .ops import arena_fill_batch_ptrs
+        pieces = []
+        for key, t, slot, recs in jobs:
+            src = self._host_bytes(key, t)
+            base, off = src.data_ptr(), 0
+            for pk, r in zip(((p, k) for p in PROJS for k in ARRS), recs):
+                arr = self.arena[(t, *pk)]
+                nbytes = self.layout[(t, *pk)][0]
+                pieces.append((arr.data_ptr() + slot * nbytes, base + off, r[3]))
+                off += r[3]
         with torch.cuda.device(self.device):
             self.fill_stream.wait_stream(torch.cuda.current_stream(self.device))
-            off = 0
-            for (p, k), r in zip(((p, k) for p in PROJS for k in ARRS), recs):
-                dst = self.arena[(t, p, k)][slot].view(torch.uint8).reshape(-1)
-                arena_fill(dst, src[off:off + r[3]], stream=self.fill_stream)
-                off += r[3]
+            arena_fill_batch_ptrs(pieces, self.fill_stream)
             ev = torch.cuda.Event()
             ev.record(self.fill_stream)
         return _Landed(ev)
@@ -434,11 +440,10 @@ class ArenaStore:
             self.bytes_read += self.item[t]
         for t in self.tiers:   # a whole tier before the next
             futs = []
+            batch = (self._fill_from_host(jobs[t]) if jobs[t] and self.host_source is not None
+                     and self.fill_stream is not None else None)
             for key, tt, s, recs in jobs[t]:
-                if self.host_source is not None and self.fill_stream is not None:
-                    f = self._fill_from_host(key, tt, s, recs)
-                else:
-                    f = self.pool.submit(self._fill, tt, s, recs, key)
+                f = batch if batch is not None else self.pool.submit(self._fill, tt, s, recs, key)
                 self.inflight.setdefault(key, []).append(f)
                 futs.append(f)
             plan[t] = futs + waits[t]

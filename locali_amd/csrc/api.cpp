@@ -596,6 +596,48 @@ int locali_moe_arena_fill(void *dst, const void *src_host, size_t bytes, void *s
     return 0;
 }
 
+int locali_moe_arena_fill_batch(const locali_fill_piece *pieces, int32_t n, void *stream) {
+    if (n < 0 || (n > 0 && !pieces)) return fail(LOCALI_E_ARG, "arena_fill_batch: bad piece table");
+    FillBatch b{};
+    int blocks = 0;
+    auto flush = [&]() -> int {
+        if (!b.n) return 0;
+        const hipError_t e = launch_fill(b, blocks, S(stream));
+        b.n = 0;
+        blocks = 0;
+        return e != hipSuccess ? hip_fail(e, "arena_fill_batch launch") : 0;
+    };
+    for (int32_t i = 0; i < n; ++i) {
+        const locali_fill_piece &p = pieces[i];
+        if (!p.bytes) continue;
+        if (!p.dst || !p.src_host) return fail(LOCALI_E_ARG, "arena_fill_batch: null pointer in piece %d", i);
+        void *dev_src = nullptr;
+        const bool aligned = (reinterpret_cast<uintptr_t>(p.dst) | reinterpret_cast<uintptr_t>(p.src_host) |
+                              p.bytes) % 16 == 0;
+        // the kernel reads only pinned memory that the runtime maps at the same
+        // address on the device (unified addressing); anything else is copied
+        if (!aligned || hipHostGetDevicePointer(&dev_src, const_cast<void *>(p.src_host), 0) != hipSuccess ||
+            dev_src != p.src_host) {
+            (void)hipGetLastError();   // not pinned here: an ordinary asynchronous copy
+            const hipError_t e = hipMemcpyAsync(p.dst, p.src_host, p.bytes, hipMemcpyHostToDevice, S(stream));
+            if (e != hipSuccess) return hip_fail(e, "arena_fill_batch copy");
+            continue;
+        }
+        const int64_t units = static_cast<int64_t>(p.bytes / 16);
+        const int nb = fill_blocks(units);
+        if (b.n == kFillMaxPieces || static_cast<int64_t>(blocks) + nb > (int64_t{1} << 30)) {
+            if (int rc = flush()) return rc;
+        }
+        b.first_block[b.n] = blocks;
+        b.units[b.n] = units;
+        b.src[b.n] = dev_src;
+        b.dst[b.n] = p.dst;
+        ++b.n;
+        blocks += nb;
+    }
+    return flush();
+}
+
 int locali_moe_forward(const locali_router *router, const locali_expert_arena *routed,
                        const locali_expert_arena *shared, const int32_t *slot_of_expert, const void *x,
                        int32_t x_dtype, int32_t tokens, const int32_t *input_ids, float swiglu_limit,

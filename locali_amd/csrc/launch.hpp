@@ -46,6 +46,18 @@ struct MfmaVec {
 
 struct RouterLaunch;
 
+// ---- batched host -> HBM fills (fill.hip) ------------------------------------
+constexpr int kFillMaxPieces = 64;
+struct FillBatch {
+    int32_t n;
+    int32_t first_block[kFillMaxPieces];    // first workgroup of each piece
+    int64_t units[kFillMaxPieces];          // 16-byte units of each piece
+    const void *src[kFillMaxPieces];        // device-visible address of pinned host memory
+    void *dst[kFillMaxPieces];
+};
+hipError_t launch_fill(const FillBatch &b, int blocks, hipStream_t st);
+int fill_blocks(int64_t units);
+
 // ---- decode path -----------------------------------------------------------
 struct DecodeLaunch {
     RouteArgs ra;

@@ -324,3 +324,29 @@ def arena_fill(dst: torch.Tensor, src: torch.Tensor, stream=None) -> None:
     st = stream.cuda_stream if stream is not None else _stream()
     rc = lib().locali_moe_arena_fill(_ptr(dst), ctypes.c_void_p(src.data_ptr()), nbytes, st)
     check(rc, "locali_moe_arena_fill")
+
+
+def arena_fill_batch_ptrs(pieces, stream) -> None:
+    """arena_fill_batch over raw (dst device address, src host address,
+    bytes) triples, for callers that keep their own address arithmetic."""
+    table = (_lib.FillPiece * max(len(pieces), 1))(*(_lib.FillPiece(d, s, n) for d, s, n in pieces))
+    rc = lib().locali_moe_arena_fill_batch(table, len(pieces), stream.cuda_stream)
+    check(rc, "locali_moe_arena_fill_batch")
+
+
+def arena_fill_batch(pieces, stream=None) -> None:
+    """Asynchronous host -> HBM copies of several (dst device tensor, src host
+    tensor) pairs in one call: pinned, 16-byte aligned sources go through one
+    kernel that reads the host memory directly (locali_moe_arena_fill_batch).
+    The host tensors must stay alive until the stream has passed the copy."""
+    table = (_lib.FillPiece * max(len(pieces), 1))()
+    for i, (dst, src) in enumerate(pieces):
+        if src.is_cuda or not dst.is_cuda:
+            raise ValueError("arena_fill_batch copies host tensors into device tensors")
+        nbytes = src.numel() * src.element_size()
+        if nbytes != dst.numel() * dst.element_size():
+            raise ValueError("arena_fill_batch size mismatch")
+        table[i] = _lib.FillPiece(dst.data_ptr(), src.data_ptr(), nbytes)
+    st = stream.cuda_stream if stream is not None else _stream()
+    rc = lib().locali_moe_arena_fill_batch(table, len(pieces), st)
+    check(rc, "locali_moe_arena_fill_batch")

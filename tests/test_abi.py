@@ -34,6 +34,7 @@ def test_headers_declare_the_planner_and_gpu_entry_points():
     assert planner <= names
     assert {"locali_moe_router", "locali_moe_dispatch", "locali_moe_expert_decode",
             "locali_moe_expert_grouped", "locali_moe_combine", "locali_moe_arena_fill",
+            "locali_moe_arena_fill_batch",
             "locali_moe_forward", "locali_moe_workspace_bytes"} <= names
 
 

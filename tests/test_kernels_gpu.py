@@ -239,6 +239,29 @@ def test_expert_grouped_matches_oracle(T, dtype, bits):
     assert exact_fraction(values(out), want) > (0.8 if dtype == torch.bfloat16 else 0.7)
 
 
+def test_arena_fill_batch_lands_every_byte():
+    """Batched fills: pinned, 16-byte aligned pieces through the copy kernel
+    (more pieces than one launch takes), plus an odd-sized piece and a
+    pageable source through the asynchronous-copy fallback."""
+    banner("arena fill batch")
+    g = torch.Generator().manual_seed(5)
+    sizes = [2 << 20, 256 << 10, 256 << 10, 16, 48 * 1024 + 16] * 14      # 70 pieces
+    host = torch.randint(0, 256, (sum(sizes) + 64,), generator=g, dtype=torch.uint8).pin_memory()
+    dev = torch.zeros(sum(sizes) + 64, dtype=torch.uint8, device=DEV)
+    pieces, off = [], 0
+    for n in sizes:
+        pieces.append((dev[off:off + n], host[off:off + n]))
+        off += n
+    odd = (dev[off:off + 37], host[off:off + 37])                           # not a multiple of 16
+    pageable = torch.randint(0, 256, (4096,), generator=g, dtype=torch.uint8)
+    dev2 = torch.zeros(4096, dtype=torch.uint8, device=DEV)
+    ops.arena_fill_batch(pieces + [odd, (dev2, pageable)])
+    torch.cuda.synchronize()
+    assert torch.equal(dev[:off + 37].cpu(), host[:off + 37])
+    assert torch.equal(dev[off + 37:].cpu(), torch.zeros(64 - 37, dtype=torch.uint8))
+    assert torch.equal(dev2.cpu(), pageable)
+
+
 def test_combine_kernel():
     banner("combine")
     T, k, d = 5, 6, 300
