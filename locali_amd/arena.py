@@ -6,7 +6,8 @@ with its own memory: the arena is a set of slot-major device tensors
 [n_slots, *shape] per (tier, projection, array) -- exactly the layout the
 expert kernels index by slot -- and a miss is a preadv of the expert's nine
 records into pinned host staging followed by an asynchronous host -> HBM copy
-on a dedicated fill stream (locali_moe_arena_fill). Slot 0 of every tier is
+on a dedicated fill stream (locali_moe_arena_fill_batch: one launch for the
+nine records). Slot 0 of every tier is
 reserved and all-zero: a masked-out route reads it and contributes exactly 0.
 
 Slots are claimed synchronously by the planner (so a later submit cannot
@@ -254,12 +255,14 @@ class ArenaStore:
             self._read(recs, host)
             off = 0
             if self.fill_stream is not None:
-                from .ops import arena_fill
+                from .ops import arena_fill_batch_ptrs
+                base, pieces = buf.data_ptr(), []
+                for pk, r in zip(((p, k) for p in PROJS for k in ARRS), recs):
+                    pieces.append((self.arena[(t, *pk)].data_ptr() + slot * self.layout[(t, *pk)][0],
+                                   base + off, r[3]))
+                    off += r[3]
                 with torch.cuda.device(self.device):
-                    for (p, k), r in zip(((p, k) for p in PROJS for k in ARRS), recs):
-                        dst = self.arena[(t, p, k)][slot].view(torch.uint8).reshape(-1)
-                        arena_fill(dst, buf[off:off + r[3]], stream=self.fill_stream)
-                        off += r[3]
+                    arena_fill_batch_ptrs(pieces, self.fill_stream)
                     ev = torch.cuda.Event()
                     ev.record(self.fill_stream)
                 ev.synchronize()
