@@ -270,36 +270,31 @@ __device__ __forceinline__ uint32_t ordered_bits(float f) {
 }
 
 template <int CTRL>
-__device__ __forceinline__ void key_max_dpp(uint32_t &hi, uint32_t &lo) {
-    const uint32_t h2 = static_cast<uint32_t>(
-        __builtin_amdgcn_update_dpp(0, static_cast<int>(hi), CTRL, 0xf, 0xf, false));
-    const uint32_t l2 = static_cast<uint32_t>(
-        __builtin_amdgcn_update_dpp(0, static_cast<int>(lo), CTRL, 0xf, 0xf, false));
-    const bool take = h2 > hi || (h2 == hi && l2 > lo);
-    hi = take ? h2 : hi;
-    lo = take ? l2 : lo;
+__device__ __forceinline__ uint32_t max_dpp(uint32_t v) {
+    return max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false)));
 }
 
-// Maximum of the key (hi, lo) over the wave, returned wave-uniform. Within
-// each 16-lane row: quad swaps (xor 1, xor 2), then half-row and row
-// mirrors, all DPP; across the four rows: lane reads of 0, 16, 32, 48.
+// Maximum of v over the wave, in every lane, without leaving the vector
+// unit: quad swaps (xor 1, xor 2), half-row and row mirrors (DPP) give each
+// 16-lane row its maximum, then the row pairs (permlane16 swap) and the wave
+// halves (permlane32 swap) meet.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max_dpp<0xB1>(v);    // quad_perm [1,0,3,2]
+    v = max_dpp<0x4E>(v);    // quad_perm [2,3,0,1]
+    v = max_dpp<0x141>(v);   // row_half_mirror
+    v = max_dpp<0x140>(v);   // row_mirror
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max(p[0], p[1]);
+    const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max(q[0], q[1]);
+}
+
+// Maximum of the 64-bit key (hi, lo) over the wave, in every lane: the
+// largest hi, then the largest lo among the lanes that hold it.
 __device__ __forceinline__ void wave_max_key(uint32_t &hi, uint32_t &lo) {
-    key_max_dpp<0xB1>(hi, lo);    // quad_perm [1,0,3,2]
-    key_max_dpp<0x4E>(hi, lo);    // quad_perm [2,3,0,1]
-    key_max_dpp<0x141>(hi, lo);   // row_half_mirror
-    key_max_dpp<0x140>(hi, lo);   // row_mirror
-    uint32_t bh = __builtin_amdgcn_readlane(static_cast<int>(hi), 0);
-    uint32_t bl = __builtin_amdgcn_readlane(static_cast<int>(lo), 0);
-#pragma unroll
-    for (int r = 16; r < 64; r += 16) {
-        const uint32_t h = __builtin_amdgcn_readlane(static_cast<int>(hi), r);
-        const uint32_t l = __builtin_amdgcn_readlane(static_cast<int>(lo), r);
-        const bool take = h > bh || (h == bh && l > bl);
-        bh = take ? h : bh;
-        bl = take ? l : bl;
-    }
-    hi = bh;
-    lo = bl;
+    const uint32_t mh = wave_max_u32(hi);
+    lo = wave_max_u32(hi == mh ? lo : 0u);
+    hi = mh;
 }
 
 __device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + __expf(-g)); }

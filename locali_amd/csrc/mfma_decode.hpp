@@ -176,16 +176,31 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     DiagSlice<BITS> &mw = win[wave];
 
     // Raw x of the window first (the prep waits only for it), then the
-    // workgroup's scales and biases by whole lines (thread i loads 16-byte
-    // pieces i and i + 64 * waves of the four arrays' rows), then the weights
-    // in consumption order.
+    // workgroup's scales and biases by whole lines, then the weights in
+    // consumption order. The metadata geometry does not depend on the slot
+    // and is worked out before any selection: thread i moves 16-byte pieces
+    // i and i + 64 * waves of the four arrays' rows, piece c = (array, row,
+    // part).
     uint32_t xw[16 / BITS];
     diag_prep_load<BITS>(xw, ra.x + static_cast<int64_t>(token) * K + wave * kDiagWindow, lane);
-    sched_fence();
+    const int mrs = 2 * gpr + 16;   // LDS bytes per metadata row
+    int ma[2], mo[2], md[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int c = static_cast<int>(threadIdx.x) + q * 64 * waves;
+        const int row = (c / waves) % (16 * RT), pc = c % waves;
+        ma[q] = c / (16 * RT * waves);
+        mo[q] = row * gpr + 8 * pc;   // u16 elements
+        md[q] = (ma[q] * 16 * RT + row) * mrs + 16 * pc;
+    }
     if constexpr (SELECT) {
         __shared__ float2 stage[256];
         __shared__ int s_slot;
         if (!shared) {   // uniform across the workgroup
+            // wave 1 also prepares wave 0's window while wave 0 selects
+            uint32_t xw0[16 / BITS];
+            if (wave == 1) diag_prep_load<BITS>(xw0, ra.x + static_cast<int64_t>(token) * K, lane);
+            sched_fence();
             if (wave == 0) {
                 const SelectOut o = select_token_any<1, 4>(sel, token, sel.logits + static_cast<int64_t>(token) * sel.E,
                                                            0, stage);
@@ -193,32 +208,31 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
                 const int sj = __builtin_amdgcn_readlane(o.slot, j);
                 if (lane == 0) s_slot = sj;
                 if (blockIdx.x == 0 && j == 0) select_store(sel, token, o);
+                if (waves == 1) diag_prep_store<BITS, BF16>(mw, xw, lane);
+            } else {
+                diag_prep_store<BITS, BF16>(mw, xw, lane);
+                if (wave == 1) diag_prep_store<BITS, BF16>(win[0], xw0, lane);
             }
-            diag_prep_store<BITS, BF16>(mw, xw, lane);
             __syncthreads();
             slot = s_slot;
         } else {
             diag_prep_store<BITS, BF16>(mw, xw, lane);
         }
     }
+    sched_fence();
     const bool valid_slot = slot >= 0 && slot < n_slots;
     const int sl = valid_slot ? slot : 0;
-    const int mrs = 2 * gpr + 16;   // LDS bytes per metadata row
     const int64_t mrow0 = static_cast<int64_t>(n0) * gpr;
     const uint16_t *m_gs = (shared ? sgate.s : gate.s) + sl * gm_slot + mrow0;
     const uint16_t *m_gb = (shared ? sgate.b : gate.b) + sl * gm_slot + mrow0;
     const uint16_t *m_us = (shared ? sup.s : up.s) + sl * um_slot + mrow0;
     const uint16_t *m_ub = (shared ? sup.b : up.b) + sl * um_slot + mrow0;
-    u32x4 mv0, mv1;
-    int md0, md1;
-    auto meta_piece = [&](int c, u32x4 &v, int &dst) {
-        const int a = c / (16 * RT * waves), row = (c / waves) % (16 * RT), pc = c % waves;
-        const uint16_t *arr = a == 0 ? m_gs : a == 1 ? m_gb : a == 2 ? m_us : m_ub;
-        v = reinterpret_cast<const u32x4 *>(arr + static_cast<int64_t>(row) * gpr)[pc];
-        dst = (a * 16 * RT + row) * mrs + 16 * pc;
-    };
-    meta_piece(static_cast<int>(threadIdx.x), mv0, md0);
-    meta_piece(static_cast<int>(threadIdx.x) + 64 * waves, mv1, md1);
+    u32x4 mv[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const uint16_t *arr = ma[q] == 0 ? m_gs : ma[q] == 1 ? m_gb : ma[q] == 2 ? m_us : m_ub;
+        mv[q] = *reinterpret_cast<const u32x4 *>(arr + mo[q]);
+    }
     sched_fence();
     const uint32_t wbytes = 4u * 16 * RT * wpr;
     const int64_t wrow0 = static_cast<int64_t>(n0) * wpr;
@@ -238,8 +252,8 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
         }
     sched_fence();
     if constexpr (!SELECT) diag_prep_store<BITS, BF16>(mw, xw, lane);
-    *reinterpret_cast<u32x4 *>(mlds + md0) = mv0;
-    *reinterpret_cast<u32x4 *>(mlds + md1) = mv1;
+    *reinterpret_cast<u32x4 *>(mlds + md[0]) = mv[0];
+    *reinterpret_cast<u32x4 *>(mlds + md[1]) = mv[1];
     __syncthreads();
     const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
     // diagonal A: lane (m, kb) feeds unit 8 line + 4 ((m / 2) % 2) + kb when m / 4 == kb

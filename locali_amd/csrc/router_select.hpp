@@ -22,7 +22,8 @@ constexpr int kRouterMaxExpertsPerLane = 8;   // E <= 512
 // everything the selection can need (logits, bias, the expert -> slot map,
 // the hash row) is loaded up front at clamped in-bounds addresses; scores use
 // the hardware exp/log; each lane sorts its M keys once, after which a round
-// of top-k is one wave-wide arg-max of the lane heads plus a pop; scores and
+// of top-k is one wave-wide arg-max of the lane heads (two 32-bit maxima
+// that stay in the vector unit) plus a pop; scores and
 // slots of the chosen experts are fetched back from LDS (`stage`, 64 * M
 // float2 per wave) by the owning lanes.
 // --------------------------------------------------------------------------
@@ -131,15 +132,15 @@ __device__ SelectOut select_token(const RouterLaunch &L, int t, const float *log
             uint32_t bh = kh[0], bl = kl[0];
             wave_max_key(bh, bl);
             best_e = bh == 0 && bl == 0 ? -1 : static_cast<int>(~bl);
-            if (kh[0] == bh && kl[0] == bl && best_e >= 0) {   // the winner pops its head
+            // the winner pops its head (keys are unique: lo holds the expert)
+            const bool pop = kh[0] == bh && kl[0] == bl && best_e >= 0;
 #pragma unroll
-                for (int i = 0; i + 1 < M; ++i) {
-                    kh[i] = kh[i + 1];
-                    kl[i] = kl[i + 1];
-                }
-                kh[M - 1] = 0u;
-                kl[M - 1] = 0u;
+            for (int i = 0; i + 1 < M; ++i) {
+                kh[i] = pop ? kh[i + 1] : kh[i];
+                kl[i] = pop ? kl[i + 1] : kl[i];
             }
+            kh[M - 1] = pop ? 0u : kh[M - 1];
+            kl[M - 1] = pop ? 0u : kl[M - 1];
         }
         if (lane == j) my_e = best_e;
     }

@@ -98,6 +98,38 @@ def test_router_precomputed_logits_zipf():
     assert np.array_equal(idx.cpu().numpy(), oi)
 
 
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_select_exact_ties(T):
+    """Integer logits in [-3, 3] tie often. They reach the router exactly:
+    x[:, :E] holds them and the identity router makes x . Wg^T = x[:, :E]
+    with one nonzero product per logit. The select kernel and (T <= 8) the
+    decode gate/up kernel's own selection must both return the stable
+    order -- descending score, ties to the lower expert id -- which is the
+    oracle's order."""
+    banner(f"select exact ties T={T}")
+    d, E, dff, k = 1024, 256, 512, 6
+    g = torch.Generator().manual_seed(40 + T)
+    x = torch.randn(T, d, generator=g)
+    x[:, :E] = torch.randint(-3, 4, (T, E), generator=g).float()
+    x = x.to(torch.bfloat16)
+    w = synth.identity_router(E, d, torch.bfloat16)
+    logits = values(x)[:, :E].astype(np.float64)
+    want = np.argsort(-logits, axis=1, kind="stable")[:, :k]
+    oi, _, _, _ = moe.route(values(x), values(w), k, routed_scale=1.5)
+    assert np.array_equal(oi, want)
+    spec = ops.RouterSpec(w.to(DEV), k, routed_scale=1.5)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    xd = x.to(DEV)
+    ridx, rw, rs = ops.router(spec, xd, ops.Workspace(), slot_of_expert=slot_of, n_slots=E + 1)
+    arena = synth.expert_arena(E + 1, d, dff, dtype=torch.bfloat16, seed=41, device=DEV)
+    out, idx, wts = ops.forward(spec, arena, None, slot_of, xd, ops.Workspace())
+    torch.cuda.synchronize()
+    assert np.array_equal(ridx.cpu().numpy(), want)
+    assert np.array_equal(idx.cpu().numpy(), want)
+    assert torch.equal(wts, rw)
+    assert torch.equal(rs.cpu(), (ridx + 1).cpu())
+
+
 # ---------------------------------------------------------------------------
 # Expert math, decode path
 # ---------------------------------------------------------------------------
