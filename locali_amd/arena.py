@@ -554,10 +554,10 @@ class ArenaMoE:
     def _apply(self, flat, ii, placed, gates, dtype, reads=None):
         from . import ops
         T = len(ii)
-        tiers = {placed[e][0] for row in ii for e in row}
-        if len(tiers) != 1:
-            raise NotImplementedError("routes spanning two tiers in one call are not supported")
-        t = tiers.pop()
+        present = [t for t in self.store.tiers if any(placed[e][0] == t for row in ii for e in row)]
+        if len(present) > 1:
+            return self._apply_tiers(flat, ii, placed, gates, dtype, reads, present)
+        t = present[0]
         if reads is not None:
             self.store.wait(reads[t])
         slots = torch.tensor([[placed[e][1] for e in row] for row in ii], dtype=torch.int32,
@@ -577,3 +577,55 @@ class ArenaMoE:
             y = ops.expert_grouped(arena, self.shared_expert, x_in, slots, ident, w, ws, n_experts=n,
                                    swiglu_limit=self.swiglu_limit, fp32_swiglu=self.fp32_swiglu)
         return y.to(dtype)
+
+    def _routes(self, arena, x_in, slots, ws):
+        """Unweighted expert outputs, one route per row of x_in: a one-route
+        call with weight 1 returns the route's down output rounded to x_in's
+        dtype."""
+        from . import ops
+        n = x_in.shape[0]
+        ones = torch.ones(n, 1, dtype=torch.float32, device=x_in.device)
+        kw = dict(swiglu_limit=self.swiglu_limit, fp32_swiglu=self.fp32_swiglu)
+        if n <= 2:
+            return ops.expert_decode(arena, None, x_in, slots, ones, ws=ws, **kw)
+        ident = torch.arange(arena.n_slots, dtype=torch.int32, device=x_in.device)
+        return ops.expert_grouped(arena, None, x_in, slots, ident, ones, ws, n_experts=arena.n_slots, **kw)
+
+    def _apply_tiers(self, flat, ii, placed, gates, dtype, reads, present):
+        """Routes spanning tiers (reference arena.py:626-672). Each tier's
+        own (token, k) entries run through that tier's experts, one route per
+        entry; a float32 accumulator takes y * w (w = the score rounded to the
+        activation dtype, then float32) tier by tier in the store's tier order
+        and, within a tier, k position by k position -- per token that is the
+        reference's row-major entry order, and each index_add_ touches a token
+        once, so the sum order is fixed. One rounding at the end, then the
+        shared expert (when folded) with one more."""
+        k = self.top_k
+        dev = flat.device
+        g = gates.to(dtype).to(torch.float32)
+        out = torch.zeros(flat.shape[0], flat.shape[1], dtype=torch.float32, device=dev)
+        ws = self._workspace()
+        for t in present:
+            if reads is not None:
+                self.store.wait(reads[t])
+            ent = [(r, j) for r, row in enumerate(ii) for j, e in enumerate(row) if placed[e][0] == t]
+            rows = torch.tensor([r for r, _ in ent], dtype=torch.long, device=dev)
+            cols = torch.tensor([j for _, j in ent], dtype=torch.long, device=dev)
+            slots = torch.tensor([[placed[ii[r][j]][1]] for r, j in ent], dtype=torch.int32, device=dev)
+            x_in = flat.index_select(0, rows).contiguous()
+            if self.store.use_f16(t) and x_in.dtype == torch.bfloat16:
+                x_in = x_in.to(torch.float16)
+            y = self._routes(self.store.expert_arena(t), x_in, slots, ws)
+            val = y.to(torch.float32) * g[rows, cols].unsqueeze(1)
+            for j in range(k):
+                sel = (cols == j).nonzero().squeeze(1)
+                if sel.numel():
+                    out.index_add_(0, rows.index_select(0, sel), val.index_select(0, sel))
+        res = out.to(dtype)
+        if self.shared_expert is not None:
+            x_s = flat.contiguous()
+            if x_s.dtype != self.shared_expert.gate.scales.dtype and x_s.dtype == torch.bfloat16:
+                x_s = x_s.to(torch.float16)
+            zero = torch.zeros(flat.shape[0], 1, dtype=torch.int32, device=dev)
+            res = res + self._routes(self.shared_expert, x_s, zero, ws).to(dtype)
+        return res

@@ -115,6 +115,35 @@ def combine(y, weights, dtype, mode="single"):
     raise ValueError(mode)
 
 
+def mixed_tiers(x, tier_of, slot, weights, arenas, order, dtype, *, limit=10.0, fp32_swiglu=False):
+    """Routes spanning tiers (arena.py:626-672). tier_of/slot [T, k] place
+    route (t, j) in arena arenas[tier_of[t, j]] at slot[t, j]; order is the
+    tiers' accumulation order (the store's tier list). Each route's y is the
+    expert output rounded to dtype; a float32 accumulator takes the float32
+    product y * w, w the weight rounded to dtype (arena.py:543, 661-662),
+    tier by tier in `order` and within a tier in row-major (token, k) order
+    (arena.py:669-672); the sum is rounded once. Returns (out, terms), terms
+    the per-element sum of |y * w|."""
+    x = np.asarray(x, dtype=np.float64)
+    T, k = np.shape(slot)
+    w = affine.round_to(weights, dtype).astype(np.float32)
+    out = np.zeros((T, x.shape[-1]), dtype=np.float32)
+    terms = np.zeros((T, x.shape[-1]))
+    for tier in order:
+        arena = arenas[tier]
+        for t in range(T):
+            for j in range(k):
+                if tier_of[t][j] != tier:
+                    continue
+                s = int(slot[t][j])
+                proj = {p: (a[0][s], a[1][s], a[2][s], a[3], a[4]) for p, a in arena.items()}
+                y = expert(x[t:t + 1], proj, dtype, limit, fp32_swiglu)[0]
+                val = y.astype(np.float32) * w[t, j]
+                out[t] = out[t] + val
+                terms[t] += np.abs(val.astype(np.float64))
+    return affine.round_to(out.astype(np.float64), dtype), terms
+
+
 def add_shared(routed, shared, dtype):
     return affine.round_to(np.asarray(routed, np.float64) + np.asarray(shared, np.float64), dtype)
 

@@ -251,3 +251,69 @@ def test_shared_expert_folds_into_the_call(ckpt, oracle_lib, T):
         assert_close_terms(folded.float().cpu().numpy(), want, terms, "folded shared vs oracle")
     finally:
         store.close()
+
+
+class _TwoTiers:
+    """The store surface ArenaMoE._apply reads, over two resident tiers."""
+    tiers = ["cold", "hot"]
+
+    def __init__(self, arenas):
+        self.arenas, self.device, self.workspace = arenas, torch.device("cuda"), None
+
+    def expert_arena(self, t):
+        return self.arenas[t]
+
+    def use_f16(self, t):
+        return False
+
+    def wait(self, reads):
+        pass
+
+    def slot_identity(self, t):
+        return torch.arange(self.arenas[t].n_slots, dtype=torch.int32, device="cuda")
+
+
+@pytest.mark.parametrize("T", [1, 2, 7])
+def test_routes_spanning_two_tiers(T):
+    """A call whose routes land in two tiers with different quantisation
+    (2-bit cold, 4-bit hot) takes the reference's mixed path (arena.py:626-672):
+    each tier's own entries through its experts, float32 products of y and the
+    dtype-rounded scores summed tier by tier, one rounding. Within the term
+    rounding bound of the oracle's restatement of that order; and a call with
+    every route in one tier still takes the single-tier path unchanged."""
+    from locali_amd.arena import ArenaMoE
+    from oracle import moe as moe_oracle
+    banner(f"two tiers T={T}")
+    d, dff, k = 1024, 512, 4
+    cold = synth.expert_arena(9, d, dff, bits_gate_up=2, dtype=torch.bfloat16, seed=51, device="cuda")
+    hot = synth.expert_arena(5, d, dff, bits_gate_up=4, dtype=torch.bfloat16, seed=52, device="cuda")
+    store = _TwoTiers({"cold": cold, "hot": hot})
+    moe = ArenaMoE(store, 0, None, None, k)
+    moe.swiglu_limit = 10.0
+    # experts 0..7 in cold slots 1..8, experts 8..11 in hot slots 1..4
+    placed = {e: ("cold", e + 1) for e in range(8)}
+    placed.update({e: ("hot", e - 7) for e in range(8, 12)})
+    g = torch.Generator().manual_seed(60 + T)
+    ii = [torch.randperm(12, generator=g)[:k].tolist() for _ in range(T)]
+    ii[0] = [9, 2, 11, 5]                  # both tiers, interleaved
+    gates = torch.rand(T, k, generator=g)
+    x = synth.activations(T, d, torch.bfloat16, seed=53, device="cuda")
+    out = moe._apply(x, ii, placed, gates.cuda(), torch.bfloat16)
+    torch.cuda.synchronize()
+    tier_of = [[placed[e][0] for e in row] for row in ii]
+    slot = np.array([[placed[e][1] for e in row] for row in ii])
+    want, terms = moe_oracle.mixed_tiers(
+        x.float().cpu().numpy(), tier_of, slot, gates.numpy(),
+        {"cold": arena_numpy(cold), "hot": arena_numpy(hot)}, ["cold", "hot"], "bf16", limit=10.0)
+    assert_close_terms(out.float().cpu().numpy(), want, terms, f"two tiers T={T}")
+    # one tier only: the single-tier path (rounded products) is what runs
+    one = [[e % 8 for e in row] for row in ii]
+    got1 = moe._apply(x, one, placed, gates.cuda(), torch.bfloat16)
+    slots1 = torch.tensor([[placed[e][1] for e in row] for row in one], dtype=torch.int32, device="cuda")
+    w = gates.cuda().float()
+    if T <= 2:
+        ref1 = ops.expert_decode(cold, None, x, slots1, w, swiglu_limit=10.0)
+    else:
+        ref1 = ops.expert_grouped(cold, None, x, slots1, torch.arange(9, dtype=torch.int32, device="cuda"),
+                                  w, ops.Workspace(), n_experts=9, swiglu_limit=10.0)
+    assert torch.equal(got1, ref1)

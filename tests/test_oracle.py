@@ -219,3 +219,43 @@ def test_dispatch_is_stable_slot_sort():
         assert counts[int(s)] == members.size
     assert np.array_equal(order[undo], np.arange(flat.size))
     assert moe.first_appearance([[3, 1], [1, 4], [3, 2]]) == [3, 1, 4, 2]
+
+
+def test_mixed_tiers_reduces_to_fp32_combine():
+    """With weights 1 and 0.5 and two routes per token every float32 product
+    and sum is exact, so the mixed-tier accumulation (arena.py:626-672) must
+    equal the fp32 combine of the same routes -- whether the routes sit in
+    one tier or are split across two tiers holding the same weights at other
+    slots. A wrong tier, slot or weight index breaks the equality; the zero
+    slot contributes nothing."""
+    rng = np.random.default_rng(21)
+    S, d, dff, k, T = 5, 256, 128, 2, 4
+    arena = {}
+    for name, (N, K, bits) in {"gate_proj": (dff, d, 2), "up_proj": (dff, d, 2),
+                               "down_proj": (d, dff, 4)}.items():
+        ws, ss, bs = [], [], []
+        for _ in range(S):
+            _, w, s, b = _rand_proj(rng, N, K, bits, 64, "bf16")
+            ws.append(w), ss.append(s), bs.append(b)
+        arena[name] = (np.stack(ws), np.stack(ss), np.stack(bs), bits, 64)
+    # tier "b" holds the same experts in reversed slot order
+    rev = {p: (a[0][::-1].copy(), a[1][::-1].copy(), a[2][::-1].copy(), a[3], a[4]) for p, a in arena.items()}
+    x = affine.round_to(rng.standard_normal((T, d)), "bf16")
+    idx = np.array([[1, 3], [4, 1], [2, 2], [3, 4]])
+    wts = np.array([[1.0, 0.5], [0.5, 1.0], [1.0, 1.0], [0.5, 0.5]], dtype=np.float32)
+    want = moe.moe_layer(x, idx, wts, arena, {e: e for e in range(S)}, "bf16", limit=1.5,
+                         combine_mode="fp32")
+    one, _ = moe.mixed_tiers(x, [["a"] * k] * T, idx, wts, {"a": arena}, ["a"], "bf16", limit=1.5)
+    assert np.array_equal(one, want)
+    tier_of = [["a", "b"], ["b", "a"], ["b", "b"], ["a", "a"]]
+    slot = np.array([[e if t == "a" else S - 1 - e for t, e in zip(tr, row)] for tr, row in zip(tier_of, idx)])
+    two, _ = moe.mixed_tiers(x, tier_of, slot, wts, {"a": arena, "b": rev}, ["a", "b"], "bf16", limit=1.5)
+    assert np.array_equal(two, want)
+    # a route in the zero slot adds exactly nothing
+    zero = {p: (np.zeros_like(a[0]), np.zeros_like(a[1]), np.zeros_like(a[2]), a[3], a[4]) for p, a in arena.items()}
+    z, _ = moe.mixed_tiers(x, [["a", "z"]] * T, np.array([[r[0], 0] for r in idx]),
+                           wts, {"a": arena, "z": zero}, ["a", "z"], "bf16", limit=1.5)
+    w1 = wts.copy()
+    w1[:, 1] = 0.0
+    assert np.array_equal(z, moe.moe_layer(x, idx, w1, arena, {e: e for e in range(S)}, "bf16", limit=1.5,
+                                           combine_mode="fp32"))
