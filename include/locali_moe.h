@@ -72,7 +72,9 @@ enum {
 
 /* One projection arena: every slot holds one expert's affine-quantised
  * matrix in MLX layout (reference arena.py:150-160 per (tier, proj, kind)):
- *   weight  uint32   [n_slots, rows, cols * bits / 32]  (LSB-first codes)
+ *   weight  uint32   [n_slots, rows, cols * bits / 32]  (codes as one
+ *           little-endian bit stream per row, least-significant bits first;
+ *           3-bit codes cross word boundaries, 32 values per 3 words)
  *   scales  dtype    [n_slots, rows, cols / group_size]
  *   biases  dtype    [n_slots, rows, cols / group_size]
  * rows = outputs, cols = inputs; dtype = meta_dtype (F16 or BF16), which must
@@ -82,7 +84,7 @@ typedef struct {
     const void *weight;
     const void *scales;
     const void *biases;
-    int32_t bits;          /* 2, 4 or 8 */
+    int32_t bits;          /* 2, 3, 4 or 8 */
     int32_t group_size;    /* 32, 64 or 128 */
     int32_t rows;
     int32_t cols;

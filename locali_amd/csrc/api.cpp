@@ -108,8 +108,8 @@ T *at(void *ws, size_t off) {
 int check_proj(const locali_qproj &p, const char *name, int32_t x_dtype) {
     if (!p.weight || !p.scales || !p.biases)
         return fail(LOCALI_E_ARG, "%s: null array", name);
-    if (p.bits != 2 && p.bits != 4 && p.bits != 8)
-        return fail(LOCALI_E_ARG, "%s: bits %d not in {2,4,8}", name, p.bits);
+    if (p.bits != 2 && p.bits != 3 && p.bits != 4 && p.bits != 8)
+        return fail(LOCALI_E_ARG, "%s: bits %d not in {2,3,4,8}", name, p.bits);
     if (p.group_size != 32 && p.group_size != 64 && p.group_size != 128)
         return fail(LOCALI_E_ARG, "%s: group_size %d not in {32,64,128}", name, p.group_size);
     if (p.rows <= 0 || p.cols <= 0 || p.cols % p.group_size)
@@ -119,14 +119,17 @@ int check_proj(const locali_qproj &p, const char *name, int32_t x_dtype) {
     if (!dtype16(p.meta_dtype) || p.meta_dtype != x_dtype)
         return fail(LOCALI_E_ARG, "%s: metadata dtype %d must equal activation dtype %d", name,
                     p.meta_dtype, x_dtype);
-    const int64_t bits_row = static_cast<int64_t>(p.cols) * p.bits;
+    // chunk geometry in the width the kernels compute in (3-bit rows are
+    // widened to 4-bit chunks of 32 values on load)
+    const int lb = lane_bits(p.bits);
+    const int64_t bits_row = static_cast<int64_t>(p.cols) * lb;
     const int64_t cpr = bits_row / 128;
     if (bits_row % 128 || !(cpr == 8 || cpr == 16 || cpr == 32 || cpr == 64 || cpr == 128 || cpr == 256))
         return fail(LOCALI_E_ARG,
                     "%s: cols*bits/128 = %lld 16-byte chunks per row unsupported "
                     "(need 8, 16, 32, 64, 128 or 256)",
                     name, static_cast<long long>(cpr));
-    const int vpc = 128 / p.bits;
+    const int vpc = 128 / lb;
     if (p.group_size < vpc && !(p.bits == 2 && p.group_size == 32))
         return fail(LOCALI_E_ARG, "%s: group %d smaller than a 16-byte chunk", name, p.group_size);
     return 0;
@@ -222,7 +225,8 @@ DecodeLaunch decode_launch(const locali_expert_arena *routed, const locali_exper
     L.ca.out = static_cast<uint16_t *>(out);
     L.ca.mode = combine_mode;
     const bool bf16 = x_dtype == LOCALI_DT_BF16;
-    L.hprep = prep_batch(at<void>(ws, lay.hprep), L.routes, routed->down.cols, routed->down.bits, bf16);
+    L.hprep = prep_batch(at<void>(ws, lay.hprep), L.routes, routed->down.cols, lane_bits(routed->down.bits),
+                         bf16);
     return L;
 }
 

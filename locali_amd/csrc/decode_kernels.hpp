@@ -38,7 +38,9 @@ template <int LPR>
 constexpr int gateup_rows_per_wave_load() { return LPR >= 16 ? 8 : LPR / 2; }
 
 // ---------------------------------------------------------------------------
-template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J>
+// SB: bits of the stored codes (BITS, or 3 for 3-bit rows widened to the
+// 4-bit geometry on load).
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int SB = BITS>
 __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_route_kernel(
     RouteArgs ra, QProj gate, QProj up, QProj sgate, QProj sup, uint16_t *__restrict__ h,
     PrepVec hout, int down_bits, float limit, int fp32_swiglu) {
@@ -66,7 +68,7 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_route_kernel(
     const bool active = row0 < N;
     const bool valid_slot = slot >= 0 && slot < pg.n_slots;
     const int sl = valid_slot ? slot : 0;
-    const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;   // words per row
+    const int64_t wpr = static_cast<int64_t>(K) * SB / 32;     // words per row
     const int gpr = K / pg.group;                               // groups per row
 
     // The token's activations first (loads retire in issue order, so rows
@@ -112,8 +114,8 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_route_kernel(
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-        load_row_weights<CPL, LPR, GPC>(wg[j], gw + row * wpr, lane_in_row);
-        load_row_weights<CPL, LPR, GPC>(wu[j], uw + row * wpr, lane_in_row);
+        load_row_weights<CPL, LPR, GPC, SB>(wg[j], gw + row * wpr, lane_in_row);
+        load_row_weights<CPL, LPR, GPC, SB>(wu[j], uw + row * wpr, lane_in_row);
     }
     sched_fence();
     // Prepare x into LDS while the weights stream in (waits only for the x
@@ -170,7 +172,7 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_route_kernel(
 }
 
 // ---------------------------------------------------------------------------
-template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int WAVES>
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int WAVES, int SB = BITS>
 __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, QProj down,
                                                                    QProj sdown, PrepVec hin,
                                                                    CombineArgs ca) {
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, 
     const int per_token = ra.top_k + ra.n_shared;
     const int routed = ra.tokens * ra.top_k;
     const int row0 = blockIdx.x * RB;
-    const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+    const int64_t wpr = static_cast<int64_t>(K) * SB / 32;
     const int gpr = K / down.group;
 
     if (wave < per_token) {
@@ -214,7 +216,7 @@ __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, 
 #pragma unroll
         for (int q = 0; q < J; ++q) {
             const int row = min(row0 + q * G::kRPL + row_sub, N - 1);
-            load_row_weights<CPL, LPR, GPC>(rd[q], w + row * wpr, lane_in_row);
+            load_row_weights<CPL, LPR, GPC, SB>(rd[q], w + row * wpr, lane_in_row);
         }
         sched_fence();
         xvec_finish(xv);
@@ -249,21 +251,23 @@ __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, 
 // translation unit (decode_b<bits>_<dtype>.hip) so the variants compile in
 // parallel.
 // ---------------------------------------------------------------------------
-template <int BITS, bool BF16, int CPL, int LPR, int GPC>
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int SB = BITS>
 hipError_t launch_gateup_t(const DecodeLaunch &L, hipStream_t st) {
     constexpr int J = gateup_rows_per_wave_load<LPR>();
     using G = Geom<BITS, CPL, LPR, GPC>;
     const int rows_per_block = kGateUpWaves * J * G::kRPL;
-    // the epilogue prepares whole words of the down input
-    if (L.hprep.pairs && rows_per_block % (32 / L.down.bits)) return hipErrorInvalidValue;
+    // the epilogue prepares whole words of the down input, in the geometry the
+    // down kernel computes in (4-bit for 3-bit codes)
+    const int down_bits = lane_bits(L.down.bits);
+    if (L.hprep.pairs && rows_per_block % (32 / down_bits)) return hipErrorInvalidValue;
     dim3 grid((L.gate.rows + rows_per_block - 1) / rows_per_block, L.routes);
-    hipLaunchKernelGGL((gateup_route_kernel<BITS, BF16, CPL, LPR, GPC, J>), grid,
+    hipLaunchKernelGGL((gateup_route_kernel<BITS, BF16, CPL, LPR, GPC, J, SB>), grid,
                        dim3(64 * kGateUpWaves), 0, st, L.ra, L.gate, L.up, L.sgate, L.sup,
-                       L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu);
+                       L.h, L.hprep, down_bits, L.limit, L.fp32_swiglu);
     return hipGetLastError();
 }
 
-template <int BITS, bool BF16, int CPL, int LPR, int GPC>
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int SB = BITS>
 hipError_t launch_down_t(const DecodeLaunch &L, hipStream_t st) {
     constexpr int J = LPR >= 8 ? 8 : LPR;
     using G = Geom<BITS, CPL, LPR, GPC>;
@@ -271,10 +275,10 @@ hipError_t launch_down_t(const DecodeLaunch &L, hipStream_t st) {
     const int rows_per_block = J * G::kRPL;
     dim3 grid((L.down.rows + rows_per_block - 1) / rows_per_block, L.ra.tokens);
     if (per_token <= 8) {
-        hipLaunchKernelGGL((down_combine_kernel<BITS, BF16, CPL, LPR, GPC, J, 8>), grid,
+        hipLaunchKernelGGL((down_combine_kernel<BITS, BF16, CPL, LPR, GPC, J, 8, SB>), grid,
                            dim3(64 * per_token), 0, st, L.ra, L.down, L.sdown, L.hprep, L.ca);
     } else if (per_token <= 16) {
-        hipLaunchKernelGGL((down_combine_kernel<BITS, BF16, CPL, LPR, GPC, J, 16>), grid,
+        hipLaunchKernelGGL((down_combine_kernel<BITS, BF16, CPL, LPR, GPC, J, 16, SB>), grid,
                            dim3(64 * per_token), 0, st, L.ra, L.down, L.sdown, L.hprep, L.ca);
     } else {
         return hipErrorInvalidValue;
@@ -283,11 +287,11 @@ hipError_t launch_down_t(const DecodeLaunch &L, hipStream_t st) {
 }
 
 // which: 0 = gate/up, 1 = down+combine. (CPL, LPR) from 16-byte chunks per row.
-template <int BITS, bool BF16, int GPC>
+template <int BITS, bool BF16, int GPC, int SB = BITS>
 hipError_t decode_geometry(int which, int cpr, const DecodeLaunch &L, hipStream_t st) {
 #define LOCALI_GEOM(CPL, LPR)                                                  \
-    return which == 0 ? launch_gateup_t<BITS, BF16, CPL, LPR, GPC>(L, st)      \
-                      : launch_down_t<BITS, BF16, CPL, LPR, GPC>(L, st)
+    return which == 0 ? launch_gateup_t<BITS, BF16, CPL, LPR, GPC, SB>(L, st)  \
+                      : launch_down_t<BITS, BF16, CPL, LPR, GPC, SB>(L, st)
     switch (cpr) {
     case 8: LOCALI_GEOM(1, 8);
     case 16: LOCALI_GEOM(1, 16);

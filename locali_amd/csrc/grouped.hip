@@ -177,6 +177,8 @@ hipError_t grouped_b4_bf16(int, int, int, const GroupedKernelLaunch &, hipStream
 hipError_t grouped_b4_f16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
 hipError_t grouped_b8_bf16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
 hipError_t grouped_b8_f16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
+hipError_t grouped_b3_bf16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
+hipError_t grouped_b3_f16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
 
 // which: 0 = gate/up + SwiGLU, 1 = down.
 hipError_t launch_grouped_kernels(int which, const GroupedKernelLaunch &L, hipStream_t st) {
@@ -186,6 +188,7 @@ hipError_t launch_grouped_kernels(int which, const GroupedKernelLaunch &L, hipSt
     case 2: return L.bf16 ? grouped_b2_bf16(which, gpc, cpr, L, st) : grouped_b2_f16(which, gpc, cpr, L, st);
     case 4: return L.bf16 ? grouped_b4_bf16(which, gpc, cpr, L, st) : grouped_b4_f16(which, gpc, cpr, L, st);
     case 8: return L.bf16 ? grouped_b8_bf16(which, gpc, cpr, L, st) : grouped_b8_f16(which, gpc, cpr, L, st);
+    case 3: return L.bf16 ? grouped_b3_bf16(which, gpc, cpr, L, st) : grouped_b3_f16(which, gpc, cpr, L, st);
     default: return hipErrorInvalidValue;
     }
 }

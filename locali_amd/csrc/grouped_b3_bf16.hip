@@ -1,0 +1,13 @@
+// Grouped kernels for 3-bit codes with bf16 activations: the 4-bit kernels
+// reading 3-bit rows (each 32-value chunk widened to 4-bit codes on load).
+#include "grouped_kernels.hpp"
+
+namespace locali {
+
+hipError_t grouped_b3_bf16(int which, int gpc, int cpr, const GroupedKernelLaunch &L,
+                            hipStream_t st) {
+    if (gpc != 1) return hipErrorInvalidValue;
+    return grouped_geometry<4, true, 1, 3>(which, cpr, L, st);
+}
+
+}  // namespace locali

@@ -80,7 +80,9 @@ __device__ __forceinline__ void prep_tile(XLds<BITS, BF16, CPL, LPR> (&xl)[TT], 
     }
 }
 
-template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int TT>
+// SB: bits of the stored codes (BITS, or 3 for 3-bit rows widened to the
+// 4-bit geometry on load).
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int TT, int SB = BITS>
 __global__ __launch_bounds__(64 * kGroupedWaves) void gateup_grouped_kernel(
     TileArgs ta, QProj gate, QProj up, QProj sgate, QProj sup, uint16_t *__restrict__ h, float limit,
     int fp32_swiglu) {
@@ -109,7 +111,7 @@ __global__ __launch_bounds__(64 * kGroupedWaves) void gateup_grouped_kernel(
     const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * RPW;
     if (row0 >= N) return;
     const int sl = shared ? 0 : slot;
-    const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+    const int64_t wpr = static_cast<int64_t>(K) * SB / 32;
     const int gpr = K / pg.group;
     const uint32_t *gw = pg.w + sl * pg.w_slot, *uw = pu.w + sl * pu.w_slot;
     const uint16_t *gs = pg.s + sl * pg.m_slot, *gb = pg.b + sl * pg.m_slot;
@@ -118,9 +120,9 @@ __global__ __launch_bounds__(64 * kGroupedWaves) void gateup_grouped_kernel(
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-        load_row<BITS, CPL, LPR, GPC>(wg[j], gw + row * wpr, gs + row * gpr, gb + row * gpr,
+        load_row<BITS, CPL, LPR, GPC, SB>(wg[j], gw + row * wpr, gs + row * gpr, gb + row * gpr,
                                       pg.group, lane_in_row);
-        load_row<BITS, CPL, LPR, GPC>(wu[j], uw + row * wpr, us + row * gpr, ub + row * gpr,
+        load_row<BITS, CPL, LPR, GPC, SB>(wu[j], uw + row * wpr, us + row * gpr, ub + row * gpr,
                                       pu.group, lane_in_row);
     }
     XVec<BITS, BF16, CPL, GPC> xv[TT];
@@ -153,7 +155,7 @@ __global__ __launch_bounds__(64 * kGroupedWaves) void gateup_grouped_kernel(
     }
 }
 
-template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int TT>
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int J, int TT, int SB = BITS>
 __global__ __launch_bounds__(64 * kGroupedWaves) void down_grouped_kernel(
     TileArgs ta, QProj down, QProj sdown, const uint16_t *__restrict__ h, uint16_t *__restrict__ y) {
     using G = Geom<BITS, CPL, LPR, GPC>;
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(64 * kGroupedWaves) void down_grouped_kernel(
     const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * RPW;
     if (row0 >= N) return;
     const int sl = shared ? 0 : slot;
-    const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+    const int64_t wpr = static_cast<int64_t>(K) * SB / 32;
     const int gpr = K / p.group;
     const uint32_t *w = p.w + sl * p.w_slot;
     const uint16_t *s = p.s + sl * p.m_slot, *b = p.b + sl * p.m_slot;
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(64 * kGroupedWaves) void down_grouped_kernel(
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-        load_row<BITS, CPL, LPR, GPC>(rd[j], w + row * wpr, s + row * gpr, b + row * gpr, p.group,
+        load_row<BITS, CPL, LPR, GPC, SB>(rd[j], w + row * wpr, s + row * gpr, b + row * gpr, p.group,
                                       lane_in_row);
     }
     XVec<BITS, BF16, CPL, GPC> xv[TT];
@@ -227,7 +229,7 @@ struct GroupedKernelLaunch {
     int32_t max_tiles;
 };
 
-template <int BITS, bool BF16, int CPL, int LPR, int GPC>
+template <int BITS, bool BF16, int CPL, int LPR, int GPC, int SB = BITS>
 hipError_t launch_grouped_t(int which, const GroupedKernelLaunch &L, hipStream_t st) {
     constexpr int TT = kGroupedTileTokens;
     using G = Geom<BITS, CPL, LPR, GPC>;
@@ -236,28 +238,28 @@ hipError_t launch_grouped_t(int which, const GroupedKernelLaunch &L, hipStream_t
         constexpr int J = (LPR >= 4 * TT) ? 2 : 1;
         const int rpb = waves * J * G::kRPL;
         dim3 grid((L.gate.rows + rpb - 1) / rpb, L.max_tiles);
-        hipLaunchKernelGGL((gateup_grouped_kernel<BITS, BF16, CPL, LPR, GPC, J, TT>), grid,
+        hipLaunchKernelGGL((gateup_grouped_kernel<BITS, BF16, CPL, LPR, GPC, J, TT, SB>), grid,
                            dim3(64 * waves), 0, st, L.ta, L.gate, L.up, L.sgate, L.sup, L.h, L.limit,
                            L.fp32_swiglu);
     } else {
         constexpr int J = (LPR >= 4 * TT) ? 4 : ((LPR >= 2 * TT) ? 2 : 1);
         const int rpb = waves * J * G::kRPL;
         dim3 grid((L.down.rows + rpb - 1) / rpb, L.max_tiles);
-        hipLaunchKernelGGL((down_grouped_kernel<BITS, BF16, CPL, LPR, GPC, J, TT>), grid,
+        hipLaunchKernelGGL((down_grouped_kernel<BITS, BF16, CPL, LPR, GPC, J, TT, SB>), grid,
                            dim3(64 * waves), 0, st, L.ta, L.down, L.sdown, L.h, L.y);
     }
     return hipGetLastError();
 }
 
-template <int BITS, bool BF16, int GPC>
+template <int BITS, bool BF16, int GPC, int SB = BITS>
 hipError_t grouped_geometry(int which, int cpr, const GroupedKernelLaunch &L, hipStream_t st) {
     switch (cpr) {
-    case 8: return launch_grouped_t<BITS, BF16, 1, 8, GPC>(which, L, st);
-    case 16: return launch_grouped_t<BITS, BF16, 1, 16, GPC>(which, L, st);
-    case 32: return launch_grouped_t<BITS, BF16, 1, 32, GPC>(which, L, st);
-    case 64: return launch_grouped_t<BITS, BF16, 1, 64, GPC>(which, L, st);
-    case 128: return launch_grouped_t<BITS, BF16, 2, 64, GPC>(which, L, st);
-    case 256: return launch_grouped_t<BITS, BF16, 4, 64, GPC>(which, L, st);
+    case 8: return launch_grouped_t<BITS, BF16, 1, 8, GPC, SB>(which, L, st);
+    case 16: return launch_grouped_t<BITS, BF16, 1, 16, GPC, SB>(which, L, st);
+    case 32: return launch_grouped_t<BITS, BF16, 1, 32, GPC, SB>(which, L, st);
+    case 64: return launch_grouped_t<BITS, BF16, 1, 64, GPC, SB>(which, L, st);
+    case 128: return launch_grouped_t<BITS, BF16, 2, 64, GPC, SB>(which, L, st);
+    case 256: return launch_grouped_t<BITS, BF16, 4, 64, GPC, SB>(which, L, st);
     default: return hipErrorInvalidValue;
     }
 }

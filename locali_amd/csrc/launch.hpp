@@ -76,6 +76,10 @@ struct DecodeLaunch {
     const RouterLaunch *sel;
 };
 
+// Bit width the kernels compute in: 3-bit codes are widened to 4-bit on load
+// (the 4-bit kernels with 3-bit row loads), every other width is its own.
+__host__ __device__ inline int lane_bits(int bits) { return bits == 3 ? 4 : bits; }
+
 hipError_t launch_gateup_decode(const DecodeLaunch &L, hipStream_t st);
 hipError_t launch_down_combine_decode(const DecodeLaunch &L, hipStream_t st);
 int chunks_per_row(const QProj &p);

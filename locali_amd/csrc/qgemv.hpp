@@ -269,23 +269,49 @@ __device__ __forceinline__ void load_row_meta(RowData<CPL, GPC> &rd,
     }
 }
 
+// Eight 3-bit codes (the low 24 bits of v, LSB first) moved to the eight
+// nibbles of a 4-bit word: 12-bit halves to 16-bit halves, 6-bit quarters to
+// bytes, then each byte's two codes to its nibbles.
+__device__ __forceinline__ uint32_t spread3_word(uint32_t v) {
+    v = (v & 0x00000FFFu) | ((v << 4) & 0x0FFF0000u);
+    v = (v & 0x003F003Fu) | ((v << 2) & 0x3F003F00u);
+    return (v & 0x07070707u) | ((v << 1) & 0x70707070u);
+}
+
+// A 32-value chunk of 3-bit codes (three words of the row's little-endian
+// bit stream) as the chunk of 4-bit codes the 4-bit dot products read.
+__device__ __forceinline__ u32x4 spread3_chunk(uint32_t w0, uint32_t w1, uint32_t w2) {
+    return u32x4{spread3_word(w0 & 0xFFFFFFu), spread3_word(__builtin_amdgcn_alignbit(w1, w0, 24)),
+                 spread3_word(__builtin_amdgcn_alignbit(w2, w1, 16)), spread3_word(w2 >> 8)};
+}
+
 // Packed weights of one row for one lane: CPL 16-byte chunks, streamed once.
-template <int CPL, int LPR, int GPC>
+// SB = 3: the row holds 3-bit codes (chunk c of 32 values is words 3c..3c+2)
+// and each chunk is widened to 4-bit codes on load, for kernels built with
+// the 4-bit geometry.
+template <int CPL, int LPR, int GPC, int SB = 4>
 __device__ __forceinline__ void load_row_weights(RowData<CPL, GPC> &rd,
                                                  const uint32_t *__restrict__ wrow,
                                                  int lane_in_row) {
 #pragma unroll
-    for (int i = 0; i < CPL; ++i)
-        rd.c[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4 *>(wrow) + lane_in_row + LPR * i);
+    for (int i = 0; i < CPL; ++i) {
+        const int c = lane_in_row + LPR * i;
+        if constexpr (SB == 3) {
+            const uint32_t *p = wrow + 3 * c;
+            rd.c[i] = spread3_chunk(__builtin_nontemporal_load(p), __builtin_nontemporal_load(p + 1),
+                                    __builtin_nontemporal_load(p + 2));
+        } else {
+            rd.c[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wrow) + c);
+        }
+    }
 }
 
-template <int BITS, int CPL, int LPR, int GPC>
+template <int BITS, int CPL, int LPR, int GPC, int SB = BITS>
 __device__ __forceinline__ void load_row(RowData<CPL, GPC> &rd, const uint32_t *__restrict__ wrow,
                                          const uint16_t *__restrict__ srow,
                                          const uint16_t *__restrict__ brow, int group,
                                          int lane_in_row) {
-    load_row_weights<CPL, LPR, GPC>(rd, wrow, lane_in_row);
+    load_row_weights<CPL, LPR, GPC, SB>(rd, wrow, lane_in_row);
     load_row_meta<BITS, CPL, LPR, GPC>(rd, srow, brow, group, lane_in_row);
 }
 

@@ -4,7 +4,10 @@ ONLY (see oracle/__init__.py).
 Layout (reference dsv4_kernels.py:26-29, 59-79, 241; dsv4_arena.py:169-171):
   weight  uint32 [N, K*bits/32]; value j of a row sits in word (j*bits)//32 at
           bit offset (j*bits)%32, least-significant bits first (2-bit: 16
-          values per word, 4-bit: 8, 8-bit: 4)
+          values per word, 4-bit: 8, 8-bit: 4). 3-bit rows are the same
+          little-endian bit stream with values crossing word boundaries: 32
+          values per 3 words, 8 per 3 bytes (MLX's 3-bit packing, used by the
+          DSpark/MTP tier whose bit width dsv4_index.py:202-207 infers)
   scales  [N, K/group]   (bf16 or fp16)
   biases  [N, K/group]
   w[n, j] = scales[n, j//group] * q[n, j] + biases[n, j//group]
@@ -17,31 +20,33 @@ from __future__ import annotations
 
 import numpy as np
 
-SUPPORTED_BITS = (2, 4, 8)
+SUPPORTED_BITS = (2, 3, 4, 8)
 
 
 def pack(q: np.ndarray, bits: int) -> np.ndarray:
-    """uint8 codes [..., K] -> uint32 words [..., K*bits/32], LSB first."""
+    """uint8 codes [..., K] -> uint32 words [..., K*bits/32]: the codes'
+    bits concatenated least-significant first into one little-endian
+    stream."""
     if bits not in SUPPORTED_BITS:
         raise ValueError(f"bits must be one of {SUPPORTED_BITS}")
-    q = np.asarray(q, dtype=np.uint64)
-    per = 32 // bits
+    q = np.asarray(q, dtype=np.uint8)
     K = q.shape[-1]
-    if K % per:
-        raise ValueError("K must be a multiple of values per word")
-    q = q.reshape(*q.shape[:-1], K // per, per)
-    shifts = (np.arange(per, dtype=np.uint64) * bits)
-    words = (q << shifts).sum(axis=-1)
-    return words.astype(np.uint32)
+    if (K * bits) % 32:
+        raise ValueError("K * bits must be a multiple of 32")
+    stream = np.unpackbits(q[..., None], axis=-1, bitorder="little")[..., :bits]
+    stream = stream.reshape(*q.shape[:-1], K * bits)
+    raw = np.packbits(stream, axis=-1, bitorder="little")
+    return np.ascontiguousarray(raw).view("<u4").astype(np.uint32)
 
 
 def unpack(w: np.ndarray, bits: int) -> np.ndarray:
     """uint32 words [..., W] -> uint8 codes [..., W*32/bits]."""
-    per = 32 // bits
-    w = np.asarray(w, dtype=np.uint32)[..., None]
-    shifts = (np.arange(per, dtype=np.uint32) * bits)
-    q = (w >> shifts) & np.uint32((1 << bits) - 1)
-    return q.reshape(*q.shape[:-2], -1).astype(np.uint8)
+    w = np.ascontiguousarray(np.asarray(w, dtype=np.uint32).astype("<u4"))
+    stream = np.unpackbits(w.view(np.uint8), axis=-1, bitorder="little")
+    n = stream.shape[-1] // bits
+    vals = stream[..., :n * bits].reshape(*stream.shape[:-1], n, bits)
+    weights = (1 << np.arange(bits, dtype=np.uint32)).astype(np.uint32)
+    return (vals.astype(np.uint32) * weights).sum(axis=-1).astype(np.uint8)
 
 
 def dequant(w, scales, biases, bits: int, group: int) -> np.ndarray:

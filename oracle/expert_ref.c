@@ -96,7 +96,6 @@ typedef struct {
 static void qmv_rows(const oracle_proj *p, int slot, const float *v, float *out,
                      int n0, int n1) {
     const int words = p->K * p->bits / 32, groups = p->K / p->group;
-    const int per = 32 / p->bits;
     const uint32_t mask = (1u << p->bits) - 1u;
     const uint32_t *W = p->w + (size_t)slot * p->N * words;
     const uint16_t *S = p->s + (size_t)slot * p->N * groups;
@@ -106,8 +105,13 @@ static void qmv_rows(const oracle_proj *p, int slot, const float *v, float *out,
         for (int g = 0; g < groups; g++) {
             float dot = 0.f, vs = 0.f;
             for (int k = g * p->group; k < (g + 1) * p->group; k++) {
-                uint32_t word = W[(size_t)n * words + k / per];
-                float q = (float)((word >> ((k % per) * p->bits)) & mask);
+                /* value k starts at bit k * bits of the row's little-endian
+                   stream; a 3-bit value may continue into the next word */
+                const uint32_t *row = W + (size_t)n * words;
+                const int off = k * p->bits, wi = off >> 5, sh = off & 31;
+                uint32_t code = row[wi] >> sh;
+                if (sh + p->bits > 32) code |= row[wi + 1] << (32 - sh);
+                float q = (float)(code & mask);
                 dot += v[k] * q;
                 vs += v[k];
             }

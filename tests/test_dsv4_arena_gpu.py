@@ -317,3 +317,29 @@ def test_routes_spanning_two_tiers(T):
         ref1 = ops.expert_grouped(cold, None, x, slots1, torch.arange(9, dtype=torch.int32, device="cuda"),
                                   w, ops.Workspace(), n_experts=9, swiglu_limit=10.0)
     assert torch.equal(got1, ref1)
+
+
+def test_streamed_3bit_experts_match_resident_kernels(tmp_path):
+    """A checkpoint of 3-bit experts (the DSpark/MTP tier's width, whose
+    codes cross word boundaries) streams from disk through the store and
+    gives exactly what the expert kernels give on the same weights held
+    resident, for a prefill-sized and a decode-sized call."""
+    banner("v4 arena streamed 3-bit")
+    truth = make_snapshot(tmp_path, layers=1, experts=E, top_k=K, d=D, dff=DFF, bits=3, seed=5)
+    index = make_index(tmp_path)
+    store = V4ArenaStore(index, ceiling_gb=(E + 1) * _item(index) / 1e9 + 1e-6, threads=2,
+                         nocache=False, cache_policy="lru")
+    try:
+        assert store.quant("cold", "bits") == 3
+        assert store.expert_arena("cold").gate.bits == 3
+        g = torch.Generator().manual_seed(8)
+        x = (torch.randn(3, D, generator=g) * 0.5).to(torch.bfloat16).cuda()
+        indices = torch.tensor([[1, 4], [4, 5], [5, 1]], dtype=torch.int32, device="cuda")
+        scores = torch.tensor([[0.6, 0.4], [0.3, 0.7], [0.5, 0.5]], dtype=torch.float32, device="cuda")
+        moe = V4ArenaMoE(store, 0, FixedGate(indices, scores), K, swiglu_limit=10.0)
+        assert torch.equal(moe(x), _direct(_gpu(truth[0]), x, indices, scores))
+        dx, di = x[:1], torch.tensor([[5, 2]], dtype=torch.int32, device="cuda")
+        moe.gate = FixedGate(di, scores[:1])
+        assert torch.equal(moe(dx), _direct(_gpu(truth[0]), dx, di, scores[:1]))
+    finally:
+        store.close()

@@ -147,6 +147,11 @@ DECODE_CASES = [
     (torch.float16, 8, 4, 128, 512, 256),
     (torch.bfloat16, 2, 2, 64, 4096, 2048),
     (torch.bfloat16, 2, 4, 64, 4096, 2048),
+    # 3-bit codes (the DSpark/MTP tier): 4-bit kernels widening 3-bit rows
+    (torch.bfloat16, 3, 3, 64, 1024, 512),
+    (torch.float16, 3, 3, 32, 1024, 512),
+    (torch.bfloat16, 2, 3, 64, 1024, 512),
+    (torch.bfloat16, 3, 2, 64, 4096, 2048),
 ]
 
 
@@ -246,7 +251,9 @@ def test_dispatch_stable_sort():
 
 
 @pytest.mark.parametrize("T,dtype,bits", [(3, torch.bfloat16, (2, 2)), (17, torch.bfloat16, (2, 4)),
-                                          (64, torch.bfloat16, (2, 2)), (9, torch.float16, (4, 4))])
+                                          (64, torch.bfloat16, (2, 2)), (9, torch.float16, (4, 4)),
+                                          (5, torch.bfloat16, (3, 3)), (33, torch.float16, (3, 3)),
+                                          (9, torch.bfloat16, (2, 3))])
 def test_expert_grouped_matches_oracle(T, dtype, bits):
     banner(f"grouped T={T} {dtype} {bits}")
     d, dff, E, k = 1024, 512, 16, 4

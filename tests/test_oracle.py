@@ -30,6 +30,22 @@ def test_pack_literal_words():
     assert affine.pack(np.array([[1, 2, 3, 0] * 4]), 2)[0, 0] == 0x39393939
     # 8-bit: bytes in order
     assert affine.pack(np.array([[0x11, 0x22, 0x33, 0xF4]]), 8)[0, 0] == 0xF4332211
+    # 3-bit: codes 0..7 are the 24-bit stream 0o76543210 = 0xFAC688 (bytes
+    # 88 C6 FA), repeated; 32 values fill three words, values 10 and 21
+    # crossing word boundaries
+    assert list(affine.pack(np.array([list(range(8)) * 4]), 3)[0]) == [0x88FAC688, 0xC688FAC6, 0xFAC688FA]
+
+
+def test_3bit_stream_is_one_little_endian_integer():
+    """Value j of a 3-bit row is bits [3j, 3j+3) of the row's words read as
+    one little-endian integer (checked with Python integers)."""
+    rng = np.random.default_rng(9)
+    q = rng.integers(0, 8, size=(4, 96), dtype=np.uint8)
+    w = affine.pack(q, 3)
+    assert w.shape == (4, 9)
+    for r in range(4):
+        big = sum(int(v) << (32 * i) for i, v in enumerate(w[r]))
+        assert [(big >> (3 * j)) & 7 for j in range(96)] == list(q[r])
 
 
 def test_unpack_matches_reference_kernel_text_extraction():
@@ -48,7 +64,7 @@ def test_unpack_matches_reference_kernel_text_extraction():
                     uw >>= 2
 
 
-@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
 def test_pack_unpack_roundtrip(bits):
     rng = np.random.default_rng(bits)
     q = rng.integers(0, 2**bits, size=(5, 256), dtype=np.uint8)
@@ -83,7 +99,7 @@ def _rand_proj(rng, N, K, bits, group, dt="bf16"):
     return q, affine.pack(q, bits), s, b
 
 
-@pytest.mark.parametrize("bits,group", [(2, 64), (4, 64), (2, 128), (4, 32), (8, 64)])
+@pytest.mark.parametrize("bits,group", [(2, 64), (4, 64), (2, 128), (4, 32), (8, 64), (3, 64), (3, 32)])
 def test_qmv_equals_torch_dense_matmul(bits, group):
     rng = np.random.default_rng(bits * 1000 + group)
     N, K = 48, 512
@@ -116,13 +132,13 @@ def test_qmv_special_cases():
     assert np.all(affine.qmv(x, zero_codes, 0 * s, 0 * b, 2, G) == 0.0)
 
 
-@pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_c_oracle_layer_matches_numpy_oracle(oracle_lib, dt):
+@pytest.mark.parametrize("dt,bits", [("bf16", (2, 4)), ("f16", (2, 4)), ("bf16", (3, 3))])
+def test_c_oracle_layer_matches_numpy_oracle(oracle_lib, dt, bits):
     rng = np.random.default_rng(11)
     S, d, dff, k, T = 5, 256, 128, 2, 3
     arena, arena_c = {}, {}
-    for name, (N, K, bits) in {"gate_proj": (dff, d, 2), "up_proj": (dff, d, 2),
-                               "down_proj": (d, dff, 4)}.items():
+    for name, (N, K, bits) in {"gate_proj": (dff, d, bits[0]), "up_proj": (dff, d, bits[0]),
+                               "down_proj": (d, dff, bits[1])}.items():
         ws, ss, bs = [], [], []
         for _ in range(S):
             _, w, s, b = _rand_proj(rng, N, K, bits, 64, dt)
