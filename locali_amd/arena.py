@@ -558,6 +558,9 @@ class ArenaMoE:
         if len(present) > 1:
             return self._apply_tiers(flat, ii, placed, gates, dtype, reads, present)
         t = present[0]
+        pending = getattr(reads, "pending_experts", ()) if reads is not None else ()
+        if self.overlap_hits and T == 1 and pending and len(pending) < self.top_k:
+            return self._apply_overlap(flat, ii[0], placed, gates, dtype, reads, t, pending)
         if reads is not None:
             self.store.wait(reads[t])
         slots = torch.tensor([[placed[e][1] for e in row] for row in ii], dtype=torch.int32,
@@ -590,6 +593,45 @@ class ArenaMoE:
             return ops.expert_decode(arena, None, x_in, slots, ones, ws=ws, **kw)
         ident = torch.arange(arena.n_slots, dtype=torch.int32, device=x_in.device)
         return ops.expert_grouped(arena, None, x_in, slots, ident, ones, ws, n_experts=arena.n_slots, **kw)
+
+    def _apply_overlap(self, flat, row, placed, gates, dtype, reads, t, pending):
+        """One token with some experts still filling (reference
+        arena.py:575-618): the routes whose slots are resident are launched
+        before the host blocks on the pending fills, the others after. The
+        per-route outputs then meet in the kernels' single-tier combine --
+        products of y and the rounded weight rounded, summed in k order in
+        float32, one rounding, then the folded shared expert with one more --
+        so the result is bit-identical to the unsplit call."""
+        dev = flat.device
+        ready = [j for j, e in enumerate(row) if e not in pending]
+        late = [j for j, e in enumerate(row) if e in pending]
+        arena = self.store.expert_arena(t)
+        x_in = flat.contiguous()
+        if self.store.use_f16(t) and x_in.dtype == torch.bfloat16:
+            x_in = x_in.to(torch.float16)
+        ws = self._workspace()
+
+        def run(pos):
+            slots = torch.tensor([[placed[row[j]][1]] for j in pos], dtype=torch.int32, device=dev)
+            return self._routes(arena, x_in.expand(len(pos), -1).contiguous(), slots, ws)
+
+        y_ready = run(ready)
+        self.store.wait(reads[t])
+        y_late = run(late)
+        y = torch.empty(len(row), x_in.shape[1], dtype=x_in.dtype, device=dev)
+        y[ready] = y_ready
+        y[late] = y_late
+        w = gates.reshape(-1)[:len(row)].to(torch.float32).to(x_in.dtype).to(torch.float32)
+        prod = (y.to(torch.float32) * w.unsqueeze(1)).to(x_in.dtype).to(torch.float32)
+        acc = torch.zeros(x_in.shape[1], dtype=torch.float32, device=dev)
+        for j in range(len(row)):
+            acc = acc + prod[j]
+        out = acc.to(x_in.dtype)
+        if self.shared_expert is not None:
+            zero = torch.zeros(1, 1, dtype=torch.int32, device=dev)
+            ys = self._routes(self.shared_expert, x_in, zero, ws)
+            out = (out.to(torch.float32) + ys.to(torch.float32).reshape(-1)).to(x_in.dtype)
+        return out.reshape(1, -1).to(dtype)
 
     def _apply_tiers(self, flat, ii, placed, gates, dtype, reads, present):
         """Routes spanning tiers (reference arena.py:626-672). Each tier's

@@ -343,3 +343,39 @@ def test_streamed_3bit_experts_match_resident_kernels(tmp_path):
         assert torch.equal(moe(dx), _direct(_gpu(truth[0]), dx, di, scores[:1]))
     finally:
         store.close()
+
+
+@pytest.mark.parametrize("with_shared", [False, True])
+def test_overlap_hits_splits_a_decode_call_and_stays_exact(ckpt, with_shared):
+    """overlap_hits with one token and some of its experts still filling
+    (reference arena.py:575-618): the resident routes run before the host
+    waits, the pending ones after, and the split call gives bit-for-bit what
+    the unsplit call gives (with and without a folded shared expert). The
+    split is forced with a read plan that names expert 4 as pending; a real
+    streamed call with overlap_hits on must agree as well."""
+    from locali_amd.arena import ReadPlan
+    truth, index, _ = ckpt
+    banner(f"overlap_hits shared={with_shared}")
+    store = V4ArenaStore(index, ceiling_gb=(E + 1) * _item(index) / 1e9 + 1e-6, threads=2,
+                         cache_policy="lru")
+    try:
+        sh = (synth.expert_arena(1, D, DFF, dtype=torch.bfloat16, seed=91, device="cuda", zero_slot=False)
+              if with_shared else None)
+        g = torch.Generator().manual_seed(12)
+        x = (torch.randn(1, D, generator=g) * 0.5).to(torch.bfloat16).cuda()
+        di = torch.tensor([[1, 4]], dtype=torch.int32, device="cuda")
+        sc = torch.tensor([[0.55, 0.45]], dtype=torch.float32, device="cuda")
+        want = V4ArenaMoE(store, 0, FixedGate(di, sc), K, swiglu_limit=10.0, shared_expert=sh)(x)
+        mo = V4ArenaMoE(store, 0, FixedGate(di, sc), K, swiglu_limit=10.0, overlap_hits=True,
+                        shared_expert=sh)
+        placed = store.slots_for(0, [1, 4])
+        reads = ReadPlan({t: [] for t in store.tiers}, pending_experts={4})
+        got = mo._apply(x, [[1, 4]], placed, sc, x.dtype, reads)
+        assert torch.equal(got, want)
+        store.tier_overlap = True
+        di2 = torch.tensor([[4, 5]], dtype=torch.int32, device="cuda")   # 5 is new: a real miss
+        mo.gate = FixedGate(di2, sc)
+        ref = V4ArenaMoE(store, 0, FixedGate(di2, sc), K, swiglu_limit=10.0, shared_expert=sh)
+        assert torch.equal(mo(x), ref(x))
+    finally:
+        store.close()
