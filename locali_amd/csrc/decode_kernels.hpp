@@ -60,16 +60,17 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_route_kernel(
     int token, slot;
     bool shared;
     route_of(ra, r, token, slot, shared);
-    const QProj &pg = shared ? sgate : gate;
-    const QProj &pu = shared ? sup : up;
-    const int N = pg.rows, K = pg.cols;
+    // the route's projections field by field (a reference to one of two
+    // parameter structs would make every field a dependent memory load);
+    // the shared expert has the routed experts' shapes and quantisation
+    const int N = gate.rows, K = gate.cols, group = gate.group;
     const int n0 = blockIdx.x * RB;
     const int row0 = n0 + wave * RPW;
     const bool active = row0 < N;
-    const bool valid_slot = slot >= 0 && slot < pg.n_slots;
+    const bool valid_slot = slot >= 0 && slot < (shared ? sgate.n_slots : gate.n_slots);
     const int sl = valid_slot ? slot : 0;
     const int64_t wpr = static_cast<int64_t>(K) * SB / 32;     // words per row
-    const int gpr = K / pg.group;                               // groups per row
+    const int gpr = K / group;                                  // groups per row
 
     // The token's activations first (loads retire in issue order, so rows
     // can be consumed as they land only if x is already in): each thread
@@ -99,15 +100,16 @@ __global__ __launch_bounds__(64 * kGateUpWaves) void gateup_route_kernel(
     // re-reads it and stores nothing) so that the wait for x above does not
     // merge with a path on which no weight loads are outstanding.
     RowData<CPL, GPC> wg[J], wu[J];
-    const uint32_t *gw = pg.w + sl * pg.w_slot, *uw = pu.w + sl * pu.w_slot;
-    const uint16_t *gs = pg.s + sl * pg.m_slot, *gb = pg.b + sl * pg.m_slot;
-    const uint16_t *us = pu.s + sl * pu.m_slot, *ub = pu.b + sl * pu.m_slot;
+    const int64_t w_slot = shared ? sgate.w_slot : gate.w_slot, m_slot = shared ? sgate.m_slot : gate.m_slot;
+    const uint32_t *gw = (shared ? sgate.w : gate.w) + sl * w_slot, *uw = (shared ? sup.w : up.w) + sl * w_slot;
+    const uint16_t *gs = (shared ? sgate.s : gate.s) + sl * m_slot, *gb = (shared ? sgate.b : gate.b) + sl * m_slot;
+    const uint16_t *us = (shared ? sup.s : up.s) + sl * m_slot, *ub = (shared ? sup.b : up.b) + sl * m_slot;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int row = min(row0 + j * G::kRPL + row_sub, N - 1);
-        load_row_meta<BITS, CPL, LPR, GPC>(wg[j], gs + row * gpr, gb + row * gpr, pg.group,
+        load_row_meta<BITS, CPL, LPR, GPC>(wg[j], gs + row * gpr, gb + row * gpr, group,
                                            lane_in_row);
-        load_row_meta<BITS, CPL, LPR, GPC>(wu[j], us + row * gpr, ub + row * gpr, pu.group,
+        load_row_meta<BITS, CPL, LPR, GPC>(wu[j], us + row * gpr, ub + row * gpr, group,
                                            lane_in_row);
     }
     sched_fence();
@@ -180,7 +182,10 @@ __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, 
     constexpr int RB = J * G::kRPL;               // rows per workgroup
     __shared__ float ylds[WAVES][RB];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave index in an SGPR: the route's fields are then selected in scalar
+    // registers (a reference to one of the two parameter structs would make
+    // every field a dependent memory load)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane_in_row = lane % LPR;
     const int row_sub = lane / LPR;
     const int t = blockIdx.y;
@@ -195,22 +200,24 @@ __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, 
         const int j = wave;
         const bool sh = j >= ra.top_k;
         const int r = sh ? routed + t : t * ra.top_k + j;
-        const int slot = sh ? 0 : ra.route_slot[r];
-        const QProj &p = sh ? sdown : down;
-        const bool valid_slot = slot >= 0 && slot < p.n_slots;
-        const int sl = valid_slot ? slot : 0;
-        const uint32_t *w = p.w + sl * p.w_slot;
-        const uint16_t *s = p.s + sl * p.m_slot, *b = p.b + sl * p.m_slot;
+        // the route's prepared input first: it does not depend on the slot,
+        // so its loads are in flight while the slot is looked up
         XVec<BITS, BF16, CPL, GPC> xv;
         load_xvec_global<BITS, BF16, CPL, LPR, GPC>(xv, hin.pairs + r * hin.pairs_stride,
                                                     hin.parts + r * hin.parts_stride, lane_in_row);
         sched_fence();
+        const int slot = sh ? 0 : ra.route_slot[r];
+        const bool valid_slot = slot >= 0 && slot < (sh ? sdown.n_slots : down.n_slots);
+        const int sl = valid_slot ? slot : 0;
+        const int group = sh ? sdown.group : down.group;
+        const uint32_t *w = (sh ? sdown.w : down.w) + sl * (sh ? sdown.w_slot : down.w_slot);
+        const int64_t m_slot = sh ? sdown.m_slot : down.m_slot;
+        const uint16_t *s = (sh ? sdown.s : down.s) + sl * m_slot, *b = (sh ? sdown.b : down.b) + sl * m_slot;
         RowData<CPL, GPC> rd[J];
 #pragma unroll
         for (int q = 0; q < J; ++q) {
             const int row = min(row0 + q * G::kRPL + row_sub, N - 1);
-            load_row_meta<BITS, CPL, LPR, GPC>(rd[q], s + row * gpr, b + row * gpr, p.group,
-                                               lane_in_row);
+            load_row_meta<BITS, CPL, LPR, GPC>(rd[q], s + row * gpr, b + row * gpr, group, lane_in_row);
         }
         sched_fence();
 #pragma unroll

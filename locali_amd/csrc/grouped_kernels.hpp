@@ -96,8 +96,10 @@ __global__ __launch_bounds__(64 * kGroupedWaves) void gateup_grouped_kernel(
     const int slot = ta.tiles[4 * tile], first = ta.tiles[4 * tile + 1];
     const int count = ta.tiles[4 * tile + 2];
     const bool shared = slot == -2;
-    const QProj &pg = shared ? sgate : gate;
-    const QProj &pu = shared ? sup : up;
+    // by value: the fields are selected in registers (a reference to one of
+    // two parameter structs would make each field a dependent memory load)
+    const QProj pg = shared ? sgate : gate;
+    const QProj pu = shared ? sup : up;
     if (count <= 0 || (!shared && (slot < 0 || slot >= pg.n_slots || first < 0 ||
                                    first + count > ta.R)))
         return;
@@ -168,7 +170,7 @@ __global__ __launch_bounds__(64 * kGroupedWaves) void down_grouped_kernel(
     const int slot = ta.tiles[4 * tile], first = ta.tiles[4 * tile + 1];
     const int count = ta.tiles[4 * tile + 2];
     const bool shared = slot == -2;
-    const QProj &p = shared ? sdown : down;
+    const QProj p = shared ? sdown : down;   // by value (see the gate/up kernel)
     if (count <= 0 || (!shared && (slot < 0 || slot >= p.n_slots || first < 0 ||
                                    first + count > ta.R)))
         return;
