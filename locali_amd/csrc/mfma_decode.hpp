@@ -202,12 +202,15 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
             if (wave == 1) diag_prep_load<BITS>(xw0, ra.x + static_cast<int64_t>(token) * K, lane);
             sched_fence();
             if (wave == 0) {
-                const SelectOut o = select_token_any<1, 4>(sel, token, sel.logits + static_cast<int64_t>(token) * sel.E,
-                                                           0, stage);
+                // this route needs choice j only; the workgroup that stores the
+                // token's choices (blockIdx.x 0, j 0) runs every round
                 const int j = r - token * ra.top_k;
+                const bool store = blockIdx.x == 0 && j == 0;
+                const SelectOut o = select_token_any<1, 4>(sel, token, sel.logits + static_cast<int64_t>(token) * sel.E,
+                                                           0, stage, store ? ra.top_k : j + 1);
                 const int sj = __builtin_amdgcn_readlane(o.slot, j);
                 if (lane == 0) s_slot = sj;
-                if (blockIdx.x == 0 && j == 0) select_store(sel, token, o);
+                if (store) select_store(sel, token, o);
                 if (waves == 1) diag_prep_store<BITS, BF16>(mw, xw, lane);
             } else {
                 diag_prep_store<BITS, BF16>(mw, xw, lane);

@@ -232,7 +232,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(RouterLaunch L) {
     const int t = blockIdx.x * 4 + wave;
     if (t >= L.tokens) return;
     const SelectOut o = select_token<NS, SF, M>(L, t, L.logits + static_cast<int64_t>(t) * L.E,
-                                                static_cast<int64_t>(L.tokens) * L.E, stage[wave]);
+                                                static_cast<int64_t>(L.tokens) * L.E, stage[wave], L.top_k);
     select_store(L, t, o);
 }
 

@@ -33,7 +33,7 @@ __device__ __forceinline__ float score_of(float l, float lmax, float denom) {
         // sqrt(softplus(l)); log1p(e) ~ e within 1.5e-7 relative below -15
         const float e = __expf(l);
         const float sp = l > 20.0f ? l : (l < -15.0f ? e : __logf(1.0f + e));
-        return sqrtf(sp);
+        return __builtin_amdgcn_sqrtf(sp);   // hardware square root (1 ulp)
     } else if constexpr (SF == 1) {
         return 1.0f / (1.0f + __expf(-l));
     } else {
@@ -54,7 +54,7 @@ struct SelectOut {
 
 template <int NS, int SF, int M>
 __device__ SelectOut select_token(const RouterLaunch &L, int t, const float *logit_row, int64_t split_stride,
-                                  float2 *stage) {
+                                  float2 *stage, int rounds) {
     const int lane = threadIdx.x & 63;
     float part[NS][M], bias[M];
     int slot_of[M];
@@ -122,8 +122,10 @@ __device__ SelectOut select_token(const RouterLaunch &L, int t, const float *log
             kl[j - 1] = sw ? tl : kl[j - 1];
         }
     }
+    // rounds < top_k: only the first `rounds` choices (and their slots) are
+    // needed; later lanes keep expert -1 and the weights are not final
     int my_e = -1;
-    for (int j = 0; j < L.top_k; ++j) {
+    for (int j = 0; j < rounds; ++j) {
         int best_e;
         if (L.tid2eid) {
             best_e = __builtin_amdgcn_readlane(hash_e, j);
@@ -178,11 +180,11 @@ __device__ __forceinline__ void select_store(const RouterLaunch &L, int t, const
 // Score function chosen at run time (for kernels that select on the side).
 template <int NS, int M>
 __device__ SelectOut select_token_any(const RouterLaunch &L, int t, const float *logit_row,
-                                      int64_t split_stride, float2 *stage) {
+                                      int64_t split_stride, float2 *stage, int rounds) {
     switch (L.score_func) {
-    case 0: return select_token<NS, 0, M>(L, t, logit_row, split_stride, stage);
-    case 1: return select_token<NS, 1, M>(L, t, logit_row, split_stride, stage);
-    default: return select_token<NS, 2, M>(L, t, logit_row, split_stride, stage);
+    case 0: return select_token<NS, 0, M>(L, t, logit_row, split_stride, stage, rounds);
+    case 1: return select_token<NS, 1, M>(L, t, logit_row, split_stride, stage, rounds);
+    default: return select_token<NS, 2, M>(L, t, logit_row, split_stride, stage, rounds);
     }
 }
 
