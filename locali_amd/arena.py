@@ -274,6 +274,15 @@ class ArenaStore:
         finally:
             self.staging.give(buf)
 
+    def _slot_ptrs(self, t):
+        """(base address, bytes per slot) of tier t's nine arrays in record
+        order (gate, up, down) x (weight, scales, biases)."""
+        cache = self.__dict__.setdefault("_slot_ptr_cache", {})
+        if t not in cache:
+            cache[t] = [(self.arena[(t, p, k)].data_ptr(), self.layout[(t, p, k)][0])
+                        for p in PROJS for k in ARRS]
+        return cache[t]
+
     def _host_bytes(self, key, t) -> torch.Tensor:
         src = self.host_source(*key)
         if src.is_cuda or src.dtype != torch.uint8 or src.numel() != self.item[t]:
@@ -290,16 +299,22 @@ class ArenaStore:
         for key, t, slot, recs in jobs:
             src = self._host_bytes(key, t)
             base, off = src.data_ptr(), 0
-            for pk, r in zip(((p, k) for p in PROJS for k in ARRS), recs):
-                arr = self.arena[(t, *pk)]
-                nbytes = self.layout[(t, *pk)][0]
-                pieces.append((arr.data_ptr() + slot * nbytes, base + off, r[3]))
+            for (arr_ptr, nbytes), r in zip(self._slot_ptrs(t), recs):
+                pieces.append((arr_ptr + slot * nbytes, base + off, r[3]))
                 off += r[3]
-        with torch.cuda.device(self.device):
-            self.fill_stream.wait_stream(torch.cuda.current_stream(self.device))
-            arena_fill_batch_ptrs(pieces, self.fill_stream)
-            ev = torch.cuda.Event()
-            ev.record(self.fill_stream)
+        if self.device.index is not None and torch.cuda.current_device() != self.device.index:
+            with torch.cuda.device(self.device):
+                return self._fill_from_host(jobs)
+        # the fill stream waits for the compute stream through one reused
+        # event (a wait takes the event's state when it is queued)
+        order = self.__dict__.get("_order_event")
+        if order is None:
+            order = self._order_event = torch.cuda.Event()
+        order.record(torch.cuda.current_stream(self.device))
+        self.fill_stream.wait_event(order)
+        arena_fill_batch_ptrs(pieces, self.fill_stream)
+        ev = torch.cuda.Event()
+        ev.record(self.fill_stream)
         return _Landed(ev)
 
     # ---- Python planner (reference arena.py:212-289) ---------------------
@@ -464,11 +479,22 @@ class ArenaStore:
         return placed
 
     def wait(self, futs):
+        """Every fill in futs has landed before work queued afterwards on the
+        caller's current stream reads it. Copies from host memory are ordered
+        on the device (the stream waits for their event and the host goes
+        on); file reads block the host until their copies have landed."""
         if not futs:
             return
         t0 = time.perf_counter()
+        seen, cur = set(), None
         for f in futs:
-            f.result()
+            if isinstance(f, _Landed):
+                if id(f) not in seen:
+                    seen.add(id(f))
+                    cur = cur or torch.cuda.current_stream(self.device)
+                    cur.wait_event(f.event)
+            else:
+                f.result()
         self.t_stall += time.perf_counter() - t0
 
     def stats(self):
@@ -563,8 +589,7 @@ class ArenaMoE:
             return self._apply_overlap(flat, ii[0], placed, gates, dtype, reads, t, pending)
         if reads is not None:
             self.store.wait(reads[t])
-        slots = torch.tensor([[placed[e][1] for e in row] for row in ii], dtype=torch.int32,
-                             device=flat.device)
+        slots = self._device_slots([[placed[e][1] for e in row] for row in ii], flat.device)
         arena = self.store.expert_arena(t)
         x_in = flat.contiguous()
         if self.store.use_f16(t) and x_in.dtype == torch.bfloat16:
@@ -580,6 +605,31 @@ class ArenaMoE:
             y = ops.expert_grouped(arena, self.shared_expert, x_in, slots, ident, w, ws, n_experts=n,
                                    swiglu_limit=self.swiglu_limit, fp32_swiglu=self.fp32_swiglu)
         return y.to(dtype)
+
+    def _device_slots(self, rows, device):
+        """[T, k] int32 slots on the device by an asynchronous copy from a
+        small ring of pinned host buffers (a copy from pageable memory would
+        block the host behind everything queued on the stream, fills
+        included). Each layer call syncs on its routing before it plans, so a
+        buffer is reused only after the copies of earlier calls have run."""
+        flat = [s for row in rows for s in row]
+        if device.type != "cuda":
+            return torch.tensor(rows, dtype=torch.int32, device=device)
+        ring = self.__dict__.setdefault("_slot_ring", [])
+        if not ring or ring[0][0].numel() < len(flat):
+            n = max(64, len(flat))
+            ring[:] = [[torch.empty(n, dtype=torch.int32, pin_memory=True), None] for _ in range(4)]
+            self._slot_next = 0
+        entry = ring[self._slot_next]
+        self._slot_next = (self._slot_next + 1) % len(ring)
+        if entry[1] is not None:
+            entry[1].synchronize()        # the buffer's previous copy has run
+        host = entry[0][:len(flat)]
+        host.copy_(torch.tensor(flat, dtype=torch.int32))
+        out = host.to(device, non_blocking=True).view(len(rows), -1)
+        entry[1] = torch.cuda.Event()
+        entry[1].record(torch.cuda.current_stream(device))
+        return out
 
     def _routes(self, arena, x_in, slots, ws):
         """Unweighted expert outputs, one route per row of x_in: a one-route

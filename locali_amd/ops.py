@@ -73,6 +73,17 @@ class ProjArena:
 
     def struct(self) -> _lib.QProj:
         w, s, b = self.weight, self.scales, self.biases
+        key = (w.data_ptr(), s.data_ptr(), b.data_ptr(), tuple(w.shape), tuple(s.shape), self.bits,
+               self.group_size, w.dtype, s.dtype)
+        cached = self.__dict__.get("_struct")
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        st = self._build_struct()
+        self.__dict__["_struct"] = (key, st)
+        return st
+
+    def _build_struct(self) -> _lib.QProj:
+        w, s, b = self.weight, self.scales, self.biases
         if w.dtype not in (torch.int32, torch.uint32):
             raise TypeError("packed weights must be 32-bit")
         if s.shape != b.shape or s.dtype != b.dtype:
