@@ -70,7 +70,9 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_gemv_fast_kernel(Rou
     if (have) {
 #pragma unroll
         for (int i = 0; i < NCH; ++i)
-            w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gw) + lane + 64 * i);
+            // ordinary (cacheable) loads: the gate is read again on every token,
+            // while the expert weights streamed between its uses are non-temporal
+            w[i] = reinterpret_cast<const u32x4 *>(gw)[lane + 64 * i];
     }
     if (have) {
         for (int t0 = 0; t0 < L.tokens; t0 += TB) {
