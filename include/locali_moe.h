@@ -9,7 +9,8 @@
  * zero-filled once before first use (the library leaves its counters at zero
  * after every call). Return value: 0 on success, a negative LOCALI_E_* code
  * otherwise; locali_moe_last_error() describes the last failure on the
- * calling thread.
+ * calling thread. A call with tokens == 0 is an empty batch: it returns 0
+ * and touches nothing (the reference returns an empty output).
  *
  * What each entry point replaces in the reference (MLX) implementation:
  *   locali_moe_router          the gate call V4ArenaMoE.route -> MoEGate

@@ -558,6 +558,8 @@ class ArenaMoE:
     def __call__(self, x, input_ids=None):
         shape = x.shape
         flat = x.reshape(-1, shape[-1])
+        if flat.shape[0] == 0:        # no tokens: an empty output, nothing routed or placed
+            return torch.zeros(shape, dtype=x.dtype, device=x.device)
         inds, gates = self.route(x, input_ids)
         ii = inds.reshape(-1, self.top_k).tolist()          # host sync, as the reference
         experts = [e for row in ii for e in row]

@@ -477,6 +477,7 @@ int locali_moe_router(const locali_router *router, const void *x, int32_t x_dtyp
                       int32_t d_model, const int32_t *input_ids, const float *logits_in,
                       const int32_t *slot_of_expert, int32_t n_slots, int32_t *idx, float *weights,
                       int32_t *route_slot, void *workspace, size_t workspace_bytes, void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
     int rc;
     if ((rc = check_router(router, d_model))) return rc;
     if (tokens < 1 || !x || !dtype16(x_dtype) || !idx || !weights || !workspace)
@@ -490,6 +491,7 @@ int locali_moe_router(const locali_router *router, const void *x, int32_t x_dtyp
 
 int locali_moe_dispatch(const int32_t *route_slot, int32_t tokens, int32_t top_k, int32_t n_slots,
                         int32_t *sorted_route, int32_t *seg_start, void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
     if (!route_slot || !sorted_route || !seg_start || tokens < 1 || top_k < 1 || n_slots < 1 ||
         n_slots > kMaxSlots)
         return fail(LOCALI_E_ARG, "dispatch: bad arguments");
@@ -514,6 +516,7 @@ int locali_moe_expert_decode(const locali_expert_arena *routed, const locali_exp
                              const int32_t *route_slot, const float *weights, float swiglu_limit,
                              int32_t fp32_swiglu, int32_t combine_mode, void *hidden, void *out,
                              void *workspace, size_t workspace_bytes, void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
     if (!x || !weights || !hidden || !out) return fail(LOCALI_E_ARG, "expert_decode: null buffer");
     int rc = check_decode_args(routed, shared, x_dtype, tokens, top_k, route_slot, combine_mode);
     if (rc) return rc;
@@ -527,6 +530,7 @@ int locali_moe_decode_gateup(const locali_expert_arena *routed, const locali_exp
                              const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k,
                              const int32_t *route_slot, float swiglu_limit, int32_t fp32_swiglu,
                              void *hidden, void *workspace, size_t workspace_bytes, void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
     if (!x || !hidden) return fail(LOCALI_E_ARG, "decode_gateup: null buffer");
     int rc = check_decode_args(routed, shared, x_dtype, tokens, top_k, route_slot,
                                LOCALI_COMBINE_ROUNDED);
@@ -543,6 +547,7 @@ int locali_moe_decode_down_combine(const locali_expert_arena *routed,
                                    int32_t top_k, const int32_t *route_slot, const float *weights,
                                    int32_t combine_mode, void *out, void *workspace,
                                    size_t workspace_bytes, void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
     if (!weights || !out) return fail(LOCALI_E_ARG, "decode_down_combine: null buffer");
     int rc = check_decode_args(routed, shared, x_dtype, tokens, top_k, route_slot, combine_mode);
     if (rc) return rc;
@@ -559,6 +564,7 @@ int locali_moe_expert_grouped(const locali_expert_arena *routed, const locali_ex
                               const float *weights, float swiglu_limit, int32_t fp32_swiglu,
                               int32_t combine_mode, void *out, void *workspace, size_t workspace_bytes,
                               void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
     int rc, dff = 0;
     if (!x || !dtype16(x_dtype) || tokens < 1 || top_k < 1 || !idx || !slot_of_expert || !weights ||
         !out || !workspace || n_experts < 1)
@@ -582,6 +588,7 @@ int locali_moe_expert_grouped(const locali_expert_arena *routed, const locali_ex
 int locali_moe_combine(const void *y, const void *shared_y, const float *weights, int32_t dtype,
                        int32_t tokens, int32_t top_k, int32_t d, int32_t combine_mode, void *out,
                        void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
     if (!y || !weights || !out || !dtype16(dtype) || tokens < 1 || top_k < 1 || d < 1)
         return fail(LOCALI_E_ARG, "combine: bad arguments");
     hipError_t e = launch_combine(static_cast<const uint16_t *>(y), nullptr,
@@ -647,6 +654,7 @@ int locali_moe_forward(const locali_router *router, const locali_expert_arena *r
                        int32_t x_dtype, int32_t tokens, const int32_t *input_ids, float swiglu_limit,
                        int32_t fp32_swiglu, void *out, int32_t *idx, float *weights, void *workspace,
                        size_t workspace_bytes, void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
     int rc, dff = 0;
     if (!routed || !x || !out || !idx || !weights || !workspace || !slot_of_expert || tokens < 1 ||
         !dtype16(x_dtype))

@@ -50,9 +50,17 @@ def test_python_bindings_cover_the_headers():
 
 def test_argument_errors_are_reported_without_a_gpu():
     lib = _lib.lib()
-    rc = lib.locali_moe_dispatch(None, 0, 6, 257, None, None, None)
+    rc = lib.locali_moe_dispatch(None, -1, 6, 257, None, None, None)
     assert rc == -1
     assert lib.locali_moe_last_error().startswith(b"dispatch:")
+
+
+def test_empty_batch_returns_without_touching_anything():
+    """tokens == 0 is a no-op that succeeds (no pointer is read, no GPU is
+    needed)."""
+    lib = _lib.lib()
+    assert lib.locali_moe_dispatch(None, 0, 6, 257, None, None, None) == 0
+    assert lib.locali_moe_combine(None, None, None, 2, 0, 6, 4096, 0, None, None) == 0
 
 
 def test_workspace_size_is_positive_and_monotone():

@@ -229,6 +229,34 @@ def test_expert_decode_rejects_bad_shapes():
                           torch.ones(1, 2, dtype=torch.int32, device=DEV), torch.ones(1, 2, device=DEV))
 
 
+def test_empty_batch_is_a_no_op():
+    """Zero tokens: every entry point returns at once with empty outputs (the
+    reference's layer call on an empty batch returns an empty output), and
+    the arena MoE returns an empty tensor of x's shape without routing."""
+    from locali_amd.arena import ArenaMoE
+    banner("empty batch")
+    d, dff, E, k = 1024, 512, 16, 4
+    arena = synth.expert_arena(E + 1, d, dff, seed=3, device=DEV)
+    shared = synth.expert_arena(1, d, dff, seed=4, device=DEV, zero_slot=False)
+    x = torch.zeros(0, d, dtype=torch.bfloat16, device=DEV)
+    w, _ = synth.uniform_router(E, d, torch.bfloat16, seed=5, device=DEV)
+    spec = ops.RouterSpec(w, k, routed_scale=1.5)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    idx, wts, _ = ops.router(spec, x, ops.Workspace(), slot_of_expert=slot_of, n_slots=E + 1)
+    assert tuple(idx.shape) == (0, k) and tuple(wts.shape) == (0, k)
+    none_i = torch.zeros(0, k, dtype=torch.int32, device=DEV)
+    none_w = torch.zeros(0, k, device=DEV)
+    assert tuple(ops.expert_decode(arena, shared, x, none_i, none_w).shape) == (0, d)
+    assert tuple(ops.expert_grouped(arena, shared, x, none_i, slot_of, none_w, ops.Workspace(),
+                                    n_experts=E).shape) == (0, d)
+    out, idx, wts = ops.forward(spec, arena, shared, slot_of, x, ops.Workspace())
+    assert tuple(out.shape) == (0, d) and tuple(idx.shape) == (0, k)
+    moe_ = ArenaMoE(None, 0, None, None, k)
+    y = moe_(torch.zeros(1, 0, d, dtype=torch.bfloat16, device=DEV))
+    assert tuple(y.shape) == (1, 0, d) and y.dtype == torch.bfloat16
+    torch.cuda.synchronize()
+
+
 # ---------------------------------------------------------------------------
 # Grouped path, dispatch, combine
 # ---------------------------------------------------------------------------
