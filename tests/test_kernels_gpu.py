@@ -70,6 +70,42 @@ def test_router_matches_oracle(T, score):
     assert checked >= 0.9 * T
 
 
+@pytest.mark.parametrize("E,k", [(64, 1), (384, 8), (512, 16)])
+@pytest.mark.parametrize("T", [1, 40])
+def test_router_expert_count_and_top_k_limits(E, k, T):
+    """Expert counts up to 512 (eight per lane) and top-k from 1 to 16, on the
+    gemv (T=1) and matrix-core (T=40) logits paths; and the decode forward,
+    which selects in its own kernel only for E <= 256, agrees with router +
+    expert_decode."""
+    banner(f"router limits E={E} k={k} T={T}")
+    d = 1024
+    w, bias = synth.uniform_router(E, d, torch.bfloat16, seed=E + k, bias_std=0.01)
+    x = synth.activations(T, d, torch.bfloat16, seed=T + E)
+    spec = ops.RouterSpec(w.to(DEV), k, routed_scale=1.5, score_bias=bias.to(DEV))
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    idx, wts, rs = ops.router(spec, x.to(DEV), ops.Workspace(), slot_of_expert=slot_of, n_slots=E + 1)
+    torch.cuda.synchronize()
+    oi, ow, margin, scores = moe.route(values(x), values(w), k, bias=values(bias), routed_scale=1.5)
+    scale = np.abs(scores).max(axis=1) + np.abs(values(bias)).max()
+    idx, wts, rs = idx.cpu().numpy(), wts.cpu().numpy(), rs.cpu().numpy()
+    checked = 0
+    for t in range(T):
+        if margin[t] < 1e-4 * scale[t]:
+            continue
+        checked += 1
+        assert list(idx[t]) == list(oi[t]), f"token {t}"
+        np.testing.assert_allclose(wts[t], ow[t], rtol=1e-5, atol=1e-7)
+        assert list(rs[t]) == [e + 1 for e in idx[t]]
+    assert checked >= 0.9 * T
+    if T == 1:
+        dff = 512
+        arena = synth.expert_arena(E + 1, d, dff, seed=E, device=DEV)
+        out, fi, fw = ops.forward(spec, arena, None, slot_of, x.to(DEV), ops.Workspace())
+        ri, rw, rslot = ops.router(spec, x.to(DEV), ops.Workspace(), slot_of_expert=slot_of, n_slots=E + 1)
+        assert torch.equal(fi, ri) and torch.equal(fw, rw)
+        assert torch.equal(out, ops.expert_decode(arena, None, x.to(DEV), rslot, rw))
+
+
 def test_router_hash_mode():
     banner("router hash")
     E, d, k, V, T = 64, 512, 6, 50, 20
