@@ -314,6 +314,35 @@ def test_dispatch_stable_sort():
         assert seg[s + 1] - seg[s] == counts.get(s, 0)
 
 
+@pytest.mark.parametrize("fp32_swiglu", [False, True])
+@pytest.mark.parametrize("bits", [(2, 2), (3, 3)])
+def test_expert_grouped_swiglu_modes_and_limit(fp32_swiglu, bits):
+    """The grouped kernels' SwiGLU epilogues (matrix-core 64-position and
+    small tiles for 2-bit, VALU for 3-bit) with the clamp driven (x scaled
+    by 4) at limits 10 and 0.5, and with it off (limit 0, unscaled x: with
+    no clamp the scaled inputs make h large enough that a last-place flip of
+    one h value moves y past the combine-term bound), op by op in the
+    activation dtype or in fp32."""
+    banner(f"grouped swiglu fp32={fp32_swiglu} bits={bits}")
+    d, dff, E, k, T = 1024, 512, 16, 4, 24
+    arena = synth.expert_arena(E + 1, d, dff, bits_gate_up=bits[0], bits_down=bits[1], seed=45)
+    x1 = synth.activations(T, d, seed=46)
+    x4 = (x1.float() * 4).to(torch.bfloat16)
+    gen = torch.Generator().manual_seed(47)
+    idx = torch.stack([torch.randperm(E, generator=gen)[:k] for _ in range(T)]).to(torch.int32)
+    idx[: T // 2, 0] = 3                      # one expert with a 64-position-kernel tile
+    slot_of = torch.arange(E, dtype=torch.int32) + 1
+    wts = torch.rand(T, k, generator=gen)
+    for limit in (10.0, 0.5, 0.0):
+        x = x4 if limit > 0 else x1
+        out = ops.expert_grouped(_dev(arena), None, x.to(DEV), idx.to(DEV), slot_of.to(DEV), wts.to(DEV),
+                                 ops.Workspace(), n_experts=E, swiglu_limit=limit, fp32_swiglu=fp32_swiglu)
+        torch.cuda.synchronize()
+        want, terms = _oracle_layer(x, idx.numpy(), wts.numpy(), arena, {e: e + 1 for e in range(E)},
+                                    torch.bfloat16, limit=limit, fp32_swiglu=fp32_swiglu, return_terms=True)
+        assert_close_terms(values(out), want, terms, f"grouped limit {limit}")
+
+
 @pytest.mark.parametrize("T,dtype,bits", [(3, torch.bfloat16, (2, 2)), (17, torch.bfloat16, (2, 4)),
                                           (64, torch.bfloat16, (2, 2)), (9, torch.float16, (4, 4)),
                                           (5, torch.bfloat16, (3, 3)), (33, torch.float16, (3, 3)),
