@@ -314,6 +314,34 @@ def test_dispatch_stable_sort():
         assert seg[s + 1] - seg[s] == counts.get(s, 0)
 
 
+@pytest.mark.parametrize("T", [2, 9, 40])
+def test_fp32_combine_mode_in_the_layer_kernels(T):
+    """combine_mode 1 (float32 products, the mixed-tier form) through the
+    decode kernels' fused combine (T=2) and the grouped path's (T=9, 40),
+    with the shared expert added after one rounding."""
+    banner(f"fp32 combine T={T}")
+    d, dff, E, k = 1024, 512, 16, 4
+    arena = synth.expert_arena(E + 1, d, dff, seed=61)
+    shared = synth.expert_arena(1, d, dff, seed=62, zero_slot=False)
+    x = synth.activations(T, d, seed=63)
+    gen = torch.Generator().manual_seed(64)
+    idx = torch.stack([torch.randperm(E, generator=gen)[:k] for _ in range(T)]).to(torch.int32)
+    slot_of = torch.arange(E, dtype=torch.int32) + 1
+    wts = torch.rand(T, k, generator=gen)
+    if T <= 2:
+        out = ops.expert_decode(_dev(arena), _dev(shared), x.to(DEV), (idx + 1).to(DEV), wts.to(DEV),
+                                combine_mode=ops.COMBINE_FP32)
+    else:
+        out = ops.expert_grouped(_dev(arena), _dev(shared), x.to(DEV), idx.to(DEV), slot_of.to(DEV),
+                                 wts.to(DEV), ops.Workspace(), n_experts=E, combine_mode=ops.COMBINE_FP32)
+    torch.cuda.synchronize()
+    sh = {kk: (v[0][0], v[1][0], v[2][0], v[3], v[4]) for kk, v in arena_numpy(shared).items()}
+    want, terms = moe.moe_layer(values(x), idx.numpy(), wts.numpy(), arena_numpy(arena),
+                                {e: e + 1 for e in range(E)}, "bf16", limit=10.0, shared=sh,
+                                combine_mode="fp32", return_terms=True)
+    assert_close_terms(values(out), want, terms, f"fp32 combine T={T}")
+
+
 @pytest.mark.parametrize("fp32_swiglu", [False, True])
 @pytest.mark.parametrize("bits", [(2, 2), (3, 3)])
 def test_expert_grouped_swiglu_modes_and_limit(fp32_swiglu, bits):
