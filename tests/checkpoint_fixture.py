@@ -98,3 +98,29 @@ def expert_bytes(truth, layer: int, expert: int) -> bytes:
         out += p.scales[expert].contiguous().view(torch.int16).numpy().tobytes()
         out += p.biases[expert].contiguous().view(torch.int16).numpy().tobytes()
     return out
+
+
+def add_mtp_stage(root: Path, *, experts, d, dff, bits=3, group=64, seed=0):
+    """Appends one embedded DSpark (MTP) stage to the snapshot at root: its
+    stacked routed experts as mtp.0.ffn.switch_mlp.* in a shard of their own
+    (bits-bit codes, bf16 metadata) and the config fields that declare the
+    head. Returns the stage's ExpertArenaT (slot e = expert e)."""
+    root = Path(root)
+    arena = synth.expert_arena(experts, d, dff, bits_gate_up=bits, group=group, dtype=torch.bfloat16,
+                               seed=seed, zero_slot=False)
+    shard = "model-mtp.safetensors"
+    wm = json.loads((root / "model.safetensors.index.json").read_text())["weight_map"]
+    tensors = {}
+    for proj, p in zip(PROJS, (arena.gate, arena.up, arena.down)):
+        base = f"mtp.0.ffn.switch_mlp.{proj}"
+        tensors[f"{base}.weight"] = (p.weight.numpy().view(np.uint32), "U32")
+        tensors[f"{base}.scales"] = (_bits16(p.scales), "BF16")
+        tensors[f"{base}.biases"] = (_bits16(p.biases), "BF16")
+        for arr in ARRS:
+            wm[f"{base}.{arr}"] = shard
+    write_safetensors(root / shard, tensors)
+    (root / "model.safetensors.index.json").write_text(json.dumps({"weight_map": wm}))
+    cfg = json.loads((root / "config.json").read_text())
+    cfg.update(n_mtp_layers=1, dspark_block_size=2, dspark_target_layer_ids=[cfg["num_hidden_layers"] - 1])
+    (root / "config.json").write_text(json.dumps(cfg))
+    return arena

@@ -379,3 +379,40 @@ def test_overlap_hits_splits_a_decode_call_and_stays_exact(ckpt, with_shared):
         assert torch.equal(mo(x), ref(x))
     finally:
         store.close()
+
+
+def test_two_tier_store_streams_cold_and_hot_layers(tmp_path):
+    """An index extended with the DSpark/MTP stage (reference
+    dsv4_index.py:146-249): main layers in the 2-bit cold tier, the stage as
+    logical layer 2 in a 3-bit hot tier, both sharing one ceiling split by
+    hot_share. Each layer streams from disk through its own tier and gives
+    exactly what the kernels give on the same weights held resident."""
+    import json
+    from checkpoint_fixture import add_mtp_stage
+    from locali_amd.index import build_index, extend_with_mtp
+    banner("two-tier store: cold 2-bit + hot 3-bit")
+    truth = make_snapshot(tmp_path, layers=2, experts=E, top_k=K, d=D, dff=DFF, seed=9)
+    hot_truth = add_mtp_stage(tmp_path, experts=E, d=D, dff=DFF, bits=3, seed=10)
+    index = extend_with_mtp(build_index(tmp_path), tmp_path)
+    path = tmp_path / "two_tier.idx"
+    path.write_text(json.dumps(index))
+    cold_item = _item(path)
+    hot_item = sum(index["experts"]["L2.E0"][p][a][3] for p in ("gate_proj", "up_proj", "down_proj")
+                   for a in ("weight", "scales", "biases"))
+    ceiling = 2 * (E + 1) * max(cold_item, hot_item)
+    store = V4ArenaStore(path, ceiling_gb=ceiling / 1e9, hot_share=0.5, threads=2, cache_policy="lru")
+    try:
+        assert store.tiers == ["cold", "hot"]
+        assert store.quant("hot", "bits") == 3 and store.expert_arena("hot").gate.bits == 3
+        assert store.expert_arena("cold").gate.bits == 2
+        g = torch.Generator().manual_seed(13)
+        x = (torch.randn(3, D, generator=g) * 0.5).to(torch.bfloat16).cuda()
+        ind = torch.tensor([[1, 4], [4, 0], [5, 1]], dtype=torch.int32, device="cuda")
+        sc = torch.tensor([[0.6, 0.4], [0.3, 0.7], [0.5, 0.5]], dtype=torch.float32, device="cuda")
+        for layer, t in ((0, truth[0]), (2, hot_truth), (1, truth[1])):
+            moe_ = V4ArenaMoE(store, layer, FixedGate(ind, sc), K, swiglu_limit=10.0)
+            assert torch.equal(moe_(x), _direct(_gpu(t), x, ind, sc)), f"layer {layer}"
+            moe_.gate = FixedGate(ind[:1], sc[:1])
+            assert torch.equal(moe_(x[:1]), _direct(_gpu(t), x[:1], ind[:1], sc[:1])), f"layer {layer} decode"
+    finally:
+        store.close()
