@@ -511,11 +511,16 @@ class ArenaStore:
     def close(self):
         """Drain the fills, close the files and release the arena's memory."""
         self.pool.shutdown(wait=True)
+        if self.fill_stream is not None:
+            # fills from host memory are queued on the device only: they must
+            # have landed before the arena's memory goes back to the allocator
+            self.fill_stream.synchronize()
         for fd in self.fds.values():
             os.close(fd)
         self.fds.clear()
         self.arena.clear()
         self.__dict__.pop("_expert_arena", None)
+        self.__dict__.pop("_slot_ptr_cache", None)
         self.staging.free.clear()
 
 
