@@ -181,6 +181,7 @@ __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, 
     using G = Geom<BITS, CPL, LPR, GPC>;
     constexpr int RB = J * G::kRPL;               // rows per workgroup
     __shared__ float ylds[WAVES][RB];
+    __shared__ float wlds[WAVES];   // the token's router weights, rounded to the activation dtype
     const int lane = threadIdx.x & 63;
     // wave index in an SGPR: the route's fields are then selected in scalar
     // registers (a reference to one of the two parameter structs would make
@@ -195,6 +196,9 @@ __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, 
     const int row0 = blockIdx.x * RB;
     const int64_t wpr = static_cast<int64_t>(K) * SB / 32;
     const int gpr = K / down.group;
+    // the combine's weights are loaded first, so that the epilogue after the
+    // barrier reads LDS instead of waiting on memory
+    if (threadIdx.x < ra.top_k) wlds[threadIdx.x] = round16<BF16>(ca.weights[t * ra.top_k + threadIdx.x]);
 
     if (wave < per_token) {
         const int j = wave;
@@ -243,7 +247,7 @@ __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, 
         if (row >= N) continue;
         float acc = 0.f;
         for (int j = 0; j < ra.top_k; ++j) {
-            const float w = round16<BF16>(ca.weights[t * ra.top_k + j]);
+            const float w = wlds[j];
             const float y = ylds[j][q];
             acc += ca.mode == 0 ? round16<BF16>(y * w) : y * w;
         }
