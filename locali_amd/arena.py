@@ -18,8 +18,10 @@ victim search while a cross-layer prefetch claims slots; `inflight` maps a
 resident key to the fills still writing it.
 
 The planner is the compiled one (locali_amd.native, the reference C ABI) in
-V4ArenaStore; this base class also carries the reference's Python SLRU
-(arena.py:212-354) for native_scheduler=False.
+V4ArenaStore. For native_scheduler=False this base class plans with a slot
+ledger of its own (_SlotLedger: per-slot holder, segment and recency stamp)
+that follows the rules of the reference's Python fallback planner
+(arena.py:212-354): a call's hits resolve before its misses.
 """
 
 from __future__ import annotations
@@ -28,8 +30,9 @@ import json
 import os
 import threading
 import time
-from collections import OrderedDict
+from collections import Counter
 from concurrent.futures import ThreadPoolExecutor
+from dataclasses import dataclass
 from pathlib import Path
 
 import numpy as np
@@ -40,6 +43,125 @@ ARRS = ("weight", "scales", "biases")
 TORCH_DT = {"U32": torch.int32, "I32": torch.int32, "F16": torch.float16, "BF16": torch.bfloat16,
             "F32": torch.float32, "U8": torch.uint8}
 POLICIES = ("lru", "slru-cold", "slru-all", "lfu-decay")
+
+
+@dataclass(frozen=True)
+class TierGeometry:
+    """Shape of one tier's slot pool."""
+    expert_bytes: int   # one expert's nine records
+    slots: int          # slot 0 (the zero expert) included
+    protected: int      # SLRU protected-segment capacity (0: plain LRU)
+    arrays: dict        # (proj, array) -> (bytes per slot, shape, dtype name)
+
+
+def tier_geometry(meta, ceiling: int, hot_share: float, cache_policy: str) -> dict:
+    """{tier: TierGeometry} for an index's experts under a byte ceiling
+    (reference arena.py:100-165).
+
+    Every expert of a tier has the same nine arrays, so the first expert the
+    index lists for a tier fixes its shapes; the search stops once two tiers
+    (hot and cold) are seen. A lone tier gets the whole ceiling; hot and cold
+    get hot_share and the rest; each holds as many whole experts as its bytes
+    allow, the reserved zero slot counted in. Under slru-all every tier, under
+    slru-cold only the cold one, keeps (slots - 1) // 2 slots for protected
+    entries."""
+    first: dict = {}
+    for m in meta.values():
+        if m["tier"] not in first:
+            first[m["tier"]] = m
+            if len(first) == 2:
+                break
+    names = sorted(first)
+    out = {}
+    for t in names:
+        if len(names) == 1:
+            frac = 1.0
+        else:
+            frac = {"hot": hot_share, "cold": 1.0 - hot_share}.get(t, 0.5)
+        arrays = {(p, k): (int(first[t][p][k][3]), tuple(first[t][p][k][4]), first[t][p][k][5])
+                  for p in PROJS for k in ARRS}
+        per = sum(nb for nb, _, _ in arrays.values())
+        n = int(ceiling * frac / per)
+        slru = cache_policy == "slru-all" or (cache_policy == "slru-cold" and t == "cold")
+        out[t] = TierGeometry(per, n, (n - 1) // 2 if slru and n > 0 else 0, arrays)
+    return out
+
+
+class _SlotLedger:
+    """The Python planner's record of one tier's slots: the key each slot
+    holds, the SLRU segment it sits in and a recency stamp.
+
+    New keys enter probation. A demand hit on a probation entry moves it to
+    the protected segment (when the tier has one); once that segment is over
+    capacity its least recently used entry drops back to probation. A
+    segment's least recently used entry is its smallest stamp (a counter
+    bumped on every entry and refresh). Slots never used yet are handed out
+    from the highest number down, and only while probation has room; slot 0
+    is the reserved zero expert and is never handed out."""
+
+    PROBATION, PROTECTED = 1, 2
+
+    def __init__(self, n_slots: int, protected_cap: int):
+        self.protected_cap = protected_cap
+        self.probation_cap = n_slots - 1 - protected_cap
+        self.holder: list = [None] * n_slots
+        self.segment = np.zeros(n_slots, dtype=np.int8)     # 0: never used
+        self.stamp = np.zeros(n_slots, dtype=np.int64)
+        self.slot_of: dict = {}
+        self.unused = n_slots - 1
+        self.size = {self.PROBATION: 0, self.PROTECTED: 0}
+        self.clock = 0
+
+    def lookup(self, key):
+        return self.slot_of.get(key)
+
+    def _enter(self, slot: int, segment: int) -> None:
+        if self.segment[slot]:
+            self.size[int(self.segment[slot])] -= 1
+        self.segment[slot] = segment
+        self.size[segment] += 1
+        self.clock += 1
+        self.stamp[slot] = self.clock
+
+    def _oldest(self, segment: int, held=()):
+        cand = np.flatnonzero(self.segment == segment)
+        if held:
+            cand = cand[~np.isin(cand, np.fromiter(held, dtype=np.int64))]
+        return int(cand[np.argmin(self.stamp[cand])]) if cand.size else None
+
+    def refresh(self, key) -> None:
+        """A demand hit: the entry becomes the most recent of its segment, or
+        moves from probation to the protected segment."""
+        slot = self.slot_of[key]
+        if self.segment[slot] == self.PROTECTED or self.protected_cap == 0:
+            self._enter(slot, int(self.segment[slot]))
+            return
+        self._enter(slot, self.PROTECTED)
+        if self.size[self.PROTECTED] > self.protected_cap:
+            self._enter(self._oldest(self.PROTECTED), self.PROBATION)
+
+    def claim(self, key, held):
+        """(slot, evicted key or None) for a key not resident, never taking a
+        slot in `held`; (None, None) when every candidate is held."""
+        if self.unused and self.size[self.PROBATION] < self.probation_cap:
+            slot, evicted = self.unused, None
+            self.unused -= 1
+        else:
+            slot = self._oldest(self.PROBATION, held)
+            if slot is None:
+                slot = self._oldest(self.PROTECTED, held)
+            if slot is None:
+                return None, None
+            evicted = self.holder[slot]
+            del self.slot_of[evicted]
+        self.holder[slot] = key
+        self.slot_of[key] = slot
+        self._enter(slot, self.PROBATION)
+        return slot, evicted
+
+    @property
+    def protected_size(self) -> int:
+        return self.size[self.PROTECTED]
 
 
 class ReadPlan(dict):
@@ -115,40 +237,27 @@ class ArenaStore:
         self.pf_keys: set = set()
         self.prefetched = self.prefetch_used = self.prefetch_wasted = 0
 
-        sample = {}
-        for m in self.meta.values():
-            sample.setdefault(m["tier"], m)
-            if len(sample) == 2:
-                break
-        self.tiers = sorted(sample)
-        share = ({self.tiers[0]: 1.0} if len(self.tiers) == 1
-                 else {"hot": hot_share, "cold": 1.0 - hot_share})
-        self.arena, self.item, self.slots = {}, {}, {}
-        self.lru, self.protected, self.protected_cap, self.free = {}, {}, {}, {}
+        geometry = tier_geometry(self.meta, self.ceiling, hot_share, cache_policy)
+        self.tiers = sorted(geometry)
+        self.arena, self.item, self.slots, self.protected_cap = {}, {}, {}, {}
+        self.ledger = {}   # tier -> _SlotLedger (the Python planner's state)
         self.layout = {}   # (tier, proj, array) -> (nbytes per slot, shape, dtype name)
         for t in self.tiers:
-            m = sample[t]
-            per = sum(m[p][k][3] for p in PROJS for k in ARRS)
-            self.item[t] = per
-            n = int(self.ceiling * share.get(t, 0.5) / per)
-            if n < 2:
+            g = geometry[t]
+            if g.slots < 2:
                 raise ValueError(f"{ceiling_gb:.3f} GB gives tier {t} no usable expert slot after "
                                  "its reserved zero slot; raise ceiling_gb or adjust hot_share")
-            self.slots[t] = n
-            self.lru[t] = OrderedDict()
-            self.protected[t] = OrderedDict()
-            slru = cache_policy == "slru-all" or (cache_policy == "slru-cold" and t == "cold")
-            self.protected_cap[t] = (n - 1) // 2 if slru else 0
-            self.free[t] = list(range(1, n))
-            for p in PROJS:
-                for k in ARRS:
-                    _, _, _, nb, shape, dt = m[p][k]
-                    if dt not in TORCH_DT:
-                        raise ValueError(f"tier {t} {p}.{k}: unsupported dtype {dt}")
-                    self.layout[(t, p, k)] = (nb, tuple(shape), dt)
-                    # zero-filled: slot 0 stays the all-zero expert
-                    self.arena[(t, p, k)] = torch.zeros((n, *shape), dtype=TORCH_DT[dt],
-                                                        device=self.device)
+            n = self.slots[t] = g.slots
+            self.item[t] = g.expert_bytes
+            self.protected_cap[t] = g.protected
+            self.ledger[t] = _SlotLedger(n, g.protected)
+            for (p, k), (nb, shape, dt) in g.arrays.items():
+                if dt not in TORCH_DT:
+                    raise ValueError(f"tier {t} {p}.{k}: unsupported dtype {dt}")
+                self.layout[(t, p, k)] = (nb, shape, dt)
+                # zero-filled: slot 0 stays the all-zero expert
+                self.arena[(t, p, k)] = torch.zeros((n, *shape), dtype=TORCH_DT[dt],
+                                                    device=self.device)
         self.resident = sum(self.slots[t] * self.item[t] for t in self.tiers)
         if self.resident > self.ceiling:
             raise AssertionError(f"arena allocated {self.resident} bytes against {self.ceiling}")
@@ -317,35 +426,7 @@ class ArenaStore:
         ev.record(self.fill_stream)
         return _Landed(ev)
 
-    # ---- Python planner (reference arena.py:212-289) ---------------------
-    def _claim(self, t, key, also_pinned=()):
-        """A slot for `key`: a free slot while probation has room, else the
-        least recently used unpinned probation entry, else the least recently
-        used unpinned protected entry; None when every candidate is pinned.
-        Pinned: the previous demand call's slots and `also_pinned` (the slots
-        the current call resolved already)."""
-        pin = set(self.pinned.get(t, ())) | set(also_pinned)
-        probation_cap = self.slots[t] - 1 - self.protected_cap[t]
-        probation_full = len(self.lru[t]) >= probation_cap
-        victim = segment = None
-        if probation_full or not self.free[t]:
-            victim = next((k for k, v in self.lru[t].items() if v not in pin), None)
-            if victim is not None:
-                segment = self.lru[t]
-        if victim is None and not probation_full and self.free[t]:
-            s = self.free[t].pop()
-        else:
-            if victim is None:
-                victim = next((k for k, v in self.protected[t].items() if v not in pin), None)
-                if victim is not None:
-                    segment = self.protected[t]
-            if victim is None:
-                return None
-            s = segment.pop(victim)
-            self._evicted(victim)
-        self.lru[t][key] = s
-        return s
-
+    # ---- Python planner (native_scheduler=False) ----------------------------
     def _evicted(self, victim):
         self.inflight.pop(victim, None)
         if victim in self.pf_keys:
@@ -353,29 +434,8 @@ class ArenaStore:
             self.prefetch_wasted += 1
         self.evictions += 1
 
-    def _slot(self, t, key):
-        return self.protected[t][key] if key in self.protected[t] else self.lru[t][key]
-
-    def _resident(self, t, key):
-        return key in self.lru[t] or key in self.protected[t]
-
     def _protected_size(self, t):
-        return len(self.protected[t])
-
-    def _touch(self, t, key):
-        """Refresh a hit: move to the fresh end, or promote a probation hit
-        (demoting the oldest protected entry when over capacity)."""
-        if key in self.protected[t]:
-            self.protected[t].move_to_end(key)
-            return
-        if self.protected_cap[t] == 0:
-            self.lru[t].move_to_end(key)
-            return
-        slot = self.lru[t].pop(key)
-        self.protected[t][key] = slot
-        if len(self.protected[t]) > self.protected_cap[t]:
-            old, old_slot = self.protected[t].popitem(last=False)
-            self.lru[t][old] = old_slot
+        return self.ledger[t].protected_size
 
     def _hit(self, key, t, prefetch, waits):
         if not prefetch:
@@ -391,43 +451,43 @@ class ArenaStore:
                 waits[t].extend(futs)
 
     def _place_keys(self, layer, want, prefetch):
-        """Resolve a layer's unique experts to slots (hits first, then misses
-        in order), returning (placed, issued fills, fills to wait for)."""
-        out, miss = {}, []
+        """The Python planner's placement of a layer's unique experts
+        (the reference's fallback planner, arena.py:212-354): the resident
+        ones are resolved first (a demand hit refreshes its entry), then the
+        misses take slots in call order; no miss takes a slot that the
+        previous demand call or this call already holds. Returns (placed,
+        issued fills, fills to wait for)."""
+        out, issued, misses = {}, [], []
         waits = {t: [] for t in self.tiers}
+        held = {t: set() for t in self.tiers}
         for e in want:
             key, t = (layer, e), self.tier(layer, e)
-            if self._resident(t, key):
-                out[e] = (t, self._slot(t, key))
-                if not prefetch:
-                    self._touch(t, key)
-                self._hit(key, t, prefetch, waits)
-            else:
-                if not prefetch:
-                    self.misses += 1
-                miss.append((e, t))
+            slot = self.ledger[t].lookup(key)
+            if slot is None:
+                misses.append((e, t))
+                continue
+            out[e] = (t, slot)
+            held[t].add(slot)
+            if not prefetch:
+                self.ledger[t].refresh(key)
+            self._hit(key, t, prefetch, waits)
         if not prefetch:
-            need: dict = {}
-            for _, t in miss:
-                need[t] = need.get(t, 0) + 1
-            for t, n in need.items():
+            self.misses += len(misses)
+            for t, n in Counter(t for _, t in misses).items():
                 if n > self.slots[t] - 1:
                     raise ValueError(f"layer {layer} needs {n} {t} experts but the arena has "
                                      f"{self.slots[t] - 1}; raise ceiling_gb or hot_share")
-        issued = []
-        taken = {t: {s for tt, s in out.values() if tt == t} for t in self.tiers}
-        for e, t in miss:
-            s = self._claim(t, (layer, e), taken[t])
-            if s is None:
+        for e, t in misses:
+            slot, evicted = self.ledger[t].claim((layer, e), held[t] | set(self.pinned.get(t, ())))
+            if slot is None:
                 continue
-            out[e] = (t, s)
-            taken[t].add(s)
-            issued.append((e, t, s))
+            if evicted is not None:
+                self._evicted(evicted)
+            out[e] = (t, slot)
+            held[t].add(slot)
+            issued.append((e, t, slot))
         if not prefetch:
-            pin = {t: set() for t in self.tiers}
-            for t, s in out.values():
-                pin[t].add(s)
-            self.pinned = pin
+            self.pinned = held
         return out, issued, waits
 
     # ---- public surface (reference arena.py:291-457) ---------------------

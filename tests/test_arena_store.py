@@ -174,6 +174,81 @@ def test_python_planner_is_lru_with_pins(ckpt):
         _store(index, 3, native_scheduler=False, cache_policy="lfu-decay")
 
 
+@pytest.mark.parametrize("policy,slots", [("lru", 4), ("lru", 9), ("slru-all", 9), ("slru-all", 14),
+                                          ("slru-cold", 11)])
+def test_python_planner_matches_the_oracle_hits_first(ckpt, policy, slots):
+    """native_scheduler=False follows the reference's fallback planner
+    (arena.py:305-354): a call's resident experts resolve first (a demand
+    hit refreshes its entry, a prefetch hit does not), then its misses in
+    call order, each miss pinning the previous demand call's slots and every
+    slot this call holds. That is the oracle planner driven one key at a
+    time in that order; slots, evictions and segment sizes must agree."""
+    _, _, index, _ = ckpt
+    st = _store(index, slots, native_scheduler=False, cache_policy=policy)
+    prot = (slots - 1) // 2 if policy in ("slru-all", "slru-cold") else 0
+    ref = OraclePlanner(LAYERS * EXPERTS, slots, prot, SLRU)
+    rng = random.Random(11 + slots)
+    pinned: set = set()
+    evictions = 0
+    try:
+        for step in range(60):
+            layer = rng.randrange(LAYERS)
+            prefetch = step % 5 == 4
+            want = list(dict.fromkeys(rng.randrange(EXPERTS) for _ in range(rng.randint(1, 3))))
+            keys = {e: layer * EXPERTS + e for e in want}
+            hits = [e for e in want if ref.peek(keys[e]) >= 0]
+            miss = [e for e in want if ref.peek(keys[e]) < 0]
+            expect, held = {}, set()
+            for e in hits:
+                _, (r,) = ref.plan([keys[e]], pinned_slots=(), touch_hits=not prefetch)
+                expect[e] = r.slot
+                held.add(r.slot)
+            for e in miss:
+                _, (r,) = ref.plan([keys[e]], pinned_slots=pinned | held, touch_hits=not prefetch)
+                if r.placed:
+                    expect[e] = r.slot
+                    held.add(r.slot)
+                    evictions += r.evicted_key >= 0
+            if prefetch:
+                out, plan = st.submit(layer, want, prefetch=True)
+                st.wait([f for fs in plan.values() for f in fs])
+            else:
+                out = st.slots_for(layer, want)
+                pinned = held
+            assert {e: s for e, (_, s) in out.items()} == expect, f"step {step}"
+            assert st.stats()["protected"]["cold"] == ref.protected_size
+            assert st.ledger["cold"].size[st.ledger["cold"].PROBATION] == ref.probation_size
+        assert st.stats()["evictions"] == evictions and st.stats()["scheduler"] == "python"
+    finally:
+        st.close()
+
+
+def test_tier_geometry_splits_the_ceiling():
+    """Slot counts per tier from the byte ceiling (reference arena.py:100-165):
+    hot and cold take hot_share and the rest in whole experts (zero slot
+    counted in); slru-cold protects half of the cold tier's usable slots only;
+    the first expert listed for a tier fixes its arrays."""
+    from locali_amd.arena import tier_geometry
+
+    def expert(tier, rows):
+        recs = {k: ["/r", "s", 0, rows * w, [rows, w], dt]
+                for k, w, dt in (("weight", 8, "U32"), ("scales", 1, "BF16"), ("biases", 1, "BF16"))}
+        return {"tier": tier, **{p: dict(recs) for p in PROJS}}
+
+    meta = {"L0.E0": expert("cold", 10), "L0.E1": expert("hot", 20), "L0.E2": expert("hot", 99)}
+    per_cold, per_hot = 3 * 10 * 10, 3 * 20 * 10
+    g = tier_geometry(meta, 100_000, 0.33, "slru-cold")
+    assert sorted(g) == ["cold", "hot"]
+    assert (g["cold"].expert_bytes, g["hot"].expert_bytes) == (per_cold, per_hot)
+    assert g["hot"].slots == int(100_000 * 0.33 / per_hot) == 55
+    assert g["cold"].slots == int(100_000 * 0.67 / per_cold) == 223
+    assert (g["cold"].protected, g["hot"].protected) == (111, 0)
+    assert g["hot"].arrays[("up_proj", "weight")][1] == (20, 8)
+    one = tier_geometry({"L0.E0": expert("cold", 10)}, 10_000, 0.33, "slru-all")["cold"]
+    assert (one.slots, one.protected) == (33, 16)
+    assert tier_geometry(meta, 100_000, 0.33, "lru")["cold"].protected == 0
+
+
 def test_prefetch_is_best_effort_and_accounted(ckpt):
     _, truth, index, _ = ckpt
     st = _store(index, 5)
