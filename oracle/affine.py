@@ -81,7 +81,11 @@ def bf16_value(bits16) -> np.ndarray:
 
 
 def round_to(a, dtype: str) -> np.ndarray:
-    """Round to bf16 / fp16 and return the value as float32 ('f32' keeps fp32)."""
+    """Round to bf16 / fp16 and return the value as float32 ('f32' keeps fp32;
+    'f64' rounds nothing: the exact formula, for comparisons with float64
+    references)."""
+    if dtype == "f64":
+        return np.asarray(a, dtype=np.float64)
     if dtype == "bf16":
         return bf16_value(bf16_bits(np.asarray(a, dtype=np.float64).astype(np.float32)))
     if dtype == "f16":

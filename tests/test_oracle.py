@@ -157,6 +157,133 @@ def test_c_oracle_layer_matches_numpy_oracle(oracle_lib, dt, bits):
     assert np.mean(got == want) > 0.9
 
 
+# -- SwiGLU and the expert: transformers DeepSeek-V4 expert classes ------------
+# tests/golden/make_swiglu_vectors.py ran DeepseekV4Experts._apply_gate,
+# DeepseekV4MLP and DeepseekV4Experts (modeling_deepseek_v4.py:965-1021) in
+# float64 on dense matrices expanded from affine codes; "f64" runs the oracle
+# with no rounding, so the two must agree to float64 noise.
+
+PROJ_NAMES = ("gate_proj", "up_proj", "down_proj")
+
+
+def _swiglu_gold():
+    return np.load(GOLD / "swiglu_vectors.npz")
+
+
+def _gold_experts(g, case):
+    bits, group, E = (int(v) for v in g[f"{case}_meta"][:3])
+    return [{p: (affine.pack(g[f"{case}_{p}_q_{e}"], bits), g[f"{case}_{p}_s_{e}"],
+                 g[f"{case}_{p}_b_{e}"], bits, group) for p in PROJ_NAMES} for e in range(E)]
+
+
+def _check_against_transformers(g):
+    """Every golden comparison for the SwiGLU and the expert (AssertionError
+    on the first mismatch)."""
+    for i, limit in enumerate(g["limits"]):
+        np.testing.assert_allclose(moe.swiglu(g["gate"], g["up"], "f64", limit=float(limit)),
+                                   g[f"h64_{i}"], rtol=1e-13, atol=1e-13)
+    for case in ("a", "b"):
+        limit = float(g[f"{case}_limit"])
+        x = g[f"{case}_x"]
+        experts = _gold_experts(g, case)
+        for e, proj in enumerate(experts):
+            np.testing.assert_allclose(moe.expert(x, proj, "f64", limit), g[f"{case}_mlp"][:, e],
+                                       rtol=1e-11, atol=1e-11)
+        arena = {p: (np.stack([ex[p][0] for ex in experts]), np.stack([ex[p][1] for ex in experts]),
+                     np.stack([ex[p][2] for ex in experts]), experts[0][p][3], experts[0][p][4])
+                 for p in PROJ_NAMES}
+        routed = moe.moe_layer(x, g[f"{case}_idx"], g[f"{case}_wts"], arena,
+                               {e: e for e in range(len(experts))}, "f64", limit=limit)
+        np.testing.assert_allclose(routed, g[f"{case}_routed"], rtol=1e-11, atol=1e-10)
+
+
+def test_swiglu_and_expert_match_transformers_deepseek_v4():
+    g = _swiglu_gold()
+    assert min(float(g["a_clamped"]), float(g["b_clamped"])) > 0.2    # the clamp is exercised
+    _check_against_transformers(g)
+
+
+@pytest.mark.parametrize("i", [0, 1, 2])
+def test_fp32_swiglu_matches_transformers_float32_gate(i):
+    """fp32_swiglu (dsv4_arena.py:228-232): SiLU(gate) * up in float32, one
+    rounding to the activation dtype. Against _apply_gate run in float32 and
+    rounded to bf16: float32 SiLU implementations may differ in the last fp32
+    place, which can move a bf16 rounding by one place, never more."""
+    g = _swiglu_gold()
+    limit = float(g["limits"][i])
+    got = moe.swiglu(g["gate"], g["up"], "bf16", limit=limit, fp32_swiglu=True)
+    want = affine.round_to(g[f"h32_{i}"], "bf16")
+    assert np.mean(got == want) > 0.97
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-30)
+
+
+def _silu(v):
+    return v / (1.0 + np.exp(-v))
+
+
+SWIGLU_MUTANTS = {
+    "gate clipped from below too": lambda g, u, L: _silu(np.clip(g, -L, L)) * np.clip(u, -L, L),
+    "cap applied after SiLU": lambda g, u, L: np.minimum(_silu(g), L) * np.clip(u, -L, L),
+    "up not clipped": lambda g, u, L: _silu(np.minimum(g, L)) * u,
+    "up clipped from above only": lambda g, u, L: _silu(np.minimum(g, L)) * np.minimum(u, L),
+    "gate and up swapped": lambda g, u, L: _silu(np.minimum(u, L)) * np.clip(g, -L, L),
+    "sigmoid in place of SiLU": lambda g, u, L: (1 / (1 + np.exp(-np.minimum(g, L)))) * np.clip(u, -L, L),
+}
+
+
+@pytest.mark.parametrize("mutant", sorted(SWIGLU_MUTANTS))
+def test_golden_vectors_reject_planted_swiglu_mistakes(mutant, monkeypatch):
+    """A misreading of the clamp (dsv4_arena.py:225-227) planted in the oracle
+    must fail the transformers comparison."""
+    wrong = SWIGLU_MUTANTS[mutant]
+
+    def planted(gate, up, dtype, limit=10.0, fp32_swiglu=False):
+        g64, u64 = np.asarray(gate, np.float64), np.asarray(up, np.float64)
+        return affine.round_to(wrong(g64, u64, limit) if limit > 0 else _silu(g64) * u64, dtype)
+
+    monkeypatch.setattr(moe, "swiglu", planted)
+    with pytest.raises(AssertionError):
+        _check_against_transformers(_swiglu_gold())
+
+
+def test_swiglu_closed_forms():
+    rng = np.random.default_rng(17)
+    gate, up = rng.uniform(-20, 20, 500), rng.uniform(-20, 20, 500)
+    # limit <= 0: no clamp at all (dsv4_arena.py:225); SiLU from torch
+    silu = torch.nn.functional.silu(torch.from_numpy(gate)).numpy()
+    for limit in (0.0, -1.0):
+        np.testing.assert_allclose(moe.swiglu(gate, up, "f64", limit=limit), silu * up, rtol=1e-14)
+    # gate at or above the limit: SiLU(limit) * clip(up)
+    L = 3.0
+    hi = L + rng.uniform(0, 50, 500)
+    np.testing.assert_allclose(moe.swiglu(hi, up, "f64", limit=L),
+                               (L / (1 + np.exp(-L))) * np.clip(up, -L, L), rtol=1e-14)
+    # up beyond +-limit saturates at +-limit; gate is not raised from below
+    low = np.full(4, -40.0)
+    out = moe.swiglu(low, np.array([-50.0, -5.0, 5.0, 50.0]), "f64", limit=10.0)
+    np.testing.assert_allclose(out, _silu(-40.0) * np.array([-10.0, -5.0, 5.0, 10.0]), rtol=1e-14)
+
+
+def test_expert_closed_form_all_zero_codes():
+    """All-zero codes leave w = bias: with constant biases and x = 0.1 the
+    projections are bias * sum(x), worked out by hand; the clamp then acts on
+    the hand values."""
+    d, dff, group = 128, 64, 64
+
+    def proj(rows, cols, bias):
+        return (affine.pack(np.zeros((rows, cols), np.uint8), 2), np.full((rows, cols // group), 0.03),
+                np.full((rows, cols // group), bias), 2, group)
+
+    experts = {"gate_proj": proj(dff, d, 0.25), "up_proj": proj(dff, d, 0.5), "down_proj": proj(d, dff, 0.125)}
+    x = np.full((1, d), 0.1)
+    sx = 0.1 * d                                      # 12.8: up = 6.4, gate = 3.2
+    for limit, (g, u) in ((10.0, (3.2, 6.4)), (2.0, (2.0, 2.0)), (0.0, (3.2, 6.4))):
+        assert (0.25 * sx, 0.5 * sx) == pytest.approx((3.2, 6.4))
+        h = g / (1 + np.exp(-g)) * u
+        y = moe.expert(x, experts, "f64", limit)
+        np.testing.assert_allclose(y, np.full((1, d), 0.125 * dff * h), rtol=1e-13)
+
+
 # -- router -------------------------------------------------------------------
 
 @pytest.mark.parametrize("case", ["a", "b", "c"])
