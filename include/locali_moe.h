@@ -190,6 +190,21 @@ int locali_moe_combine(const void *y, const void *shared_y, const float *weights
                        int32_t dtype, int32_t tokens, int32_t top_k, int32_t d,
                        int32_t combine_mode, void *out, void *stream);
 
+/* The combine of route outputs that sit anywhere in y: route (t, j) reads
+ * row route_pos[t * top_k + j] of y (no term when negative), terms summed in
+ * j order, rounded as locali_moe_combine rounds them (weights rounded to
+ * out_dtype; ROUNDED: each product rounded; FP32: products and sum in fp32),
+ * plus round(out + shared_y[t]) when shared_y is non-NULL. y rows [*, d] in
+ * y_dtype (F32, F16 or BF16); shared_y, out [tokens, d] in out_dtype.
+ * Replaces the unsort + fp32 scatter-add of routes that span tiers
+ * (arena.py:657-672; the caller orders each token's routes tier by tier) and
+ * the reassembly of a decode token's split hit / miss routes
+ * (arena.py:605-618). */
+int locali_moe_combine_routes(const void *y, int32_t y_dtype, const int32_t *route_pos,
+                              const void *shared_y, const float *weights, int32_t out_dtype,
+                              int32_t tokens, int32_t top_k, int32_t d, int32_t combine_mode,
+                              void *out, void *stream);
+
 /* Asynchronous host -> device copy of `bytes` into an arena slot region
  * (src should be pinned host memory for a truly asynchronous copy). */
 int locali_moe_arena_fill(void *dst, const void *src_host, size_t bytes, void *stream);

@@ -98,6 +98,7 @@ _SIGNATURES = {
     "locali_moe_expert_grouped": ([ctypes.POINTER(ExpertArena), ctypes.POINTER(ExpertArena), _P, _I,
                                    _I, _I, _I, _P, _P, _P, _F, _I, _I, _P, _P, _SZ, _P], ctypes.c_int),
     "locali_moe_combine": ([_P, _P, _P, _I, _I, _I, _I, _I, _P, _P], ctypes.c_int),
+    "locali_moe_combine_routes": ([_P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P], ctypes.c_int),
     "locali_moe_arena_fill": ([_P, _P, _SZ, _P], ctypes.c_int),
     "locali_moe_arena_fill_batch": ([ctypes.POINTER(FillPiece), ctypes.c_int32, _P], ctypes.c_int),
     "locali_moe_forward": ([ctypes.POINTER(Router), ctypes.POINTER(ExpertArena),

@@ -175,16 +175,23 @@ class ReadPlan(dict):
 
 class _Landed:
     """Future of a fill copied from pinned host memory: an event recorded on
-    the fill stream after the expert's copies."""
+    the fill stream after the experts' copies. It holds the source tensors
+    until the event has passed (the copy kernel reads them asynchronously),
+    so a host_source that hands out fresh pinned tensors stays correct."""
 
-    def __init__(self, event):
+    def __init__(self, event, sources=()):
         self.event = event
+        self.sources = list(sources)
 
     def done(self) -> bool:
-        return self.event.query()
+        if self.event.query():
+            self.sources.clear()
+            return True
+        return False
 
     def result(self, timeout=None):
         self.event.synchronize()
+        self.sources.clear()
 
 
 class _Staging:
@@ -394,8 +401,9 @@ class ArenaStore:
 
     def _host_bytes(self, key, t) -> torch.Tensor:
         src = self.host_source(*key)
-        if src.is_cuda or src.dtype != torch.uint8 or src.numel() != self.item[t]:
-            raise ValueError(f"host_source{key}: expected {self.item[t]} host bytes (uint8)")
+        if (src.is_cuda or src.dtype != torch.uint8 or src.numel() != self.item[t]
+                or not src.is_contiguous()):
+            raise ValueError(f"host_source{key}: expected {self.item[t]} contiguous host bytes (uint8)")
         return src
 
     def _fill_from_host(self, jobs) -> _Landed:
@@ -404,9 +412,10 @@ class ArenaStore:
         queued on the compute stream (a refilled slot may still be read there),
         and return the event that follows them. jobs: (key, tier, slot, recs)."""
         from .ops import arena_fill_batch_ptrs
-        pieces = []
+        pieces, sources = [], []
         for key, t, slot, recs in jobs:
             src = self._host_bytes(key, t)
+            sources.append(src)
             base, off = src.data_ptr(), 0
             for (arr_ptr, nbytes), r in zip(self._slot_ptrs(t), recs):
                 pieces.append((arr_ptr + slot * nbytes, base + off, r[3]))
@@ -424,7 +433,7 @@ class ArenaStore:
         arena_fill_batch_ptrs(pieces, self.fill_stream)
         ev = torch.cuda.Event()
         ev.record(self.fill_stream)
-        return _Landed(ev)
+        return _Landed(ev, sources)
 
     # ---- Python planner (native_scheduler=False) ----------------------------
     def _evicted(self, victim):
@@ -715,10 +724,12 @@ class ArenaMoE:
         """One token with some experts still filling (reference
         arena.py:575-618): the routes whose slots are resident are launched
         before the host blocks on the pending fills, the others after. The
-        per-route outputs then meet in the kernels' single-tier combine --
-        products of y and the rounded weight rounded, summed in k order in
-        float32, one rounding, then the folded shared expert with one more --
-        so the result is bit-identical to the unsplit call."""
+        per-route outputs then meet in the library's combine in k order with
+        the kernels' single-tier rounding (products of y and the rounded
+        weight rounded, summed in float32, one rounding, then the folded
+        shared expert with one more), so the result is bit-identical to the
+        unsplit call."""
+        from . import ops
         dev = flat.device
         ready = [j for j, e in enumerate(row) if e not in pending]
         late = [j for j, e in enumerate(row) if e in pending]
@@ -729,62 +740,60 @@ class ArenaMoE:
         ws = self._workspace()
 
         def run(pos):
-            slots = torch.tensor([[placed[row[j]][1]] for j in pos], dtype=torch.int32, device=dev)
+            slots = self._device_slots([[placed[row[j]][1]] for j in pos], dev)
             return self._routes(arena, x_in.expand(len(pos), -1).contiguous(), slots, ws)
 
         y_ready = run(ready)
         self.store.wait(reads[t])
-        y_late = run(late)
-        y = torch.empty(len(row), x_in.shape[1], dtype=x_in.dtype, device=dev)
-        y[ready] = y_ready
-        y[late] = y_late
-        w = gates.reshape(-1)[:len(row)].to(torch.float32).to(x_in.dtype).to(torch.float32)
-        prod = (y.to(torch.float32) * w.unsqueeze(1)).to(x_in.dtype).to(torch.float32)
-        acc = torch.zeros(x_in.shape[1], dtype=torch.float32, device=dev)
-        for j in range(len(row)):
-            acc = acc + prod[j]
-        out = acc.to(x_in.dtype)
+        y = torch.cat([y_ready, run(late)])            # rows: the ready routes, then the late ones
+        where = {j: i for i, j in enumerate(ready + late)}
+        route_pos = self._device_slots([[where[j] for j in range(len(row))]], dev)
+        ys = None
         if self.shared_expert is not None:
             zero = torch.zeros(1, 1, dtype=torch.int32, device=dev)
             ys = self._routes(self.shared_expert, x_in, zero, ws)
-            out = (out.to(torch.float32) + ys.to(torch.float32).reshape(-1)).to(x_in.dtype)
-        return out.reshape(1, -1).to(dtype)
+        out = ops.combine_routes(y, route_pos, gates.reshape(-1)[:len(row)].reshape(1, -1).to(torch.float32),
+                                 x_in.dtype, shared_y=ys, mode=ops.COMBINE_ROUNDED)
+        return out.to(dtype)
 
     def _apply_tiers(self, flat, ii, placed, gates, dtype, reads, present):
         """Routes spanning tiers (reference arena.py:626-672). Each tier's
         own (token, k) entries run through that tier's experts, one route per
-        entry; a float32 accumulator takes y * w (w = the score rounded to the
-        activation dtype, then float32) tier by tier in the store's tier order
-        and, within a tier, k position by k position -- per token that is the
-        reference's row-major entry order, and each index_add_ touches a token
-        once, so the sum order is fixed. One rounding at the end, then the
-        shared expert (when folded) with one more."""
+        entry; the library's combine then takes each token's routes tier by
+        tier in the store's tier order and, within a tier, in k order -- the
+        reference's row-major entry order of its per-tier scatter-adds --
+        with float32 products of y and the score rounded to the activation
+        dtype, a float32 sum and one rounding, then the shared expert (when
+        folded) with one more."""
+        from . import ops
         k = self.top_k
         dev = flat.device
-        g = gates.to(dtype).to(torch.float32)
-        out = torch.zeros(flat.shape[0], flat.shape[1], dtype=torch.float32, device=dev)
         ws = self._workspace()
+        rank = {t: i for i, t in enumerate(present)}
+        entry, ys, base = {}, [], 0
         for t in present:
             if reads is not None:
                 self.store.wait(reads[t])
             ent = [(r, j) for r, row in enumerate(ii) for j, e in enumerate(row) if placed[e][0] == t]
-            rows = torch.tensor([r for r, _ in ent], dtype=torch.long, device=dev)
-            cols = torch.tensor([j for _, j in ent], dtype=torch.long, device=dev)
-            slots = torch.tensor([[placed[ii[r][j]][1]] for r, j in ent], dtype=torch.int32, device=dev)
+            rows = self._device_slots([[r for r, _ in ent]], dev).reshape(-1).to(torch.long)
+            slots = self._device_slots([[placed[ii[r][j]][1]] for r, j in ent], dev)
             x_in = flat.index_select(0, rows).contiguous()
             if self.store.use_f16(t) and x_in.dtype == torch.bfloat16:
                 x_in = x_in.to(torch.float16)
-            y = self._routes(self.store.expert_arena(t), x_in, slots, ws)
-            val = y.to(torch.float32) * g[rows, cols].unsqueeze(1)
-            for j in range(k):
-                sel = (cols == j).nonzero().squeeze(1)
-                if sel.numel():
-                    out.index_add_(0, rows.index_select(0, sel), val.index_select(0, sel))
-        res = out.to(dtype)
+            ys.append(self._routes(self.store.expert_arena(t), x_in, slots, ws))
+            for i, rj in enumerate(ent):
+                entry[rj] = base + i
+            base += len(ent)
+        order = [sorted(range(k), key=lambda j: (rank[placed[row[j]][0]], j)) for row in ii]
+        route_pos = self._device_slots([[entry[(r, j)] for j in order[r]] for r in range(len(ii))], dev)
+        perm = self._device_slots(order, dev).to(torch.long)
+        w = torch.gather(gates.to(torch.float32), 1, perm).contiguous()
+        y = torch.cat(ys) if len({v.dtype for v in ys}) == 1 else torch.cat([v.float() for v in ys])
+        shared_y = None
         if self.shared_expert is not None:
             x_s = flat.contiguous()
             if x_s.dtype != self.shared_expert.gate.scales.dtype and x_s.dtype == torch.bfloat16:
                 x_s = x_s.to(torch.float16)
             zero = torch.zeros(flat.shape[0], 1, dtype=torch.int32, device=dev)
-            res = res + self._routes(self.shared_expert, x_s, zero, ws).to(dtype)
-        return res
+            shared_y = self._routes(self.shared_expert, x_s, zero, ws).to(dtype)
+        return ops.combine_routes(y, route_pos, w, dtype, shared_y=shared_y, mode=ops.COMBINE_FP32)

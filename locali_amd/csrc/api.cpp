@@ -599,6 +599,25 @@ int locali_moe_combine(const void *y, const void *shared_y, const float *weights
     return 0;
 }
 
+int locali_moe_combine_routes(const void *y, int32_t y_dtype, const int32_t *route_pos,
+                              const void *shared_y, const float *weights, int32_t out_dtype,
+                              int32_t tokens, int32_t top_k, int32_t d, int32_t combine_mode,
+                              void *out, void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
+    if (!y || !route_pos || !weights || !out || !dtype16(out_dtype) || tokens < 1 || top_k < 1 || d < 1)
+        return fail(LOCALI_E_ARG, "combine_routes: bad arguments");
+    if (y_dtype != LOCALI_DT_F32 && !dtype16(y_dtype))
+        return fail(LOCALI_E_ARG, "combine_routes: y dtype %d", y_dtype);
+    if (combine_mode != LOCALI_COMBINE_ROUNDED && combine_mode != LOCALI_COMBINE_FP32)
+        return fail(LOCALI_E_ARG, "combine_routes: combine mode %d", combine_mode);
+    const int y_type = y_dtype == LOCALI_DT_F32 ? 0 : (y_dtype == LOCALI_DT_F16 ? 1 : 2);
+    hipError_t e = launch_combine_routes(y, y_type, route_pos, static_cast<const uint16_t *>(shared_y), weights,
+                                         tokens, top_k, d, combine_mode, out_dtype == LOCALI_DT_BF16,
+                                         static_cast<uint16_t *>(out), S(stream));
+    if (e != hipSuccess) return hip_fail(e, "combine_routes launch");
+    return 0;
+}
+
 int locali_moe_arena_fill(void *dst, const void *src_host, size_t bytes, void *stream) {
     if (!dst || !src_host) return fail(LOCALI_E_ARG, "arena_fill: null pointer");
     if (!bytes) return 0;

@@ -170,6 +170,40 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict
     out[static_cast<int64_t>(t) * d + col] = from_float<BF16>(o);
 }
 
+// Weighted combine of route outputs held anywhere in `y`: route (t, j) reads
+// row route_pos[t * top_k + j] (skipped when negative), in j order. YT is the
+// rows' type (0 fp32, 1 fp16, 2 bf16); BF16 the output / shared / weight
+// rounding type.
+template <int YT>
+__device__ __forceinline__ float load_row_value(const void *y, int64_t i) {
+    if constexpr (YT == 0) return static_cast<const float *>(y)[i];
+    else return to_float<YT == 2>(static_cast<const uint16_t *>(y)[i]);
+}
+
+template <int YT, bool BF16>
+__global__ __launch_bounds__(256) void combine_routes_kernel(const void *__restrict__ y,
+                                                             const int32_t *__restrict__ route_pos,
+                                                             const uint16_t *__restrict__ shared_y,
+                                                             const float *__restrict__ weights,
+                                                             int top_k, int d, int mode,
+                                                             uint16_t *__restrict__ out) {
+    const int t = blockIdx.y;
+    const int col = blockIdx.x * blockDim.x + threadIdx.x;
+    if (col >= d) return;
+    float acc = 0.f;
+    for (int j = 0; j < top_k; ++j) {
+        const int r = t * top_k + j;
+        const int p = route_pos[r];
+        if (p < 0) continue;
+        const float w = round16<BF16>(weights[r]);
+        const float v = load_row_value<YT>(y, static_cast<int64_t>(p) * d + col);
+        acc += mode == 0 ? round16<BF16>(v * w) : v * w;
+    }
+    float o = round16<BF16>(acc);
+    if (shared_y) o = round16<BF16>(o + to_float<BF16>(shared_y[static_cast<int64_t>(t) * d + col]));
+    out[static_cast<int64_t>(t) * d + col] = from_float<BF16>(o);
+}
+
 // --------------------------------------------------------------------------
 hipError_t grouped_b2_bf16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
 hipError_t grouped_b2_f16(int, int, int, const GroupedKernelLaunch &, hipStream_t);
@@ -252,6 +286,26 @@ hipError_t launch_combine(const uint16_t *y, const int32_t *route_pos, const uin
     else
         hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(256), 0, st, y, route_pos, shared_y, weights,
                            tokens, top_k, d, mode, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine_routes(const void *y, int y_type, const int32_t *route_pos,
+                                 const uint16_t *shared_y, const float *weights, int tokens, int top_k,
+                                 int d, int mode, bool bf16, uint16_t *out, hipStream_t st) {
+    dim3 grid((d + 255) / 256, tokens);
+#define LOCALI_COMBINE_ROUTES(YT, B)                                                                   \
+    hipLaunchKernelGGL((combine_routes_kernel<YT, B>), grid, dim3(256), 0, st, y, route_pos, shared_y, \
+                       weights, top_k, d, mode, out)
+    if (bf16) {
+        if (y_type == 0) LOCALI_COMBINE_ROUTES(0, true);
+        else if (y_type == 1) LOCALI_COMBINE_ROUTES(1, true);
+        else LOCALI_COMBINE_ROUTES(2, true);
+    } else {
+        if (y_type == 0) LOCALI_COMBINE_ROUTES(0, false);
+        else if (y_type == 1) LOCALI_COMBINE_ROUTES(1, false);
+        else LOCALI_COMBINE_ROUTES(2, false);
+    }
+#undef LOCALI_COMBINE_ROUTES
     return hipGetLastError();
 }
 

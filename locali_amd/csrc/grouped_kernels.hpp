@@ -276,5 +276,8 @@ hipError_t launch_route_slots(const int32_t *idx, int R, int E, const int32_t *s
 hipError_t launch_combine(const uint16_t *y, const int32_t *route_pos, const uint16_t *shared_y,
                           const float *weights, int tokens, int top_k, int d, int mode, bool bf16,
                           uint16_t *out, hipStream_t st);
+hipError_t launch_combine_routes(const void *y, int y_type, const int32_t *route_pos,
+                                 const uint16_t *shared_y, const float *weights, int tokens, int top_k,
+                                 int d, int mode, bool bf16, uint16_t *out, hipStream_t st);
 
 }  // namespace locali

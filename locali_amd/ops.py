@@ -2,8 +2,11 @@
 
 Tensors must already live on the GPU; the wrappers pass raw device pointers
 and the current HIP stream, check shapes on the host, and raise on any error.
-PyTorch supplies device memory and streams only -- every byte of arithmetic
-runs in the library's HIP kernels.
+PyTorch supplies device memory, streams, data movement (index selects,
+concatenation) and the dtype casts the reference itself makes (activations to
+fp16 for an fp16-metadata tier, dsv4_arena.py:172-173; the output back to x's
+dtype, arena.py:547); every product and sum runs in the library's HIP
+kernels.
 """
 
 from __future__ import annotations
@@ -19,7 +22,8 @@ from ._lib import (COMBINE_FP32, COMBINE_ROUNDED, DT_BF16, DT_F16, DT_F32, SCORE
 
 __all__ = [
     "ProjArena", "ExpertArenaT", "RouterSpec", "Workspace", "router", "dispatch",
-    "expert_decode", "decode_gateup", "decode_down_combine", "expert_grouped", "combine", "forward", "arena_fill",
+    "expert_decode", "decode_gateup", "decode_down_combine", "expert_grouped", "combine", "combine_routes",
+    "forward", "arena_fill",
     "COMBINE_ROUNDED", "COMBINE_FP32",
 ]
 
@@ -295,6 +299,23 @@ def combine(y: torch.Tensor, weights: torch.Tensor, shared_y=None, mode=COMBINE_
     rc = lib().locali_moe_combine(_ptr(y.contiguous()), _ptr(shared_y), _ptr(weights.contiguous()),
                                   _dt(y), T, k, d, int(mode), _ptr(out), _stream())
     check(rc, "locali_moe_combine")
+    return out
+
+
+def combine_routes(y: torch.Tensor, route_pos: torch.Tensor, weights: torch.Tensor, out_dtype,
+                   shared_y=None, mode=COMBINE_ROUNDED):
+    """out[t] = combine over j of y[route_pos[t, j]] (rows skipped where
+    route_pos < 0) with weights[t, j], in j order; y rows in fp32, fp16 or
+    bf16, out and shared_y in out_dtype (locali_moe_combine_routes)."""
+    T, k = route_pos.shape
+    d = y.shape[-1]
+    out = torch.empty(T, d, dtype=out_dtype, device=y.device)
+    if shared_y is not None and shared_y.dtype != out_dtype:
+        raise TypeError("shared_y must be in the output dtype")
+    rc = lib().locali_moe_combine_routes(_ptr(y.contiguous()), _dt(y), _ptr(route_pos.contiguous()),
+                                         _ptr(shared_y), _ptr(weights.contiguous()), DTYPES[out_dtype],
+                                         T, k, d, int(mode), _ptr(out), _stream())
+    check(rc, "locali_moe_combine_routes")
     return out
 
 

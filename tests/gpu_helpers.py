@@ -78,3 +78,23 @@ def assert_close_terms(got, want, terms, what, rtol=RTOL, atol=ATOL):
 
 def exact_fraction(got, want) -> float:
     return float(np.mean(np.asarray(got) == np.asarray(want)))
+
+
+def ulp(v, dtype) -> np.ndarray:
+    """Spacing of the 16-bit format at |v| (bf16: 8 significant bits, fp16:
+    11), subnormal spacing below the smallest normal."""
+    a = np.abs(np.asarray(v, dtype=np.float64))
+    if dtype == torch.bfloat16:
+        e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+        return 2.0 ** (e - 7)
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def ulp_distance(got, want, dtype) -> np.ndarray:
+    """|got - want| in units of the format's spacing at want (a value one
+    rounding step away from want, on either side, is at distance 1 or less:
+    at a power of two the spacing below is half the one above)."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    return np.abs(got - want) / ulp(want, dtype)
