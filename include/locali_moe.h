@@ -235,6 +235,23 @@ int locali_moe_forward(const locali_router *router, const locali_expert_arena *r
                        int32_t fp32_swiglu, void *out, int32_t *idx, float *weights,
                        void *workspace, size_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference. For callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops): locali_moe_forward without
+ * the workspace arguments. Its scratch is a static device array of
+ * LOCALI_NOALLOC_SCRATCH_BYTES per GPU inside the library (enough for 64
+ * tokens of a d_model 4096, 256-expert, d_ff 2048 layer with a shared
+ * expert), set up and cleared by the first call on each device and held
+ * until the process ends; a call needing more returns LOCALI_E_WORKSPACE.
+ * It calls no allocator. All calls on one GPU share that GPU's array, so
+ * calls that overlap on one GPU race: serialise them. */
+#define LOCALI_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int locali_moe_forward_noalloc(const locali_router *router, const locali_expert_arena *routed,
+                               const locali_expert_arena *shared, const int32_t *slot_of_expert,
+                               const void *x, int32_t x_dtype, int32_t tokens,
+                               const int32_t *input_ids, float swiglu_limit,
+                               int32_t fp32_swiglu, void *out, int32_t *idx, float *weights,
+                               void *stream);
+
 const char *locali_moe_last_error(void);
 
 #ifdef __cplusplus

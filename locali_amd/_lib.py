@@ -104,6 +104,9 @@ _SIGNATURES = {
     "locali_moe_forward": ([ctypes.POINTER(Router), ctypes.POINTER(ExpertArena),
                             ctypes.POINTER(ExpertArena), _P, _P, _I, _I, _P, _F, _I, _P, _P, _P, _P,
                             _SZ, _P], ctypes.c_int),
+    "locali_moe_forward_noalloc": ([ctypes.POINTER(Router), ctypes.POINTER(ExpertArena),
+                                    ctypes.POINTER(ExpertArena), _P, _P, _I, _I, _P, _F, _I, _P, _P, _P,
+                                    _P], ctypes.c_int),
     "locali_moe_last_error": ([], ctypes.c_char_p),
 }
 

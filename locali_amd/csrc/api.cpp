@@ -33,6 +33,16 @@ int hip_fail(hipError_t e, const char *where) {
     return fail(LOCALI_E_HIP, "%s: %s", where, hipGetErrorString(e));
 }
 
+}  // namespace
+
+namespace locali {
+// The library's error record for entry points defined in other translation
+// units (locali_moe_last_error reads it).
+int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
+}  // namespace locali
+
+namespace {
+
 constexpr size_t kAlign = 256;
 constexpr int kMaxSlots = 16000;
 constexpr int kMaxExperts = 512;
