@@ -184,9 +184,10 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     uint32_t xw[16 / BITS];
     diag_prep_load<BITS>(xw, ra.x + static_cast<int64_t>(token) * K + wave * kDiagWindow, lane);
     const int mrs = 2 * gpr + 16;   // LDS bytes per metadata row
-    int ma[2], mo[2], md[2];
+    // 4 arrays x 16 RT rows x `waves` pieces: RT pieces per thread
+    int ma[RT], mo[RT], md[RT];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < RT; ++q) {
         const int c = static_cast<int>(threadIdx.x) + q * 64 * waves;
         const int row = (c / waves) % (16 * RT), pc = c % waves;
         ma[q] = c / (16 * RT * waves);
@@ -230,9 +231,9 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     const uint16_t *m_gb = (shared ? sgate.b : gate.b) + sl * gm_slot + mrow0;
     const uint16_t *m_us = (shared ? sup.s : up.s) + sl * um_slot + mrow0;
     const uint16_t *m_ub = (shared ? sup.b : up.b) + sl * um_slot + mrow0;
-    u32x4 mv[2];
+    u32x4 mv[RT];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < RT; ++q) {
         const uint16_t *arr = ma[q] == 0 ? m_gs : ma[q] == 1 ? m_gb : ma[q] == 2 ? m_us : m_ub;
         mv[q] = *reinterpret_cast<const u32x4 *>(arr + mo[q]);
     }
@@ -255,8 +256,8 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
         }
     sched_fence();
     if constexpr (!SELECT) diag_prep_store<BITS, BF16>(mw, xw, lane);
-    *reinterpret_cast<u32x4 *>(mlds + md[0]) = mv[0];
-    *reinterpret_cast<u32x4 *>(mlds + md[1]) = mv[1];
+#pragma unroll
+    for (int q = 0; q < RT; ++q) *reinterpret_cast<u32x4 *>(mlds + md[q]) = mv[q];
     __syncthreads();
     const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
     // diagonal A: lane (m, kb) feeds unit 8 line + 4 ((m / 2) % 2) + kb when m / 4 == kb

@@ -59,10 +59,13 @@ constexpr int kRouterWaves = 4;   // experts per workgroup (one per wave)
 // tokens per pass. Every lane issues all NCH gate chunks of its expert and
 // the TB tokens' x chunks before the first dot; tokens beyond L.tokens in
 // the last pass re-read the last token and are not stored.
+// One wave per workgroup: each expert's row then streams on its own compute
+// unit (the 2 MiB gate spread over all of them; the workgroup -> XCD mapping
+// is the same every step, so each gate row stays in one L2).
 template <bool XBF16, int NCH, int TB>
-__global__ __launch_bounds__(64 * kRouterWaves) void router_gemv_fast_kernel(RouterLaunch L) {
+__global__ __launch_bounds__(64) void router_gemv_fast_kernel(RouterLaunch L) {
     const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+    const int e = blockIdx.x;
     const bool have = e < L.E;
     const uint16_t *gw = static_cast<const uint16_t *>(L.gate_w) +
                          static_cast<int64_t>(min(e, L.E - 1)) * L.d;
@@ -280,7 +283,8 @@ hipError_t launch_router(const RouterLaunch &L, hipStream_t st, bool logits_only
     const int nch = L.d % 512 == 0 ? L.d / 512 : 0;
     if (dot_ok && (nch == 2 || nch == 4 || nch == 8 || nch == 16)) {
         const int tb = L.tokens == 1 ? 1 : L.tokens == 2 ? 2 : 4;
-#define LOCALI_FAST(XB, N, T) hipLaunchKernelGGL((router_gemv_fast_kernel<XB, N, T>), grid, block, 0, st, L)
+#define LOCALI_FAST(XB, N, T) \
+    hipLaunchKernelGGL((router_gemv_fast_kernel<XB, N, T>), dim3(L.E), dim3(64), 0, st, L)
 #define LOCALI_FAST_TB(XB, N) \
     if (tb == 1) LOCALI_FAST(XB, N, 1); else if (tb == 2) LOCALI_FAST(XB, N, 2); else LOCALI_FAST(XB, N, 4);
 #define LOCALI_FAST_N(XB) \
