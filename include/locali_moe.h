@@ -170,6 +170,38 @@ int locali_moe_decode_down_combine(const locali_expert_arena *routed,
                                    int32_t combine_mode, void *out, void *workspace,
                                    size_t workspace_bytes, void *stream);
 
+/* The decode forward's own first two kernels, callable separately (for a
+ * caller that times or interleaves them; locali_moe_forward runs the same
+ * kernels back to back):
+ *   locali_moe_router_logits       logits [tokens, n_experts] fp32 = x . Wg^T
+ *                                  (the gate product of V4ArenaMoE.route,
+ *                                  dsv4_arena.py:165-166), tokens <= 8;
+ *   locali_moe_decode_gateup_select gate/up + clamped SwiGLU with each token's
+ *                                  routes chosen inside the kernel from those
+ *                                  logits (score function, selection-only bias,
+ *                                  top-k, renormalised and scaled weights, slot
+ *                                  lookup: the rest of the gate and the
+ *                                  expert -> slot lookup of arena.py:558-567),
+ *                                  writing idx, weights, route_slot [tokens,
+ *                                  top_k] and hidden; tokens <= 2, n_experts
+ *                                  <= 256, gate/up of 2- or 4-bit codes in
+ *                                  groups of 64, d_model a multiple of 512 up
+ *                                  to 4096; the workspace is laid out as for
+ *                                  locali_moe_decode_gateup, and
+ *                                  locali_moe_decode_down_combine on the same
+ *                                  workspace then finishes the layer. */
+int locali_moe_router_logits(const locali_router *router, const void *x, int32_t x_dtype,
+                             int32_t tokens, int32_t d_model, float *logits, void *stream);
+int locali_moe_decode_gateup_select(const locali_router *router,
+                                    const locali_expert_arena *routed,
+                                    const locali_expert_arena *shared,
+                                    const int32_t *slot_of_expert, const void *x,
+                                    int32_t x_dtype, int32_t tokens, const int32_t *input_ids,
+                                    const float *logits, float swiglu_limit,
+                                    int32_t fp32_swiglu, int32_t *idx, float *weights,
+                                    int32_t *route_slot, void *hidden, void *workspace,
+                                    size_t workspace_bytes, void *stream);
+
 /* Grouped form of locali_moe_expert_decode for many tokens: (token, k) entries
  * are grouped by slot on the device and every slot's weights are streamed
  * once per group; expert ids idx [tokens, top_k] and slot_of_expert [n_experts]

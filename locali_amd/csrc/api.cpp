@@ -434,13 +434,10 @@ int check_router(const locali_router *r, int d) {
 // Builds the router launch; with logits_only (and a decode-sized call whose
 // gate/up kernel selects on its own, router_select_fusable) only the logits
 // kernel is launched and `*launch` carries what that kernel needs.
-int route(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens, int32_t d_model,
-          const int32_t *input_ids, const float *logits_in, const int32_t *slot_of_expert,
-          int32_t n_slots, int32_t *idx, float *weights, int32_t *route_slot, void *workspace,
-          const Layout &lay, hipStream_t st, bool logits_only = false, RouterLaunch *launch = nullptr) {
-    if (router->tid2eid && !input_ids) return fail(LOCALI_E_ARG, "router: hash routing needs input_ids");
-    if (route_slot && (!slot_of_expert || n_slots < 1))
-        return fail(LOCALI_E_ARG, "router: route_slot needs slot_of_expert and n_slots");
+RouterLaunch router_launch(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens,
+                           int32_t d_model, const int32_t *input_ids, const float *logits_in,
+                           const int32_t *slot_of_expert, int32_t n_slots, int32_t *idx, float *weights,
+                           int32_t *route_slot, float *logits) {
     RouterLaunch L{};
     L.x = static_cast<const uint16_t *>(x);
     L.x_bf16 = x_dtype == LOCALI_DT_BF16;
@@ -462,8 +459,20 @@ int route(const locali_router *router, const void *x, int32_t x_dtype, int32_t t
     L.idx = idx;
     L.weights = weights;
     L.route_slot = route_slot;
-    L.logits = at<float>(workspace, lay.logits);
+    L.logits = logits;
     L.logits_in = logits_in;
+    return L;
+}
+
+int route(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens, int32_t d_model,
+          const int32_t *input_ids, const float *logits_in, const int32_t *slot_of_expert,
+          int32_t n_slots, int32_t *idx, float *weights, int32_t *route_slot, void *workspace,
+          const Layout &lay, hipStream_t st, bool logits_only = false, RouterLaunch *launch = nullptr) {
+    if (router->tid2eid && !input_ids) return fail(LOCALI_E_ARG, "router: hash routing needs input_ids");
+    if (route_slot && (!slot_of_expert || n_slots < 1))
+        return fail(LOCALI_E_ARG, "router: route_slot needs slot_of_expert and n_slots");
+    const RouterLaunch L = router_launch(router, x, x_dtype, tokens, d_model, input_ids, logits_in, slot_of_expert,
+                                         n_slots, idx, weights, route_slot, at<float>(workspace, lay.logits));
     if (launch) *launch = L;
     if (logits_only && !router_select_fusable(L)) return fail(LOCALI_E_ARG, "router: selection cannot be deferred");
     hipError_t e = launch_router(L, st, logits_only);
@@ -676,6 +685,58 @@ int locali_moe_arena_fill_batch(const locali_fill_piece *pieces, int32_t n, void
         blocks += nb;
     }
     return flush();
+}
+
+int locali_moe_router_logits(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens,
+                             int32_t d_model, float *logits, void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
+    int rc;
+    if ((rc = check_router(router, d_model))) return rc;
+    if (!x || !logits || tokens < 1 || !dtype16(x_dtype)) return fail(LOCALI_E_ARG, "router_logits: bad arguments");
+    if (tokens > kFusedSelectMaxTokens)
+        return fail(LOCALI_E_ARG, "router_logits: %d tokens; at most %d (decode)", tokens, kFusedSelectMaxTokens);
+    const RouterLaunch L = router_launch(router, x, x_dtype, tokens, d_model, nullptr, nullptr, nullptr, 0, nullptr,
+                                         nullptr, nullptr, logits);
+    hipError_t e = launch_router(L, S(stream), true);
+    if (e != hipSuccess) return hip_fail(e, "router_logits launch");
+    return 0;
+}
+
+int locali_moe_decode_gateup_select(const locali_router *router, const locali_expert_arena *routed,
+                                    const locali_expert_arena *shared, const int32_t *slot_of_expert,
+                                    const void *x, int32_t x_dtype, int32_t tokens, const int32_t *input_ids,
+                                    const float *logits, float swiglu_limit, int32_t fp32_swiglu, int32_t *idx,
+                                    float *weights, int32_t *route_slot, void *hidden, void *workspace,
+                                    size_t workspace_bytes, void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
+    int rc, dff = 0;
+    if (!routed || !x || !logits || !idx || !weights || !route_slot || !hidden || !workspace || !slot_of_expert ||
+        tokens < 1 || !dtype16(x_dtype))
+        return fail(LOCALI_E_ARG, "decode_gateup_select: bad arguments");
+    const int d = routed->gate.cols;
+    if ((rc = check_router(router, d))) return rc;
+    if ((rc = check_arena(routed, "routed", x_dtype, d, &dff))) return rc;
+    if ((rc = check_shared(routed, shared))) return rc;
+    if (router->tid2eid && !input_ids) return fail(LOCALI_E_ARG, "decode_gateup_select: hash routing needs input_ids");
+    const int k = router->top_k;
+    if (tokens > kDecodeMaxTokens)
+        return fail(LOCALI_E_ARG, "decode_gateup_select: %d tokens; at most %d", tokens, kDecodeMaxTokens);
+    if (k + (shared ? 1 : 0) > 16) return fail(LOCALI_E_ARG, "decode_gateup_select: top_k + shared > 16");
+    if (routed->gate.n_slots > kMaxSlots) return fail(LOCALI_E_ARG, "decode_gateup_select: n_slots > %d", kMaxSlots);
+    // the decode stages' layout (no logits region: the logits are the caller's), so
+    // that locali_moe_decode_down_combine finds the prepared hidden vectors
+    const Layout lay = layout(tokens, d, dff, 1, k, shared ? 1 : 0);
+    if (workspace_bytes < lay.total)
+        return fail(LOCALI_E_WORKSPACE, "decode_gateup_select: workspace %zu < %zu bytes", workspace_bytes, lay.total);
+    const RouterLaunch RL = router_launch(router, x, x_dtype, tokens, d, input_ids, nullptr, slot_of_expert,
+                                          routed->gate.n_slots, idx, weights, route_slot, const_cast<float *>(logits));
+    const DecodeLaunch DL = decode_launch(routed, shared, x, x_dtype, tokens, k, route_slot, weights, swiglu_limit,
+                                          fp32_swiglu, LOCALI_COMBINE_ROUNDED, hidden, nullptr, workspace, lay);
+    if (!router_select_fusable(RL) || !gateup_diag_eligible(DL))
+        return fail(LOCALI_E_ARG, "decode_gateup_select: needs n_experts <= 256 and a gate/up of 2- or 4-bit "
+                                  "codes in groups of 64 with d_model a multiple of 512 up to 4096");
+    return run_decode(routed, shared, x, x_dtype, tokens, k, route_slot, weights, swiglu_limit, fp32_swiglu,
+                      LOCALI_COMBINE_ROUNDED, hidden, nullptr, S(stream), 1, workspace, lay, &RL);
 }
 
 int locali_moe_forward(const locali_router *router, const locali_expert_arena *routed,

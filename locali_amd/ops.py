@@ -22,7 +22,8 @@ from ._lib import (COMBINE_FP32, COMBINE_ROUNDED, DT_BF16, DT_F16, DT_F32, SCORE
 
 __all__ = [
     "ProjArena", "ExpertArenaT", "RouterSpec", "Workspace", "router", "dispatch",
-    "expert_decode", "decode_gateup", "decode_down_combine", "expert_grouped", "combine", "combine_routes",
+    "expert_decode", "decode_gateup", "decode_down_combine", "router_logits", "decode_gateup_select",
+    "expert_grouped", "combine", "combine_routes",
     "forward", "arena_fill",
     "COMBINE_ROUNDED", "COMBINE_FP32",
 ]
@@ -270,6 +271,47 @@ def decode_down_combine(arena: ExpertArenaT, shared: ExpertArenaT | None, route_
                                               _stream())
     check(rc, "locali_moe_decode_down_combine")
     return out
+
+
+def router_logits(spec: RouterSpec, x: torch.Tensor, logits=None):
+    """fp32 logits [T, E] = x . Wg^T (the decode forward's logits kernel; T <= 8)."""
+    x2 = _flat(x)
+    T, d = x2.shape
+    out = torch.empty(T, spec.n_experts, dtype=torch.float32, device=x.device) if logits is None else logits
+    st = spec.struct()
+    rc = lib().locali_moe_router_logits(ctypes.byref(st), _ptr(x2), _dt(x2), T, d, _ptr(out), _stream())
+    check(rc, "locali_moe_router_logits")
+    return out
+
+
+def decode_gateup_select(spec: RouterSpec, arena: ExpertArenaT, shared: ExpertArenaT | None,
+                         slot_of_expert: torch.Tensor, x: torch.Tensor, logits: torch.Tensor,
+                         hidden: torch.Tensor, ws: "Workspace", *, input_ids=None, swiglu_limit=10.0,
+                         fp32_swiglu=False, idx=None, weights=None, route_slot=None):
+    """The decode forward's gate/up kernel with the routes selected inside it
+    from `logits`; returns (idx, weights, route_slot). decode_down_combine on
+    the same workspace finishes the layer."""
+    x2 = _flat(x)
+    T = x2.shape[0]
+    k = spec.top_k
+    dev = x.device
+    idx = torch.empty(T, k, dtype=torch.int32, device=dev) if idx is None else idx
+    weights = torch.empty(T, k, dtype=torch.float32, device=dev) if weights is None else weights
+    route_slot = torch.empty(T, k, dtype=torch.int32, device=dev) if route_slot is None else route_slot
+    buf = _decode_ws(ws, arena, T, k, shared)
+    ids = None
+    if input_ids is not None:
+        ids = input_ids.reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
+    r, a = spec.struct(), arena.struct()
+    s = shared.struct() if shared is not None else None
+    rc = lib().locali_moe_decode_gateup_select(ctypes.byref(r), ctypes.byref(a),
+                                               ctypes.byref(s) if s is not None else None,
+                                               _ptr(slot_of_expert), _ptr(x2), _dt(x2), T, _ptr(ids),
+                                               _ptr(logits.contiguous()), float(swiglu_limit), int(fp32_swiglu),
+                                               _ptr(idx), _ptr(weights), _ptr(route_slot), _ptr(hidden),
+                                               _ptr(buf), buf.numel(), _stream())
+    check(rc, "locali_moe_decode_gateup_select")
+    return idx, weights, route_slot
 
 
 def expert_grouped(arena: ExpertArenaT, shared: ExpertArenaT | None, x: torch.Tensor,

@@ -604,6 +604,34 @@ def test_forward_decode_selects_in_gateup(mode):
             np.testing.assert_allclose(wts[t].cpu().numpy(), ow[t], rtol=1e-5)
 
 
+@pytest.mark.parametrize("T", [1, 2])
+def test_decode_forward_in_separate_stages(T):
+    """router_logits -> decode_gateup_select -> decode_down_combine are the
+    decode forward's own kernels called one at a time: routes, weights and
+    output equal locali_moe_forward's bit for bit, and routing on the
+    returned logits through the router equals the router's own."""
+    banner(f"decode forward stages T={T}")
+    d, E, dff, k = 4096, 256, 2048, 6
+    arena = synth.expert_arena(E + 1, d, dff, dtype=torch.bfloat16, seed=81, device=DEV)
+    shared = synth.expert_arena(1, d, dff, dtype=torch.bfloat16, seed=82, device=DEV, zero_slot=False)
+    w, bias = synth.uniform_router(E, d, torch.bfloat16, seed=83, device=DEV, bias_std=0.01)
+    spec = ops.RouterSpec(w, k, routed_scale=1.5, score_bias=bias)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    x = synth.activations(T, d, torch.bfloat16, seed=84, device=DEV)
+    ref, ridx, rw = ops.forward(spec, arena, shared, slot_of, x, ops.Workspace())
+    ws = ops.Workspace()
+    logits = ops.router_logits(spec, x)
+    hidden = torch.empty(T * (k + 1), dff, dtype=torch.bfloat16, device=DEV)
+    idx, wts, rs = ops.decode_gateup_select(spec, arena, shared, slot_of, x, logits, hidden, ws)
+    out = torch.empty_like(x)
+    ops.decode_down_combine(arena, shared, rs, wts, out, ws)
+    li, lw, lrs = ops.router(spec, x, ops.Workspace(), logits=logits, slot_of_expert=slot_of, n_slots=E + 1)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, ridx) and torch.equal(wts, rw) and torch.equal(out, ref)
+    assert torch.equal(li, idx) and torch.equal(lw, wts) and torch.equal(lrs, rs)
+    assert torch.equal(rs, idx + 1)
+
+
 def test_forward_full_width_decode(oracle_lib):
     """d 4096, 256 experts + shared, d_ff 2048, 2-bit g64 bf16, 1 token; checked
     against the C oracle (fp32) on the GPU's own routing."""
