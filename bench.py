@@ -485,6 +485,7 @@ def main(argv=None):
     ap.add_argument("--no-graph", action="store_true", help="launch steps eagerly")
     ap.add_argument("--prefill-calls", type=int, default=20)
     ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--prefill-sizes", default="64,512", help="tokens per prefill call, comma-separated")
     ap.add_argument("--skip-mixed", action="store_true")
     ap.add_argument("--skip-stack", action="store_true")
     ap.add_argument("--stack-steps", type=int, default=128)
@@ -592,7 +593,7 @@ def main(argv=None):
         },
     }
     if not args.skip_prefill:
-        for tokens in (64, 512):
+        for tokens in (int(v) for v in args.prefill_sizes.split(",")):
             phase(f"prefill {tokens} tokens")
             result[f"prefill{tokens}"] = prefill_run(arena, shared, slot_of, dev, tokens,
                                                      args.prefill_calls, args.seed + 100)
