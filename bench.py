@@ -73,6 +73,10 @@ EXPERT_BYTES = 2 * proj_bytes(DFF, D) + proj_bytes(D, DFF)          # 7,864,320
 MIXED_EXPERT_BYTES = 2 * proj_bytes(DFF, D) + proj_bytes(D, DFF, bits=4)   # 9,961,472
 GATEUP_ROUTE_BYTES = 2 * proj_bytes(DFF, D)                           # 5,242,880
 ROUTER_BYTES = E * D * 2
+# copula correlation between the next layer's gate applied to the current
+# input and that layer's own routing logits (the stack's lookahead); 0.9
+# puts about two thirds of a lookahead top-6 among the next layer's top-6
+LOOKAHEAD_RHO = 0.9
 # per decode gate/up launch: 7 routes' gate+up slots, x read once, h written
 GATEUP_ALG_BYTES = (K_TOP + 1) * GATEUP_ROUTE_BYTES + D * 2 + (K_TOP + 1) * DFF * 2   # 36,737,024
 # the decode step's gate/up kernel also reads the token's logits and writes its
@@ -271,9 +275,20 @@ def mixed_run(dev, tokens, calls, seed):
                         "down 4-bit affine g64 bf16, 32 tokens per call, uniform routing"}
 
 
-def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96):
+def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetch_k=None,
+              lookahead_rho=LOOKAHEAD_RHO):
     """Decode through a stack of full-width layers sharing one bounded arena,
-    misses copied from pinned host memory (V4ArenaStore host_source)."""
+    misses copied from pinned host memory (V4ArenaStore host_source).
+
+    Even layers' gates read the routing logits from x[:, :E], odd layers'
+    from x[:, E:2E]; a layer's input carries its own logits in its slice and,
+    in the other, a lookahead view of the next layer's logits (Gumbel noise
+    with copula correlation lookahead_rho to that layer's), which is what the
+    next layer's gate sees when it is applied to the current input.
+
+    prefetch_k: each layer also routes its input through the next layer's
+    gate and prefetches that call's prefetch_k highest-weight experts
+    (cross-layer prefetch at depth 1)."""
     import tempfile
     from locali_amd.dsv4_arena import V4ArenaMoE, V4ArenaStore, V4Gate
     tmp = tempfile.TemporaryDirectory()
@@ -295,18 +310,34 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96):
                                                 p.biases[layer:layer + 1], p.bits, p.group_size)
                                   for p in (shared.gate, shared.up, shared.down)))
 
-    gate = V4Gate(synth.identity_router(E, D, torch.bfloat16, dev), top_k=K_TOP,
-                  routed_scaling_factor=1.5)
-    mods = [V4ArenaMoE(store, layer, gate, K_TOP, shared_expert=shared_of(layer))
+    w_even = synth.identity_router(E, D, torch.bfloat16, dev)
+    gates = [V4Gate(w, top_k=K_TOP, routed_scaling_factor=1.5)
+             for w in (w_even, torch.roll(w_even, E, dims=1).contiguous())]
+    mods = [V4ArenaMoE(store, layer, gates[layer % 2], K_TOP, shared_expert=shared_of(layer))
             for layer in range(layers)]
+    if prefetch_k:
+        for cur, nxt in zip(mods, mods[1:]):
+            cur.nxt, cur.prefetch_k = nxt, prefetch_k
     n_tok = warmup + steps
     X = synth.activations(n_tok * layers, D, torch.bfloat16, seed=seed + 2, device=dev).view(n_tok, layers, D)
-    X[:, :, :E] = synth.layered_zipf_logits(n_tok, layers, E, 1.1, 0.6, seed=seed + 3).to(dev, torch.bfloat16)
+    logits, ahead = synth.layered_zipf_lookahead(n_tok, layers, E, 1.1, 0.6, lookahead_rho, seed=seed + 3)
+    for layer in range(layers):
+        own = (layer % 2) * E
+        X[:, layer, own:own + E] = logits[:, layer].to(dev, torch.bfloat16)
+        if layer + 1 < layers:
+            other = E - own
+            X[:, layer, other:other + E] = ahead[:, layer].to(dev, torch.bfloat16)
+    # how often a lookahead top-j expert is among the next layer's top-k
+    # (timed tokens; bf16 rounding of the inputs aside)
+    act = logits[warmup:, 1:].topk(K_TOP, dim=-1).indices
+    precision = {j: (ahead[warmup:].topk(j, dim=-1).indices.unsqueeze(-1) == act.unsqueeze(-2))
+                 .any(-1).float().mean().item() for j in sorted({1, 3, K_TOP, prefetch_k or K_TOP})}
     for t in range(warmup):
         for layer in range(layers):
             mods[layer](X[t, layer:layer + 1])
     torch.cuda.synchronize()
     store.hits = store.misses = store.evictions = store.bytes_read = 0
+    store.prefetched = store.prefetch_used = store.prefetch_wasted = 0
     store.t_stall = 0.0
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -326,16 +357,24 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96):
     moved = st["bytes_read"]
     return {"layers": layers, "slots": n_slots, "usable_slots_per_layer": per_layer,
             "arena_GB": n_slots * EXPERT_BYTES / 1e9, "cache_policy": policy,
+            "prefetch": (None if not prefetch_k else
+                         {"depth": 1, "top": prefetch_k, "prefetched": st["prefetched"],
+                          "used": st["prefetch_used"], "wasted": st["prefetch_wasted"]}),
+            "lookahead": {"rho": lookahead_rho,
+                          "precision_at": {str(j): round(p, 4) for j, p in precision.items()}},
             "steps": steps, "warmup_tokens": warmup, "value": steps / secs, "unit": "tokens/s",
             "ms_per_token": secs / steps * 1e3, "wall_s": wall, "hit_rate": st["hit_rate"],
             "hits": st["hits"], "misses": st["misses"], "evictions": st["evictions"],
             "h2d_bytes": moved, "h2d_bytes_per_token": moved / steps,
             "h2d_GBps": moved / secs / 1e9, "host_stall_s": st["t_stall"],
             "hbm_expert_bytes_per_token": layers * (K_TOP + 1) * EXPERT_BYTES + layers * ROUTER_BYTES,
+            "demand_miss_bytes_per_token": st["misses"] * EXPERT_BYTES / steps,
             "workload": "43 full-width layers (d 4096, 256 experts top-6 + shared, d_ff 2048, 2-bit "
-                        "g64), one arena of 43 x 96 + 1 slots, Zipf(1.1) routing with AR(1) "
-                        "cross-layer noise rho 0.6, misses from pinned host memory (256 distinct "
-                        "expert payloads; expert e of every layer copies payload e)"}
+                        "g64), one arena of 43 x 96 + 1 slots, Zipf(1.1) routing with a per-layer "
+                        "expert ranking and AR(1) cross-layer noise rho 0.6, misses from pinned host "
+                        "memory (256 distinct expert payloads; expert e of every layer copies "
+                        f"payload e); next-layer gate on the current input sees the next layer's "
+                        f"logits through copula noise of correlation {lookahead_rho}"}
 
 
 def cpu_baseline(arena, shared, spec, X, seconds):
@@ -492,6 +531,11 @@ def main(argv=None):
     ap.add_argument("--stack-warmup", type=int, default=16)
     ap.add_argument("--stack-policies", default="slru-all,lfu-decay",
                     help="comma-separated arena cache policies for the 43-layer stack")
+    ap.add_argument("--stack-prefetch", default="6",
+                    help="comma-separated prefetch widths for extra slru-all stack legs with "
+                         "cross-layer prefetch at depth 1 (0: none)")
+    ap.add_argument("--stack-lookahead-rho", type=float, default=LOOKAHEAD_RHO,
+                    help="correlation of the stack's lookahead routing with the next layer's")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=1)
@@ -605,7 +649,12 @@ def main(argv=None):
         for policy in args.stack_policies.split(","):
             phase(f"43-layer bounded arena, {policy}")
             result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, policy,
-                                               args.seed + 300))
+                                               args.seed + 300, lookahead_rho=args.stack_lookahead_rho))
+        for k in (int(v) for v in args.stack_prefetch.split(",") if v.strip() and int(v)):
+            phase(f"43-layer bounded arena, slru-all, prefetch top-{k} at depth 1")
+            result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, "slru-all",
+                                               args.seed + 300, prefetch_k=k,
+                                               lookahead_rho=args.stack_lookahead_rho))
     if not args.skip_cpu:
         phase("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(arena, shared, spec, X, args.cpu_seconds)

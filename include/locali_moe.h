@@ -258,6 +258,17 @@ typedef struct {
  * stream has passed the copy. */
 int locali_moe_arena_fill_batch(const locali_fill_piece *pieces, int32_t n, void *stream);
 
+/* The fills of n whole experts into their slots (the host-memory fills of
+ * ArenaStore.submit, arena.py:356-435): expert i's records lie back to back
+ * in host memory at src_host[i] (record a is slot_bytes[a] bytes), and record
+ * a lands at dst_base[a] + slots[i] * slot_bytes[a], array a being the
+ * slot-major device array of (projection, weight/scales/biases) a. Same copy
+ * kernel and rules as locali_moe_arena_fill_batch; the arrays' and slots'
+ * bounds are the caller's. */
+int locali_moe_arena_fill_slots(void *const *dst_base, const size_t *slot_bytes, int32_t n_arrays,
+                                const int32_t *slots, const void *const *src_host, int32_t n,
+                                void *stream);
+
 /* Whole layer on an all-resident arena: router, dispatch (decode or grouped
  * by token count), experts, combine, shared expert. out [tokens, d_model]. */
 int locali_moe_forward(const locali_router *router, const locali_expert_arena *routed,

@@ -1,4 +1,5 @@
-"""ctypes binding of liblocali_amd.so (include/locali_core.h, include/locali_moe.h).
+"""ctypes binding of liblocali_amd.so (include/locali_core.h, include/locali_planner.h,
+include/locali_moe.h).
 
 The library is built in-tree by ``python -m locali_amd.build``. There is no
 CPU or eager fallback: if the library is missing, every entry point raises.
@@ -81,6 +82,8 @@ _SIGNATURES = {
     "locali_cache_note_token": ([_P], None),
     "locali_cache_plan": ([_P, ctypes.POINTER(ctypes.c_int32), _SZ, ctypes.POINTER(ctypes.c_int32),
                            _SZ, ctypes.c_int, ctypes.POINTER(CacheResult)], ctypes.c_int),
+    "locali_cache_plan_each": ([_P, ctypes.POINTER(ctypes.c_int32), _SZ, ctypes.POINTER(ctypes.c_int32),
+                                _SZ, ctypes.c_int, ctypes.POINTER(CacheResult)], ctypes.c_int),
     "locali_cache_peek": ([_P, _I], _I),
     "locali_cache_probation_size": ([_P], _I),
     "locali_cache_protected_size": ([_P], _I),
@@ -105,6 +108,9 @@ _SIGNATURES = {
     "locali_moe_combine_routes": ([_P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P], ctypes.c_int),
     "locali_moe_arena_fill": ([_P, _P, _SZ, _P], ctypes.c_int),
     "locali_moe_arena_fill_batch": ([ctypes.POINTER(FillPiece), ctypes.c_int32, _P], ctypes.c_int),
+    "locali_moe_arena_fill_slots": ([ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t), _I,
+                                     ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_void_p), _I, _P],
+                                    ctypes.c_int),
     "locali_moe_forward": ([ctypes.POINTER(Router), ctypes.POINTER(ExpertArena),
                             ctypes.POINTER(ExpertArena), _P, _P, _I, _I, _P, _F, _I, _P, _P, _P, _P,
                             _SZ, _P], ctypes.c_int),

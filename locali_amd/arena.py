@@ -371,14 +371,9 @@ class ArenaStore:
             self._read(recs, host)
             off = 0
             if self.fill_stream is not None:
-                from .ops import arena_fill_batch_ptrs
-                base, pieces = buf.data_ptr(), []
-                for pk, r in zip(((p, k) for p in PROJS for k in ARRS), recs):
-                    pieces.append((self.arena[(t, *pk)].data_ptr() + slot * self.layout[(t, *pk)][0],
-                                   base + off, r[3]))
-                    off += r[3]
+                from .ops import arena_fill_slots
                 with torch.cuda.device(self.device):
-                    arena_fill_batch_ptrs(pieces, self.fill_stream)
+                    arena_fill_slots(self._slot_table(t), [slot], [buf.data_ptr()], self.fill_stream)
                     ev = torch.cuda.Event()
                     ev.record(self.fill_stream)
                 ev.synchronize()
@@ -390,13 +385,13 @@ class ArenaStore:
         finally:
             self.staging.give(buf)
 
-    def _slot_ptrs(self, t):
-        """(base address, bytes per slot) of tier t's nine arrays in record
-        order (gate, up, down) x (weight, scales, biases)."""
-        cache = self.__dict__.setdefault("_slot_ptr_cache", {})
+    def _slot_table(self, t):
+        """Tier t's nine slot-major arrays in record order (gate, up, down) x
+        (weight, scales, biases), as ops.arena_fill_slots takes them."""
+        from .ops import slot_table
+        cache = self.__dict__.setdefault("_slot_tables", {})
         if t not in cache:
-            cache[t] = [(self.arena[(t, p, k)].data_ptr(), self.layout[(t, p, k)][0])
-                        for p in PROJS for k in ARRS]
+            cache[t] = slot_table([self.arena[(t, p, k)] for p in PROJS for k in ARRS])
         return cache[t]
 
     def _host_bytes(self, key, t) -> torch.Tensor:
@@ -411,26 +406,26 @@ class ArenaStore:
         host_source on the fill stream as one batch, behind the work already
         queued on the compute stream (a refilled slot may still be read there),
         and return the event that follows them. jobs: (key, tier, slot, recs)."""
-        from .ops import arena_fill_batch_ptrs
-        pieces, sources = [], []
-        for key, t, slot, recs in jobs:
-            src = self._host_bytes(key, t)
-            sources.append(src)
-            base, off = src.data_ptr(), 0
-            for (arr_ptr, nbytes), r in zip(self._slot_ptrs(t), recs):
-                pieces.append((arr_ptr + slot * nbytes, base + off, r[3]))
-                off += r[3]
+        from .ops import arena_fill_slots
         if self.device.index is not None and torch.cuda.current_device() != self.device.index:
             with torch.cuda.device(self.device):
                 return self._fill_from_host(jobs)
+        t = jobs[0][1]                   # the caller batches one tier at a time
+        sources = [self._host_bytes(key, t) for key, _, _, _ in jobs]
         # the fill stream waits for the compute stream through one reused
-        # event (a wait takes the event's state when it is queued)
-        order = self.__dict__.get("_order_event")
-        if order is None:
-            order = self._order_event = torch.cuda.Event()
-        order.record(torch.cuda.current_stream(self.device))
-        self.fill_stream.wait_event(order)
-        arena_fill_batch_ptrs(pieces, self.fill_stream)
+        # event (a wait takes the event's state when it is queued), unless
+        # that stream has nothing left to run (a layer call has just synced
+        # on its routing)
+        from .ops import current_stream
+        cur = current_stream(self.device)
+        if not cur.query():
+            order = self.__dict__.get("_order_event")
+            if order is None:
+                order = self._order_event = torch.cuda.Event()
+            order.record(cur)
+            self.fill_stream.wait_event(order)
+        arena_fill_slots(self._slot_table(t), [slot for _, _, slot, _ in jobs],
+                         [src.data_ptr() for src in sources], self.fill_stream)
         ev = torch.cuda.Event()
         ev.record(self.fill_stream)
         return _Landed(ev, sources)
@@ -522,13 +517,15 @@ class ArenaStore:
                 out.pop(e, None)
         plan = ReadPlan()
         jobs = {t: [] for t in self.tiers}
+        from_host = self.host_source is not None and self.fill_stream is not None
         for e, t, s in issued:
-            jobs[t].append(((layer, e), t, s, self._records(layer, e, t)))
+            # a copy from host memory moves the whole expert; a file read
+            # follows its records
+            jobs[t].append(((layer, e), t, s, None if from_host else self._records(layer, e, t)))
             self.bytes_read += self.item[t]
         for t in self.tiers:   # a whole tier before the next
             futs = []
-            batch = (self._fill_from_host(jobs[t]) if jobs[t] and self.host_source is not None
-                     and self.fill_stream is not None else None)
+            batch = self._fill_from_host(jobs[t]) if jobs[t] and from_host else None
             for key, tt, s, recs in jobs[t]:
                 f = batch if batch is not None else self.pool.submit(self._fill, tt, s, recs, key)
                 self.inflight.setdefault(key, []).append(f)
@@ -554,13 +551,14 @@ class ArenaStore:
         on); file reads block the host until their copies have landed."""
         if not futs:
             return
+        from .ops import current_stream
         t0 = time.perf_counter()
         seen, cur = set(), None
         for f in futs:
             if isinstance(f, _Landed):
                 if id(f) not in seen:
                     seen.add(id(f))
-                    cur = cur or torch.cuda.current_stream(self.device)
+                    cur = cur or current_stream(self.device)
                     cur.wait_event(f.event)
             else:
                 f.result()
@@ -589,8 +587,34 @@ class ArenaStore:
         self.fds.clear()
         self.arena.clear()
         self.__dict__.pop("_expert_arena", None)
-        self.__dict__.pop("_slot_ptr_cache", None)
+        self.__dict__.pop("_slot_tables", None)
         self.staging.free.clear()
+
+
+def _host_ints(tensors):
+    """Host numpy int32 copies of 32-bit tensors, through one device-to-host
+    copy (fp32 values travel as their bits)."""
+    flat = [t.reshape(-1).to(torch.float32 if t.is_floating_point() else torch.int32).view(torch.int32)
+            for t in tensors]
+    host = torch.cat(flat).cpu().numpy()
+    out, off = [], 0
+    for t in flat:
+        out.append(host[off:off + t.numel()])
+        off += t.numel()
+    return out
+
+
+def _lookahead_experts(idx, weight_bits, top_k, k=None):
+    """The experts a prefetch asks for: per row of the lookahead routing,
+    the k highest gate weights (all top_k when k is unset or not smaller),
+    ties in row order (reference arena.py:527-532). idx and weight_bits are
+    the host int32 arrays of _host_ints (weights as fp32 bits)."""
+    pi = idx.reshape(-1, top_k)
+    if k and k < top_k:
+        pg = weight_bits.view(np.float32).reshape(-1, top_k)
+        order = np.argsort(-pg, axis=-1, kind="stable")
+        pi = np.take_along_axis(pi, order[:, :k], axis=-1)
+    return pi.reshape(-1).tolist()
 
 
 class ArenaMoE:
@@ -635,21 +659,30 @@ class ArenaMoE:
         if flat.shape[0] == 0:        # no tokens: an empty output, nothing routed or placed
             return torch.zeros(shape, dtype=x.dtype, device=x.device)
         inds, gates = self.route(x, input_ids)
-        ii = inds.reshape(-1, self.top_k).tolist()          # host sync, as the reference
-        experts = [e for row in ii for e in row]
-        if self.store.tier_overlap:
-            placed, reads = self.store.submit(self.layer, experts)
+        # The lookahead routing of the cross-layer prefetch (reference
+        # arena.py:518-541) is a function of x alone: it is launched with this
+        # layer's and all of it reaches the host in one copy and one wait.
+        ahead = [(blk, k) + blk.route(x, input_ids)
+                 for blk, k in ((self.nxt, self.prefetch_k), (self.nxt2, self.prefetch_k2))
+                 if blk is not None]
+        if ahead:
+            parts = _host_ints([inds] + [t for a in ahead for t in a[2:]])
+            ii = parts[0].reshape(-1, self.top_k).tolist()
         else:
-            placed, reads = self.store.slots_for(self.layer, experts), None
-        for blk, k in ((self.nxt, self.prefetch_k), (self.nxt2, self.prefetch_k2)):
-            if blk is None:
-                continue
-            pi, pg = blk.route(x, input_ids)
-            pi = pi.reshape(-1, self.top_k)
-            if k and k < self.top_k:
-                order = torch.argsort(-pg.reshape(-1, self.top_k).float(), dim=-1, stable=True)
-                pi = torch.gather(pi, 1, order[:, :k])
-            self.store.submit(blk.layer, [e for row in pi.tolist() for e in row], prefetch=True)
+            ii = inds.reshape(-1, self.top_k).tolist()      # host sync, as the reference
+        experts = [e for row in ii for e in row]
+        # The demand fills are queued first, the prefetch is planned next, and
+        # only then is the compute stream made to wait for this call's fills
+        # (without tier overlap, for every one of them: slots_for's order,
+        # reference arena.py:513-516). The planner calls are the reference's,
+        # in its order; the prefetch no longer sits behind the copies.
+        placed, reads = self.store.submit(self.layer, experts)
+        for n, (blk, k, _, _) in enumerate(ahead):
+            self.store.submit(blk.layer, _lookahead_experts(parts[1 + 2 * n], parts[2 + 2 * n],
+                                                            self.top_k, k), prefetch=True)
+        if not self.store.tier_overlap:
+            self.store.wait([f for futs in reads.values() for f in futs])
+            reads = None
         out = self._apply(flat, ii, placed, gates.reshape(-1, self.top_k), x.dtype, reads)
         return out.reshape(shape).to(x.dtype)
 
@@ -691,20 +724,22 @@ class ArenaMoE:
         flat = [s for row in rows for s in row]
         if device.type != "cuda":
             return torch.tensor(rows, dtype=torch.int32, device=device)
+        from .ops import current_stream
         ring = self.__dict__.setdefault("_slot_ring", [])
         if not ring or ring[0][0].numel() < len(flat):
             n = max(64, len(flat))
-            ring[:] = [[torch.empty(n, dtype=torch.int32, pin_memory=True), None] for _ in range(4)]
+            ring[:] = [[torch.empty(n, dtype=torch.int32, pin_memory=True), None, None] for _ in range(4)]
+            for entry in ring:
+                entry[2] = entry[0].numpy()
             self._slot_next = 0
         entry = ring[self._slot_next]
         self._slot_next = (self._slot_next + 1) % len(ring)
         if entry[1] is not None:
             entry[1].synchronize()        # the buffer's previous copy has run
-        host = entry[0][:len(flat)]
-        host.copy_(torch.tensor(flat, dtype=torch.int32))
-        out = host.to(device, non_blocking=True).view(len(rows), -1)
+        entry[2][:len(flat)] = flat
+        out = entry[0][:len(flat)].to(device, non_blocking=True).view(len(rows), -1)
         entry[1] = torch.cuda.Event()
-        entry[1].record(torch.cuda.current_stream(device))
+        entry[1].record(current_stream(device))
         return out
 
     def _routes(self, arena, x_in, slots, ws):

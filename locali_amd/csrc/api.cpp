@@ -645,34 +645,33 @@ int locali_moe_arena_fill(void *dst, const void *src_host, size_t bytes, void *s
     return 0;
 }
 
-int locali_moe_arena_fill_batch(const locali_fill_piece *pieces, int32_t n, void *stream) {
-    if (n < 0 || (n > 0 && !pieces)) return fail(LOCALI_E_ARG, "arena_fill_batch: bad piece table");
+}  // extern "C"
+
+namespace {
+
+// Pieces for the fill kernel, launched 64 pieces at a time.
+struct FillQueue {
     FillBatch b{};
     int blocks = 0;
-    auto flush = [&]() -> int {
+    hipStream_t st;
+    const char *what;
+    explicit FillQueue(hipStream_t s, const char *w) : st(s), what(w) {}
+    int flush() {
         if (!b.n) return 0;
-        const hipError_t e = launch_fill(b, blocks, S(stream));
+        const hipError_t e = launch_fill(b, blocks, st);
         b.n = 0;
         blocks = 0;
-        return e != hipSuccess ? hip_fail(e, "arena_fill_batch launch") : 0;
-    };
-    for (int32_t i = 0; i < n; ++i) {
-        const locali_fill_piece &p = pieces[i];
-        if (!p.bytes) continue;
-        if (!p.dst || !p.src_host) return fail(LOCALI_E_ARG, "arena_fill_batch: null pointer in piece %d", i);
-        void *dev_src = nullptr;
-        const bool aligned = (reinterpret_cast<uintptr_t>(p.dst) | reinterpret_cast<uintptr_t>(p.src_host) |
-                              p.bytes) % 16 == 0;
-        // the kernel reads only pinned memory that the runtime maps at the same
-        // address on the device (unified addressing); anything else is copied
-        if (!aligned || hipHostGetDevicePointer(&dev_src, const_cast<void *>(p.src_host), 0) != hipSuccess ||
-            dev_src != p.src_host) {
-            (void)hipGetLastError();   // not pinned here: an ordinary asynchronous copy
-            const hipError_t e = hipMemcpyAsync(p.dst, p.src_host, p.bytes, hipMemcpyHostToDevice, S(stream));
-            if (e != hipSuccess) return hip_fail(e, "arena_fill_batch copy");
-            continue;
+        return e != hipSuccess ? hip_fail(e, what) : 0;
+    }
+    // dev_src: the device's address of pinned host memory at src (the same
+    // address under unified addressing), or null: then an asynchronous copy
+    int add(void *dst, const void *src, const void *dev_src, size_t bytes) {
+        if (!bytes) return 0;
+        if (!dev_src || (reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes) % 16) {
+            const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st);
+            return e != hipSuccess ? hip_fail(e, what) : 0;
         }
-        const int64_t units = static_cast<int64_t>(p.bytes / 16);
+        const int64_t units = static_cast<int64_t>(bytes / 16);
         const int nb = fill_blocks(units);
         if (b.n == kFillMaxPieces || static_cast<int64_t>(blocks) + nb > (int64_t{1} << 30)) {
             if (int rc = flush()) return rc;
@@ -680,11 +679,60 @@ int locali_moe_arena_fill_batch(const locali_fill_piece *pieces, int32_t n, void
         b.first_block[b.n] = blocks;
         b.units[b.n] = units;
         b.src[b.n] = dev_src;
-        b.dst[b.n] = p.dst;
+        b.dst[b.n] = dst;
         ++b.n;
         blocks += nb;
+        return 0;
     }
-    return flush();
+};
+
+// The kernel reads only pinned memory that the runtime maps at the same
+// address on the device; anything else is copied.
+const void *device_view(const void *host) {
+    void *dev = nullptr;
+    if (hipHostGetDevicePointer(&dev, const_cast<void *>(host), 0) != hipSuccess || dev != host) {
+        (void)hipGetLastError();   // not pinned here
+        return nullptr;
+    }
+    return dev;
+}
+
+}  // namespace
+
+extern "C" {
+
+int locali_moe_arena_fill_batch(const locali_fill_piece *pieces, int32_t n, void *stream) {
+    if (n < 0 || (n > 0 && !pieces)) return fail(LOCALI_E_ARG, "arena_fill_batch: bad piece table");
+    FillQueue q(S(stream), "arena_fill_batch");
+    for (int32_t i = 0; i < n; ++i) {
+        const locali_fill_piece &p = pieces[i];
+        if (!p.bytes) continue;
+        if (!p.dst || !p.src_host) return fail(LOCALI_E_ARG, "arena_fill_batch: null pointer in piece %d", i);
+        if (int rc = q.add(p.dst, p.src_host, device_view(p.src_host), p.bytes)) return rc;
+    }
+    return q.flush();
+}
+
+int locali_moe_arena_fill_slots(void *const *dst_base, const size_t *slot_bytes, int32_t n_arrays,
+                                const int32_t *slots, const void *const *src_host, int32_t n, void *stream) {
+    if (n < 0 || n_arrays < 1 || (n > 0 && (!dst_base || !slot_bytes || !slots || !src_host)))
+        return fail(LOCALI_E_ARG, "arena_fill_slots: bad arguments");
+    for (int32_t a = 0; a < n_arrays; ++a)
+        if (!dst_base[a]) return fail(LOCALI_E_ARG, "arena_fill_slots: null array %d", a);
+    FillQueue q(S(stream), "arena_fill_slots");
+    for (int32_t i = 0; i < n; ++i) {
+        const char *src = static_cast<const char *>(src_host[i]);
+        if (!src) return fail(LOCALI_E_ARG, "arena_fill_slots: null source %d", i);
+        if (slots[i] < 0) return fail(LOCALI_E_ARG, "arena_fill_slots: slot %d of expert %d", slots[i], i);
+        const char *dev = static_cast<const char *>(device_view(src));
+        size_t off = 0;
+        for (int32_t a = 0; a < n_arrays; ++a) {
+            char *dst = static_cast<char *>(dst_base[a]) + static_cast<size_t>(slots[i]) * slot_bytes[a];
+            if (int rc = q.add(dst, src + off, dev ? dev + off : nullptr, slot_bytes[a])) return rc;
+            off += slot_bytes[a];
+        }
+    }
+    return q.flush();
 }
 
 int locali_moe_router_logits(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens,

@@ -14,6 +14,7 @@
 // Everything is sized at creation; plan() never allocates.
 
 #include "locali_core.h"
+#include "locali_planner.h"
 
 #include <algorithm>
 #include <cstring>
@@ -225,10 +226,14 @@ void locali_cache_note_token(locali_cache *cache) {
     for (uint32_t &h : cache->hot) h >>= 1;
 }
 
-int locali_cache_plan(locali_cache *cache, const int32_t *keys,
-                      size_t key_count, const int32_t *pinned_slots,
-                      size_t pinned_count, int touch_hits,
-                      locali_cache_result *results) {
+}  // extern "C"
+
+namespace {
+
+// plan() of the C ABI; with pin_resolved every slot a key resolves to (hit
+// or placed) is pinned for the keys after it in the same call.
+int plan_keys(locali_cache *cache, const int32_t *keys, size_t key_count, const int32_t *pinned_slots,
+              size_t pinned_count, int touch_hits, locali_cache_result *results, bool pin_resolved) {
     if (!cache) return -1;
     if (key_count && (!keys || !results)) return -1;
     if (++cache->epoch == 0) {
@@ -265,8 +270,26 @@ int locali_cache_plan(locali_cache *cache, const int32_t *keys,
             r.placed = ok ? 1 : 0;
         }
         results[i] = r;
+        if (pin_resolved && r.placed && r.slot > 0 && r.slot < cache->n_slots) cache->pin_stamp[r.slot] = cache->epoch;
     }
     return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int locali_cache_plan(locali_cache *cache, const int32_t *keys,
+                      size_t key_count, const int32_t *pinned_slots,
+                      size_t pinned_count, int touch_hits,
+                      locali_cache_result *results) {
+    return plan_keys(cache, keys, key_count, pinned_slots, pinned_count, touch_hits, results, false);
+}
+
+int locali_cache_plan_each(locali_cache *cache, const int32_t *keys, size_t key_count,
+                           const int32_t *pinned_slots, size_t pinned_count, int touch_hits,
+                           locali_cache_result *results) {
+    return plan_keys(cache, keys, key_count, pinned_slots, pinned_count, touch_hits, results, true);
 }
 
 int32_t locali_cache_peek(const locali_cache *cache, int32_t key) {

@@ -29,7 +29,7 @@ from pathlib import Path
 import torch
 
 from . import ops
-from .arena import PROJS, ArenaMoE, ArenaStore
+from .arena import PROJS, ArenaMoE, ArenaStore, ReadPlan
 from .native import NativeCache
 
 
@@ -88,20 +88,15 @@ class V4ArenaStore(ArenaStore):
         if not prefetch and len(want) > self.slots[t] - 1:
             raise ValueError(f"layer {layer} needs {len(want)} {t} experts but the arena has "
                              f"{self.slots[t] - 1}; raise ceiling_gb")
-        # One planner call per key, each pinning the previous demand call's
-        # slots plus every slot this call has resolved so far: a multi-key
-        # call could hand a slot claimed (or hit) earlier in the same call to
-        # a later miss when the tier is nearly full, leaving two experts on
-        # one slot. Whenever that cannot happen the assignments equal one
-        # multi-key call's (same operations in the same order).
-        pins = set(self.pinned.get(t, ()))
-        results = []
-        for e in want:
-            (r,) = cache.plan([layer * self.E + e], pinned_slots=tuple(pins),
-                              touch_hits=not prefetch)
-            results.append(r)
-            if r.placed:
-                pins.add(r.slot)
+        # Each key is planned with the previous demand call's slots pinned
+        # plus every slot this call has resolved so far (locali_cache_plan_each,
+        # one native call): a multi-key call could hand a slot claimed (or
+        # hit) earlier in the same call to a later miss when the tier is
+        # nearly full, leaving two experts on one slot. Whenever that cannot
+        # happen the assignments equal one multi-key call's (same operations
+        # in the same order).
+        results = cache.plan_each([layer * self.E + e for e in want],
+                                  pinned_slots=tuple(self.pinned.get(t, ())), touch_hits=not prefetch)
         out, issued = {}, []
         waits = {name: [] for name in self.tiers}
         for e, r in zip(want, results):
@@ -122,6 +117,71 @@ class V4ArenaStore(ArenaStore):
         if not prefetch:
             self.pinned = {t: {s for _, s in out.values()}}
         return out, issued, waits
+
+    def _layer_tier(self, layer, want):
+        """The one tier of a layer's experts (a V4 layer never spans two)."""
+        cache = self.__dict__.setdefault("_tier_of_layer", {})
+        tiers = cache.get(layer)
+        if tiers is None:
+            tiers = cache[layer] = {self.tier(layer, e) for e in range(self.E)}
+        if len(tiers) != 1:
+            tiers = {self.tier(layer, e) for e in want}
+            if len(tiers) != 1:
+                raise ValueError(f"layer {layer} spans multiple expert tiers: {tiers}")
+        return next(iter(tiers))
+
+    def submit(self, layer, experts, prefetch=False):
+        """ArenaStore.submit; with the compiled planner and fills from host
+        memory, a layer's misses are queued on the fill stream straight after
+        the one planner call and the bookkeeping follows. Planner calls,
+        slots, counters, futures and pins are the general path's."""
+        if not self.native_caches or self.host_source is None or self.fill_stream is None:
+            return super().submit(layer, experts, prefetch)
+        want = list(dict.fromkeys(int(e) for e in experts))
+        if not want:
+            return {}, ReadPlan({t: [] for t in self.tiers})
+        t = self._layer_tier(layer, want)
+        cache = self.native_caches[t]
+        if layer == 0 and not prefetch and len(want) <= self.top_k:
+            for c in self.native_caches.values():
+                c.note_token()
+        if not prefetch and len(want) > self.slots[t] - 1:
+            raise ValueError(f"layer {layer} needs {len(want)} {t} experts but the arena has "
+                             f"{self.slots[t] - 1}; raise ceiling_gb")
+        base = layer * self.E
+        res = cache.plan_each_into([base + e for e in want], tuple(self.pinned.get(t, ())),
+                                   not prefetch)
+        issued = [(e, r.slot) for e, r in zip(want, res) if r.placed and not r.hit]
+        landed = (self._fill_from_host([((layer, e), t, s, None) for e, s in issued])
+                  if issued else None)
+        out, waits = {}, {name: [] for name in self.tiers}
+        for e, r in zip(want, res):
+            if r.hit:
+                self._hit((layer, e), t, prefetch, waits)
+            else:
+                if not prefetch:
+                    self.misses += 1
+                if r.evicted_key >= 0:
+                    self._evicted(self._decode_key(r.evicted_key))
+            if r.placed:
+                out[e] = (t, r.slot)
+            elif not prefetch:
+                raise RuntimeError(f"native scheduler could not place demanded L{layer}.E{e}")
+        if not prefetch:
+            self.pinned = {t: {s for _, s in out.values()}}
+        futs = []
+        for e, _ in issued:
+            self.bytes_read += self.item[t]
+            self.inflight.setdefault((layer, e), []).append(landed)
+            futs.append(landed)
+        plan = ReadPlan({name: [] for name in self.tiers})
+        plan[t] = futs + waits[t]
+        plan.pending_experts = frozenset(
+            e for e in want if any(not f.done() for f in self.inflight.get((layer, e), ())))
+        if prefetch:
+            self.prefetched += len(issued)
+            self.pf_keys.update((layer, e) for e, _ in issued)
+        return out, plan
 
     def _protected_size(self, t):
         if t in self.native_caches:

@@ -63,6 +63,37 @@ class NativeCache:
         return [CacheResult(r.key, r.slot, r.evicted_key, bool(r.hit), bool(r.placed))
                 for r in results]
 
+    def plan_each(self, keys, *, pinned_slots=(), touch_hits: bool = True) -> list[CacheResult]:
+        """plan() one key at a time in a single call, each key also pinning
+        the slots the keys before it resolved to (locali_cache_plan_each)."""
+        if not keys:
+            return []
+        n = len(keys)
+        key_array = (ctypes.c_int32 * n)(*keys)
+        pinned_array = ((ctypes.c_int32 * len(pinned_slots))(*pinned_slots)
+                        if pinned_slots else None)
+        results = (_lib.CacheResult * n)()
+        rc = self._lib.locali_cache_plan_each(self._cache, key_array, n, pinned_array,
+                                              len(pinned_slots), int(touch_hits), results)
+        if rc:
+            raise ValueError(f"native cache plan failed with error {rc}")
+        return [CacheResult(r.key, r.slot, r.evicted_key, bool(r.hit), bool(r.placed))
+                for r in results]
+
+    def plan_each_into(self, keys, pinned_slots=(), touch_hits: bool = True):
+        """plan_each() returning the ctypes CacheResult array itself (fields
+        key, slot, evicted_key, hit, placed), for per-layer hot loops."""
+        n = len(keys)
+        key_array = (ctypes.c_int32 * n)(*keys)
+        pinned_array = ((ctypes.c_int32 * len(pinned_slots))(*pinned_slots)
+                        if pinned_slots else None)
+        results = (_lib.CacheResult * n)()
+        rc = self._lib.locali_cache_plan_each(self._cache, key_array, n, pinned_array,
+                                              len(pinned_slots), int(touch_hits), results)
+        if rc:
+            raise ValueError(f"native cache plan failed with error {rc}")
+        return results
+
     def plan_raw(self, keys, pinned_slots=(), touch_hits: bool = True):
         """(rc, [(key, slot, evicted_key, hit, placed)]) without raising; the
         results of an rc=-3 call are the ones the planner wrote before the

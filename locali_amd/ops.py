@@ -34,7 +34,23 @@ SCORE_FUNCS = {"sqrtsoftplus": SCORE_SQRTSOFTPLUS, "sigmoid": SCORE_SIGMOID,
 
 
 def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    """The current HIP stream of the current device (raw handle)."""
+    return torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())
+
+
+_STREAMS: dict = {}
+
+
+def current_stream(device=None) -> torch.cuda.Stream:
+    """torch.cuda.current_stream(device), one Stream object per raw stream
+    (the torch call costs several microseconds; this lookup about one)."""
+    idx = torch._C._cuda_getDevice() if device is None or torch.device(device).index is None \
+        else torch.device(device).index
+    raw = torch._C._cuda_getCurrentRawStream(idx)
+    s = _STREAMS.get((idx, raw))
+    if s is None:
+        s = _STREAMS[(idx, raw)] = torch.cuda.current_stream(idx)
+    return s
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -106,7 +122,11 @@ class ExpertArenaT:
     down: ProjArena
 
     def struct(self) -> _lib.ExpertArena:
-        return _lib.ExpertArena(self.gate.struct(), self.up.struct(), self.down.struct())
+        parts = (self.gate.struct(), self.up.struct(), self.down.struct())
+        cached = self.__dict__.get("_struct")
+        if cached is None or any(a is not b for a, b in zip(cached[0], parts)):
+            cached = self.__dict__["_struct"] = (parts, _lib.ExpertArena(*parts))
+        return cached[1]
 
     @property
     def d_model(self) -> int:
@@ -133,6 +153,18 @@ class RouterSpec:
     tid2eid: torch.Tensor | None = None       # [vocab, top_k] int32
 
     def struct(self) -> _lib.Router:
+        key = (self.weight.data_ptr(), tuple(self.weight.shape), self.weight.dtype, self.top_k, self.score_func,
+               self.norm_topk, self.routed_scale,
+               None if self.score_bias is None else self.score_bias.data_ptr(),
+               None if self.tid2eid is None else (self.tid2eid.data_ptr(), tuple(self.tid2eid.shape)))
+        cached = self.__dict__.get("_struct")
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        st = self._build_struct()
+        self.__dict__["_struct"] = (key, st)
+        return st
+
+    def _build_struct(self) -> _lib.Router:
         E = int(self.weight.shape[0])
         bias = self.score_bias
         if bias is not None and (bias.dtype != torch.float32 or bias.numel() != E):
@@ -167,9 +199,15 @@ class Workspace:
         return self.get(workspace_bytes(tokens, d_model, d_ff, n_experts, top_k, has_shared))
 
 
+_WS_BYTES: dict = {}
+
+
 def workspace_bytes(tokens, d_model, d_ff, n_experts, top_k, has_shared) -> int:
-    return int(lib().locali_moe_workspace_bytes(tokens, d_model, d_ff, n_experts, top_k,
-                                                int(bool(has_shared))))
+    key = (int(tokens), int(d_model), int(d_ff), int(n_experts), int(top_k), bool(has_shared))
+    n = _WS_BYTES.get(key)
+    if n is None:
+        n = _WS_BYTES[key] = int(lib().locali_moe_workspace_bytes(*key[:5], int(key[5])))
+    return n
 
 
 def _flat(x: torch.Tensor) -> torch.Tensor:
@@ -406,6 +444,28 @@ def arena_fill_batch_ptrs(pieces, stream) -> None:
     table = (_lib.FillPiece * max(len(pieces), 1))(*(_lib.FillPiece(d, s, n) for d, s, n in pieces))
     rc = lib().locali_moe_arena_fill_batch(table, len(pieces), stream.cuda_stream)
     check(rc, "locali_moe_arena_fill_batch")
+
+
+def slot_table(arrays) -> tuple:
+    """(dst_base, slot_bytes) ctypes arrays of slot-major device arrays, in
+    record order, for arena_fill_slots."""
+    base = (ctypes.c_void_p * len(arrays))(*(a.data_ptr() for a in arrays))
+    per = (ctypes.c_size_t * len(arrays))(*(a[0].numel() * a.element_size() for a in arrays))
+    return base, per
+
+
+def arena_fill_slots(table, slots, sources, stream) -> None:
+    """Asynchronous fills of whole experts (locali_moe_arena_fill_slots):
+    expert i's records lie back to back in host memory at address sources[i]
+    and land in slot slots[i] of the arrays of `table` (slot_table). Pinned
+    sources go through the copy kernel; the host memory must stay until the
+    stream has passed the copy."""
+    n = len(slots)
+    base, per = table
+    sl = (ctypes.c_int32 * max(n, 1))(*slots)
+    src = (ctypes.c_void_p * max(n, 1))(*sources)
+    rc = lib().locali_moe_arena_fill_slots(base, per, len(base), sl, src, n, stream.cuda_stream)
+    check(rc, "locali_moe_arena_fill_slots")
 
 
 def arena_fill_batch(pieces, stream=None) -> None:

@@ -112,6 +112,32 @@ def layered_zipf_logits(tokens: int, layers: int, n_experts: int, s: float = 1.1
     g = -log(-log Phi(z))). Each layer's marginal is therefore exactly the
     Zipf sample without replacement of zipf_logits, and a token's noise at
     consecutive layers is correlated."""
+    return _layered_zipf(tokens, layers, n_experts, s, rho, seed, device)[0]
+
+
+def layered_zipf_lookahead(tokens: int, layers: int, n_experts: int, s: float = 1.1, rho: float = 0.6,
+                           lookahead_rho: float = 0.9, *, seed: int, device="cpu"):
+    """(logits [tokens, layers, E], lookahead [tokens, layers - 1, E]).
+
+    logits are layered_zipf_logits(seed)'s. lookahead[:, l] is a noisy view
+    of layer l + 1's logits: the same Zipf ranking with Gumbel noise whose
+    Gaussian copula has correlation lookahead_rho with that layer's
+    (z' = r z_{l+1} + sqrt(1-r^2) n). It stands for the next layer's gate
+    applied to the current hidden state, the input of a cross-layer
+    prefetch: r = 1 predicts the next layer's routing exactly."""
+    out, base, zs = _layered_zipf(tokens, layers, n_experts, s, rho, seed, device)
+    g = _gen(seed + 1_000_003, device)
+    ahead = torch.empty(tokens, max(layers - 1, 0), n_experts, dtype=torch.float32, device=device)
+    c = math.sqrt(max(0.0, 1.0 - lookahead_rho * lookahead_rho))
+    for layer in range(layers - 1):
+        z = lookahead_rho * zs[layer + 1] + c * torch.randn(tokens, n_experts, generator=g, device=device,
+                                                            dtype=torch.float64)
+        u = (0.5 * torch.erfc(-z / math.sqrt(2.0))).clamp(1e-12, 1.0 - 1e-12)
+        ahead[:, layer] = (base[layer + 1] - torch.log(-torch.log(u))).float()
+    return out, ahead
+
+
+def _layered_zipf(tokens, layers, n_experts, s, rho, seed, device):
     g = _gen(seed, device)
     logp = -s * torch.log(torch.arange(1, n_experts + 1, device=device, dtype=torch.float64))
     base = torch.empty(layers, n_experts, dtype=torch.float64, device=device)
@@ -120,13 +146,15 @@ def layered_zipf_logits(tokens: int, layers: int, n_experts: int, s: float = 1.1
     z = torch.randn(tokens, n_experts, generator=g, device=device, dtype=torch.float64)
     out = torch.empty(tokens, layers, n_experts, dtype=torch.float32, device=device)
     c = math.sqrt(1.0 - rho * rho)
+    zs = []
     for layer in range(layers):
         if layer:
             z = rho * z + c * torch.randn(tokens, n_experts, generator=g, device=device,
                                           dtype=torch.float64)
+        zs.append(z)
         u = (0.5 * torch.erfc(-z / math.sqrt(2.0))).clamp(1e-12, 1.0 - 1e-12)
         out[:, layer] = (base[layer] - torch.log(-torch.log(u))).float()
-    return out
+    return out, base, zs
 
 
 def identity_router(n_experts: int, d_model: int, dtype=torch.bfloat16, device="cpu"):

@@ -8,6 +8,8 @@ from __future__ import annotations
 
 import random
 
+import numpy as np
+
 import pytest
 import torch
 
@@ -312,3 +314,82 @@ def test_stats_surface(ckpt):
     finally:
         st.close()
     assert not st.arena and not st.fds
+
+
+def test_lookahead_selection_matches_a_stable_weight_sort():
+    """The prefetch's lookahead selection (reference arena.py:527-532): the k
+    highest gate weights per row, ties kept in row order, through one host
+    copy of indices and weight bits."""
+    from locali_amd.arena import _host_ints, _lookahead_experts
+    g = torch.Generator().manual_seed(3)
+    idx = torch.randint(0, 256, (5, 6), generator=g, dtype=torch.int32)
+    w = torch.rand(5, 6, generator=g)
+    w[1, 2] = w[1, 4] = w[1].max() + 1.0          # a tie at the top of row 1
+    inds, ib, wb = _host_ints([idx, idx, w])
+    assert np.array_equal(inds, idx.reshape(-1).numpy())
+    for k in (1, 3, 5):
+        order = torch.argsort(-w, dim=-1, stable=True)[:, :k]
+        want = torch.gather(idx, 1, order).reshape(-1).tolist()
+        assert _lookahead_experts(ib, wb, 6, k) == want
+    for k in (6, None):              # the whole routing, in the router's order
+        assert _lookahead_experts(ib, wb, 6, k) == idx.reshape(-1).tolist()
+    assert _lookahead_experts(ib, wb, 6, 2)[2:4] == [int(idx[1, 2]), int(idx[1, 4])]
+
+
+class _FakeLanded:
+    """A fill future that lands two submits after it was issued."""
+
+    def __init__(self, clock):
+        self.clock, self.born = clock, clock[0]
+
+    def done(self):
+        return self.clock[0] >= self.born + 2
+
+
+@pytest.mark.parametrize("policy,slots", [("slru-all", 14), ("lfu-decay", 9), ("lru", 10)])
+def test_fast_submit_equals_the_general_path(ckpt, policy, slots):
+    """V4ArenaStore.submit's host-fill path (one planner call, fills queued
+    before the bookkeeping) gives the general ArenaStore.submit's placements,
+    fills, futures, pending experts, pins and counters on the same calls,
+    demand and prefetch mixed, with fills that land late."""
+    _, _, index, _ = ckpt
+    stores, logs, clocks = [], [], []
+    for _ in range(2):
+        st = _store(index, slots, cache_policy=policy)
+        log, clock = [], [0]
+        st.host_source = lambda layer, e: None
+        st.fill_stream = object()
+
+        def fake(jobs, log=log, clock=clock):
+            log.append([(key, tt, s) for key, tt, s, _ in jobs])
+            return _FakeLanded(clock)
+        st._fill_from_host = fake
+        stores.append(st)
+        logs.append(log)
+        clocks.append(clock)
+    fast, general = stores
+    rng = random.Random(17 + slots)
+    try:
+        for step in range(90):
+            layer = rng.randrange(LAYERS)
+            prefetch = step % 4 == 3
+            want = [rng.randrange(EXPERTS) for _ in range(rng.randint(1, 3))]
+            got = []
+            for st, clock in ((fast, clocks[0]), (general, clocks[1])):
+                clock[0] = step
+                if st is fast:
+                    out, plan = st.submit(layer, want, prefetch=prefetch)
+                else:
+                    out, plan = ArenaStore.submit(st, layer, want, prefetch=prefetch)
+                got.append((out, {t: len(f) for t, f in plan.items()}, plan.pending_experts,
+                            {k: len(v) for k, v in st.inflight.items()}, dict(st.pinned)))
+            assert got[0] == got[1], f"step {step}"
+            assert logs[0] == logs[1]
+        keys = ("hits", "misses", "evictions", "bytes_read", "prefetched", "prefetch_used",
+                "prefetch_wasted", "protected")
+        assert {k: fast.stats()[k] for k in keys} == {k: general.stats()[k] for k in keys}
+        assert fast.stats()["misses"] > 0 and fast.stats()["prefetched"] > 0
+    finally:
+        for st in stores:
+            st.fill_stream = None
+            st.close()

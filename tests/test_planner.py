@@ -193,3 +193,36 @@ def test_live_reference_library_agrees_on_random_workloads():
         a = pt.resolve_and_run(pt.CPlanner(ref, 90, slots, prot, pol), ops, pt.PROBE, 90)
         b = pt.resolve_and_run(_Ours(90, slots, prot, pol), ops, pt.PROBE, 90)
         assert a == b
+
+
+@pytest.mark.parametrize("policy,slots,prot", [("slru", 6, 0), ("slru", 9, 4), ("lfu-decay", 7, 0)])
+def test_plan_each_equals_one_call_per_key_with_growing_pins(policy, slots, prot):
+    """locali_cache_plan_each (include/locali_planner.h) against the oracle
+    planner driven one key per call, each call pinning the caller's slots plus
+    the slots the earlier keys resolved to -- slots, hits, evictions, segment
+    sizes and the -3 state, on nearly full tiers where the pins matter."""
+    import random
+    rng = random.Random(slots * 7 + prot)
+    ours = NativeCache(40, slots, prot, policy=policy)
+    ref = OraclePlanner(40, slots, prot, LFU_DECAY if policy == "lfu-decay" else SLRU)
+    pinned: set = set()
+    for step in range(300):
+        if step % 7 == 0:
+            ours.note_token()
+            ref.note_token()
+        keys = list(dict.fromkeys(rng.randrange(40) for _ in range(rng.randint(1, slots - 1))))
+        touch = step % 5 != 4
+        got = ours.plan_each(keys, pinned_slots=tuple(pinned), touch_hits=touch)
+        pins, want = set(pinned), []
+        for k in keys:
+            rc, (r,) = ref.plan([k], pinned_slots=pins, touch_hits=touch)
+            assert rc == 0
+            want.append((r.key, r.slot, r.evicted_key, bool(r.hit), bool(r.placed)))
+            if r.placed:
+                pins.add(r.slot)
+        assert [(r.key, r.slot, r.evicted_key, r.hit, r.placed) for r in got] == want, f"step {step}"
+        assert (ours.probation_size, ours.protected_size) == (ref.probation_size, ref.protected_size)
+        if touch:
+            pinned = {r.slot for r in got if r.placed}
+    with pytest.raises(ValueError):
+        ours.plan_each([1, 99, 2])
