@@ -175,13 +175,15 @@ class ReadPlan(dict):
 
 class _Landed:
     """Future of a fill copied from pinned host memory: an event recorded on
-    the fill stream after the experts' copies. It holds the source tensors
-    until the event has passed (the copy kernel reads them asynchronously),
-    so a host_source that hands out fresh pinned tensors stays correct."""
+    the stream that ran the experts' copies (`stream`, its raw handle). It
+    holds the source tensors until the event has passed (the copy kernel
+    reads them asynchronously), so a host_source that hands out fresh pinned
+    tensors stays correct."""
 
-    def __init__(self, event, sources=()):
+    def __init__(self, event, sources=(), stream=None):
         self.event = event
         self.sources = list(sources)
+        self.stream = stream
 
     def done(self) -> bool:
         if self.event.query():
@@ -192,6 +194,27 @@ class _Landed:
     def result(self, timeout=None):
         self.event.synchronize()
         self.sources.clear()
+
+
+class _SlotFills:
+    """The latest host fill queued into each (tier, slot): a copy into a slot
+    on one stream first waits for the previous copy into it when that one
+    ran on the other stream and may still be pending."""
+
+    def __init__(self):
+        self.by_slot: dict = {}
+
+    def pop_slots(self, t, slots):
+        out = []
+        for s in slots:
+            f = self.by_slot.pop((t, s), None)
+            if f is not None:
+                out.append(f)
+        return out
+
+    def note(self, t, slots, landed):
+        for s in slots:
+            self.by_slot[(t, s)] = landed
 
 
 class _Staging:
@@ -270,6 +293,7 @@ class ArenaStore:
             raise AssertionError(f"arena allocated {self.resident} bytes against {self.ceiling}")
         gpu = self.device.type == "cuda"
         self.fill_stream = torch.cuda.Stream(device=self.device) if gpu else None
+        self._slot_fills = _SlotFills()
         self.staging = _Staging(max(self.item.values()), max(2, threads), pinned=gpu)
 
     # ---- kernel views ----------------------------------------------------
@@ -401,34 +425,44 @@ class ArenaStore:
             raise ValueError(f"host_source{key}: expected {self.item[t]} contiguous host bytes (uint8)")
         return src
 
-    def _fill_from_host(self, jobs) -> _Landed:
+    def _fill_from_host(self, jobs, on_caller_stream=False) -> _Landed:
         """Queue the host -> HBM copies of several experts' records from
-        host_source on the fill stream as one batch, behind the work already
-        queued on the compute stream (a refilled slot may still be read there),
-        and return the event that follows them. jobs: (key, tier, slot, recs)."""
-        from .ops import arena_fill_slots
+        host_source as one batch and return the future of their event.
+        jobs: (key, tier, slot, recs), one tier.
+
+        on_caller_stream: the copies run on the caller's current stream, in
+        order with the work around them (a demand call's fills, which its own
+        gather needs next). Otherwise they run on the fill stream, behind the
+        work queued on the caller's stream (a refilled slot may still be read
+        there). Either way a copy into a slot waits for the pending fill of
+        that slot's previous owner when it runs on the other stream."""
+        from .ops import arena_fill_slots, current_stream
         if self.device.index is not None and torch.cuda.current_device() != self.device.index:
             with torch.cuda.device(self.device):
-                return self._fill_from_host(jobs)
+                return self._fill_from_host(jobs, on_caller_stream)
         t = jobs[0][1]                   # the caller batches one tier at a time
         sources = [self._host_bytes(key, t) for key, _, _, _ in jobs]
-        # the fill stream waits for the compute stream through one reused
-        # event (a wait takes the event's state when it is queued), unless
-        # that stream has nothing left to run (a layer call has just synced
-        # on its routing)
-        from .ops import current_stream
         cur = current_stream(self.device)
-        if not cur.query():
+        stream = cur if on_caller_stream else self.fill_stream
+        for f in self._slot_fills.pop_slots(t, [slot for _, _, slot, _ in jobs]):
+            if f.stream != stream.cuda_stream and not f.done():
+                stream.wait_event(f.event)
+        if not on_caller_stream and not cur.query():
+            # the fill stream waits for the caller's stream through one reused
+            # event (a wait takes the event's state when it is queued); a
+            # stream with nothing left to run needs no wait
             order = self.__dict__.get("_order_event")
             if order is None:
                 order = self._order_event = torch.cuda.Event()
             order.record(cur)
             self.fill_stream.wait_event(order)
         arena_fill_slots(self._slot_table(t), [slot for _, _, slot, _ in jobs],
-                         [src.data_ptr() for src in sources], self.fill_stream)
+                         [src.data_ptr() for src in sources], stream)
         ev = torch.cuda.Event()
-        ev.record(self.fill_stream)
-        return _Landed(ev, sources)
+        ev.record(stream)
+        landed = _Landed(ev, sources, stream.cuda_stream)
+        self._slot_fills.note(t, [slot for _, _, slot, _ in jobs], landed)
+        return landed
 
     # ---- Python planner (native_scheduler=False) ----------------------------
     def _evicted(self, victim):
@@ -495,10 +529,17 @@ class ArenaStore:
         return out, issued, waits
 
     # ---- public surface (reference arena.py:291-457) ---------------------
-    def submit(self, layer, experts, prefetch=False):
+    def submit(self, layer, experts, prefetch=False, fills_on_caller_stream=None):
         """Claim slots now; queue the fills; return ({expert: (tier, slot)},
         ReadPlan). prefetch=True is best effort: it never evicts a pinned slot,
-        never raises on a full arena and leaves hit/miss accounting alone."""
+        never raises on a full arena and leaves hit/miss accounting alone.
+
+        Copies from host memory run on the caller's current stream for a
+        demand call and on the fill stream for a prefetch, unless
+        fills_on_caller_stream says otherwise (a call that overlaps its hits
+        with its misses wants its fills beside its own stream)."""
+        if fills_on_caller_stream is None:
+            fills_on_caller_stream = not prefetch
         want = list(dict.fromkeys(int(e) for e in experts))
         out, issued, waits = self._place_keys(layer, want, prefetch)
         # A later miss of the same call may have taken an earlier one's slot
@@ -525,7 +566,8 @@ class ArenaStore:
             self.bytes_read += self.item[t]
         for t in self.tiers:   # a whole tier before the next
             futs = []
-            batch = self._fill_from_host(jobs[t]) if jobs[t] and from_host else None
+            batch = (self._fill_from_host(jobs[t], fills_on_caller_stream)
+                     if jobs[t] and from_host else None)
             for key, tt, s, recs in jobs[t]:
                 f = batch if batch is not None else self.pool.submit(self._fill, tt, s, recs, key)
                 self.inflight.setdefault(key, []).append(f)
@@ -559,7 +601,9 @@ class ArenaStore:
                 if id(f) not in seen:
                     seen.add(id(f))
                     cur = cur or current_stream(self.device)
-                    cur.wait_event(f.event)
+                    # copies queued on this very stream are already in order
+                    if f.stream != cur.cuda_stream and not f.done():
+                        cur.wait_event(f.event)
             else:
                 f.result()
         self.t_stall += time.perf_counter() - t0
@@ -579,9 +623,11 @@ class ArenaStore:
         """Drain the fills, close the files and release the arena's memory."""
         self.pool.shutdown(wait=True)
         if self.fill_stream is not None:
-            # fills from host memory are queued on the device only: they must
-            # have landed before the arena's memory goes back to the allocator
-            self.fill_stream.synchronize()
+            # fills from host memory are queued on the device only (the fill
+            # stream's and the callers' streams): they must have landed before
+            # the arena's memory goes back to the allocator
+            torch.cuda.synchronize(self.device)
+        self._slot_fills.by_slot.clear()
         for fd in self.fds.values():
             os.close(fd)
         self.fds.clear()
@@ -671,28 +717,42 @@ class ArenaMoE:
         else:
             ii = inds.reshape(-1, self.top_k).tolist()      # host sync, as the reference
         experts = [e for row in ii for e in row]
-        # The demand fills are queued first, the prefetch is planned next, and
-        # only then is the compute stream made to wait for this call's fills
-        # (without tier overlap, for every one of them: slots_for's order,
-        # reference arena.py:513-516). The planner calls are the reference's,
-        # in its order; the prefetch no longer sits behind the copies.
-        placed, reads = self.store.submit(self.layer, experts)
-        for n, (blk, k, _, _) in enumerate(ahead):
-            self.store.submit(blk.layer, _lookahead_experts(parts[1 + 2 * n], parts[2 + 2 * n],
-                                                            self.top_k, k), prefetch=True)
+        # Planner calls in the reference's order: this layer's demand, then
+        # the prefetch, nearest layer first. Without tier overlap the gather
+        # waits for every demand fill (slots_for's order, reference
+        # arena.py:513-516). When fills are copies from host memory the waits
+        # are on the device, so the gather is queued before the prefetch is
+        # planned (the prefetch never takes this call's slots: they are
+        # pinned); file reads block the host in the wait, so their prefetch
+        # is queued first, beside the demand reads, as in the reference.
+        split = self.overlap_hits and self.store.tier_overlap   # hits run beside the fills
+        placed, reads = self.store.submit(self.layer, experts, fills_on_caller_stream=not split)
+        device_waits = self.store.host_source is not None and self.store.fill_stream is not None
+
+        def prefetch():
+            for n, (blk, k, _, _) in enumerate(ahead):
+                self.store.submit(blk.layer, _lookahead_experts(parts[1 + 2 * n], parts[2 + 2 * n],
+                                                                self.top_k, k), prefetch=True)
+        if not device_waits:
+            prefetch()
         if not self.store.tier_overlap:
             self.store.wait([f for futs in reads.values() for f in futs])
             reads = None
         out = self._apply(flat, ii, placed, gates.reshape(-1, self.top_k), x.dtype, reads)
+        if device_waits:
+            prefetch()
         return out.reshape(shape).to(x.dtype)
 
     def _apply(self, flat, ii, placed, gates, dtype, reads=None):
         from . import ops
         T = len(ii)
-        present = [t for t in self.store.tiers if any(placed[e][0] == t for row in ii for e in row)]
-        if len(present) > 1:
-            return self._apply_tiers(flat, ii, placed, gates, dtype, reads, present)
-        t = present[0]
+        if len(self.store.tiers) == 1:
+            t = self.store.tiers[0]
+        else:
+            present = [t for t in self.store.tiers if any(placed[e][0] == t for row in ii for e in row)]
+            if len(present) > 1:
+                return self._apply_tiers(flat, ii, placed, gates, dtype, reads, present)
+            t = present[0]
         pending = getattr(reads, "pending_experts", ()) if reads is not None else ()
         if self.overlap_hits and T == 1 and pending and len(pending) < self.top_k:
             return self._apply_overlap(flat, ii[0], placed, gates, dtype, reads, t, pending)
@@ -701,7 +761,7 @@ class ArenaMoE:
         slots = self._device_slots([[placed[e][1] for e in row] for row in ii], flat.device)
         arena = self.store.expert_arena(t)
         x_in = flat.contiguous()
-        if self.store.use_f16(t) and x_in.dtype == torch.bfloat16:
+        if x_in.dtype == torch.bfloat16 and self.store.use_f16(t):
             x_in = x_in.to(torch.float16)
         w = gates.to(torch.float32).contiguous()
         ws = self._workspace()

@@ -130,13 +130,15 @@ class V4ArenaStore(ArenaStore):
                 raise ValueError(f"layer {layer} spans multiple expert tiers: {tiers}")
         return next(iter(tiers))
 
-    def submit(self, layer, experts, prefetch=False):
+    def submit(self, layer, experts, prefetch=False, fills_on_caller_stream=None):
         """ArenaStore.submit; with the compiled planner and fills from host
-        memory, a layer's misses are queued on the fill stream straight after
-        the one planner call and the bookkeeping follows. Planner calls,
-        slots, counters, futures and pins are the general path's."""
+        memory, a layer's misses are queued straight after the one planner
+        call and the bookkeeping follows. Planner calls, slots, counters,
+        futures, pins and streams are the general path's."""
         if not self.native_caches or self.host_source is None or self.fill_stream is None:
-            return super().submit(layer, experts, prefetch)
+            return super().submit(layer, experts, prefetch, fills_on_caller_stream)
+        if fills_on_caller_stream is None:
+            fills_on_caller_stream = not prefetch
         want = list(dict.fromkeys(int(e) for e in experts))
         if not want:
             return {}, ReadPlan({t: [] for t in self.tiers})
@@ -152,8 +154,8 @@ class V4ArenaStore(ArenaStore):
         res = cache.plan_each_into([base + e for e in want], tuple(self.pinned.get(t, ())),
                                    not prefetch)
         issued = [(e, r.slot) for e, r in zip(want, res) if r.placed and not r.hit]
-        landed = (self._fill_from_host([((layer, e), t, s, None) for e, s in issued])
-                  if issued else None)
+        landed = (self._fill_from_host([((layer, e), t, s, None) for e, s in issued],
+                                       fills_on_caller_stream) if issued else None)
         out, waits = {}, {name: [] for name in self.tiers}
         for e, r in zip(want, res):
             if r.hit:

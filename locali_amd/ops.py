@@ -198,6 +198,15 @@ class Workspace:
     def reserve(self, tokens, d_model, d_ff, n_experts, top_k, has_shared) -> torch.Tensor:
         return self.get(workspace_bytes(tokens, d_model, d_ff, n_experts, top_k, has_shared))
 
+    def scratch(self, name: str, shape: tuple, dtype: torch.dtype) -> torch.Tensor:
+        """A named intermediate kept between calls (calls on one stream
+        reuse it in order)."""
+        cache = self.__dict__.setdefault("_scratch", {})
+        t = cache.get(name)
+        if t is None or t.shape != shape or t.dtype != dtype:
+            t = cache[name] = torch.empty(shape, dtype=dtype, device=self.device)
+        return t
+
 
 _WS_BYTES: dict = {}
 
@@ -262,7 +271,8 @@ def expert_decode(arena: ExpertArenaT, shared: ExpertArenaT | None, x: torch.Ten
     k = route_slot.shape[-1]
     routes = T * k + (T if shared is not None else 0)
     if hidden is None:
-        hidden = torch.empty(routes, arena.d_ff, dtype=x2.dtype, device=x.device)
+        hidden = (ws.scratch("decode_hidden", (routes, arena.d_ff), x2.dtype) if ws is not None
+                  else torch.empty(routes, arena.d_ff, dtype=x2.dtype, device=x.device))
     out = torch.empty_like(x2)
     buf = _decode_ws(ws, arena, T, k, shared)
     a = arena.struct()

@@ -360,8 +360,8 @@ def test_fast_submit_equals_the_general_path(ckpt, policy, slots):
         st.host_source = lambda layer, e: None
         st.fill_stream = object()
 
-        def fake(jobs, log=log, clock=clock):
-            log.append([(key, tt, s) for key, tt, s, _ in jobs])
+        def fake(jobs, on_caller_stream=False, log=log, clock=clock):
+            log.append(([(key, tt, s) for key, tt, s, _ in jobs], on_caller_stream))
             return _FakeLanded(clock)
         st._fill_from_host = fake
         stores.append(st)
