@@ -538,7 +538,7 @@ def main(argv=None):
     ap.add_argument("--stack-warmup", type=int, default=16)
     ap.add_argument("--stack-policies", default="slru-all,lfu-decay",
                     help="comma-separated arena cache policies for the 43-layer stack")
-    ap.add_argument("--stack-prefetch", default="6",
+    ap.add_argument("--stack-prefetch", default="5",
                     help="comma-separated prefetch widths for extra slru-all stack legs with "
                          "cross-layer prefetch at depth 1 (0: none)")
     ap.add_argument("--stack-lookahead-rho", type=float, default=LOOKAHEAD_RHO,
