@@ -409,6 +409,15 @@ class ArenaStore:
         finally:
             self.staging.give(buf)
 
+    def _mark_demand(self):
+        """Record, on the caller's stream, the point before a demand call's
+        fills and gather (see _fill_from_host)."""
+        from .ops import current_stream
+        mark = self.__dict__.get("_demand_mark")
+        if mark is None:
+            mark = self._demand_mark = torch.cuda.Event()
+        mark.record(current_stream(self.device))
+
     def _slot_table(self, t):
         """Tier t's nine slot-major arrays in record order (gate, up, down) x
         (weight, scales, biases), as ops.arena_fill_slots takes them."""
@@ -433,9 +442,14 @@ class ArenaStore:
         on_caller_stream: the copies run on the caller's current stream, in
         order with the work around them (a demand call's fills, which its own
         gather needs next). Otherwise they run on the fill stream, behind the
-        work queued on the caller's stream (a refilled slot may still be read
-        there). Either way a copy into a slot waits for the pending fill of
-        that slot's previous owner when it runs on the other stream."""
+        caller's work that may still read a slot they overwrite: everything
+        queued before the latest demand call (its mark). What that call queued
+        after its mark -- its own fills and gather -- touches only its own
+        slots, which stay pinned until the next demand call, so a copy on the
+        fill stream never takes one of them. Without a demand mark the copies
+        wait for everything queued on the caller's stream. Either way a copy
+        into a slot waits for the pending fill of that slot's previous owner
+        when it ran on the other stream."""
         from .ops import arena_fill_slots, current_stream
         if self.device.index is not None and torch.cuda.current_device() != self.device.index:
             with torch.cuda.device(self.device):
@@ -447,15 +461,19 @@ class ArenaStore:
         for f in self._slot_fills.pop_slots(t, [slot for _, _, slot, _ in jobs]):
             if f.stream != stream.cuda_stream and not f.done():
                 stream.wait_event(f.event)
-        if not on_caller_stream and not cur.query():
-            # the fill stream waits for the caller's stream through one reused
-            # event (a wait takes the event's state when it is queued); a
-            # stream with nothing left to run needs no wait
-            order = self.__dict__.get("_order_event")
-            if order is None:
-                order = self._order_event = torch.cuda.Event()
-            order.record(cur)
-            self.fill_stream.wait_event(order)
+        if not on_caller_stream:
+            mark = self.__dict__.get("_demand_mark")
+            if mark is not None:
+                if not mark.query():
+                    self.fill_stream.wait_event(mark)
+            elif not cur.query():
+                # one reused event (a wait takes the event's state when it is
+                # queued); a stream with nothing left to run needs no wait
+                order = self.__dict__.get("_order_event")
+                if order is None:
+                    order = self._order_event = torch.cuda.Event()
+                order.record(cur)
+                self.fill_stream.wait_event(order)
         arena_fill_slots(self._slot_table(t), [slot for _, _, slot, _ in jobs],
                          [src.data_ptr() for src in sources], stream)
         ev = torch.cuda.Event()
@@ -559,6 +577,8 @@ class ArenaStore:
         plan = ReadPlan()
         jobs = {t: [] for t in self.tiers}
         from_host = self.host_source is not None and self.fill_stream is not None
+        if from_host and not prefetch:
+            self._mark_demand()
         for e, t, s in issued:
             # a copy from host memory moves the whole expert; a file read
             # follows its records

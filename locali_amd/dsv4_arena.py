@@ -154,6 +154,8 @@ class V4ArenaStore(ArenaStore):
         res = cache.plan_each_into([base + e for e in want], tuple(self.pinned.get(t, ())),
                                    not prefetch)
         issued = [(e, r.slot) for e, r in zip(want, res) if r.placed and not r.hit]
+        if not prefetch:
+            self._mark_demand()
         landed = (self._fill_from_host([((layer, e), t, s, None) for e, s in issued],
                                        fills_on_caller_stream) if issued else None)
         out, waits = {}, {name: [] for name in self.tiers}

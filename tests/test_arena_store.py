@@ -364,6 +364,7 @@ def test_fast_submit_equals_the_general_path(ckpt, policy, slots):
             log.append(([(key, tt, s) for key, tt, s, _ in jobs], on_caller_stream))
             return _FakeLanded(clock)
         st._fill_from_host = fake
+        st._mark_demand = lambda: None
         stores.append(st)
         logs.append(log)
         clocks.append(clock)
