@@ -394,3 +394,22 @@ def test_fast_submit_equals_the_general_path(ckpt, policy, slots):
         for st in stores:
             st.fill_stream = None
             st.close()
+
+
+def test_a_truncated_shard_is_a_short_read(tmp_path):
+    """A record past the end of its shard raises IOError from the fill (the
+    reference's short-read check, arena.py:183-184, 199-200); the arena's
+    other slots are untouched."""
+    root = tmp_path / "ckpt"
+    root.mkdir()
+    make_snapshot(root, layers=LAYERS, experts=EXPERTS, top_k=TOP_K, d=128, dff=64)
+    index = make_index(root)
+    shard = root / "model-00002-of-00003.safetensors"
+    shard.write_bytes(shard.read_bytes()[: shard.stat().st_size // 2])
+    st = _store(index, 6)
+    try:
+        st.slots_for(0, [1])                         # layer 0's shard is whole
+        with pytest.raises(IOError, match="short read"):
+            st.slots_for(1, [EXPERTS - 1])
+    finally:
+        st.close()
