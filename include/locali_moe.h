@@ -28,6 +28,7 @@
  *   locali_moe_expert_grouped  the same expert math with (token, k) entries
  *                              grouped by slot (arena.py:641-672), one pass of
  *                              each slot's weights per group, then combine
+ *                              (also exported as locali_moe_expert_prefill)
  *   locali_moe_combine         sum_k y * w in the activation dtype
  *                              (arena.py:623-624) or fp32 (arena.py:661-672)
  *   locali_moe_arena_fill      the slot fill ArenaStore._read_into/_read_many
@@ -207,6 +208,19 @@ int locali_moe_decode_gateup_select(const locali_router *router,
  * once per group; expert ids idx [tokens, top_k] and slot_of_expert [n_experts]
  * give the slots. Scratch comes from the workspace. */
 int locali_moe_expert_grouped(const locali_expert_arena *routed,
+                              const locali_expert_arena *shared, const void *x,
+                              int32_t x_dtype, int32_t tokens, int32_t top_k,
+                              int32_t n_experts, const int32_t *idx,
+                              const int32_t *slot_of_expert, const float *weights,
+                              float swiglu_limit, int32_t fp32_swiglu,
+                              int32_t combine_mode, void *out, void *workspace,
+                              size_t workspace_bytes, void *stream);
+
+/* The prefill entry point (the many-token path of V4ArenaMoE._gather,
+ * dsv4_arena.py:168-235, grouped by slot as arena.py:641-672): the same call
+ * as locali_moe_expert_grouped, under the name the decode / prefill split of
+ * the layer gives it. */
+int locali_moe_expert_prefill(const locali_expert_arena *routed,
                               const locali_expert_arena *shared, const void *x,
                               int32_t x_dtype, int32_t tokens, int32_t top_k,
                               int32_t n_experts, const int32_t *idx,

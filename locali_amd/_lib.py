@@ -100,6 +100,8 @@ _SIGNATURES = {
                                         _I, _I, _P, _P, _I, _P, _P, _SZ, _P], ctypes.c_int),
     "locali_moe_expert_grouped": ([ctypes.POINTER(ExpertArena), ctypes.POINTER(ExpertArena), _P, _I,
                                    _I, _I, _I, _P, _P, _P, _F, _I, _I, _P, _P, _SZ, _P], ctypes.c_int),
+    "locali_moe_expert_prefill": ([ctypes.POINTER(ExpertArena), ctypes.POINTER(ExpertArena), _P, _I,
+                                   _I, _I, _I, _P, _P, _P, _F, _I, _I, _P, _P, _SZ, _P], ctypes.c_int),
     "locali_moe_router_logits": ([ctypes.POINTER(Router), _P, _I, _I, _I, _P, _P], ctypes.c_int),
     "locali_moe_decode_gateup_select": ([ctypes.POINTER(Router), ctypes.POINTER(ExpertArena),
                                          ctypes.POINTER(ExpertArena), _P, _P, _I, _I, _P, _P, _F, _I, _P, _P,

@@ -637,6 +637,17 @@ int locali_moe_combine_routes(const void *y, int32_t y_dtype, const int32_t *rou
     return 0;
 }
 
+int locali_moe_expert_prefill(const locali_expert_arena *routed, const locali_expert_arena *shared,
+                              const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k,
+                              int32_t n_experts, const int32_t *idx, const int32_t *slot_of_expert,
+                              const float *weights, float swiglu_limit, int32_t fp32_swiglu,
+                              int32_t combine_mode, void *out, void *workspace, size_t workspace_bytes,
+                              void *stream) {
+    return locali_moe_expert_grouped(routed, shared, x, x_dtype, tokens, top_k, n_experts, idx, slot_of_expert,
+                                     weights, swiglu_limit, fp32_swiglu, combine_mode, out, workspace,
+                                     workspace_bytes, stream);
+}
+
 int locali_moe_arena_fill(void *dst, const void *src_host, size_t bytes, void *stream) {
     if (!dst || !src_host) return fail(LOCALI_E_ARG, "arena_fill: null pointer");
     if (!bytes) return 0;

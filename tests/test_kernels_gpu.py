@@ -475,6 +475,33 @@ def test_expert_grouped_matches_oracle(T, dtype, bits):
     assert close_fraction(values(out), want, dtype) > 0.8
 
 
+def test_expert_prefill_is_the_grouped_path():
+    """locali_moe_expert_prefill (the prefill name of the grouped entry
+    point) returns locali_moe_expert_grouped's output bit for bit."""
+    import ctypes
+    from locali_amd._lib import lib
+    banner("expert_prefill == expert_grouped")
+    d, dff, E, k, T = 1024, 512, 16, 4, 24
+    arena = _dev(synth.expert_arena(E + 1, d, dff, bits_gate_up=2, dtype=torch.bfloat16, seed=5))
+    x = synth.activations(T, d, torch.bfloat16, seed=6).to(DEV)
+    gen = torch.Generator().manual_seed(7)
+    idx = torch.stack([torch.randperm(E, generator=gen)[:k] for _ in range(T)]).to(torch.int32).to(DEV)
+    slot_of = (torch.arange(E, dtype=torch.int32) + 1).to(DEV)
+    wts = torch.rand(T, k, generator=gen).to(DEV)
+    ws = ops.Workspace()
+    want = ops.expert_grouped(arena, None, x, idx, slot_of, wts, ws, n_experts=E)
+    out = torch.empty_like(x)
+    buf = ws.reserve(T, d, dff, E, k, False)
+    a = arena.struct()
+    rc = lib().locali_moe_expert_prefill(ctypes.byref(a), None, x.data_ptr(), ops.DT_BF16, T, k, E,
+                                         idx.data_ptr(), slot_of.data_ptr(), wts.data_ptr(), 10.0, 0,
+                                         ops.COMBINE_ROUNDED, out.data_ptr(), buf.data_ptr(), buf.numel(),
+                                         torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+
+
 def test_arena_fill_batch_lands_every_byte():
     """Batched fills: pinned, 16-byte aligned pieces through the copy kernel
     (more pieces than one launch takes), plus an odd-sized piece and a
