@@ -170,6 +170,48 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict
     out[static_cast<int64_t>(t) * d + col] = from_float<BF16>(o);
 }
 
+// The same combine, eight consecutive columns per thread with 16-byte loads
+// and stores (d a multiple of 8, rows 16-byte aligned); every element's
+// arithmetic and order are those of combine_kernel.
+template <bool BF16>
+__global__ __launch_bounds__(256) void combine8_kernel(const uint16_t *__restrict__ y,
+                                                       const int32_t *__restrict__ route_pos,
+                                                       const uint16_t *__restrict__ shared_y,
+                                                       const float *__restrict__ weights, int tokens,
+                                                       int top_k, int d, int mode,
+                                                       uint16_t *__restrict__ out) {
+    const int t = blockIdx.y;
+    const int c8 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (8 * c8 >= d) return;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+    for (int j = 0; j < top_k; ++j) {
+        const int r = t * top_k + j;
+        const int p = route_pos ? route_pos[r] : r;
+        if (p < 0) continue;
+        const float w = round16<BF16>(weights[r]);
+        const uint4 v = reinterpret_cast<const uint4 *>(y + static_cast<int64_t>(p) * d)[c8];
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float f = to_float<BF16>(static_cast<uint16_t>(vw[i / 2] >> (16 * (i % 2))));
+            acc[i] += mode == 0 ? round16<BF16>(f * w) : f * w;
+        }
+    }
+    uint4 sv = make_uint4(0u, 0u, 0u, 0u);
+    if (shared_y) sv = reinterpret_cast<const uint4 *>(shared_y + static_cast<int64_t>(t) * d)[c8];
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    uint32_t o[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float v = round16<BF16>(acc[i]);
+        if (shared_y) v = round16<BF16>(v + to_float<BF16>(static_cast<uint16_t>(sw[i / 2] >> (16 * (i % 2)))));
+        o[i / 2] |= static_cast<uint32_t>(from_float<BF16>(v)) << (16 * (i % 2));
+    }
+    reinterpret_cast<uint4 *>(out + static_cast<int64_t>(t) * d)[c8] = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 // Weighted combine of route outputs held anywhere in `y`: route (t, j) reads
 // row route_pos[t * top_k + j] (skipped when negative), in j order. YT is the
 // rows' type (0 fp32, 1 fp16, 2 bf16); BF16 the output / shared / weight
@@ -279,6 +321,19 @@ hipError_t launch_route_slots(const int32_t *idx, int R, int E, const int32_t *s
 hipError_t launch_combine(const uint16_t *y, const int32_t *route_pos, const uint16_t *shared_y,
                           const float *weights, int tokens, int top_k, int d, int mode, bool bf16,
                           uint16_t *out, hipStream_t st) {
+    const bool vec = d % 8 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(shared_y) |
+                       reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    if (vec) {
+        dim3 grid((d / 8 + 255) / 256, tokens);
+        if (bf16)
+            hipLaunchKernelGGL(combine8_kernel<true>, grid, dim3(256), 0, st, y, route_pos, shared_y, weights,
+                               tokens, top_k, d, mode, out);
+        else
+            hipLaunchKernelGGL(combine8_kernel<false>, grid, dim3(256), 0, st, y, route_pos, shared_y, weights,
+                               tokens, top_k, d, mode, out);
+        return hipGetLastError();
+    }
     dim3 grid((d + 255) / 256, tokens);
     if (bf16)
         hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, st, y, route_pos, shared_y, weights,
