@@ -109,17 +109,29 @@ __global__ __launch_bounds__(256) void dispatch_place_kernel(
     if (s >= n_slots) return;
     const int base = seg_start[s], end = seg_start[s + 1];
     if (base == end) return;
+    // 8 x 64 routes per pass: the loads of a pass are in flight together,
+    // then the ballots place them in route order
+    constexpr int U = 8;
     int pos = base;
-    for (int r0 = 0; r0 < R && pos < end; r0 += 64) {
-        const int r = r0 + lane;
-        const bool mine = r < R && route_slot[r] == s;
-        const uint64_t m = __ballot(mine);
-        if (mine) {
-            const int p = pos + __popcll(m & ((1ull << lane) - 1ull));
-            sorted_route[p] = r;
-            if (route_pos) route_pos[r] = p;
+    for (int r0 = 0; r0 < R && pos < end; r0 += 64 * U) {
+        int v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int r = r0 + 64 * u + lane;
+            v[u] = r < R ? route_slot[r] : -1;
         }
-        pos += __popcll(m);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int r = r0 + 64 * u + lane;
+            const bool mine = v[u] == s;
+            const uint64_t m = __ballot(mine);
+            if (mine) {
+                const int p = pos + __popcll(m & ((1ull << lane) - 1ull));
+                sorted_route[p] = r;
+                if (route_pos) route_pos[r] = p;
+            }
+            pos += __popcll(m);
+        }
     }
 }
 
