@@ -8,9 +8,10 @@
 //                           (seg_start), per-slot tile counts and the tile
 //                           list (slot, first position, token count); the
 //                           shared expert, when present, is one more segment
-//                           holding every token, placed after the routed ones
-//   dispatch_place_kernel   one wave per slot: walks the routes 64 at a time
-//                           with a ballot and writes sorted_route / route_pos
+//                           holding every token, placed after the routed ones;
+//                           routes outside the arena get route_pos -1
+//   dispatch_place_kernel   one wave per slot: walks the routes 512 at a time
+//                           with ballots and writes sorted_route / route_pos
 //                           in route order (stable)
 //   combine_kernel          out[t] = round(sum_j round(y[pos(t,j)] * w)) (+ shared)
 #include "mfma_grouped.hpp"
@@ -23,7 +24,7 @@ constexpr int kMaxDispatchSlots = 16000;   // counts live in 64 KiB of LDS
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
     const int32_t *__restrict__ route_slot, int R, int n_slots, int n_shared_tokens, int tile_tokens,
     int32_t *__restrict__ seg_start, int32_t *__restrict__ tiles, int32_t *__restrict__ n_tiles,
-    int max_tiles) {
+    int max_tiles, int32_t *__restrict__ route_pos) {
     extern __shared__ int32_t cnt[];              // [n_slots + 1]
     __shared__ int32_t wsum[kDispatchThreads / 64];
     __shared__ int32_t carry;
@@ -33,6 +34,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
     for (int r = tid; r < R; r += blockDim.x) {
         const int s = route_slot[r];
         if (s >= 0 && s < n_slots) atomicAdd(&cnt[s], 1);
+        else if (route_pos) route_pos[r] = -1;   // outside the arena: never placed
     }
     __syncthreads();
     // Two exclusive scans over slots in chunks of blockDim.x: positions and tiles.
@@ -132,16 +134,6 @@ __global__ __launch_bounds__(256) void dispatch_place_kernel(
             }
             pos += __popcll(m);
         }
-    }
-}
-
-// Invalid slots (outside the arena) never get a position; mark them.
-__global__ void route_pos_init_kernel(const int32_t *__restrict__ route_slot, int R, int n_slots,
-                                      int32_t *__restrict__ route_pos) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r < R) {
-        const int s = route_slot[r];
-        if (s < 0 || s >= n_slots) route_pos[r] = -1;
     }
 }
 
@@ -310,14 +302,9 @@ hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_
     if (n_slots < 1 || n_slots > kMaxDispatchSlots) return hipErrorInvalidValue;
     const size_t lds = sizeof(int32_t) * (n_slots + 1);
     hipLaunchKernelGGL(dispatch_count_kernel, dim3(1), dim3(kDispatchThreads), lds, st, route_slot, R,
-                       n_slots, n_shared_tokens, tile_tokens, seg_start, tiles, n_tiles, max_tiles);
+                       n_slots, n_shared_tokens, tile_tokens, seg_start, tiles, n_tiles, max_tiles, route_pos);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (route_pos) {
-        hipLaunchKernelGGL(route_pos_init_kernel, dim3((R + 255) / 256), dim3(256), 0, st, route_slot,
-                           R, n_slots, route_pos);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
     hipLaunchKernelGGL(dispatch_place_kernel, dim3((n_slots + 3) / 4), dim3(256), 0, st, route_slot, R,
                        n_slots, seg_start, sorted_route, route_pos);
     return hipGetLastError();
