@@ -6,9 +6,11 @@ with its own memory: the arena is a set of slot-major device tensors
 [n_slots, *shape] per (tier, projection, array) -- exactly the layout the
 expert kernels index by slot -- and a miss is a preadv of the expert's nine
 records into pinned host staging followed by an asynchronous host -> HBM copy
-on a dedicated fill stream (locali_moe_arena_fill_batch: one launch for the
-nine records). Slot 0 of every tier is
-reserved and all-zero: a masked-out route reads it and contributes exactly 0.
+on a dedicated fill stream (one copy-kernel launch for the nine records). With
+host_source (the experts' records already in pinned host memory) a call's
+misses are copied by one launch on the caller's stream (demand) or the fill
+stream (prefetch). Slot 0 of every tier is reserved and all-zero: a
+masked-out route reads it and contributes exactly 0.
 
 Slots are claimed synchronously by the planner (so a later submit cannot
 steal a slot an earlier one is still filling); only the reads and copies are
@@ -609,8 +611,9 @@ class ArenaStore:
     def wait(self, futs):
         """Every fill in futs has landed before work queued afterwards on the
         caller's current stream reads it. Copies from host memory are ordered
-        on the device (the stream waits for their event and the host goes
-        on); file reads block the host until their copies have landed."""
+        on the device (copies queued on this stream already are; for others
+        the stream waits for their event) and the host goes on; file reads
+        block the host until their copies have landed."""
         if not futs:
             return
         from .ops import current_stream
