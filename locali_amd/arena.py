@@ -418,7 +418,9 @@ class ArenaStore:
         mark = self.__dict__.get("_demand_mark")
         if mark is None:
             mark = self._demand_mark = torch.cuda.Event()
-        mark.record(current_stream(self.device))
+        cur = current_stream(self.device)
+        mark.record(cur)
+        self._demand_stream = cur.cuda_stream
 
     def _slot_table(self, t):
         """Tier t's nine slot-major arrays in record order (gate, up, down) x
@@ -448,8 +450,9 @@ class ArenaStore:
         queued before the latest demand call (its mark). What that call queued
         after its mark -- its own fills and gather -- touches only its own
         slots, which stay pinned until the next demand call, so a copy on the
-        fill stream never takes one of them. Without a demand mark the copies
-        wait for everything queued on the caller's stream. Either way a copy
+        fill stream never takes one of them. Without a demand mark on the
+        caller's current stream the copies wait for everything queued on that
+        stream. Either way a copy
         into a slot waits for the pending fill of that slot's previous owner
         when it ran on the other stream."""
         from .ops import arena_fill_slots, current_stream
@@ -465,7 +468,7 @@ class ArenaStore:
                 stream.wait_event(f.event)
         if not on_caller_stream:
             mark = self.__dict__.get("_demand_mark")
-            if mark is not None:
+            if mark is not None and self._demand_stream == cur.cuda_stream:
                 if not mark.query():
                     self.fill_stream.wait_event(mark)
             elif not cur.query():
