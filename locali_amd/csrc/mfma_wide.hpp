@@ -69,8 +69,11 @@ constexpr int kWideStageBytes = kWideTokens * 256;
 // [stage % 3][block of the stage][position], then the positions' vectors.
 constexpr int kWideFixStages = 3;
 __host__ __device__ constexpr size_t wide_meta_offset() { return 2 * kWideStageBytes; }
+// Metadata rows per block in LDS: one spare row, so that the staging stores
+// of lanes that hold different blocks of one row fall in different banks.
+constexpr int kWideMetaRows = kWideRows + 1;
 __host__ __device__ constexpr size_t wide_gs_offset(int K, int nproj) {
-    return wide_meta_offset() + static_cast<size_t>(K / 64) * kWideRows * 2 * nproj * sizeof(uint16_t);
+    return wide_meta_offset() + static_cast<size_t>(K / 64) * kWideMetaRows * 2 * nproj * sizeof(uint16_t);
 }
 __host__ __device__ constexpr size_t wide_tok_offset(int K, int nproj) {
     return wide_gs_offset(K, nproj) + kWideFixStages * 2 * kWideTokens * sizeof(uint4);
@@ -95,32 +98,51 @@ struct WideLds {
 // Scales and biases of the workgroup's rows for every block. Item (row r,
 // 8-group piece c) is that piece of each of the 2 NPROJ arrays (arr[2 j] =
 // scales, arr[2 j + 1] = biases of projection j, rows of the workgroup), one
-// entry per 64-value block (bpg blocks per group). Loads go out for every
-// thread on every pass (past the last item they repeat it), so the waits
-// that follow count loads exactly.
+// entry per 64-value block (bpg blocks per group). With P pieces per row
+// dividing 64, a wave's 64 items are 64 / P rows x all P pieces of each
+// (whole 128-byte lines per load instruction): lane l holds row l % (64 / P),
+// piece l / (64 / P). Loads go
+// out for every thread on every pass (past the last item they repeat it), so
+// the waits that follow count loads exactly.
 template <int NPROJ>
 struct WideMetaStage {
     static constexpr int U = 2;
     uint4 v[U][2 * NPROJ];
     int items;
 
+    // (row, piece) of item e, P = gpr / 8 pieces per row. When P divides 64 a
+    // wave holds whole rows; otherwise lanes take consecutive rows of one
+    // piece.
+    __device__ __forceinline__ static void item(int e, int pieces, int &r, int &c) {
+        if (64 % pieces == 0) {
+            const int rpw = 64 / pieces, l = e & 63;
+            r = (e >> 6) * rpw + l % rpw;
+            c = l / rpw;
+        } else {
+            r = e % kWideRows;
+            c = e / kWideRows;
+        }
+    }
+
     __device__ __forceinline__ void load(const uint16_t *const (&arr)[2 * NPROJ], int gpr, int base) {
 #pragma unroll
         for (int it = 0; it < U; ++it) {
             const int e = min(base + it * kWideThreads + static_cast<int>(threadIdx.x), items - 1);
-            const int r = e % kWideRows, c = e / kWideRows;
+            int r, c;
+            item(e, gpr / 8, r, c);
 #pragma unroll
             for (int a = 0; a < 2 * NPROJ; ++a)
                 v[it][a] = reinterpret_cast<const uint4 *>(arr[a] + static_cast<int64_t>(r) * gpr)[c];
         }
     }
 
-    __device__ __forceinline__ void store(uint16_t *meta, int bpg, int base) const {
+    __device__ __forceinline__ void store(uint16_t *meta, int bpg, int base, int gpr) const {
 #pragma unroll
         for (int it = 0; it < U; ++it) {
             const int e = base + it * kWideThreads + static_cast<int>(threadIdx.x);
             if (e >= items) break;
-            const int r = e % kWideRows, c = e / kWideRows;
+            int r, c;
+            item(e, gpr / 8, r, c);
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
                 uint32_t w[NPROJ];
@@ -129,7 +151,7 @@ struct WideMetaStage {
                     w[j] = ((v[it][2 * j][q / 2] >> (16 * (q % 2))) & 0xffffu) |
                            (((v[it][2 * j + 1][q / 2] >> (16 * (q % 2))) & 0xffffu) << 16);
                 for (int t = 0; t < bpg; ++t) {
-                    uint16_t *dst = meta + (static_cast<int64_t>((c * 8 + q) * bpg + t) * kWideRows + r) * (2 * NPROJ);
+                    uint16_t *dst = meta + (static_cast<int64_t>((c * 8 + q) * bpg + t) * kWideMetaRows + r) * (2 * NPROJ);
                     if constexpr (NPROJ == 2)
                         *reinterpret_cast<uint2 *>(dst) = make_uint2(w[0], w[1]);
                     else
@@ -223,10 +245,10 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
     ms.items = kWideRows * (gpr / 8);
     const int mpass = WideMetaStage<NPROJ>::U * kWideThreads;
     auto stage_meta = [&]() {
-        ms.store(L.meta, bpg, 0);
+        ms.store(L.meta, bpg, 0, gpr);
         for (int base = mpass; base < ms.items; base += mpass) {
             ms.load(marr, gpr, base);
-            ms.store(L.meta, bpg, base);
+            ms.store(L.meta, bpg, base, gpr);
         }
     };
 
@@ -305,7 +327,7 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
 #pragma unroll
                     for (int jb = 0; jb < 2; ++jb) {
                         const int blk = 2 * s + jb;
-                        const uint16_t *mrow = L.meta + (static_cast<int64_t>(blk) * kWideRows + row) * (2 * NPROJ);
+                        const uint16_t *mrow = L.meta + (static_cast<int64_t>(blk) * kWideMetaRows + row) * (2 * NPROJ);
                         uint32_t m[NPROJ];
                         if constexpr (NPROJ == 2) {
                             const uint2 mm = *reinterpret_cast<const uint2 *>(mrow);
@@ -341,7 +363,7 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
                         // 2s - 2 + kb (stages s - 1 and s of the fixup ring)
                         const int blk = 2 * s - 2 + kb;
                         const u32x4(*fx)[kWideTokens] = L.fix[(kb < 2 ? s - 1 : s) % kWideFixStages];
-                        const uint16_t *mrow = L.meta + (static_cast<int64_t>(blk) * kWideRows + row) * (2 * NPROJ);
+                        const uint16_t *mrow = L.meta + (static_cast<int64_t>(blk) * kWideMetaRows + row) * (2 * NPROJ);
                         u32x4 fb[NPROJ];
                         if constexpr (NPROJ == 2) {
                             const uint2 mm = *reinterpret_cast<const uint2 *>(mrow);
