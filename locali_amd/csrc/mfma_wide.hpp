@@ -304,9 +304,11 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
         for (int j = 0; j < NPROJ; ++j)
             dst[j] = __builtin_amdgcn_raw_buffer_load_b128(wrs[j], w_off | past, c * 64, kAuxStream);
     };
+    // the scales and biases first: the loop waits for all of them, and the
+    // in-order load counter then lets the first weight chunks land behind
+    ms.load(marr, gpr, 0);
 #pragma unroll
     for (int q = 0; q < RING; ++q) load_w(ring[q], q);
-    ms.load(marr, gpr, 0);
     stage_meta();
     const uint32_t magic_v = opaque_vgpr(G::P::kMagic);
     const int row = wave * 16 + nl;
