@@ -55,7 +55,7 @@ bool dtype16(int32_t dt) { return dt == LOCALI_DT_F16 || dt == LOCALI_DT_BF16; }
 
 // Workspace layout for up to T tokens.
 struct Layout {
-    size_t logits, route_slot, hidden, hprep, seg_start, sorted_route, route_pos,
+    size_t logits, route_slot, hidden, hprep, seg_start, seg_tile, sorted_route, route_pos,
         tiles, n_tiles, gh, gy, mx, mh, total;
     int max_tiles;
 };
@@ -98,6 +98,7 @@ Layout layout(int T, int d, int dff, int E, int k, int has_shared) {
     L.hidden = take(sizeof(uint16_t) * static_cast<size_t>(routes) * dff);
     L.hprep = take(prep_bytes(dff) * routes);
     L.seg_start = take(sizeof(int32_t) * (kMaxSlots + 1));
+    L.seg_tile = take(sizeof(int32_t) * kMaxSlots);
     L.sorted_route = take(sizeof(int32_t) * R);
     L.route_pos = take(sizeof(int32_t) * R);
     L.tiles = take(sizeof(int32_t) * 4 * L.max_tiles);
@@ -324,9 +325,14 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     uint16_t *gy = at<uint16_t>(ws, lay.gy);
     const int max_tiles = grouped_max_tiles(tokens, top_k, shared ? 1 : 0, n_experts, kWideTokens);
     if (max_tiles > lay.max_tiles) return fail(LOCALI_E_WORKSPACE, "grouped: tile list too small");
+    // Tiles of one or two positions go to the small-tile kernels when the
+    // shapes allow; the 64-position kernels skip them. The dispatch packs
+    // such a tile's tokens into its record.
+    const bool small = small_tiles_eligible(routed);
     hipError_t e = launch_dispatch(route_slot, R, n_slots, shared ? tokens : 0, kWideTokens,
                                    at<int32_t>(ws, lay.seg_start), at<int32_t>(ws, lay.sorted_route),
-                                   route_pos, tiles, n_tiles, max_tiles, st);
+                                   route_pos, tiles, n_tiles, max_tiles, st,
+                                   small ? at<int32_t>(ws, lay.seg_tile) : nullptr, top_k);
     if (e != hipSuccess) return hip_fail(e, "dispatch launch");
     MfmaLaunch L{};
     L.ta.x = static_cast<const uint16_t *>(x);
@@ -352,9 +358,6 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     L.tokens = tokens;
     L.routes = routes;
     const bool bf16 = x_dtype == LOCALI_DT_BF16;
-    // Tiles of one or two positions go to the small-tile kernels when the
-    // shapes allow; the 64-position kernels skip them.
-    const bool small = small_tiles_eligible(routed);
     L.ta.min_count = small ? kSmallTileHost + 1 : 0;
     const int order[5] = {0, 1, 3, 2, 4};
     for (int which : order) {

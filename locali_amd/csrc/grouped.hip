@@ -24,7 +24,7 @@ constexpr int kMaxDispatchSlots = 16000;   // counts live in 64 KiB of LDS
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
     const int32_t *__restrict__ route_slot, int R, int n_slots, int n_shared_tokens, int tile_tokens,
     int32_t *__restrict__ seg_start, int32_t *__restrict__ tiles, int32_t *__restrict__ n_tiles,
-    int max_tiles, int32_t *__restrict__ route_pos) {
+    int max_tiles, int32_t *__restrict__ route_pos, int32_t *__restrict__ seg_tile, int small_pack) {
     extern __shared__ int32_t cnt[];              // [n_slots + 1]
     __shared__ int32_t wsum[kDispatchThreads / 64];
     __shared__ int32_t carry;
@@ -68,6 +68,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
                     seg_start[s] = excl;
                 } else {
                     int pos = seg_start[s];
+                    if (seg_tile) seg_tile[s] = excl;
                     for (int q = 0; q < v; ++q) {
                         const int tile = excl + q;
                         if (tiles && tile < max_tiles) {
@@ -75,7 +76,9 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
                             tiles[4 * tile + 0] = s;
                             tiles[4 * tile + 1] = first;
                             tiles[4 * tile + 2] = min(tile_tokens, c - q * tile_tokens);
-                            tiles[4 * tile + 3] = 0;
+                            // a tile of at most kPackedTokens positions gets its
+                            // tokens from the place kernel (kTokensPacked marks it)
+                            tiles[4 * tile + 3] = small_pack && c <= kPackedTokens ? kTokensPacked : 0;
                         }
                     }
                 }
@@ -105,12 +108,20 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
 
 __global__ __launch_bounds__(256) void dispatch_place_kernel(
     const int32_t *__restrict__ route_slot, int R, int n_slots, const int32_t *__restrict__ seg_start,
-    int32_t *__restrict__ sorted_route, int32_t *__restrict__ route_pos) {
+    int32_t *__restrict__ sorted_route, int32_t *__restrict__ route_pos, const int32_t *__restrict__ seg_tile,
+    int32_t *__restrict__ tiles, int max_tiles, int top_k) {
     const int lane = threadIdx.x & 63;
     const int s = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (s >= n_slots) return;
     const int base = seg_start[s], end = seg_start[s + 1];
     if (base == end) return;
+    // a slot of at most kPackedTokens routes: its tile's tokens, 15 bits each
+    // in position order, go into the tile record (see the count kernel)
+    int32_t *packed = nullptr;
+    if (seg_tile && end - base <= kPackedTokens) {
+        const int tile = seg_tile[s];
+        if (tile >= 0 && tile < max_tiles) packed = &tiles[4 * tile + 3];
+    }
     // 8 x 64 routes per pass: the loads of a pass are in flight together,
     // then the ballots place them in route order
     constexpr int U = 8;
@@ -131,6 +142,7 @@ __global__ __launch_bounds__(256) void dispatch_place_kernel(
                 const int p = pos + __popcll(m & ((1ull << lane) - 1ull));
                 sorted_route[p] = r;
                 if (route_pos) route_pos[r] = p;
+                if (packed) atomicOr(packed, (r / top_k) << (kTokenBits * (p - base)));
             }
             pos += __popcll(m);
         }
@@ -298,15 +310,19 @@ int grouped_max_tiles(int tokens, int top_k, int n_shared, int E, int tile_token
 hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
                            int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
                            int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,
-                           hipStream_t st) {
+                           hipStream_t st, int32_t *seg_tile, int top_k) {
     if (n_slots < 1 || n_slots > kMaxDispatchSlots) return hipErrorInvalidValue;
+    // tokens fit the packed field (and the tiles exist to hold it)
+    const int pack = seg_tile && tiles && top_k > 0 && R / top_k < (1 << kTokenBits) && tile_tokens > kPackedTokens;
+    if (!pack) seg_tile = nullptr;
     const size_t lds = sizeof(int32_t) * (n_slots + 1);
     hipLaunchKernelGGL(dispatch_count_kernel, dim3(1), dim3(kDispatchThreads), lds, st, route_slot, R,
-                       n_slots, n_shared_tokens, tile_tokens, seg_start, tiles, n_tiles, max_tiles, route_pos);
+                       n_slots, n_shared_tokens, tile_tokens, seg_start, tiles, n_tiles, max_tiles, route_pos,
+                       seg_tile, pack);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(dispatch_place_kernel, dim3((n_slots + 3) / 4), dim3(256), 0, st, route_slot, R,
-                       n_slots, seg_start, sorted_route, route_pos);
+                       n_slots, seg_start, sorted_route, route_pos, seg_tile, tiles, max_tiles, top_k > 0 ? top_k : 1);
     return hipGetLastError();
 }
 

@@ -28,6 +28,13 @@ __device__ __forceinline__ int tile_token(const TileArgs &ta, bool shared, int p
     return shared ? pos - ta.R : ta.sorted_route[pos] / ta.top_k;
 }
 
+// A routed tile of at most kPackedTokens positions carries its tokens in the
+// tile record's last field: kTokensPacked, then kTokenBits bits per position
+// (written by the dispatch; tokens below 2^kTokenBits).
+constexpr int kPackedTokens = 2;
+constexpr int kTokenBits = 15;
+constexpr int32_t kTokensPacked = static_cast<int32_t>(0x40000000);
+
 template <int BITS, bool BF16, int CPL, int LPR, int GPC, int TT>
 __device__ __forceinline__ void row_partial_multi(const RowData<CPL, GPC> &rd,
                                                   const XVec<BITS, BF16, CPL, GPC> (&xv)[TT],
@@ -270,7 +277,7 @@ hipError_t launch_grouped_kernels(int which, const GroupedKernelLaunch &L, hipSt
 hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
                            int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
                            int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,
-                           hipStream_t st);
+                           hipStream_t st, int32_t *seg_tile = nullptr, int top_k = 0);
 hipError_t launch_route_slots(const int32_t *idx, int R, int E, const int32_t *slot_of_expert,
                               int n_slots, int32_t *route_slot, hipStream_t st);
 hipError_t launch_combine(const uint16_t *y, const int32_t *route_pos, const uint16_t *shared_y,

@@ -26,7 +26,7 @@ constexpr int kSmallTile = 2;   // positions per small tile
 constexpr int kSmallRows = 32;  // rows per workgroup (2 tiles of 16)
 
 struct SmallTileInfo {
-    int slot, first, count;
+    int slot, first, count, packed;
     bool shared;
 };
 
@@ -37,6 +37,7 @@ __device__ __forceinline__ bool small_tile(const TileArgs &ta, int tile, int n_s
     t.slot = ta.tiles[4 * tile];
     t.first = ta.tiles[4 * tile + 1];
     t.count = ta.tiles[4 * tile + 2];
+    t.packed = ta.tiles[4 * tile + 3];
     t.shared = t.slot == -2;
     if (t.count <= 0 || t.count > kSmallTile) return false;
     return t.shared || (t.slot >= 0 && t.slot < n_slots && t.first >= 0 && t.first + t.count <= ta.R);
@@ -67,9 +68,16 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
     const int n0 = blockIdx.x * kSmallRows;
     const int wpr = K * BITS / 32, gpr = K / 64;
     const int waves = blockDim.x >> 6;   // = K / 512
+    // tokens from the tile record when the dispatch packed them there
+    static_assert(kSmallTile <= kPackedTokens, "small tiles carry packed tokens");
+    const bool packed = !shared && (ti.packed & kTokensPacked);
     int tok[kSmallTile];
 #pragma unroll
-    for (int p = 0; p < kSmallTile; ++p) tok[p] = tile_token(ta, shared, ti.first + min(p, count - 1));
+    for (int p = 0; p < kSmallTile; ++p) {
+        const int q = min(p, count - 1);
+        tok[p] = packed ? (ti.packed >> (kTokenBits * q)) & ((1 << kTokenBits) - 1)
+                        : tile_token(ta, shared, ti.first + q);
+    }
 
     // Raw x of the window of each position, the workgroup's scales and biases
     // by whole lines, then the weights in consumption order.
