@@ -32,6 +32,21 @@ class CacheResult(ctypes.Structure):
     ]
 
 
+class DPlanStats(ctypes.Structure):
+    _fields_ = [
+        ("hits", ctypes.c_uint64),
+        ("misses", ctypes.c_uint64),
+        ("evictions", ctypes.c_uint64),
+        ("calls", ctypes.c_uint64),
+        ("error", ctypes.c_int32),
+        ("probation", ctypes.c_int32),
+        ("protected_", ctypes.c_int32),
+        ("free_slots", ctypes.c_int32),
+        ("last_keys", ctypes.c_int32),
+        ("last_misses", ctypes.c_int32),
+    ]
+
+
 class QProj(ctypes.Structure):
     _fields_ = [
         ("weight", ctypes.c_void_p),
@@ -87,6 +102,16 @@ _SIGNATURES = {
     "locali_cache_peek": ([_P, _I], _I),
     "locali_cache_probation_size": ([_P], _I),
     "locali_cache_protected_size": ([_P], _I),
+    "locali_dplan_state_bytes": ([_I, _I, _I], _SZ),
+    "locali_dplan_lds_bytes": ([_I, _I, _I], _SZ),
+    "locali_dplan_init": ([_P, _SZ, _I, _I, _I, _I, _I, _P], ctypes.c_int),
+    "locali_dplan_plan": ([_P, _I, _I, _I, _I, _P, _I, _I, _I, _I, _I, _P, _P], ctypes.c_int),
+    "locali_dplan_fill": ([_P, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t), _I, _P, _I, _I,
+                           _I, _P], ctypes.c_int),
+    "locali_dplan_host_view": ([ctypes.POINTER(ctypes.c_void_p), _I, ctypes.POINTER(ctypes.c_uint64)],
+                               ctypes.c_int),
+    "locali_dplan_read": ([_P, ctypes.POINTER(DPlanStats), ctypes.POINTER(CacheResult), _I, _P], ctypes.c_int),
+    "locali_dplan_peek": ([_P, _I, _P], _I),
     # GPU (locali_moe.h)
     "locali_moe_workspace_bytes": ([_I, _I, _I, _I, _I, _I], _SZ),
     "locali_moe_router": ([ctypes.POINTER(Router), _P, _I, _I, _I, _P, _P, _P, _I, _P, _P, _P,

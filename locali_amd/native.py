@@ -125,3 +125,100 @@ class NativeCache:
 
     def __del__(self):
         self.close()
+
+
+class DevicePlanner:
+    """The planner's placement rules on the GPU (locali_dplan_*, see
+    include/locali_planner.h): the state lives in one device buffer and each
+    layer call is one kernel on the caller's current stream, so routing,
+    placement, fills and expert kernels queue without a host round trip.
+    Decisions equal NativeCache.plan_each's with the previous demand call's
+    slots pinned and the LFU token tick on layer-0 calls of at most top_k
+    experts (V4ArenaStore._place_keys)."""
+
+    LDS_LIMIT = 160 * 1024 - 4096   # the kernel's LDS less its static part
+
+    def __init__(self, key_capacity: int, slots: int, protected_capacity: int, *, n_experts: int,
+                 policy: str = "slru", max_routes: int = 16384, device=None):
+        import torch
+        from .ops import _stream
+        if policy not in POLICIES:
+            raise ValueError(f"unknown native cache policy: {policy}")
+        self._lib = _lib.lib()
+        self.key_capacity, self.slots, self.n_experts = key_capacity, slots, n_experts
+        self.policy = POLICIES[policy]
+        self.max_routes = max_routes
+        lds = self._lib.locali_dplan_lds_bytes(slots, n_experts, self.policy)
+        if lds > self.LDS_LIMIT:
+            raise ValueError(f"device planner: {slots} slots x {n_experts} experts need {lds} bytes of LDS "
+                             f"(at most {self.LDS_LIMIT}); use the host planner")
+        nbytes = self._lib.locali_dplan_state_bytes(key_capacity, slots, max_routes)
+        if not nbytes:
+            raise ValueError("device planner: bad shape")
+        self.state = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        if self.state.data_ptr() % 256:
+            raise RuntimeError("device planner state is not 256-byte aligned")
+        _lib.check(self._lib.locali_dplan_init(self.state.data_ptr(), nbytes, key_capacity, slots,
+                                                 protected_capacity, self.policy, max_routes, _stream()),
+                   "locali_dplan_init")
+        self._table = None
+
+    def plan(self, expert_idx, layer: int, top_k: int, *, touch_hits: bool = True, out=None):
+        """Slots of the routes in expert_idx (device int32, any shape) for
+        `layer`; returns a device int32 tensor of the same shape."""
+        import torch
+        from .ops import _stream
+        idx = expert_idx.reshape(-1)
+        if idx.dtype != torch.int32 or not idx.is_cuda:
+            raise ValueError("device planner: expert_idx must be a device int32 tensor")
+        idx = idx.contiguous()
+        if out is None:
+            out = torch.empty(idx.numel(), dtype=torch.int32, device=idx.device)
+        _lib.check(self._lib.locali_dplan_plan(self.state.data_ptr(), self.key_capacity, self.slots, self.policy,
+                                                 self.max_routes, idx.data_ptr(), idx.numel(), layer,
+                                                 self.n_experts, top_k, int(touch_hits), out.data_ptr(),
+                                                 _stream()),
+                   "locali_dplan_plan")
+        return out.view(expert_idx.shape)
+
+    def fill(self, table, host_src, layer: int, max_misses: int) -> None:
+        """Copy the last plan's misses into their slots. table: (bases,
+        per-slot bytes) of the arena arrays in record order; host_src: device
+        uint64 tensor of the key_capacity device-visible payload addresses."""
+        from .ops import _stream
+        if self._table is None or self._table[0] is not table:
+            base, per = table
+            self._table = (table, (ctypes.c_void_p * len(base))(*base), (ctypes.c_size_t * len(per))(*per),
+                           len(base))
+        _, bases, pers, n = self._table
+        _lib.check(self._lib.locali_dplan_fill(self.state.data_ptr(), bases, pers, n, host_src.data_ptr(), layer,
+                                                 self.n_experts, max_misses, _stream()),
+                   "locali_dplan_fill")
+
+    @staticmethod
+    def host_view(pointers) -> list[int]:
+        """Device-visible addresses of pinned host payloads (raises for any
+        that is not pinned and 16-byte aligned)."""
+        n = len(pointers)
+        src = (ctypes.c_void_p * max(n, 1))(*pointers)
+        out = (ctypes.c_uint64 * max(n, 1))()
+        _lib.check(_lib.lib().locali_dplan_host_view(src, n, out), "locali_dplan_host_view")
+        return list(out[:n])
+
+    def read(self, max_results: int = 0):
+        """(counters dict, per-key results of the last call); waits for the
+        current stream."""
+        from .ops import _stream
+        st = _lib.DPlanStats()
+        res = (_lib.CacheResult * max(max_results, 1))()
+        _lib.check(self._lib.locali_dplan_read(self.state.data_ptr(), ctypes.byref(st), res, max_results,
+                                                 _stream()),
+                   "locali_dplan_read")
+        counters = {f: getattr(st, f) for f, _ in _lib.DPlanStats._fields_}
+        n = min(max_results, st.last_keys)
+        return counters, [CacheResult(r.key, r.slot, r.evicted_key, bool(r.hit), bool(r.placed))
+                          for r in res[:n]]
+
+    def peek(self, key: int) -> int:
+        from .ops import _stream
+        return int(self._lib.locali_dplan_peek(self.state.data_ptr(), key, _stream()))

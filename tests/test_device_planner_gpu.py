@@ -1,0 +1,130 @@
+"""Device-resident planner (locali_dplan_*) against the host planner.
+
+The same call sequence goes through NativeCache.plan_each with the calling
+convention of V4ArenaStore._place_keys (the previous demand call's slots
+pinned, hits touched, the LFU token tick before layer-0 calls of at most
+top_k experts) and through DevicePlanner.plan on the GPU; every per-key
+result (key, slot, evicted key, hit, placed), every route's slot and the
+counters must be identical. The host planner is pinned separately against
+the reference planner's traces (test_planner_*.py), so equality here carries
+that parity to the device. The fill kernel's copies are checked byte for
+byte against the pinned payloads.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from locali_amd.native import DevicePlanner, NativeCache
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda")
+
+
+def zipf_calls(rng, n_calls, layers, E, top_k, multi_every=0):
+    """(layer, expert ids of one call's routes) with Zipf-skewed experts per
+    layer; every multi_every-th call carries three tokens (duplicates)."""
+    ranks = [rng.permutation(E) for _ in range(layers)]
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    calls = []
+    for c in range(n_calls):
+        layer = c % layers
+        tokens = 3 if multi_every and c % multi_every == multi_every - 1 else 1
+        routes = []
+        for _ in range(tokens):
+            routes.extend(int(ranks[layer][i]) for i in rng.choice(E, size=top_k, replace=False, p=p))
+        calls.append((layer, routes))
+    return calls
+
+
+def host_run(calls, layers, E, slots, pcap, policy, top_k):
+    cache = NativeCache(layers * E, slots, pcap, policy=policy)
+    pinned = ()
+    out = []
+    for layer, routes in calls:
+        want = list(dict.fromkeys(routes))
+        if layer == 0 and len(want) <= top_k:
+            cache.note_token()
+        res = cache.plan_each([layer * E + e for e in want], pinned_slots=pinned, touch_hits=True)
+        pinned = tuple(r.slot for r in res if r.placed)
+        out.append(res)
+    return out
+
+
+@pytest.mark.parametrize("policy,slots,pcap,multi", [
+    ("slru", 40, 12, 0),
+    ("slru", 40, 0, 0),
+    ("slru", 64, 20, 4),
+    ("lfu-decay", 40, 0, 0),
+    ("lfu-decay", 64, 0, 5),
+])
+def test_device_planner_matches_host_planner(policy, slots, pcap, multi):
+    layers, E, top_k, n_calls = 5, 64, 6, 400
+    rng = np.random.default_rng(slots * 7 + pcap + multi)
+    calls = zipf_calls(rng, n_calls, layers, E, top_k, multi)
+    expect = host_run(calls, layers, E, slots, pcap, policy, top_k)
+    dp = DevicePlanner(layers * E, slots, pcap, n_experts=E, policy=policy, max_routes=64, device=DEV)
+    hits = misses = evictions = 0
+    for c, ((layer, routes), want_res) in enumerate(zip(calls, expect)):
+        idx = torch.tensor(routes, dtype=torch.int32, device=DEV)
+        rs = dp.plan(idx, layer, top_k)
+        counters, got = dp.read(max_results=len(want_res))
+        assert counters["error"] == 0, (c, counters)
+        assert [(r.key, r.slot, r.evicted_key, r.hit, r.placed) for r in got] == \
+               [(r.key, r.slot, r.evicted_key, r.hit, r.placed) for r in want_res], f"call {c} layer {layer}"
+        slot_of = {r.key - layer * E: r.slot for r in want_res}
+        assert rs.cpu().tolist() == [slot_of[e] for e in routes], f"route slots of call {c}"
+        hits += sum(r.hit for r in want_res)
+        misses += sum(not r.hit for r in want_res)
+        evictions += sum(r.evicted_key >= 0 for r in want_res)
+    counters, _ = dp.read()
+    assert (counters["hits"], counters["misses"], counters["evictions"], counters["calls"]) == \
+           (hits, misses, evictions, n_calls)
+    assert evictions > 50        # the arena is small enough to churn
+
+
+def test_device_planner_placement_failure_matches_host():
+    """A tier with fewer unpinned slots than a call needs: the keys the host
+    planner cannot place come back unplaced, their routes get slot 0 and the
+    sticky error is set; the rest is identical."""
+    layers, E, top_k = 2, 32, 6
+    slots = 9                       # 8 usable: six pinned by the previous call leave two
+    calls = [(0, [0, 1, 2, 3, 4, 5]), (1, [6, 7, 8, 9, 10, 11])]
+    expect = host_run(calls, layers, E, slots, 0, "slru", top_k)
+    assert not all(r.placed for r in expect[1])
+    dp = DevicePlanner(layers * E, slots, 0, n_experts=E, policy="slru", max_routes=16, device=DEV)
+    for (layer, routes), want_res in zip(calls, expect):
+        rs = dp.plan(torch.tensor(routes, dtype=torch.int32, device=DEV), layer, top_k)
+        counters, got = dp.read(max_results=len(want_res))
+        assert [(r.key, r.slot, r.evicted_key, r.hit, r.placed) for r in got] == \
+               [(r.key, r.slot, r.evicted_key, r.hit, r.placed) for r in want_res]
+        placed = {r.key - layer * E: (r.slot if r.placed else 0) for r in want_res}
+        assert rs.cpu().tolist() == [placed[e] for e in routes]
+    assert counters["error"] == 2     # LOCALI_DPLAN_E_PLACE
+
+
+def test_device_planner_fill_copies_each_miss():
+    """Three records per expert of unequal sizes; after every call each
+    resident slot of the routed experts holds its expert's payload."""
+    layers, E, top_k, slots = 3, 16, 4, 12
+    sizes = [4096, 256, 1024]                   # bytes per slot of each record
+    total = sum(sizes)
+    payload = torch.randint(0, 256, (layers * E, total), dtype=torch.uint8).pin_memory()
+    arrays = [torch.zeros(slots, s, dtype=torch.uint8, device=DEV) for s in sizes]
+    table = ([a.data_ptr() for a in arrays], sizes)
+    ptrs = DevicePlanner.host_view([payload[k].data_ptr() for k in range(layers * E)])
+    host_src = torch.tensor(ptrs, dtype=torch.uint64, device=DEV)
+    dp = DevicePlanner(layers * E, slots, 3, n_experts=E, policy="slru", max_routes=16, device=DEV)
+    rng = np.random.default_rng(5)
+    for c in range(60):
+        layer = c % layers
+        routes = [int(e) for e in rng.choice(E, size=top_k, replace=False)]
+        rs = dp.plan(torch.tensor(routes, dtype=torch.int32, device=DEV), layer, top_k)
+        dp.fill(table, host_src, layer, len(routes))
+        got = torch.cat([a[rs.long()].cpu() for a in arrays], dim=1)
+        want = payload[[layer * E + e for e in routes]]
+        assert torch.equal(got, want), f"call {c}"
+    counters, _ = dp.read()
+    assert counters["error"] == 0 and counters["evictions"] > 0
