@@ -27,8 +27,9 @@ Also reported:
                 and 4-bit down projections, uniform routing: tokens/s and GB/s
   stack43       a 43-layer stack of full-width layers decoding through one
                 bounded arena (96 usable slots per layer, 4129 slots, 32.5 GB):
-                the compiled SLRU planner (and LFU-decay) picks evictions,
-                misses are copied from pinned host memory on the fill stream;
+                the compiled SLRU planner (and LFU-decay) picks evictions on
+                the host, or the same planner on the GPU (no per-layer host
+                round trip), misses copied from pinned host memory;
                 Zipf(1.1) routing with AR(1) cross-layer noise (rho 0.6);
                 hit rate, bytes moved, tokens/s and host -> HBM GB/s
   cpu_baseline  the C oracle (oracle/expert_ref.c, OpenMP) on the host cores
@@ -276,7 +277,7 @@ def mixed_run(dev, tokens, calls, seed):
 
 
 def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetch_k=None,
-              lookahead_rho=LOOKAHEAD_RHO):
+              lookahead_rho=LOOKAHEAD_RHO, device_planner=False):
     """Decode through a stack of full-width layers sharing one bounded arena,
     misses copied from pinned host memory (V4ArenaStore host_source).
 
@@ -288,7 +289,11 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetc
 
     prefetch_k: each layer also routes its input through the next layer's
     gate and prefetches that call's prefetch_k highest-weight experts
-    (cross-layer prefetch at depth 1)."""
+    (cross-layer prefetch at depth 1).
+
+    device_planner: the planner runs on the GPU (same decisions), so a
+    layer's router, planner, fills and expert kernels queue on the stream
+    with no per-layer host round trip."""
     import tempfile
     from locali_amd.dsv4_arena import V4ArenaMoE, V4ArenaStore, V4Gate
     tmp = tempfile.TemporaryDirectory()
@@ -300,7 +305,7 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetc
     del payload
     n_slots = layers * per_layer + 1
     store = V4ArenaStore(index, ceiling_gb=n_slots * EXPERT_BYTES / 1e9 + 1e-6, threads=1,
-                         cache_policy=policy, device=dev,
+                         cache_policy=policy, device=dev, device_planner=device_planner,
                          host_source=lambda layer, e: host[e])
     shared = synth.expert_arena(layers, D, DFF, bits_gate_up=BITS, group=GROUP, dtype=torch.bfloat16,
                                 seed=seed + 1, device=dev, zero_slot=False)
@@ -342,9 +347,7 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetc
             for layer in range(layers):
                 mods[layer](X[t, layer:layer + 1])
     torch.cuda.synchronize()
-    store.hits = store.misses = store.evictions = store.bytes_read = 0
-    store.prefetched = store.prefetch_used = store.prefetch_wasted = 0
-    store.t_stall = 0.0
+    store.reset_stats()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     with torch.cuda.stream(compute):
@@ -364,6 +367,7 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetc
     moved = st["bytes_read"]
     return {"layers": layers, "slots": n_slots, "usable_slots_per_layer": per_layer,
             "arena_GB": n_slots * EXPERT_BYTES / 1e9, "cache_policy": policy,
+            "planner": "device" if device_planner else "host",
             "prefetch": (None if not prefetch_k else
                          {"depth": 1, "top": prefetch_k, "prefetched": st["prefetched"],
                           "used": st["prefetch_used"], "wasted": st["prefetch_wasted"]}),
@@ -541,6 +545,8 @@ def main(argv=None):
     ap.add_argument("--stack-prefetch", default="5",
                     help="comma-separated prefetch widths for extra slru-all stack legs with "
                          "cross-layer prefetch at depth 1 (0: none)")
+    ap.add_argument("--stack-device-planner", default="slru-all,lfu-decay",
+                    help="comma-separated cache policies for extra stack legs planned on the GPU")
     ap.add_argument("--stack-lookahead-rho", type=float, default=LOOKAHEAD_RHO,
                     help="correlation of the stack's lookahead routing with the next layer's")
     ap.add_argument("--skip-cpu", action="store_true")
@@ -657,6 +663,11 @@ def main(argv=None):
             phase(f"43-layer bounded arena, {policy}")
             result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, policy,
                                                args.seed + 300, lookahead_rho=args.stack_lookahead_rho))
+        for policy in (v for v in args.stack_device_planner.split(",") if v.strip()):
+            phase(f"43-layer bounded arena, {policy}, device planner")
+            result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, policy,
+                                               args.seed + 300, lookahead_rho=args.stack_lookahead_rho,
+                                               device_planner=True))
         for k in (int(v) for v in args.stack_prefetch.split(",") if v.strip() and int(v)):
             phase(f"43-layer bounded arena, slru-all, prefetch top-{k} at depth 1")
             result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, "slru-all",

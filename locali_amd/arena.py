@@ -634,6 +634,12 @@ class ArenaStore:
                 f.result()
         self.t_stall += time.perf_counter() - t0
 
+    def reset_stats(self):
+        """Zero the hit, miss, eviction, byte, stall and prefetch counters."""
+        self.hits = self.misses = self.evictions = self.bytes_read = 0
+        self.prefetched = self.prefetch_used = self.prefetch_wasted = 0
+        self.t_stall = 0.0
+
     def stats(self):
         n = self.hits + self.misses
         return {"hits": self.hits, "misses": self.misses, "hit_rate": self.hits / n if n else 0.0,
@@ -785,6 +791,13 @@ class ArenaMoE:
         if reads is not None:
             self.store.wait(reads[t])
         slots = self._device_slots([[placed[e][1] for e in row] for row in ii], flat.device)
+        return self._run_experts(t, flat, slots, gates, dtype)
+
+    def _run_experts(self, t, flat, slots, gates, dtype):
+        """Tier t's expert kernels over device route slots [T, k]: the decode
+        kernels up to two tokens, the slot-grouped kernels beyond."""
+        from . import ops
+        T = flat.shape[0]
         arena = self.store.expert_arena(t)
         x_in = flat.contiguous()
         if x_in.dtype == torch.bfloat16 and self.store.use_f16(t):

@@ -30,14 +30,19 @@ import torch
 
 from . import ops
 from .arena import PROJS, ArenaMoE, ArenaStore, ReadPlan
-from .native import NativeCache
+from .native import DevicePlanner, NativeCache
 
 
 class V4ArenaStore(ArenaStore):
     """The arena with V4 affine quantisation metadata validated and the
     compiled planner per tier over layers * E keys (key = layer * E + e)."""
 
-    def __init__(self, index_path, native_scheduler=True, **kwargs):
+    def __init__(self, index_path, native_scheduler=True, device_planner=False, **kwargs):
+        """device_planner: plan on the GPU (native.DevicePlanner) with the
+        compiled planner's rules and fill misses from host_source's pinned
+        payloads in the same stream, so that V4ArenaMoE calls never wait for
+        the host (one tier, host_source required, no cross-layer prefetch;
+        counters are read from the device by stats())."""
         config = json.loads(Path(index_path).read_text())
         self.expert_quant = config.get("quantization", {})
         for tier, q in self.expert_quant.items():
@@ -54,6 +59,17 @@ class V4ArenaStore(ArenaStore):
                                                     self.protected_cap[t], policy=policy)
         elif self.cache_policy == "lfu-decay":
             raise RuntimeError("lfu-decay requires the compiled planner")
+        self.dplan = None
+        if device_planner:
+            if not native_scheduler:
+                raise ValueError("the device planner follows the compiled planner (native_scheduler=True)")
+            if len(self.tiers) != 1 or self.host_source is None:
+                raise ValueError("the device planner covers one expert tier filled from host_source")
+            t = self.tiers[0]
+            self.dplan = DevicePlanner(self.layers * self.E, self.slots[t], self.protected_cap[t],
+                                       n_experts=self.E, policy=policy, device=self.device)
+            self._dplan_src = None
+            self._dplan_base = None
 
     def _key_id(self, key):
         layer, expert = key
@@ -187,15 +203,55 @@ class V4ArenaStore(ArenaStore):
             self.pf_keys.update((layer, e) for e, _ in issued)
         return out, plan
 
-    def _protected_size(self, t):
-        if t in self.native_caches:
-            return self.native_caches[t].protected_size
-        return super()._protected_size(t)
+    def _dplan_sources(self, t):
+        """Device table of every key's pinned payload address (built once;
+        the payloads are held for the store's life)."""
+        if self._dplan_src is None:
+            keep = [self._host_bytes((layer, e), t) for layer in range(self.layers) for e in range(self.E)]
+            ptrs = DevicePlanner.host_view([src.data_ptr() for src in keep])
+            self._dplan_keep = keep
+            self._dplan_src = torch.tensor(ptrs, dtype=torch.int64, device=self.device)
+        return self._dplan_src
+
+    def device_plan(self, layer, expert_idx):
+        """Route slots [T, k] of one demand call planned on the device, the
+        call's misses queued as fills behind it on the current stream."""
+        t = self.tiers[0]
+        src = self._dplan_sources(t)
+        slots = self.dplan.plan(expert_idx, layer, self.top_k)
+        self.dplan.fill(self._slot_table(t), src, layer, expert_idx.numel())
+        return slots
+
+    def _dplan_counters(self):
+        c, _ = self.dplan.read()
+        if c["error"]:
+            what = {1: "a route's expert outside the layer", 2: "a demanded expert found no unpinned slot",
+                    3: "plan arguments disagree with the planner state"}.get(c["error"], c["error"])
+            raise RuntimeError(f"device planner: {what}")
+        return c
+
+    def reset_stats(self):
+        super().reset_stats()
+        if self.dplan is not None:
+            self._dplan_base = self._dplan_counters()
 
     def stats(self):
         st = super().stats()
         st["scheduler"] = "c" if self.native_caches else "python"
+        if self.dplan is not None:
+            c = self._dplan_counters()
+            base = self._dplan_base or {k: 0 for k in c}
+            hits, misses = c["hits"] - base["hits"], c["misses"] - base["misses"]
+            st.update(hits=hits, misses=misses, hit_rate=hits / (hits + misses) if hits + misses else 0.0,
+                      evictions=c["evictions"] - base["evictions"],
+                      bytes_read=misses * self.item[self.tiers[0]], scheduler="device",
+                      protected={self.tiers[0]: c["protected_"]})
         return st
+
+    def _protected_size(self, t):
+        if t in self.native_caches:
+            return self.native_caches[t].protected_size
+        return super()._protected_size(t)
 
     def close(self):
         for c in self.native_caches.values():
@@ -264,6 +320,24 @@ class V4ArenaMoE(ArenaMoE):
 
     def route(self, x, input_ids=None):
         return self.gate(x, input_ids)
+
+    def __call__(self, x, input_ids=None):
+        """With the store's device planner the call queues router, planner,
+        fills and experts on the current stream and returns without waiting
+        for the device; otherwise ArenaMoE's host-planned call."""
+        if self.store.dplan is None:
+            return super().__call__(x, input_ids)
+        if self.nxt is not None or self.nxt2 is not None:
+            raise ValueError("cross-layer prefetch plans on the host; the device planner does not take it")
+        shape = x.shape
+        flat = x.reshape(-1, shape[-1])
+        if flat.shape[0] == 0:
+            return torch.zeros(shape, dtype=x.dtype, device=x.device)
+        inds, gates = self.route(x, input_ids)
+        T = flat.shape[0]
+        slots = self.store.device_plan(self.layer, inds.reshape(T, self.top_k))
+        out = self._run_experts(self.store.tiers[0], flat, slots, gates.reshape(T, self.top_k), x.dtype)
+        return out.reshape(shape).to(x.dtype)
 
 
 __all__ = ["V4ArenaStore", "V4ArenaMoE", "V4Gate", "PROJS"]

@@ -176,7 +176,8 @@ class _Stack:
     pinned host memory; routing by the router kernel on an identity gate, x
     carrying Zipf(1.1) logits with AR(1) cross-layer noise (rho 0.6)."""
 
-    def __init__(self, tmp_path, layers, per_layer, policy, seed, steps, predict_next=False):
+    def __init__(self, tmp_path, layers, per_layer, policy, seed, steps, predict_next=False,
+                 device_planner=False):
         from locali_amd.dsv4_arena import V4ArenaMoE, V4ArenaStore, V4Gate
         self.layers = layers
         index = tmp_path / "stack.idx"
@@ -186,7 +187,7 @@ class _Stack:
         self.host = synth.host_payloads(self.payload)
         item = self.host.shape[1]
         self.store = V4ArenaStore(index, ceiling_gb=(layers * per_layer + 1) * item / 1e9 + 1e-6,
-                                  threads=1, cache_policy=policy, device=DEV,
+                                  threads=1, cache_policy=policy, device=DEV, device_planner=device_planner,
                                   host_source=lambda layer, e: self.host[1 + e % PAYLOADS])
         sh = synth.expert_arena(layers, D, DFF, bits_gate_up=2, group=GROUP, dtype=torch.bfloat16,
                                 seed=seed + 1, device=DEV, zero_slot=False)
@@ -257,6 +258,28 @@ def test_bounded_stack_full_width_host_fills(tmp_path, oracle_lib, policy):
         assert st["bytes_read"] == st["misses"] * stack.store.item["cold"]
     finally:
         stack.close()
+
+
+@pytest.mark.parametrize("policy", ["slru-all", "lfu-decay"])
+def test_bounded_stack_device_planner_equals_host_planner(tmp_path, policy):
+    """The same four-layer stack planned on the GPU (V4ArenaStore
+    device_planner=True: router, planner, fills and experts queued with no
+    host round trip): every layer call equals the resident weights bit for
+    bit, and hits, misses, evictions and bytes equal the host-planned run's."""
+    banner(f"full-width bounded stack, device planner, policy={policy}")
+    steps = 16
+    counts = []
+    for device_planner in (False, True):
+        stack = _Stack(tmp_path, layers=4, per_layer=12, policy=policy, seed=500, steps=steps,
+                       device_planner=device_planner)
+        try:
+            _run_stack(stack, steps)
+            st = stack.store.stats()
+            counts.append((st["hits"], st["misses"], st["evictions"], st["bytes_read"]))
+        finally:
+            stack.close()
+    assert counts[0] == counts[1]
+    assert counts[0][1] > 0 and counts[0][2] > 0
 
 
 def test_cross_layer_prefetch_is_exact_and_accounted(tmp_path):
