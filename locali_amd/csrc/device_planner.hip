@@ -275,7 +275,10 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     const PlanLds L = carve(plds, n_slots, E, lfu);
     const int kbase = layer * E;
 
-    // ---- state into LDS
+    // ---- state into LDS; the first routes and pins travel with it
+    const int n_pinned_prev = H->n_pinned;
+    const int my_e = tid < routes ? idx[tid] : -1;
+    const int my_pin = tid < n_pinned_prev ? g_pinned[tid] : 0;
     for (int s = tid; s < n_slots; s += kPlanThreads) {
         const int k = g_owner[s];
         L.owner[s] = k;
@@ -297,11 +300,16 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     if (tid == 0) sh.bad = 0;
     __syncthreads();
 
-    // ---- the routes' experts in first-appearance order
+    // ---- the routes' experts in first-appearance order; the previous
+    // demand call's slots pinned
     for (int r = tid; r < routes; r += kPlanThreads) {
-        const int e = idx[r];
+        const int e = r < kPlanThreads ? my_e : idx[r];
         if (e >= 0 && e < E) atomicMin(&L.first[e], r);
         else sh.bad = 1;
+    }
+    for (int j = tid; j < n_pinned_prev; j += kPlanThreads) {
+        const int s = j < kPlanThreads ? my_pin : g_pinned[j];
+        if (s > 0 && s < n_slots) L.pin[s] = 1;
     }
     __syncthreads();
     int carry = 0;
@@ -310,7 +318,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
         int e = -1;
         bool head = false;
         if (r < routes) {
-            e = idx[r];
+            e = r0 == 0 ? my_e : idx[r];
             head = e >= 0 && e < E && L.first[e] == r;
         }
         const uint64_t m = __ballot(head);
@@ -324,11 +332,6 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
         for (int w = 0; w < kPlanWaves; ++w) total += sh.wave_count[w];
         carry += total;
         __syncthreads();
-    }
-    const int n_pinned_prev = H->n_pinned;
-    for (int j = tid; j < n_pinned_prev; j += kPlanThreads) {
-        const int s = g_pinned[j];
-        if (s > 0 && s < n_slots) L.pin[s] = 1;
     }
     if (tid == 0) {
         sh.n_want = carry;
