@@ -282,6 +282,34 @@ def test_bounded_stack_device_planner_equals_host_planner(tmp_path, policy):
     assert counts[0][1] > 0 and counts[0][2] > 0
 
 
+def test_device_planner_prefill_batches_equal_host_planner(tmp_path):
+    """Multi-token calls (16 tokens per layer: the routes are planned on the
+    device and the grouped kernels read its slot table) give the same
+    outputs, bit for bit, and the same counters as the host-planned store."""
+    banner("full-width bounded stack, 16-token calls, device planner")
+    steps = 16
+    outs, counts = [], []
+    for device_planner in (False, True):
+        stack = _Stack(tmp_path, layers=4, per_layer=64, policy="slru-all", seed=520, steps=steps,
+                       device_planner=device_planner)
+        try:
+            got = []
+            for rep in range(2):
+                for layer in range(stack.layers):
+                    # twice in a row: the second call hits what the first placed
+                    got.append(stack.mods[layer](stack.X[:, layer]))
+                    got.append(stack.mods[layer](stack.X[:, layer]))
+            torch.cuda.synchronize()
+            outs.append(got)
+            st = stack.store.stats()
+            counts.append((st["hits"], st["misses"], st["evictions"], st["bytes_read"]))
+        finally:
+            stack.close()
+    assert counts[0] == counts[1] and counts[0][0] > 0 and counts[0][1] > 0
+    for i, (a, b) in enumerate(zip(*outs)):
+        assert torch.equal(a, b), f"call {i}"
+
+
 def test_cross_layer_prefetch_is_exact_and_accounted(tmp_path):
     """The reference's cross-layer prefetch (arena.py:520-541, wired by
     dsv4_engine.py:237-246): each layer's call also routes the next layer's
