@@ -494,7 +494,7 @@ def summarize_trace(trace_csv, phases_json):
     unassigned = 0
     for r in csv.DictReader(open(trace_csv)):
         t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
-        name = r["Kernel_Name"].split("(")[0].replace("void ", "")
+        name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
         for ph, a, b in bounds:
             if a <= t0 < b:
                 per[ph].setdefault(name, []).append((t1 - t0) / 1e3)
