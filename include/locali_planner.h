@@ -16,7 +16,6 @@
 #define LOCALI_PLANNER_H
 
 #include "locali_core.h"
-#include "locali_moe.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -87,16 +86,6 @@ int locali_dplan_init(void *state, size_t state_bytes, int32_t key_capacity, int
 int locali_dplan_plan(void *state, int32_t key_capacity, int32_t slots, int32_t policy, int32_t max_routes,
                       const int32_t *expert_idx, int32_t routes, int32_t layer, int32_t n_experts, int32_t top_k,
                       int32_t touch_hits, int32_t *route_slot, void *stream);
-/* locali_moe_router's logits kernel followed by one locali_dplan_plan call
- * whose routes are the router's selection, made inside the planner kernel
- * (one launch less per layer): writes idx and weights as locali_moe_router
- * does (the gemv path: at most 8 tokens, n_experts <= 256) and the routes'
- * slots as locali_dplan_plan. workspace as locali_moe_router's. */
-int locali_dplan_route_plan(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens,
-                            int32_t d_model, const int32_t *input_ids, int32_t *idx, float *weights,
-                            void *workspace, size_t workspace_bytes, void *state, int32_t key_capacity,
-                            int32_t slots, int32_t policy, int32_t max_routes, int32_t layer,
-                            int32_t touch_hits, int32_t *route_slot, void *stream);
 int locali_dplan_fill(const void *state, void *const *dst_base, const size_t *slot_bytes, int32_t n_arrays,
                       const uint64_t *host_src, int32_t layer, int32_t n_experts, int32_t max_misses,
                       void *stream);

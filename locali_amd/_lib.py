@@ -106,8 +106,6 @@ _SIGNATURES = {
     "locali_dplan_lds_bytes": ([_I, _I, _I], _SZ),
     "locali_dplan_init": ([_P, _SZ, _I, _I, _I, _I, _I, _P], ctypes.c_int),
     "locali_dplan_plan": ([_P, _I, _I, _I, _I, _P, _I, _I, _I, _I, _I, _P, _P], ctypes.c_int),
-    "locali_dplan_route_plan": ([ctypes.POINTER(Router), _P, _I, _I, _I, _P, _P, _P, _P, _SZ, _P, _I, _I, _I, _I,
-                                 _I, _I, _P, _P], ctypes.c_int),
     "locali_dplan_fill": ([_P, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t), _I, _P, _I, _I,
                            _I, _P], ctypes.c_int),
     "locali_dplan_host_view": ([ctypes.POINTER(ctypes.c_void_p), _I, ctypes.POINTER(ctypes.c_uint64)],

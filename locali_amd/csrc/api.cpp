@@ -511,28 +511,6 @@ int locali_moe_router(const locali_router *router, const void *x, int32_t x_dtyp
                  weights, route_slot, workspace, lay, S(stream));
 }
 
-int locali_dplan_route_plan(const locali_router *router, const void *x, int32_t x_dtype, int32_t tokens,
-                            int32_t d_model, const int32_t *input_ids, int32_t *idx, float *weights,
-                            void *workspace, size_t workspace_bytes, void *state, int32_t key_capacity,
-                            int32_t slots, int32_t policy, int32_t max_routes, int32_t layer,
-                            int32_t touch_hits, int32_t *route_slot, void *stream) {
-    if (tokens == 0) return 0;   // an empty batch is a no-op
-    int rc;
-    if ((rc = check_router(router, d_model))) return rc;
-    if (tokens < 1 || !x || !dtype16(x_dtype) || !idx || !weights || !workspace || !state || !route_slot)
-        return fail(LOCALI_E_ARG, "dplan_route_plan: bad tokens/x/outputs/workspace/state");
-    const Layout lay = layout(tokens, d_model, 1, router->n_experts, router->top_k, 0);
-    if (workspace_bytes < lay.route_slot)
-        return fail(LOCALI_E_WORKSPACE, "dplan_route_plan: workspace %zu < %zu bytes", workspace_bytes,
-                    lay.route_slot);
-    RouterLaunch RL{};
-    if ((rc = route(router, x, x_dtype, tokens, d_model, input_ids, nullptr, nullptr, 0, idx, weights, nullptr,
-                    workspace, lay, S(stream), /*logits_only=*/true, &RL)))
-        return rc;
-    return dplan_select_launch(RL, state, key_capacity, slots, policy, max_routes, layer, touch_hits, route_slot,
-                               S(stream));
-}
-
 int locali_moe_dispatch(const int32_t *route_slot, int32_t tokens, int32_t top_k, int32_t n_slots,
                         int32_t *sorted_route, int32_t *seg_start, void *stream) {
     if (tokens == 0) return 0;   // an empty batch is a no-op

@@ -23,12 +23,6 @@
 // the slot of every route, the fill list (the call's misses) and the
 // per-key results are written, and the LDS state goes back to device memory.
 //
-// The routing variant (dplan_select_kernel, decode batches of at most
-// kFusedSelectMaxTokens tokens) takes the router's logits instead of the
-// routes: its first waves select each token's top-k (the router's own
-// selection, router_select.hpp) and write the routes and weights, while the
-// other waves load the planner state; then the call plans as above.
-//
 // dplan_fill_kernel copies each miss of the last call from its pinned host
 // payload (the expert's records back to back) into its slot, reading the
 // host memory over PCIe itself; workgroups past the miss count return.
@@ -41,7 +35,6 @@
 
 #include "locali_moe.h"
 #include "locali_planner.h"
-#include "router_select.hpp"
 
 namespace locali {
 int set_error(int code, const char *msg);
@@ -56,10 +49,6 @@ constexpr int kFillUnits = 8;                  // 16-byte units per thread
 constexpr uint8_t kNowhere = 0, kProbation = 1, kProtected = 2;
 constexpr size_t kPlanMaxLds = 160 * 1024;
 constexpr size_t kPlanMaxDynamicLds = kPlanMaxLds - 4096;   // the rest is the kernel's static LDS
-// The routing variant's static LDS also holds one selection stage per token.
-constexpr int kSelectM = 4;                                  // experts per lane: E <= 256
-constexpr size_t kPlanSelectStage = sizeof(float2) * locali::kFusedSelectMaxTokens * 64 * kSelectM;
-constexpr size_t kPlanMaxDynamicLdsSelect = kPlanMaxDynamicLds - kPlanSelectStage - 1024;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -257,35 +246,19 @@ struct Planner {
 };
 
 // The planner's shape travels in the arguments (the launch sized its LDS by
-// them); a state whose header disagrees is left alone and marked. SELECT:
-// the routes come from the selection over sel's logits (sel.tokens tokens,
-// routes = sel.tokens * top_k), not from idx.
-template <bool SELECT>
+// them); a state whose header disagrees is left alone and marked.
 __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__restrict__ state, int n_keys,
                                                              int n_slots, int policy, int max_routes,
                                                              const int32_t *__restrict__ idx, int routes,
                                                              int layer, int E, int top_k, int touch_hits,
-                                                             int32_t *__restrict__ route_slot,
-                                                             locali::RouterLaunch sel) {
+                                                             int32_t *__restrict__ route_slot) {
     extern __shared__ __align__(16) unsigned char plds[];
     __shared__ PlanShared sh;
-    __shared__ float2 stage[SELECT ? locali::kFusedSelectMaxTokens : 1][SELECT ? 64 * kSelectM : 1];
-    __shared__ int32_t sel_routes[SELECT ? locali::kFusedSelectMaxTokens * 16 : 1];
     DPlanHeader *H = reinterpret_cast<DPlanHeader *>(state);
     const int tid = threadIdx.x;
     if (H->n_keys != n_keys || H->n_slots != n_slots || H->policy != policy || H->max_routes != max_routes) {
         if (tid == 0 && !H->error) H->error = LOCALI_DPLAN_E_CONFIG;
         return;
-    }
-    if constexpr (SELECT) {
-        // one wave per token: its top-k, the routes and weights the experts read
-        const int wave = tid >> 6, lane = tid & 63;
-        if (wave < sel.tokens) {
-            const locali::SelectOut o = locali::select_token_any<1, kSelectM>(
-                sel, wave, sel.logits + static_cast<int64_t>(wave) * sel.E, 0, stage[wave], sel.top_k);
-            locali::select_store(sel, wave, o);
-            if (lane < sel.top_k) sel_routes[wave * sel.top_k + lane] = o.e;
-        }
     }
     const bool lfu = policy == LOCALI_CACHE_LFU_DECAY;
     const DPlanLayout G = dplan_layout(n_keys, n_slots, max_routes);
@@ -304,10 +277,8 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
 
     // ---- state into LDS; the first routes and pins travel with it
     const int n_pinned_prev = H->n_pinned;
-    int my_e = !SELECT && tid < routes ? idx[tid] : -1;
+    const int my_e = tid < routes ? idx[tid] : -1;
     const int my_pin = tid < n_pinned_prev ? g_pinned[tid] : 0;
-    // route r's expert (the selection's routes are all below kPlanThreads)
-    auto route_at = [&](int r) { return SELECT ? sel_routes[r] : (r < kPlanThreads ? my_e : idx[r]); };
     for (int s = tid; s < n_slots; s += kPlanThreads) {
         const int k = g_owner[s];
         L.owner[s] = k;
@@ -328,12 +299,11 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     }
     if (tid == 0) sh.bad = 0;
     __syncthreads();
-    if constexpr (SELECT) my_e = tid < routes ? sel_routes[tid] : -1;
 
     // ---- the routes' experts in first-appearance order; the previous
     // demand call's slots pinned
     for (int r = tid; r < routes; r += kPlanThreads) {
-        const int e = route_at(r);
+        const int e = r < kPlanThreads ? my_e : idx[r];
         if (e >= 0 && e < E) atomicMin(&L.first[e], r);
         else sh.bad = 1;
     }
@@ -348,7 +318,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
         int e = -1;
         bool head = false;
         if (r < routes) {
-            e = route_at(r);
+            e = r0 == 0 ? my_e : idx[r];
             head = e >= 0 && e < E && L.first[e] == r;
         }
         const uint64_t m = __ballot(head);
@@ -541,7 +511,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
 
     // ---- outputs and state back to device memory
     for (int r = tid; r < routes; r += kPlanThreads) {
-        const int x = route_at(r);
+        const int x = idx[r];
         route_slot[r] = (x >= 0 && x < E) ? L.eslot[x] : 0;
     }
     for (int s = tid; s < n_slots; s += kPlanThreads) {
@@ -655,52 +625,7 @@ int dhip(hipError_t e, const char *where) {
     return dfail(LOCALI_E_HIP, "%s: %s", where, hipGetErrorString(e));
 }
 
-template <bool SELECT>
-int plan_launch(void *state, int32_t key_capacity, int32_t slots, int32_t policy, int32_t max_routes,
-                const int32_t *expert_idx, int32_t routes, int32_t layer, int32_t n_experts, int32_t top_k,
-                int32_t touch_hits, int32_t *route_slot, const locali::RouterLaunch &sel, hipStream_t st) {
-    if (!state || !route_slot || routes < 0 || routes > max_routes || n_experts < 1 ||
-        n_experts > LOCALI_DPLAN_MAX_EXPERTS || layer < 0 || top_k < 1)
-        return dfail(LOCALI_E_ARG, "dplan_plan: bad arguments");
-    if (static_cast<int64_t>(layer + 1) * n_experts > key_capacity)
-        return dfail(LOCALI_E_ARG, "dplan_plan: layer %d x %d experts outside %d keys", layer, n_experts,
-                     key_capacity);
-    if (slots < 2 || key_capacity < 1 || max_routes < 1 ||
-        (policy != LOCALI_CACHE_SLRU && policy != LOCALI_CACHE_LFU_DECAY))
-        return dfail(LOCALI_E_ARG, "dplan_plan: bad planner shape");
-    const size_t lds = plan_lds_bytes(slots, n_experts, policy == LOCALI_CACHE_LFU_DECAY);
-    const size_t limit = SELECT ? kPlanMaxDynamicLdsSelect : kPlanMaxDynamicLds;
-    if (lds > limit)
-        return dfail(LOCALI_E_ARG, "dplan_plan: %d slots need %zu bytes of LDS; at most %zu", slots, lds, limit);
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&dplan_kernel<SELECT>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       static_cast<int>(limit));
-    if (attr != hipSuccess) return dhip(attr, "dplan_plan attribute");
-    hipLaunchKernelGGL(dplan_kernel<SELECT>, dim3(1), dim3(kPlanThreads), lds, st,
-                       static_cast<unsigned char *>(state), key_capacity, slots, policy, max_routes, expert_idx,
-                       routes, layer, n_experts, top_k, touch_hits ? 1 : 0, route_slot, sel);
-    const hipError_t e = hipGetLastError();
-    return e != hipSuccess ? dhip(e, "dplan_plan launch") : 0;
-}
-
 }  // namespace
-
-namespace locali {
-
-// One planner call whose routes are the selection over sel's logits (the
-// router's logits kernel already queued; at most kFusedSelectMaxTokens
-// tokens, E <= 64 * kSelectM). sel writes idx and weights as the router does.
-int dplan_select_launch(const RouterLaunch &sel, void *state, int32_t key_capacity, int32_t slots,
-                        int32_t policy, int32_t max_routes, int32_t layer, int32_t touch_hits,
-                        int32_t *route_slot, hipStream_t st) {
-    if (sel.tokens < 1 || sel.tokens > kFusedSelectMaxTokens || sel.E > 64 * kSelectM || sel.top_k > 16 ||
-        !sel.idx || !sel.weights || !sel.logits || sel.logits_in)
-        return dfail(LOCALI_E_ARG, "dplan_route_plan: the routing cannot be planned in one kernel");
-    return plan_launch<true>(state, key_capacity, slots, policy, max_routes, nullptr, sel.tokens * sel.top_k, layer,
-                             sel.E, sel.top_k, touch_hits, route_slot, sel, st);
-}
-
-}  // namespace locali
 
 extern "C" {
 
@@ -737,10 +662,28 @@ int locali_dplan_plan(void *state, int32_t key_capacity, int32_t slots, int32_t 
                       const int32_t *expert_idx, int32_t routes, int32_t layer, int32_t n_experts, int32_t top_k,
                       int32_t touch_hits, int32_t *route_slot, void *stream) {
     if (routes == 0) return 0;
-    if (!expert_idx) return dfail(LOCALI_E_ARG, "dplan_plan: null routes");
-    return plan_launch<false>(state, key_capacity, slots, policy, max_routes, expert_idx, routes, layer,
-                              n_experts, top_k, touch_hits, route_slot, locali::RouterLaunch{},
-                              static_cast<hipStream_t>(stream));
+    if (!state || !expert_idx || !route_slot || routes < 0 || routes > max_routes || n_experts < 1 ||
+        n_experts > LOCALI_DPLAN_MAX_EXPERTS || layer < 0 || top_k < 1)
+        return dfail(LOCALI_E_ARG, "dplan_plan: bad arguments");
+    if (static_cast<int64_t>(layer + 1) * n_experts > key_capacity)
+        return dfail(LOCALI_E_ARG, "dplan_plan: layer %d x %d experts outside %d keys", layer, n_experts,
+                     key_capacity);
+    if (slots < 2 || key_capacity < 1 || max_routes < 1 ||
+        (policy != LOCALI_CACHE_SLRU && policy != LOCALI_CACHE_LFU_DECAY))
+        return dfail(LOCALI_E_ARG, "dplan_plan: bad planner shape");
+    const size_t lds = plan_lds_bytes(slots, n_experts, policy == LOCALI_CACHE_LFU_DECAY);
+    if (lds > kPlanMaxDynamicLds)
+        return dfail(LOCALI_E_ARG, "dplan_plan: %d slots need %zu bytes of LDS; at most %zu", slots, lds,
+                     kPlanMaxDynamicLds);
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&dplan_kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       static_cast<int>(kPlanMaxDynamicLds));
+    if (attr != hipSuccess) return dhip(attr, "dplan_plan attribute");
+    hipLaunchKernelGGL(dplan_kernel, dim3(1), dim3(kPlanThreads), lds, static_cast<hipStream_t>(stream),
+                       static_cast<unsigned char *>(state), key_capacity, slots, policy, max_routes, expert_idx,
+                       routes, layer, n_experts, top_k, touch_hits ? 1 : 0, route_slot);
+    const hipError_t e = hipGetLastError();
+    return e != hipSuccess ? dhip(e, "dplan_plan launch") : 0;
 }
 
 int locali_dplan_fill(const void *state, void *const *dst_base, const size_t *slot_bytes, int32_t n_arrays,

@@ -133,13 +133,6 @@ struct RouterLaunch {
 // leave the selection to the caller's kernel (router_select_fusable).
 hipError_t launch_router(const RouterLaunch &L, hipStream_t st, bool logits_only = false);
 
-// device_planner.hip: one device planner call whose routes are the selection
-// over L's logits (the logits kernel queued before it); returns a
-// LOCALI_E_* status.
-int dplan_select_launch(const RouterLaunch &L, void *state, int32_t key_capacity, int32_t slots,
-                        int32_t policy, int32_t max_routes, int32_t layer, int32_t touch_hits,
-                        int32_t *route_slot, hipStream_t st);
-
 // The decode gate/up kernel can select for its own token when the logits come
 // from the gemv path (few tokens, no precomputed logits) into one partial row
 // per token, and E <= 256.

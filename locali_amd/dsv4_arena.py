@@ -33,11 +33,6 @@ from .arena import PROJS, ArenaMoE, ArenaStore, ReadPlan
 from .native import DevicePlanner, NativeCache
 
 
-# Decode batches up to this many tokens have their top-k selected inside the
-# device planner's kernel (the router's logits kernel, then one planner launch).
-FUSED_ROUTE_PLAN_TOKENS = 8
-
-
 class V4ArenaStore(ArenaStore):
     """The arena with V4 affine quantisation metadata validated and the
     compiled planner per tier over layers * E keys (key = layer * E + e)."""
@@ -227,16 +222,6 @@ class V4ArenaStore(ArenaStore):
         self.dplan.fill(self._slot_table(t), src, layer, expert_idx.numel())
         return slots
 
-    def device_route_plan(self, layer, gate, x, input_ids=None):
-        """(idx, weights, route slots) of one decode call whose routing is
-        selected inside the planner kernel (a V4Gate, at most 8 tokens), the
-        misses queued as fills behind it."""
-        t = self.tiers[0]
-        src = self._dplan_sources(t)
-        idx, w, slots = self.dplan.route_plan(gate.spec, x, gate.ws, layer, input_ids=input_ids)
-        self.dplan.fill(self._slot_table(t), src, layer, idx.numel())
-        return idx, w, slots
-
     def _dplan_counters(self):
         c, _ = self.dplan.read()
         if c["error"]:
@@ -348,13 +333,9 @@ class V4ArenaMoE(ArenaMoE):
         flat = x.reshape(-1, shape[-1])
         if flat.shape[0] == 0:
             return torch.zeros(shape, dtype=x.dtype, device=x.device)
+        inds, gates = self.route(x, input_ids)
         T = flat.shape[0]
-        if (isinstance(self.gate, V4Gate) and T <= FUSED_ROUTE_PLAN_TOKENS and self.store.E <= 256
-                and (self.gate.spec.tid2eid is None or input_ids is not None)):
-            _, gates, slots = self.store.device_route_plan(self.layer, self.gate, flat, input_ids)
-        else:
-            inds, gates = self.route(x, input_ids)
-            slots = self.store.device_plan(self.layer, inds.reshape(T, self.top_k))
+        slots = self.store.device_plan(self.layer, inds.reshape(T, self.top_k))
         out = self._run_experts(self.store.tiers[0], flat, slots, gates.reshape(T, self.top_k), x.dtype)
         return out.reshape(shape).to(x.dtype)
 

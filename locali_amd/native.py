@@ -181,32 +181,6 @@ class DevicePlanner:
                    "locali_dplan_plan")
         return out.view(expert_idx.shape)
 
-    def route_plan(self, spec, x, ws, layer: int, *, input_ids=None, touch_hits: bool = True):
-        """The router (ops.RouterSpec spec on x [T, d], T <= 8, at most 256
-        experts) with its top-k selection made inside the planner kernel:
-        returns (idx int32 [T, k], weights fp32 [T, k], route slots int32
-        [T, k]) as ops.router followed by plan()."""
-        import torch
-        from .ops import _dt, _flat, _ptr, _stream
-        x2 = _flat(x)
-        T, d = x2.shape
-        k = spec.top_k
-        dev = x2.device
-        idx = torch.empty(T, k, dtype=torch.int32, device=dev)
-        w = torch.empty(T, k, dtype=torch.float32, device=dev)
-        rs = torch.empty(T, k, dtype=torch.int32, device=dev)
-        buf = ws.reserve(T, d, 1, spec.n_experts, k, 0)
-        ids = None
-        if input_ids is not None:
-            ids = input_ids.reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
-        st = spec.struct()
-        _lib.check(self._lib.locali_dplan_route_plan(ctypes.byref(st), _ptr(x2), _dt(x2), T, d, _ptr(ids), _ptr(idx),
-                                                       _ptr(w), _ptr(buf), buf.numel(), self.state.data_ptr(),
-                                                       self.key_capacity, self.slots, self.policy, self.max_routes,
-                                                       layer, int(touch_hits), _ptr(rs), _stream()),
-                   "locali_dplan_route_plan")
-        return idx, w, rs
-
     def fill(self, table, host_src, layer: int, max_misses: int) -> None:
         """Copy the last plan's misses into their slots. table: (bases,
         per-slot bytes) of the arena arrays in record order; host_src: device

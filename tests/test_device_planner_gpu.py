@@ -128,33 +128,3 @@ def test_device_planner_fill_copies_each_miss():
         assert torch.equal(got, want), f"call {c}"
     counters, _ = dp.read()
     assert counters["error"] == 0 and counters["evictions"] > 0
-
-
-@pytest.mark.parametrize("tokens,policy,score", [(1, "slru", "sqrtsoftplus"), (3, "lfu-decay", "sigmoid"),
-                                                 (8, "slru", "softmax")])
-def test_route_plan_equals_router_then_plan(tokens, policy, score):
-    """locali_dplan_route_plan (the router's selection made inside the
-    planner kernel) against ops.router followed by plan(): the same routes,
-    weights and slots bit for bit, and the same planner results and counters."""
-    from locali_amd import ops
-    E, d, k, layers, slots = 256, 1024, 6, 4, 60
-    g = torch.Generator().manual_seed(tokens)
-    w = (torch.randn(E, d, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
-    bias = (torch.randn(E, generator=g) * 0.1).to(DEV)
-    spec = ops.RouterSpec(w, k, score_func=score, norm_topk=True, routed_scale=1.5, score_bias=bias)
-    ws1, ws2 = ops.Workspace(DEV), ops.Workspace(DEV)
-    pcap = 20 if policy == "slru" else 0
-    a = DevicePlanner(layers * E, slots, pcap, n_experts=E, policy=policy, max_routes=64, device=DEV)
-    b = DevicePlanner(layers * E, slots, pcap, n_experts=E, policy=policy, max_routes=64, device=DEV)
-    for c in range(40):
-        layer = c % layers
-        x = torch.randn(tokens, d, generator=g).to(torch.bfloat16).to(DEV)
-        idx, wts, _ = ops.router(spec, x, ws1)
-        rs_a = a.plan(idx, layer, k)
-        idx_b, wts_b, rs_b = b.route_plan(spec, x, ws2, layer)
-        assert torch.equal(idx, idx_b) and torch.equal(wts, wts_b), f"call {c}"
-        assert torch.equal(rs_a, rs_b), f"call {c}"
-        ca, ra = a.read(64)
-        cb, rb = b.read(64)
-        assert ra == rb and ca == cb, f"call {c}"
-    assert ca["evictions"] > 0
