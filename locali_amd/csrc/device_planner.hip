@@ -21,7 +21,8 @@
 // then thread 0 plans the keys in order, each resolved slot pinned for the
 // keys after it, and the workgroup joins it for every victim search; last,
 // the slot of every route, the fill list (the call's misses) and the
-// per-key results are written, and the LDS state goes back to device memory.
+// per-key results are written, and the slots the call changed go back to
+// device memory.
 //
 // dplan_fill_kernel copies each miss of the last call from its pinned host
 // payload (the expert's records back to back) into its slot, reading the
@@ -97,7 +98,7 @@ struct PlanLds {
     uint64_t *rst, *lst, *klst;
     uint32_t *hot, *khot;
     int32_t *owner, *kslot, *first, *eslot, *want;
-    uint8_t *where, *pin;
+    uint8_t *where, *pin, *dirty;
 };
 
 __host__ __device__ inline size_t plan_lds_bytes(int n_slots, int E, bool lfu) {
@@ -105,7 +106,7 @@ __host__ __device__ inline size_t plan_lds_bytes(int n_slots, int E, bool lfu) {
     if (lfu) b += sizeof(uint64_t) * n_slots + sizeof(uint32_t) * n_slots;   // lst, hot
     b += sizeof(uint32_t) * E;                                            // khot
     b += sizeof(int32_t) * n_slots + 4 * sizeof(int32_t) * E;            // owner, kslot, first, eslot, want
-    b += 2 * sizeof(uint8_t) * n_slots;                                   // where, pin
+    b += 3 * sizeof(uint8_t) * n_slots;                                   // where, pin, dirty
     return (b + 15) & ~size_t{15};
 }
 
@@ -130,6 +131,7 @@ __device__ inline PlanLds carve(unsigned char *p, int n_slots, int E, bool lfu) 
     L.want = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * E));
     L.where = take(n_slots);
     L.pin = take(n_slots);
+    L.dirty = take(n_slots);
     return L;
 }
 
@@ -213,12 +215,16 @@ struct Planner {
 
     __device__ Planner(const PlanLds &lds) : L(lds) {}
 
+    // every change of a slot's owner, segment or stamp goes through these
+    // two, which mark the slot for the write-back
     __device__ void unlink(int s) {
         if (L.where[s] == kProbation) --n_probation;
         else if (L.where[s] == kProtected) --n_protected;
         L.where[s] = kNowhere;
+        L.dirty[s] = 1;
     }
     __device__ void push(int s, uint8_t seg) {
+        L.dirty[s] = 1;
         L.where[s] = seg;
         L.rst[s] = ++rclock;
         if (seg == kProbation) ++n_probation;
@@ -285,6 +291,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
         L.where[s] = g_where[s];
         L.rst[s] = g_rst[s];
         L.pin[s] = 0;
+        L.dirty[s] = 0;
         if (lfu) {
             L.hot[s] = k >= 0 ? g_hot[k] : 0u;
             L.lst[s] = k >= 0 ? g_lst[k] : uint64_t{0};
@@ -515,6 +522,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
         route_slot[r] = (x >= 0 && x < E) ? L.eslot[x] : 0;
     }
     for (int s = tid; s < n_slots; s += kPlanThreads) {
+        if (!L.dirty[s]) continue;   // only the slots this call changed
         g_owner[s] = L.owner[s];
         g_where[s] = L.where[s];
         g_rst[s] = L.rst[s];
