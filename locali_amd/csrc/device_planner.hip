@@ -154,6 +154,21 @@ __device__ inline uint64_t shfl_xor_u64(uint64_t v, int m) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
+// Lexicographic arg-min of (a, b, slot) over `lanes` lanes of the wave (a
+// power of two), by butterfly; ties of (a, b) take the larger slot (only
+// empty candidates tie: stamps are unique).
+__device__ inline void argmin_lanes(uint64_t &a, uint64_t &b, int &s, int lanes) {
+    for (int m = lanes / 2; m >= 1; m >>= 1) {
+        const uint64_t oa = shfl_xor_u64(a, m), ob = shfl_xor_u64(b, m);
+        const int os = __shfl_xor(s, m, 64);
+        if (oa < a || (oa == a && (ob < b || (ob == b && os > s)))) {
+            a = oa;
+            b = ob;
+            s = os;
+        }
+    }
+}
+
 // Victim search over slots 1 .. n_slots-1 by the whole workgroup; returns
 // the slot (or -1) to every thread. Stamps are unique among resident slots,
 // so the minimum is unique.
@@ -173,30 +188,20 @@ __device__ int scan_slots(const PlanLds &L, int n_slots, int kind, PlanShared &s
             bs = s;
         }
     }
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t oa = shfl_xor_u64(ba, m), ob = shfl_xor_u64(bb, m);
-        const int os = __shfl_xor(bs, m, 64);
-        if (oa < ba || (oa == ba && (ob < bb || (ob == bb && os > bs)))) {
-            ba = oa;
-            bb = ob;
-            bs = os;
-        }
-    }
+    argmin_lanes(ba, bb, bs, 64);
     if (lane == 0) {
         sh.red_a[wave] = ba;
         sh.red_b[wave] = bb;
         sh.red_s[wave] = bs;
     }
     __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < kPlanWaves; ++w) {
-            if (sh.red_a[w] < ba || (sh.red_a[w] == ba && (sh.red_b[w] < bb || (sh.red_b[w] == bb && sh.red_s[w] > bs)))) {
-                ba = sh.red_a[w];
-                bb = sh.red_b[w];
-                bs = sh.red_s[w];
-            }
-        }
-        sh.result = bs;
+    if (wave == 0) {
+        // the waves' minima, one per lane
+        ba = lane < kPlanWaves ? sh.red_a[lane] : ~uint64_t{0};
+        bb = lane < kPlanWaves ? sh.red_b[lane] : ~uint64_t{0};
+        bs = lane < kPlanWaves ? sh.red_s[lane] : -1;
+        argmin_lanes(ba, bb, bs, kPlanWaves);
+        if (lane == 0) sh.result = bs;
     }
     __syncthreads();
     return sh.result;
