@@ -61,10 +61,13 @@ class V4ArenaStore(ArenaStore):
             raise RuntimeError("lfu-decay requires the compiled planner")
         self.dplan = None
         if device_planner:
-            if not native_scheduler:
-                raise ValueError("the device planner follows the compiled planner (native_scheduler=True)")
-            if len(self.tiers) != 1 or self.host_source is None:
-                raise ValueError("the device planner covers one expert tier filled from host_source")
+            problem = ("the device planner follows the compiled planner (native_scheduler=True)"
+                       if not native_scheduler else
+                       "the device planner covers one expert tier filled from host_source"
+                       if len(self.tiers) != 1 or self.host_source is None else None)
+            if problem:
+                self.close()
+                raise ValueError(problem)
             t = self.tiers[0]
             self.dplan = DevicePlanner(self.layers * self.E, self.slots[t], self.protected_cap[t],
                                        n_experts=self.E, policy=policy, device=self.device)

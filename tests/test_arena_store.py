@@ -413,3 +413,14 @@ def test_a_truncated_shard_is_a_short_read(tmp_path):
             st.slots_for(1, [EXPERTS - 1])
     finally:
         st.close()
+
+
+def test_device_planner_refuses_what_it_does_not_cover(ckpt):
+    """device_planner=True needs the compiled planner and host-memory fills
+    of one tier; the store says so before it touches a GPU."""
+    _, truth, index, _ = ckpt
+    with pytest.raises(ValueError, match="host_source"):
+        _store(index, 5, device_planner=True)
+    src = lambda layer, e: torch.from_numpy(np.frombuffer(expert_bytes(truth, layer, e), np.uint8).copy())
+    with pytest.raises(ValueError, match="native_scheduler"):
+        _store(index, 5, device_planner=True, native_scheduler=False, host_source=src)
