@@ -58,8 +58,19 @@ int locali_cache_plan_each(locali_cache *cache, const int32_t *keys, size_t key_
  * host memory into its slot: host_src is a device array of key_capacity
  * device-visible addresses (locali_dplan_host_view), the expert's records
  * back to back in the order of dst_base; record a of an expert in slot s lands
- * at dst_base[a] + s * slot_bytes[a]. max_misses bounds the launch (the plan
- * call's routes). All of the state's calls must run in stream order.
+ * at dst_base[a] + s * slot_bytes[a]. max_misses is an upper bound on the
+ * misses (the plan call's routes); 0 launches nothing. The copy runs as a
+ * persistent grid of 64 workgroups whatever the miss count. All of the
+ * state's calls must run in stream order.
+ *
+ * locali_dplan_plan_fill is locali_dplan_plan followed by locali_dplan_fill
+ * (the same decisions, route slots, results and copies) in one launch: the
+ * planner workgroup publishes each miss in device memory as it decides it,
+ * and 16 copy workgroups of the same grid start its copy meanwhile, so the
+ * PCIe copy overlaps the planning of the keys after it and no launch
+ * separates the two. The copy workgroups wait on the planner workgroup, which
+ * is dispatched first; one that still waits after about a second gives up
+ * and sets LOCALI_DPLAN_E_FILL.
  *
  * locali_dplan_read copies the counters (and up to max_results per-key
  * results of the last call) to the host and waits for the stream.
@@ -70,6 +81,7 @@ enum {
     LOCALI_DPLAN_E_EXPERT = 1,   /* a route's expert outside [0, n_experts) */
     LOCALI_DPLAN_E_PLACE = 2,    /* a demanded key found no unpinned slot */
     LOCALI_DPLAN_E_CONFIG = 3,   /* plan arguments disagree with the state */
+    LOCALI_DPLAN_E_FILL = 4,     /* a fused copy workgroup gave up waiting for the planner */
 };
 
 typedef struct {
@@ -89,6 +101,10 @@ int locali_dplan_plan(void *state, int32_t key_capacity, int32_t slots, int32_t 
 int locali_dplan_fill(const void *state, void *const *dst_base, const size_t *slot_bytes, int32_t n_arrays,
                       const uint64_t *host_src, int32_t layer, int32_t n_experts, int32_t max_misses,
                       void *stream);
+int locali_dplan_plan_fill(void *state, int32_t key_capacity, int32_t slots, int32_t policy, int32_t max_routes,
+                           const int32_t *expert_idx, int32_t routes, int32_t layer, int32_t n_experts,
+                           int32_t top_k, int32_t touch_hits, int32_t *route_slot, void *const *dst_base,
+                           const size_t *slot_bytes, int32_t n_arrays, const uint64_t *host_src, void *stream);
 int locali_dplan_host_view(const void *const *src_host, int32_t n, uint64_t *out);
 int locali_dplan_read(const void *state, locali_dplan_stats *stats, locali_cache_result *results,
                       int32_t max_results, void *stream);

@@ -108,6 +108,8 @@ _SIGNATURES = {
     "locali_dplan_plan": ([_P, _I, _I, _I, _I, _P, _I, _I, _I, _I, _I, _P, _P], ctypes.c_int),
     "locali_dplan_fill": ([_P, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t), _I, _P, _I, _I,
                            _I, _P], ctypes.c_int),
+    "locali_dplan_plan_fill": ([_P, _I, _I, _I, _I, _P, _I, _I, _I, _I, _I, _P, ctypes.POINTER(ctypes.c_void_p),
+                                ctypes.POINTER(ctypes.c_size_t), _I, _P, _P], ctypes.c_int),
     "locali_dplan_host_view": ([ctypes.POINTER(ctypes.c_void_p), _I, ctypes.POINTER(ctypes.c_uint64)],
                                ctypes.c_int),
     "locali_dplan_read": ([_P, ctypes.POINTER(DPlanStats), ctypes.POINTER(CacheResult), _I, _P], ctypes.c_int),

@@ -217,19 +217,19 @@ class V4ArenaStore(ArenaStore):
         return self._dplan_src
 
     def device_plan(self, layer, expert_idx):
-        """Route slots [T, k] of one demand call planned on the device, the
-        call's misses queued as fills behind it on the current stream."""
+        """Route slots [T, k] of one demand call planned on the device; the
+        call's misses are copied by the same launch, each starting as soon
+        as the planner has placed it, on the current stream."""
         t = self.tiers[0]
         src = self._dplan_sources(t)
-        slots = self.dplan.plan(expert_idx, layer, self.top_k)
-        self.dplan.fill(self._slot_table(t), src, layer, expert_idx.numel())
-        return slots
+        return self.dplan.plan_fill(expert_idx, layer, self.top_k, self._slot_table(t), src)
 
     def _dplan_counters(self):
         c, _ = self.dplan.read()
         if c["error"]:
             what = {1: "a route's expert outside the layer", 2: "a demanded expert found no unpinned slot",
-                    3: "plan arguments disagree with the planner state"}.get(c["error"], c["error"])
+                    3: "plan arguments disagree with the planner state",
+                    4: "a copy workgroup gave up waiting for the planner"}.get(c["error"], c["error"])
             raise RuntimeError(f"device planner: {what}")
         return c
 

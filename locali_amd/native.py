@@ -181,19 +181,43 @@ class DevicePlanner:
                    "locali_dplan_plan")
         return out.view(expert_idx.shape)
 
+    def _records(self, table):
+        if self._table is None or self._table[0] is not table:
+            base, per = table
+            self._table = (table, (ctypes.c_void_p * len(base))(*base), (ctypes.c_size_t * len(per))(*per),
+                           len(base))
+        return self._table[1:]
+
     def fill(self, table, host_src, layer: int, max_misses: int) -> None:
         """Copy the last plan's misses into their slots. table: (bases,
         per-slot bytes) of the arena arrays in record order; host_src: device
         uint64 tensor of the key_capacity device-visible payload addresses."""
         from .ops import _stream
-        if self._table is None or self._table[0] is not table:
-            base, per = table
-            self._table = (table, (ctypes.c_void_p * len(base))(*base), (ctypes.c_size_t * len(per))(*per),
-                           len(base))
-        _, bases, pers, n = self._table
+        bases, pers, n = self._records(table)
         _lib.check(self._lib.locali_dplan_fill(self.state.data_ptr(), bases, pers, n, host_src.data_ptr(), layer,
                                                  self.n_experts, max_misses, _stream()),
                    "locali_dplan_fill")
+
+    def plan_fill(self, expert_idx, layer: int, top_k: int, table, host_src, *, touch_hits: bool = True,
+                  out=None):
+        """plan() then fill() in one launch: the misses' copies start while
+        the planner decides the keys after them. Same results."""
+        import torch
+        from .ops import _stream
+        idx = expert_idx.reshape(-1)
+        if idx.dtype != torch.int32 or not idx.is_cuda:
+            raise ValueError("device planner: expert_idx must be a device int32 tensor")
+        idx = idx.contiguous()
+        if out is None:
+            out = torch.empty(idx.numel(), dtype=torch.int32, device=idx.device)
+        bases, pers, n = self._records(table)
+        _lib.check(self._lib.locali_dplan_plan_fill(self.state.data_ptr(), self.key_capacity, self.slots,
+                                                      self.policy, self.max_routes, idx.data_ptr(), idx.numel(),
+                                                      layer, self.n_experts, top_k, int(touch_hits),
+                                                      out.data_ptr(), bases, pers, n, host_src.data_ptr(),
+                                                      _stream()),
+                   "locali_dplan_plan_fill")
+        return out.view(expert_idx.shape)
 
     @staticmethod
     def host_view(pointers) -> list[int]:

@@ -105,9 +105,11 @@ def test_device_planner_placement_failure_matches_host():
     assert counters["error"] == 2     # LOCALI_DPLAN_E_PLACE
 
 
-def test_device_planner_fill_copies_each_miss():
+@pytest.mark.parametrize("fused", [False, True])
+def test_device_planner_fill_copies_each_miss(fused):
     """Three records per expert of unequal sizes; after every call each
-    resident slot of the routed experts holds its expert's payload."""
+    resident slot of the routed experts holds its expert's payload (fused:
+    plan and copies in one launch)."""
     layers, E, top_k, slots = 3, 16, 4, 12
     sizes = [4096, 256, 1024]                   # bytes per slot of each record
     total = sum(sizes)
@@ -121,10 +123,54 @@ def test_device_planner_fill_copies_each_miss():
     for c in range(60):
         layer = c % layers
         routes = [int(e) for e in rng.choice(E, size=top_k, replace=False)]
-        rs = dp.plan(torch.tensor(routes, dtype=torch.int32, device=DEV), layer, top_k)
-        dp.fill(table, host_src, layer, len(routes))
+        idx = torch.tensor(routes, dtype=torch.int32, device=DEV)
+        if fused:
+            rs = dp.plan_fill(idx, layer, top_k, table, host_src)
+        else:
+            rs = dp.plan(idx, layer, top_k)
+            dp.fill(table, host_src, layer, len(routes))
         got = torch.cat([a[rs.long()].cpu() for a in arrays], dim=1)
         want = payload[[layer * E + e for e in routes]]
         assert torch.equal(got, want), f"call {c}"
     counters, _ = dp.read()
     assert counters["error"] == 0 and counters["evictions"] > 0
+
+
+@pytest.mark.parametrize("policy,multi", [("slru", 3), ("lfu-decay", 2)])
+def test_fused_plan_fill_equals_plan_then_fill(policy, multi):
+    """plan_fill against plan + fill on two planners fed the same calls
+    (single-token calls and calls of several tokens, so several misses per
+    call): per-key results, route slots, counters and every slot's bytes are
+    identical, and the decisions equal the host planner's."""
+    layers, E, top_k, slots, pcap = 4, 48, 6, 40, (10 if policy == "slru" else 0)
+    sizes = [8192, 4096, 256]
+    total = sum(sizes)
+    payload = torch.randint(0, 256, (layers * E, total), dtype=torch.uint8).pin_memory()
+    ptrs = DevicePlanner.host_view([payload[k].data_ptr() for k in range(layers * E)])
+    host_src = torch.tensor(ptrs, dtype=torch.uint64, device=DEV)
+    rng = np.random.default_rng(11 + multi)
+    calls = zipf_calls(rng, 160, layers, E, top_k, multi)
+    expect = host_run(calls, layers, E, slots, pcap, policy, top_k)
+    planners, arenas = [], []
+    for _ in range(2):
+        arrays = [torch.zeros(slots, sz, dtype=torch.uint8, device=DEV) for sz in sizes]
+        arenas.append((arrays, ([a.data_ptr() for a in arrays], sizes)))
+        planners.append(DevicePlanner(layers * E, slots, pcap, n_experts=E, policy=policy, max_routes=64,
+                                      device=DEV))
+    n_multi_miss = 0
+    for c, ((layer, routes), want_res) in enumerate(zip(calls, expect)):
+        idx = torch.tensor(routes, dtype=torch.int32, device=DEV)
+        rs_a = planners[0].plan(idx, layer, top_k)
+        planners[0].fill(arenas[0][1], host_src, layer, len(routes))
+        rs_b = planners[1].plan_fill(idx, layer, top_k, arenas[1][1], host_src)
+        assert torch.equal(rs_a, rs_b), f"route slots of call {c}"
+        ca, ra = planners[0].read(max_results=len(want_res))
+        cb, rb = planners[1].read(max_results=len(want_res))
+        assert ca == cb and cb["error"] == 0, (c, ca, cb)
+        assert ra == rb == want_res, f"results of call {c}"
+        for a, b in zip(arenas[0][0], arenas[1][0]):
+            assert torch.equal(a, b), f"arena bytes after call {c}"
+        got = torch.cat([a[rs_b.long()].cpu() for a in arenas[1][0]], dim=1)
+        assert torch.equal(got, payload[[layer * E + e for e in routes]]), f"payload of call {c}"
+        n_multi_miss += sum(not r.hit for r in want_res) > 1
+    assert n_multi_miss > 20
