@@ -6,7 +6,9 @@ d_model 4096, 256 routed experts (top-6, sqrt-softplus router) + 1 shared
 expert, d_ff 2048, 2-bit affine weights (group 64, bf16 scales/biases), all
 257 expert slots resident in an HBM arena, 1 token per step, uniform-random
 routing. A step is one token through router, experts, combine and shared
-expert. Steps are replayed from a captured HIP graph (inputs already in HBM).
+expert. Steps are replayed from a captured HIP graph (inputs already in HBM)
+and rotate over 64 copies of the router and shared expert, so that no step
+finds them in the 256 MB MALL (a model's layers each have their own).
 
 Also reported:
   roofline      the dominant kernel (decode gate/up + SwiGLU), its average
@@ -90,6 +92,13 @@ def layer_flops(tokens):
     return 2 * tokens * (K_TOP + 1) * 3 * D * DFF
 
 
+# The decode leg rotates its steps over this many copies of the layer's router
+# and shared expert (as a model's layers each have their own): 64 x 9.96 MB
+# is well past the 256 MB MALL, so every step reads its router and shared
+# expert from HBM like its routed experts, instead of re-reading one copy.
+DECODE_LAYERS = 64
+
+
 def layer(dev, seed=1):
     arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=BITS, group=GROUP, dtype=torch.bfloat16,
                                seed=seed, device=dev)
@@ -99,8 +108,20 @@ def layer(dev, seed=1):
     return arena, shared, slot_of
 
 
-def decode_graph_run(spec, arena, shared, slot_of, X, ws, steps, warmup, use_graph):
-    """Returns elapsed seconds for exactly `steps` decode steps."""
+def decode_layers(dev, seed, shared0, spec0, n=DECODE_LAYERS):
+    """n (router, shared expert) pairs; the first are the layer's own."""
+    specs, shareds = [spec0], [shared0]
+    for i in range(1, n):
+        shareds.append(synth.expert_arena(1, D, DFF, bits_gate_up=BITS, group=GROUP, dtype=torch.bfloat16,
+                                          seed=seed + 1000 + 2 * i, device=dev, zero_slot=False))
+        w, _ = synth.uniform_router(E, D, torch.bfloat16, seed=seed + 1001 + 2 * i, device=dev)
+        specs.append(ops.RouterSpec(w, K_TOP, routed_scale=1.5))
+    return specs, shareds
+
+
+def decode_graph_run(specs, arena, shareds, slot_of, X, ws, steps, warmup, use_graph):
+    """Returns elapsed seconds for exactly `steps` decode steps (step j uses
+    router and shared expert j % len(specs))."""
     n_in = X.shape[0]
     outs = torch.empty_like(X)
     idx = torch.empty(n_in, K_TOP, dtype=torch.int32, device=X.device)
@@ -108,7 +129,8 @@ def decode_graph_run(spec, arena, shared, slot_of, X, ws, steps, warmup, use_gra
 
     def step(i):
         j = i % n_in
-        ops.forward(spec, arena, shared, slot_of, X[j:j + 1], ws, out=outs[j:j + 1],
+        ops.forward(specs[j % len(specs)], arena, shareds[j % len(specs)], slot_of, X[j:j + 1], ws,
+                    out=outs[j:j + 1],
                     idx=idx[j:j + 1], weights=wts[j:j + 1])
 
     for i in range(max(warmup, 1)):
@@ -145,7 +167,7 @@ def decode_graph_run(spec, arena, shared, slot_of, X, ws, steps, warmup, use_gra
     return e0.elapsed_time(e1) / 1e3, wall, idx
 
 
-def stage_timing(spec, arena, shared, slot_of, X, ws, m=40, replays=5):
+def stage_timing(specs, arena, shareds, slot_of, X, ws, m=40, replays=5):
     """Average device time (s) of one launch of each kernel of the decode step
     -- router logits, gate/up with the in-kernel top-6 selection, down +
     combine -- and of the gate/up kernel fed with chosen routes (no
@@ -155,27 +177,30 @@ def stage_timing(spec, arena, shared, slot_of, X, ws, m=40, replays=5):
     launch streams different experts) into its own HIP graph; HIP events on
     the replay stream bracket `replays` replays, and the per-launch average
     is elapsed / (replays * m) -- the same quantity rocprofv3 reports as a
-    kernel's average duration."""
+    kernel's average duration. Launch i uses router and shared expert
+    i % len(specs), as the decode leg does."""
     dev = X.device
+    nl = len(specs)
     n_in = X.shape[0]
     xs = [X[i % n_in:i % n_in + 1] for i in range(m)]
     hidden = torch.empty(K_TOP + 1, DFF, dtype=torch.bfloat16, device=dev)
     out = torch.empty(1, D, dtype=torch.bfloat16, device=dev)
     dws = ops.Workspace(dev)
     dws.reserve(1, D, DFF, 1, K_TOP, True)
-    routed = [ops.router(spec, x, ws, slot_of_expert=slot_of, n_slots=E + 1) for x in xs]
-    logits = [ops.router_logits(spec, x) for x in xs]
+    routed = [ops.router(specs[i % nl], x, ws, slot_of_expert=slot_of, n_slots=E + 1) for i, x in enumerate(xs)]
+    logits = [ops.router_logits(specs[i % nl], x) for i, x in enumerate(xs)]
     lbuf = torch.empty(E, dtype=torch.float32, device=dev)
     sel = [tuple(torch.empty(1, K_TOP, dtype=dt, device=dev) for dt in (torch.int32, torch.float32, torch.int32))
            for _ in range(m)]
     stages = {
-        "router_logits": lambda i: ops.router_logits(spec, xs[i], lbuf),
-        "gateup_select": lambda i: ops.decode_gateup_select(spec, arena, shared, slot_of, xs[i], logits[i],
-                                                            hidden, dws, idx=sel[i][0], weights=sel[i][1],
-                                                            route_slot=sel[i][2]),
-        "down_combine": lambda i: ops.decode_down_combine(arena, shared, routed[i][2], routed[i][1],
+        "router_logits": lambda i: ops.router_logits(specs[i % nl], xs[i], lbuf),
+        "gateup_select": lambda i: ops.decode_gateup_select(specs[i % nl], arena, shareds[i % nl], slot_of, xs[i],
+                                                            logits[i], hidden, dws, idx=sel[i][0],
+                                                            weights=sel[i][1], route_slot=sel[i][2]),
+        "down_combine": lambda i: ops.decode_down_combine(arena, shareds[i % nl], routed[i][2], routed[i][1],
                                                           out, dws),
-        "gateup_chosen_routes": lambda i: ops.decode_gateup(arena, shared, xs[i], routed[i][2], hidden, dws),
+        "gateup_chosen_routes": lambda i: ops.decode_gateup(arena, shareds[i % nl], xs[i], routed[i][2], hidden,
+                                                            dws),
     }
     res = {}
     for name, fn in stages.items():
@@ -594,14 +619,17 @@ def main(argv=None):
     ws = ops.Workspace(dev)
     ws.reserve(1, D, DFF, E, K_TOP, True)
 
+    specs, shareds = decode_layers(dev, args.seed, shared, spec)
+
     phase("decode (graph replay)")
-    secs, wall, idx = decode_graph_run(spec, arena, shared, slot_of, X, ws, args.steps, args.warmup,
+    secs, wall, idx = decode_graph_run(specs, arena, shareds, slot_of, X, ws, args.steps, args.warmup,
                                        not args.no_graph)
     value = args.steps / secs
     layer_bytes = 7 * EXPERT_BYTES + ROUTER_BYTES
 
     phase("stage timing (router logits, gate/up with selection, down+combine graphs)")
-    st = stage_timing(spec, arena, shared, slot_of, X, ws)
+    st = stage_timing(specs, arena, shareds, slot_of, X, ws)
+    del specs, shareds
     gate_bytes = SELECT_ALG_BYTES
     achieved = gate_bytes / st["gateup_select"] / 1e9
     result = {
@@ -621,8 +649,11 @@ def main(argv=None):
             "workload": "full-width decode MoE layer: d_model 4096, 256 routed experts top-6 "
                         "(sqrt-softplus, scale 1.5) + 1 shared expert, d_ff 2048, 2-bit affine "
                         "group-64 weights with bf16 scales/biases, fp32 accumulation, all 257 "
-                        "slots resident in HBM, 1 token per step, uniform-random routing",
+                        "slots resident in HBM, 1 token per step, uniform-random routing; steps "
+                        f"rotate over {DECODE_LAYERS} copies of the router and shared expert "
+                        "(cold in the MALL, as a model's layers)",
             "tokens_per_step": 1,
+            "router_shared_copies": DECODE_LAYERS,
             "graph_replay": not args.no_graph,
             "wall_s": wall,
             "layer_bytes_per_token": layer_bytes,
