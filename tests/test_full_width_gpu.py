@@ -26,7 +26,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import arena_numpy, assert_close_terms, banner, exact_fraction, values
+from gpu_helpers import arena_numpy, assert_close_terms, banner, dt_name, exact_fraction, ulp_distance, values
 from locali_amd import ops, synth
 from oracle import moe
 
@@ -36,11 +36,11 @@ D, E, DFF, K, GROUP = 4096, 256, 2048, 6, 64
 TILE = 64            # positions per matrix-core tile (a tile of 1-2 takes the small-tile kernels)
 
 
-def _layer(seed, bits_down=2):
+def _layer(seed, bits_down=2, dtype=torch.bfloat16):
     arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=2, bits_down=bits_down, group=GROUP,
-                               dtype=torch.bfloat16, seed=seed, device=DEV)
+                               dtype=dtype, seed=seed, device=DEV)
     shared = synth.expert_arena(1, D, DFF, bits_gate_up=2, bits_down=bits_down, group=GROUP,
-                                dtype=torch.bfloat16, seed=seed + 1, device=DEV, zero_slot=False)
+                                dtype=dtype, seed=seed + 1, device=DEV, zero_slot=False)
     return arena, shared
 
 
@@ -62,10 +62,12 @@ def _check_routes(x, w, idx, wts, *, bias=None):
     return checked
 
 
-def _oracle_check(oracle_lib, arena, shared, x, slots, wts, out, tokens, what, chunk=16, exact=0.8):
+def _oracle_check(oracle_lib, arena, shared, x, slots, wts, out, tokens, what, chunk=16, exact=0.8,
+                  dtype=torch.bfloat16):
     """The C oracle on `tokens` of a call, a chunk of tokens at a time (only
     the slots a chunk uses are copied to the host). `exact`: the least
-    fraction of outputs equal to the oracle's (None: no such bar; a single
+    fraction of outputs equal to the oracle's at bf16 resolution -- equal for
+    bf16, within one fp16 spacing for fp16 (None: no such bar; a single
     decode token's 4096 outputs are too few for a stable fraction)."""
     sh = {kk: v for kk, v in arena_numpy(shared, float_meta=False).items()}
     xs, got = values(x), values(out)
@@ -76,9 +78,9 @@ def _oracle_check(oracle_lib, arena, shared, x, slots, wts, out, tokens, what, c
         remap = {s: i for i, s in enumerate(used)}
         sub = arena_numpy(arena, float_meta=False, slots=used)
         want, terms = oracle_lib.moe_layer(xs[tk], np.vectorize(remap.get)(slots[tk]).astype(np.int32),
-                                           wts[tk], sub, "bf16", shared=sh, return_terms=True)
+                                           wts[tk], sub, dt_name(dtype), shared=sh, return_terms=True)
         assert_close_terms(got[tk], want, terms, f"{what} tokens {tk[:4].tolist()}...")
-        same.append(got[tk] == want)
+        same.append(got[tk] == want if dtype == torch.bfloat16 else ulp_distance(got[tk], want, dtype) <= 1)
     if exact is not None:
         assert exact_fraction(np.concatenate(same), True) > exact
 
@@ -113,11 +115,11 @@ def _tile_sample(idx, T, heavy=6, mid=8, small=8, seed=0):
     return sorted(pick), seg
 
 
-@pytest.mark.parametrize("T", [64, 512])
-def test_prefill_full_width_zipf(oracle_lib, T):
-    banner(f"full-width prefill T={T} zipf 1.1")
-    arena, shared = _layer(seed=300 + T)
-    x, w = synth.zipf_router_inputs(T, E, D, 1.1, torch.bfloat16, seed=310 + T, device=DEV)
+@pytest.mark.parametrize("T,dtype", [(64, torch.bfloat16), (512, torch.bfloat16), (64, torch.float16)])
+def test_prefill_full_width_zipf(oracle_lib, T, dtype):
+    banner(f"full-width prefill T={T} zipf 1.1 {dtype}")
+    arena, shared = _layer(seed=300 + T, dtype=dtype)
+    x, w = synth.zipf_router_inputs(T, E, D, 1.1, dtype, seed=310 + T, device=DEV)
     spec = ops.RouterSpec(w, K, routed_scale=1.5)
     slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
     out, idx, wts = ops.forward(spec, arena, shared, slot_of, x, ops.Workspace())
@@ -131,7 +133,7 @@ def test_prefill_full_width_zipf(oracle_lib, T):
         counts = sorted((len(v) for v in seg.values()), reverse=True)
         assert counts[0] > 2 * TILE and any(c % TILE in (1, 2) for c in counts)
     _oracle_check(oracle_lib, arena, shared, x, (ih + 1).astype(np.int32), wts.cpu().numpy(), out,
-                  tokens, f"C3 T={T}")
+                  tokens, f"C3 T={T} {dtype}", dtype=dtype)
 
 
 def test_mixed_2_4_bit_batched_decode_full_width(oracle_lib):

@@ -193,6 +193,7 @@ DECODE_CASES = [
     (torch.float16, 8, 4, 128, 512, 256),
     (torch.bfloat16, 2, 2, 64, 4096, 2048),
     (torch.bfloat16, 2, 4, 64, 4096, 2048),
+    (torch.float16, 2, 2, 64, 4096, 2048),
     # 3-bit codes (the DSpark/MTP tier): 4-bit kernels widening 3-bit rows
     (torch.bfloat16, 3, 3, 64, 1024, 512),
     (torch.float16, 3, 3, 32, 1024, 512),
