@@ -391,10 +391,14 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
     }
 }
 
+// Tiles are taken from the end of the list first: the shared expert's tiles,
+// which the dispatch appends and which hold every position (full 64-position
+// tiles, the longest workgroups), start with the launch instead of forming
+// its tail.
 __device__ __forceinline__ bool wide_tile(const TileArgs &ta, int n_slots, int &slot, int &first, int &count,
                                           bool &shared) {
-    const int tile = blockIdx.y;
-    if (tile >= *ta.n_tiles) return false;
+    const int tile = *ta.n_tiles - 1 - static_cast<int>(blockIdx.y);
+    if (tile < 0) return false;
     slot = ta.tiles[4 * tile];
     first = ta.tiles[4 * tile + 1];
     count = ta.tiles[4 * tile + 2];
