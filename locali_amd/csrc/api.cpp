@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -55,7 +56,7 @@ bool dtype16(int32_t dt) { return dt == LOCALI_DT_F16 || dt == LOCALI_DT_BF16; }
 
 // Workspace layout for up to T tokens.
 struct Layout {
-    size_t logits, route_slot, hidden, hprep, seg_start, seg_tile, sorted_route, route_pos,
+    size_t sync_gen, sync_logits, logits, route_slot, hidden, hprep, seg_start, seg_tile, sorted_route, route_pos,
         tiles, n_tiles, gh, gy, mx, mh, total;
     int max_tiles;
 };
@@ -93,6 +94,10 @@ Layout layout(int T, int d, int dff, int E, int k, int has_shared) {
     const int R = T * k;
     const int routes = R + (has_shared ? T : 0);
     L.max_tiles = grouped_max_tiles(T, k, has_shared ? 1 : 0, E, kGroupedTileTokens);
+    // The decode sync region sits at the same offsets for every call shape,
+    // so calls of different sizes on one workspace agree on its generation.
+    L.sync_gen = take(sizeof(uint32_t));
+    L.sync_logits = take(sizeof(uint64_t) * kFusedRouterMaxTokens * kSyncMaxExperts);
     L.logits = take(sizeof(float) * kRouterSplitsHost * static_cast<size_t>(T) * E);
     L.route_slot = take(sizeof(int32_t) * R);
     L.hidden = take(sizeof(uint16_t) * static_cast<size_t>(routes) * dff);
@@ -235,6 +240,7 @@ DecodeLaunch decode_launch(const locali_expert_arena *routed, const locali_exper
     L.ca.weights = weights;
     L.ca.out = static_cast<uint16_t *>(out);
     L.ca.mode = combine_mode;
+    L.ca.gen = at<uint32_t>(ws, lay.sync_gen);
     const bool bf16 = x_dtype == LOCALI_DT_BF16;
     L.hprep = prep_batch(at<void>(ws, lay.hprep), L.routes, routed->down.cols, lane_bits(routed->down.bits),
                          bf16);
@@ -837,6 +843,31 @@ int locali_moe_forward(const locali_router *router, const locali_expert_arena *r
         defer = router_select_fusable(probe) && gateup_diag_eligible(DL);
     }
     RouterLaunch RL{};
+    if (defer) {
+        // The gate/up kernel also computes the logits (router rows ahead of
+        // its gate/up rows) when the router allows it: no logits kernel.
+        RL = router_launch(router, x, x_dtype, tokens, d, input_ids, nullptr, slot_of_expert, routed->gate.n_slots,
+                           idx, weights, route_slot, at<float>(workspace, lay.logits));
+        if (router->tid2eid && !input_ids) return fail(LOCALI_E_ARG, "router: hash routing needs input_ids");
+        if (router_rows_fusable(RL)) {
+            // Router work goes to the shared expert's rows (first in the grid,
+            // waiting for nothing), up to 4 experts per workgroup; rows of
+            // router work only make up any shortfall.
+            const int tiles = dff / (16 * kDiagGateUpTiles), waves = d / kDiagWindow;
+            const int sh_rows = shared ? tokens : 0;
+            int epw = waves < 2 ? waves : 2;
+            if (sh_rows) epw = std::min(waves, std::max(1, (E + sh_rows * tiles - 1) / (sh_rows * tiles)));
+            const int rest = std::max(0, E - sh_rows * tiles * epw);
+            RL.sync_gen = at<uint32_t>(workspace, lay.sync_gen);
+            RL.sync_logits = at<uint64_t>(workspace, lay.sync_logits);
+            RL.router_epw = epw;
+            RL.router_shared_rows = sh_rows;
+            RL.router_rows = sh_rows + (rest + tiles * epw - 1) / (tiles * epw);
+            return run_decode(routed, shared, x, x_dtype, tokens, k, route_slot, weights, swiglu_limit, fp32_swiglu,
+                              LOCALI_COMBINE_ROUNDED, at<void>(workspace, lay.hidden), out, S(stream), 3,
+                              workspace, lay, &RL);
+        }
+    }
     rc = route(router, x, x_dtype, tokens, d, input_ids, nullptr, slot_of_expert, routed->gate.n_slots,
                idx, weights, route_slot, workspace, lay, S(stream), defer, &RL);
     if (rc) return rc;

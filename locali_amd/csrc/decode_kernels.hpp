@@ -242,6 +242,12 @@ __global__ __launch_bounds__(64 * WAVES) void down_combine_kernel(RouteArgs ra, 
             ylds[j][vi * G::kRPL + row_sub] = valid_slot ? round16<BF16>(v[0]) : 0.f;
     }
     __syncthreads();
+    // One thread advances the decode sync generation: the gate/up kernel of
+    // this call has ended, and the next call's starts after this kernel. It
+    // is issued after the workgroup's loads have landed, so that no load
+    // waits behind it.
+    if (ca.gen && (blockIdx.x | blockIdx.y | threadIdx.x) == 0)
+        __hip_atomic_fetch_add(ca.gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int q = threadIdx.x; q < RB; q += blockDim.x) {
         const int row = row0 + q;
         if (row >= N) continue;

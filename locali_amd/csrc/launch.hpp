@@ -22,6 +22,7 @@ struct CombineArgs {
     const float *weights;       // [tokens, top_k] router weights (fp32)
     uint16_t *out;              // [tokens, d_model]
     int32_t mode;               // 0: products rounded (single tier), 1: fp32 products
+    uint32_t *gen;              // non-null: the decode sync generation, advanced once per call
 };
 
 // A batch of prepared vectors (see qgemv.hpp): vector v's pairs start at
@@ -127,7 +128,22 @@ struct RouterLaunch {
     int32_t *route_slot;        // [tokens, top_k] or null
     float *logits;              // workspace [tokens, E]
     const float *logits_in;     // optional precomputed logits [tokens, E]
+    // Router rows of the fused decode kernel (router_rows > 0): the logits
+    // travel through sync_logits as (tag, fp32 bits) words, tag =
+    // sync_tag(*sync_gen); the down kernel of the same call advances the
+    // generation, so a later call never mistakes these words for its own.
+    uint64_t *sync_logits;      // [tokens, E]
+    uint32_t *sync_gen;
+    // The first router_rows rows of the fused grid compute the logits: the
+    // first router_shared_rows of them are the shared expert's gate/up rows
+    // (which wait for nothing), the rest are rows of router work only.
+    int32_t router_rows;
+    int32_t router_shared_rows;
+    int32_t router_epw;         // experts (one per wave) per router workgroup
 };
+
+// Tag of a sync generation: odd, so zero-filled memory never matches.
+__host__ __device__ inline uint32_t sync_tag(uint32_t gen) { return 2u * gen + 1u; }
 
 // logits_only: launch only the logits kernel of the decode (gemv) path and
 // leave the selection to the caller's kernel (router_select_fusable).
@@ -139,6 +155,19 @@ hipError_t launch_router(const RouterLaunch &L, hipStream_t st, bool logits_only
 constexpr int kFusedSelectMaxTokens = 8;
 inline bool router_select_fusable(const RouterLaunch &L) {
     return !L.logits_in && L.tokens <= kFusedSelectMaxTokens && L.E <= 256 && L.top_k <= 16;
+}
+
+// The decode gate/up kernel can also compute the logits itself (router rows
+// of workgroups dispatched ahead of its gate/up rows), for at most
+// kFusedRouterMaxTokens tokens, a gate of the activations' 16-bit dtype and
+// d_model of 1024, 2048 or 4096 (the logits kernel's fast path, whose bits it
+// reproduces).
+constexpr int kFusedRouterMaxTokens = 2;
+constexpr int kSyncMaxExperts = 256;
+inline bool router_rows_fusable(const RouterLaunch &L) {
+    const bool dot_ok = L.gate_dtype != 0 && ((L.gate_dtype == 2) == L.x_bf16);
+    return router_select_fusable(L) && L.tokens <= kFusedRouterMaxTokens && L.E <= kSyncMaxExperts && dot_ok &&
+           (L.d == 1024 || L.d == 2048 || L.d == 4096);
 }
 
 // ---- grouped (prefill) path --------------------------------------------------

@@ -131,12 +131,50 @@ __device__ __forceinline__ float diag_fix(float d, uint16_t s, uint16_t b, float
 }
 
 // ---------------------------------------------------------------------------
+// Router rows (ROUTER): the first sel.router_rows rows of the grid compute the
+// logits instead of waiting for a logits kernel. Those rows are the shared
+// expert's gate/up rows, which do their own work afterwards, then (if they are
+// too few) rows of router work only; the routed rows come last. Workgroup b of
+// the router rows takes experts b + n * w (n router workgroups, wave w <
+// router_epw), one wave each, with the logits kernel's arithmetic
+// (router_load_gate / router_pass: the same bits), and hands each token's
+// logit to the routed rows as one tagged 64-bit word (poll_logits). The router
+// rows wait for nothing and are dispatched first, so the routed rows that wait
+// for them cannot hold them off the machine.
+template <bool XBF16, int NCH>
+__device__ __forceinline__ void router_row_expert(const RouterLaunch &L, int e, int lane, uint32_t tag) {
+    u32x4 w[NCH];
+    router_load_gate<NCH>(L, e, lane, w);
+    for (int t = 0; t < L.tokens; ++t) {
+        float acc[1];
+        router_pass<XBF16, NCH, 1>(L, w, t, lane, acc);
+        if (lane == 0) {
+            const uint64_t v = (static_cast<uint64_t>(tag) << 32) | __float_as_uint(acc[0]);
+            __hip_atomic_store(L.sync_logits + static_cast<int64_t>(t) * L.E + e, v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+template <bool XBF16>
+__device__ __forceinline__ void router_rows_role(const RouterLaunch &L, int lane, int wave) {
+    const int n = L.router_rows * static_cast<int>(gridDim.x);
+    const int e = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x) + n * wave;
+    if (wave >= L.router_epw || e >= L.E) return;
+    const uint32_t tag = sync_tag(__hip_atomic_load(L.sync_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if (L.d == 1024) router_row_expert<XBF16, 2>(L, e, lane, tag);
+    else if (L.d == 2048) router_row_expert<XBF16, 4>(L, e, lane, tag);
+    else router_row_expert<XBF16, 8>(L, e, lane, tag);
+}
+
+// ---------------------------------------------------------------------------
 // SELECT: the routes' slots are not chosen yet -- wave 0 of each routed
 // workgroup runs the top-k selection of its token on `sel`'s logits (one
 // partial row per token, E <= 256) while the other waves prepare x, and the
 // workgroup (blockIdx.x 0, first route of the token) stores the token's
-// choices for the down kernel and the caller.
-template <int BITS, bool BF16, bool SELECT>
+// choices for the down kernel and the caller. ROUTER (with SELECT): the
+// logits come from the kernel's own router rows (above) instead.
+template <int BITS, bool BF16, bool SELECT, bool ROUTER>
 __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     RouteArgs ra, QProj gate, QProj up, QProj sgate, QProj sup, uint16_t *__restrict__ h,
     PrepVec hout, int down_bits, float limit, int fp32_swiglu, RouterLaunch sel) {
@@ -152,7 +190,17 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     // wave index in an SGPR: it feeds the loads' scalar offsets
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nl = lane & 15, kb = lane >> 4, hh = nl >> 3, r8 = nl & 7;
-    const int r = blockIdx.y;
+    static_assert(SELECT || !ROUTER, "router rows feed the in-kernel selection");
+    int r = static_cast<int>(blockIdx.y);
+    if constexpr (ROUTER) {
+        // rows: [shared expert (router work first)] [router work only] [routed]
+        const int y = r, S = sel.router_shared_rows;
+        if (y < sel.router_rows) {
+            router_rows_role<BF16>(sel, lane, wave);
+            if (y >= S) return;
+        }
+        r = y < S ? ra.tokens * ra.top_k + y : y - sel.router_rows;
+    }
     int token, slot;
     bool shared;
     if constexpr (SELECT) {
@@ -198,6 +246,11 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
         __shared__ float2 stage[256];
         __shared__ int s_slot;
         if (!shared) {   // uniform across the workgroup
+            // the sync generation first: polling compares against its tag
+            uint32_t tag = 0;
+            if constexpr (ROUTER)
+                if (wave == 0)
+                    tag = sync_tag(__hip_atomic_load(sel.sync_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
             // wave 1 also prepares wave 0's window while wave 0 selects
             uint32_t xw0[16 / BITS];
             if (wave == 1) diag_prep_load<BITS>(xw0, ra.x + static_cast<int64_t>(token) * K, lane);
@@ -207,8 +260,13 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
                 // token's choices (blockIdx.x 0, j 0) runs every round
                 const int j = r - token * ra.top_k;
                 const bool store = blockIdx.x == 0 && j == 0;
-                const SelectOut o = select_token_any<1, 4>(sel, token, sel.logits + static_cast<int64_t>(token) * sel.E,
-                                                           0, stage, store ? ra.top_k : j + 1);
+                const int rounds = store ? ra.top_k : j + 1;
+                SelectOut o;
+                if constexpr (ROUTER)
+                    o = select_token_polled_any<4>(sel, token, tag, stage, rounds);
+                else
+                    o = select_token_any<1, 4>(sel, token, sel.logits + static_cast<int64_t>(token) * sel.E, 0, stage,
+                                               rounds);
                 const int sj = __builtin_amdgcn_readlane(o.slot, j);
                 if (lane == 0) s_slot = sj;
                 if (store) select_store(sel, token, o);
@@ -344,17 +402,22 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     }
 }
 
-// Launch shape: one workgroup per (32 rows, route) with K / 512 waves.
+// Launch shape: one workgroup per (32 rows, route) with K / 512 waves, plus
+// the rows of router work only when the kernel computes the logits itself.
 template <int BITS, bool BF16>
 hipError_t launch_gateup_diag(const DecodeLaunch &L, hipStream_t st) {
     const int waves = L.gate.cols / kDiagWindow;
-    dim3 grid(L.gate.rows / (16 * kDiagGateUpTiles), L.routes);
-    if (L.sel)
-        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, true>), grid, dim3(64 * waves), 0, st, L.ra, L.gate,
-                           L.up, L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu, *L.sel);
+    const int rr = L.sel ? L.sel->router_rows - L.sel->router_shared_rows : 0;
+    dim3 grid(L.gate.rows / (16 * kDiagGateUpTiles), L.routes + rr);
+    if (L.sel && L.sel->router_rows > 0)
+        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, true, true>), grid, dim3(64 * waves), 0, st, L.ra,
+                           L.gate, L.up, L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu, *L.sel);
+    else if (L.sel)
+        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, true, false>), grid, dim3(64 * waves), 0, st, L.ra,
+                           L.gate, L.up, L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu, *L.sel);
     else
-        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, false>), grid, dim3(64 * waves), 0, st, L.ra, L.gate,
-                           L.up, L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu,
+        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, false, false>), grid, dim3(64 * waves), 0, st, L.ra,
+                           L.gate, L.up, L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu,
                            RouterLaunch{});
     return hipGetLastError();
 }

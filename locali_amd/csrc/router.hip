@@ -66,44 +66,15 @@ template <bool XBF16, int NCH, int TB>
 __global__ __launch_bounds__(64) void router_gemv_fast_kernel(RouterLaunch L) {
     const int lane = threadIdx.x & 63;
     const int e = blockIdx.x;
-    const bool have = e < L.E;
-    const uint16_t *gw = static_cast<const uint16_t *>(L.gate_w) +
-                         static_cast<int64_t>(min(e, L.E - 1)) * L.d;
+    if (e >= L.E) return;
     u32x4 w[NCH];
-    if (have) {
-#pragma unroll
-        for (int i = 0; i < NCH; ++i)
-            // ordinary (cacheable) loads: the gate is read again on every token,
-            // while the expert weights streamed between its uses are non-temporal
-            w[i] = reinterpret_cast<const u32x4 *>(gw)[lane + 64 * i];
-    }
-    if (have) {
-        for (int t0 = 0; t0 < L.tokens; t0 += TB) {
-            uint4 xv[TB][NCH];
-#pragma unroll
-            for (int q = 0; q < TB; ++q) {
-                const uint16_t *xr = L.x + static_cast<int64_t>(min(t0 + q, L.tokens - 1)) * L.d;
-#pragma unroll
-                for (int i = 0; i < NCH; ++i)
-                    xv[q][i] = reinterpret_cast<const uint4 *>(xr)[lane + 64 * i];
-            }
-            float acc[TB];
-#pragma unroll
-            for (int q = 0; q < TB; ++q) {
-                acc[q] = 0.f;
-#pragma unroll
-                for (int i = 0; i < NCH; ++i) {
-                    acc[q] = dot2<XBF16>(xv[q][i].x, w[i].x, acc[q]);
-                    acc[q] = dot2<XBF16>(xv[q][i].y, w[i].y, acc[q]);
-                    acc[q] = dot2<XBF16>(xv[q][i].z, w[i].z, acc[q]);
-                    acc[q] = dot2<XBF16>(xv[q][i].w, w[i].w, acc[q]);
-                }
-            }
-            reduce_transposed<TB, 64>(acc, lane);
-            const int q = lane / (64 / TB);
-            if ((lane % (64 / TB)) == 0 && t0 + q < L.tokens)
-                L.logits[static_cast<int64_t>(t0 + q) * L.E + e] = acc[0];
-        }
+    router_load_gate<NCH>(L, e, lane, w);
+    for (int t0 = 0; t0 < L.tokens; t0 += TB) {
+        float acc[TB];
+        router_pass<XBF16, NCH, TB>(L, w, t0, lane, acc);
+        const int q = lane / (64 / TB);
+        if ((lane % (64 / TB)) == 0 && t0 + q < L.tokens)
+            L.logits[static_cast<int64_t>(t0 + q) * L.E + e] = acc[0];
     }
 }
 

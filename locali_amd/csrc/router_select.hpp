@@ -52,40 +52,40 @@ struct SelectOut {
     float w;
 };
 
-template <int NS, int SF, int M>
-__device__ SelectOut select_token(const RouterLaunch &L, int t, const float *logit_row, int64_t split_stride,
-                                  float2 *stage, int rounds) {
-    const int lane = threadIdx.x & 63;
-    float part[NS][M], bias[M];
+// What the selection needs besides the logits, loaded up front at clamped
+// in-bounds addresses: selection bias, the expert -> slot map and the hash row.
+template <int M>
+struct SelectInputs {
+    float bias[M];
     int slot_of[M];
-    int hash_e = -1;
+    int hash_e;
+};
+
+template <int M>
+__device__ __forceinline__ void select_inputs(const RouterLaunch &L, int t, SelectInputs<M> &in) {
+    const int lane = threadIdx.x & 63;
+    in.hash_e = -1;
     if (L.tid2eid) {
         const int id = L.input_ids[t];
         if (id >= 0 && id < L.vocab && lane < L.top_k)
-            hash_e = L.tid2eid[static_cast<int64_t>(id) * L.top_k + lane];
+            in.hash_e = L.tid2eid[static_cast<int64_t>(id) * L.top_k + lane];
     }
 #pragma unroll
     for (int i = 0; i < M; ++i) {
         const int e = min(lane + 64 * i, L.E - 1);
-        if (L.logits_in) {
-            part[0][i] = L.logits_in[static_cast<int64_t>(t) * L.E + e];
-#pragma unroll
-            for (int q = 1; q < NS; ++q) part[q][i] = 0.f;
-        } else {
-#pragma unroll
-            for (int q = 0; q < NS; ++q) part[q][i] = logit_row[q * split_stride + e];
-        }
-        bias[i] = L.bias ? L.bias[e] : 0.f;
-        slot_of[i] = L.slot_of_expert ? L.slot_of_expert[e] : -1;
+        in.bias[i] = L.bias ? L.bias[e] : 0.f;
+        in.slot_of[i] = L.slot_of_expert ? L.slot_of_expert[e] : -1;
     }
+}
+
+// The selection proper on the token's logits (lane l holds experts l + 64 i).
+template <int SF, int M>
+__device__ SelectOut select_core(const RouterLaunch &L, const float (&lg)[M], const SelectInputs<M> &in,
+                                 float2 *stage, int rounds) {
+    const int lane = threadIdx.x & 63;
     float sc[M];
 #pragma unroll
-    for (int i = 0; i < M; ++i) {
-        float l = part[0][i];
-#pragma unroll
-        for (int q = 1; q < NS; ++q) l += part[q][i];
-        sc[i] = lane + 64 * i < L.E ? l : -INFINITY;
-    }
+    for (int i = 0; i < M; ++i) sc[i] = lane + 64 * i < L.E ? lg[i] : -INFINITY;
     float denom = 1.f, lmax = -INFINITY;
     if constexpr (SF == 2) {
 #pragma unroll
@@ -105,8 +105,8 @@ __device__ SelectOut select_token(const RouterLaunch &L, int t, const float *log
         const int e = lane + 64 * i;
         const bool valid = e < L.E;
         const float s = score_of<SF>(valid ? sc[i] : 0.f, lmax, denom);
-        stage[e] = make_float2(s, __int_as_float(slot_of[i]));
-        kh[i] = valid ? ordered_bits(s + bias[i]) : 0u;
+        stage[e] = make_float2(s, __int_as_float(in.slot_of[i]));
+        kh[i] = valid ? ordered_bits(s + in.bias[i]) : 0u;
         kl[i] = valid ? ~static_cast<uint32_t>(e) : 0u;
     }
     // Sort the lane's keys descending (insertion network, M <= 8).
@@ -128,7 +128,7 @@ __device__ SelectOut select_token(const RouterLaunch &L, int t, const float *log
     for (int j = 0; j < rounds; ++j) {
         int best_e;
         if (L.tid2eid) {
-            best_e = __builtin_amdgcn_readlane(hash_e, j);
+            best_e = __builtin_amdgcn_readlane(in.hash_e, j);
             if (best_e >= L.E || best_e < 0) best_e = -1;
         } else {
             uint32_t bh = kh[0], bl = kl[0];
@@ -164,6 +164,130 @@ __device__ SelectOut select_token(const RouterLaunch &L, int t, const float *log
     if (L.norm_topk) w = w / (sum + 1e-20f);
     o.w = w * L.routed_scale;
     return o;
+}
+
+template <int NS, int SF, int M>
+__device__ SelectOut select_token(const RouterLaunch &L, int t, const float *logit_row, int64_t split_stride,
+                                  float2 *stage, int rounds) {
+    const int lane = threadIdx.x & 63;
+    float part[NS][M];
+    SelectInputs<M> in;
+    select_inputs<M>(L, t, in);
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int e = min(lane + 64 * i, L.E - 1);
+        if (L.logits_in) {
+            part[0][i] = L.logits_in[static_cast<int64_t>(t) * L.E + e];
+#pragma unroll
+            for (int q = 1; q < NS; ++q) part[q][i] = 0.f;
+        } else {
+#pragma unroll
+            for (int q = 0; q < NS; ++q) part[q][i] = logit_row[q * split_stride + e];
+        }
+    }
+    float lg[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        float l = part[0][i];
+#pragma unroll
+        for (int q = 1; q < NS; ++q) l += part[q][i];
+        lg[i] = l;
+    }
+    return select_core<SF, M>(L, lg, in, stage, rounds);
+}
+
+// ---------------------------------------------------------------------------
+// Logits handed from the router rows of the fused decode kernel: word e of a
+// token's row is (tag << 32) | fp32 bits, written by one relaxed agent-scope
+// 64-bit store, so a word is either wholly this call's or stale. The wave
+// polls the row (relaxed agent-scope loads: coherent across the XCDs' L2s)
+// until every word carries `tag`, sleeping between polls. Bounded: after
+// kSyncMaxSpins polls it gives up and returns false.
+constexpr uint32_t kSyncMaxSpins = 1u << 18;
+
+template <int M>
+__device__ __forceinline__ bool poll_logits(const uint64_t *row, int E, uint32_t tag, float (&lg)[M]) {
+    const int lane = threadIdx.x & 63;
+    for (uint32_t spin = 0;; ++spin) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            const uint64_t v = __hip_atomic_load(row + min(lane + 64 * i, E - 1), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+            ok = ok && static_cast<uint32_t>(v >> 32) == tag;
+            lg[i] = __uint_as_float(static_cast<uint32_t>(v));
+        }
+        if (__all(ok)) return true;
+        if (spin >= kSyncMaxSpins) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// select_token on logits polled from the sync row of token t. If they never
+// arrive the token gets no routes (expert -1, slot -1, weight 0).
+template <int SF, int M>
+__device__ SelectOut select_token_polled(const RouterLaunch &L, int t, uint32_t tag, float2 *stage, int rounds) {
+    SelectInputs<M> in;
+    select_inputs<M>(L, t, in);
+    float lg[M];
+    if (!poll_logits<M>(L.sync_logits + static_cast<int64_t>(t) * L.E, L.E, tag, lg)) {
+        SelectOut o;
+        o.e = -1;
+        o.slot = -1;
+        o.w = 0.f;
+        return o;
+    }
+    return select_core<SF, M>(L, lg, in, stage, rounds);
+}
+
+template <int M>
+__device__ SelectOut select_token_polled_any(const RouterLaunch &L, int t, uint32_t tag, float2 *stage, int rounds) {
+    switch (L.score_func) {
+    case 0: return select_token_polled<0, M>(L, t, tag, stage, rounds);
+    case 1: return select_token_polled<1, M>(L, t, tag, stage, rounds);
+    default: return select_token_polled<2, M>(L, t, tag, stage, rounds);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Router logits of one expert by one wave: the lane's NCH 16-byte chunks of
+// the gate row (router_load_gate), then per pass of TB tokens (tokens past
+// L.tokens re-read the last one) the x chunks, the dots and a transposed
+// reduction after which lane q * (64 / TB) holds token t0 + q's logit. The
+// logits kernel and the fused decode kernel both use these, so their logits
+// are the same bits.
+template <int NCH>
+__device__ __forceinline__ void router_load_gate(const RouterLaunch &L, int e, int lane, u32x4 (&w)[NCH]) {
+    const uint16_t *gw = static_cast<const uint16_t *>(L.gate_w) + static_cast<int64_t>(e) * L.d;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i)
+        // ordinary (cacheable) loads: the gate is read again on every token,
+        // while the expert weights streamed between its uses are non-temporal
+        w[i] = reinterpret_cast<const u32x4 *>(gw)[lane + 64 * i];
+}
+
+template <bool XBF16, int NCH, int TB>
+__device__ __forceinline__ void router_pass(const RouterLaunch &L, const u32x4 (&w)[NCH], int t0, int lane,
+                                            float (&acc)[TB]) {
+    uint4 xv[TB][NCH];
+#pragma unroll
+    for (int q = 0; q < TB; ++q) {
+        const uint16_t *xr = L.x + static_cast<int64_t>(min(t0 + q, L.tokens - 1)) * L.d;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) xv[q][i] = reinterpret_cast<const uint4 *>(xr)[lane + 64 * i];
+    }
+#pragma unroll
+    for (int q = 0; q < TB; ++q) {
+        acc[q] = 0.f;
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            acc[q] = dot2<XBF16>(xv[q][i].x, w[i].x, acc[q]);
+            acc[q] = dot2<XBF16>(xv[q][i].y, w[i].y, acc[q]);
+            acc[q] = dot2<XBF16>(xv[q][i].z, w[i].z, acc[q]);
+            acc[q] = dot2<XBF16>(xv[q][i].w, w[i].w, acc[q]);
+        }
+    }
+    reduce_transposed<TB, 64>(acc, lane);
 }
 
 // Stores token t's choices (lanes < top_k).

@@ -660,6 +660,65 @@ def test_decode_forward_in_separate_stages(T):
     assert torch.equal(rs, idx + 1)
 
 
+@pytest.mark.parametrize("d,dtype", [(4096, torch.bfloat16), (2048, torch.float16), (1024, torch.bfloat16)])
+def test_fused_router_rows_across_calls_and_replays(d, dtype):
+    """The decode forward computes the logits in router rows of its gate/up
+    kernel and hands them over as tagged words. Consecutive calls on one
+    workspace alternate between routers and between 1 and 2 tokens, so a call
+    that read the previous call's words would route like that call: every
+    call must equal the separate logits -> gate/up -> down chain bit for bit,
+    eagerly and under repeated graph replays."""
+    banner(f"fused router rows d={d} {dt_name(dtype)}")
+    E, dff, k = 256, 1024, 6
+    arena = synth.expert_arena(E + 1, d, dff, dtype=dtype, seed=91, device=DEV)
+    shared = synth.expert_arena(1, d, dff, dtype=dtype, seed=92, device=DEV, zero_slot=False)
+    specs = []
+    for i in range(3):
+        w, bias = synth.uniform_router(E, d, dtype, seed=93 + i, device=DEV, bias_std=0.01)
+        specs.append(ops.RouterSpec(w, k, routed_scale=1.5, score_bias=bias))
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    xs = [synth.activations(1 + (i % 2), d, dtype, seed=95 + i, device=DEV) for i in range(6)]
+    xs[1] = torch.cat([xs[0], xs[0]])          # same input, next router
+    calls = [(specs[i % 3], xs[i]) for i in range(6)]
+
+    def chain(spec, x):
+        T = x.shape[0]
+        ws = ops.Workspace()
+        logits = ops.router_logits(spec, x)
+        hidden = torch.empty(T * (k + 1), dff, dtype=dtype, device=DEV)
+        idx, wts, rs = ops.decode_gateup_select(spec, arena, shared, slot_of, x, logits, hidden, ws)
+        out = torch.empty_like(x)
+        ops.decode_down_combine(arena, shared, rs, wts, out, ws)
+        return out, idx, wts
+
+    want = [chain(s, x) for s, x in calls]
+    ws = ops.Workspace()
+    got = [ops.forward(s, arena, shared, slot_of, x, ws) for s, x in calls]
+    torch.cuda.synchronize()
+    for i, (g, w_) in enumerate(zip(got, want)):
+        for a, b in zip(g, w_):
+            assert torch.equal(a, b), f"eager call {i}"
+    assert not torch.equal(got[0][1][0], got[1][1][0]), "consecutive routers chose alike; the test is blind"
+    outs = [torch.empty_like(x) for _, x in calls]
+    idxs = [torch.empty(x.shape[0], k, dtype=torch.int32, device=DEV) for _, x in calls]
+    wtss = [torch.empty(x.shape[0], k, dtype=torch.float32, device=DEV) for _, x in calls]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i, (s, x) in enumerate(calls):
+            ops.forward(s, arena, shared, slot_of, x, ws, out=outs[i], idx=idxs[i], weights=wtss[i])
+    for rep in range(3):
+        for t in outs + idxs + wtss:
+            t.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        for i, w_ in enumerate(want):
+            assert torch.equal(outs[i], w_[0]) and torch.equal(idxs[i], w_[1]) and torch.equal(wtss[i], w_[2]), \
+                f"replay {rep} call {i}"
+        # eager work between replays on the same workspace
+        ops.forward(calls[0][0], arena, shared, slot_of, calls[0][1], ws)
+        torch.cuda.synchronize()
+
+
 def test_forward_full_width_decode(oracle_lib):
     """d 4096, 256 experts + shared, d_ff 2048, 2-bit g64 bf16, 1 token; checked
     against the C oracle (fp32) on the GPU's own routing."""
