@@ -216,6 +216,24 @@ int locali_moe_expert_grouped(const locali_expert_arena *routed,
                               int32_t combine_mode, void *out, void *workspace,
                               size_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference: locali_moe_expert_grouped that also hands
+ * out its intermediates, for stage-wise parity tests of the grouped kernels.
+ * Positions p are the grouped order (routed routes sorted by slot, then the
+ * shared expert's route of each token at R + t, R = tokens * top_k):
+ * h_out [routes, d_ff] holds the gate/up + SwiGLU output of every position,
+ * y_out [routes, d_model] the down projection rounded to the activation
+ * dtype, route_pos_out [R] the position of route t * top_k + j. out is the
+ * combined output as locali_moe_expert_grouped writes it. */
+int locali_moe_expert_grouped_stages(const locali_expert_arena *routed,
+                                     const locali_expert_arena *shared, const void *x,
+                                     int32_t x_dtype, int32_t tokens, int32_t top_k,
+                                     int32_t n_experts, const int32_t *idx,
+                                     const int32_t *slot_of_expert, const float *weights,
+                                     float swiglu_limit, int32_t fp32_swiglu,
+                                     int32_t combine_mode, void *out, void *h_out,
+                                     void *y_out, int32_t *route_pos_out, void *workspace,
+                                     size_t workspace_bytes, void *stream);
+
 /* The prefill entry point (the many-token path of V4ArenaMoE._gather,
  * dsv4_arena.py:168-235, grouped by slot as arena.py:641-672): the same call
  * as locali_moe_expert_grouped, under the name the decode / prefill split of
@@ -276,12 +294,13 @@ int locali_moe_arena_fill_batch(const locali_fill_piece *pieces, int32_t n, void
  * ArenaStore.submit, arena.py:356-435): expert i's records lie back to back
  * in host memory at src_host[i] (record a is slot_bytes[a] bytes), and record
  * a lands at dst_base[a] + slots[i] * slot_bytes[a], array a being the
- * slot-major device array of (projection, weight/scales/biases) a. Same copy
- * kernel and rules as locali_moe_arena_fill_batch; the arrays' and slots'
- * bounds are the caller's. */
+ * slot-major device array of (projection, weight/scales/biases) a. Every
+ * array holds n_slots slots; a slot outside [0, n_slots) fails the call with
+ * LOCALI_E_ARG before anything is queued. Same copy kernel and rules as
+ * locali_moe_arena_fill_batch. */
 int locali_moe_arena_fill_slots(void *const *dst_base, const size_t *slot_bytes, int32_t n_arrays,
-                                const int32_t *slots, const void *const *src_host, int32_t n,
-                                void *stream);
+                                int32_t n_slots, const int32_t *slots, const void *const *src_host,
+                                int32_t n, void *stream);
 
 /* Whole layer on an all-resident arena: router, dispatch (decode or grouped
  * by token count), experts, combine, shared expert. out [tokens, d_model]. */

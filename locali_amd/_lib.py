@@ -129,6 +129,9 @@ _SIGNATURES = {
                                    _I, _I, _I, _P, _P, _P, _F, _I, _I, _P, _P, _SZ, _P], ctypes.c_int),
     "locali_moe_expert_prefill": ([ctypes.POINTER(ExpertArena), ctypes.POINTER(ExpertArena), _P, _I,
                                    _I, _I, _I, _P, _P, _P, _F, _I, _I, _P, _P, _SZ, _P], ctypes.c_int),
+    "locali_moe_expert_grouped_stages": ([ctypes.POINTER(ExpertArena), ctypes.POINTER(ExpertArena), _P, _I,
+                                          _I, _I, _I, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P, _P, _SZ, _P],
+                                         ctypes.c_int),
     "locali_moe_router_logits": ([ctypes.POINTER(Router), _P, _I, _I, _I, _P, _P], ctypes.c_int),
     "locali_moe_decode_gateup_select": ([ctypes.POINTER(Router), ctypes.POINTER(ExpertArena),
                                          ctypes.POINTER(ExpertArena), _P, _P, _I, _I, _P, _P, _F, _I, _P, _P,
@@ -137,7 +140,7 @@ _SIGNATURES = {
     "locali_moe_combine_routes": ([_P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P], ctypes.c_int),
     "locali_moe_arena_fill": ([_P, _P, _SZ, _P], ctypes.c_int),
     "locali_moe_arena_fill_batch": ([ctypes.POINTER(FillPiece), ctypes.c_int32, _P], ctypes.c_int),
-    "locali_moe_arena_fill_slots": ([ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t), _I,
+    "locali_moe_arena_fill_slots": ([ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t), _I, _I,
                                      ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_void_p), _I, _P],
                                     ctypes.c_int),
     "locali_moe_forward": ([ctypes.POINTER(Router), ctypes.POINTER(ExpertArena),

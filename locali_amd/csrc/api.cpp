@@ -321,7 +321,7 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
                      const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k, int32_t n_experts,
                      const int32_t *route_slot, const float *weights, float limit,
                      int32_t fp32_swiglu, int32_t combine_mode, void *out, void *ws,
-                     const Layout &lay, hipStream_t st) {
+                     const Layout &lay, hipStream_t st, uint16_t *h_plain) {
     const int R = tokens * top_k;
     const int n_slots = routed->gate.n_slots;
     const int routes = R + (shared ? tokens : 0);
@@ -356,6 +356,7 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     L.sdown = to_dev(sh->down);
     L.xin = mfma_batch(at<void>(ws, lay.mx), tokens, routed->gate.cols);
     L.hmid = mfma_batch(at<void>(ws, lay.mh), routes, routed->down.cols);
+    L.hmid.plain = h_plain;
     L.hsum32 = at<float2>(ws, lay.gh);   // the VALU path's h buffer is free here
     L.y = gy;
     L.limit = limit;
@@ -380,10 +381,14 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
 int run_grouped(const locali_expert_arena *routed, const locali_expert_arena *shared, const void *x,
                 int32_t x_dtype, int32_t tokens, int32_t top_k, int32_t n_experts,
                 const int32_t *route_slot, const float *weights, float limit, int32_t fp32_swiglu,
-                int32_t combine_mode, void *out, void *ws, const Layout &lay, hipStream_t st) {
-    if (mfma_eligible(routed, shared, tokens, static_cast<int64_t>(tokens) * (top_k + (shared ? 1 : 0))))
+                int32_t combine_mode, void *out, void *ws, const Layout &lay, hipStream_t st,
+                uint16_t *h_plain = nullptr, bool *on_mfma = nullptr) {
+    const bool mfma =
+        mfma_eligible(routed, shared, tokens, static_cast<int64_t>(tokens) * (top_k + (shared ? 1 : 0)));
+    if (on_mfma) *on_mfma = mfma;
+    if (mfma)
         return run_grouped_mfma(routed, shared, x, x_dtype, tokens, top_k, n_experts, route_slot, weights, limit,
-                                fp32_swiglu, combine_mode, out, ws, lay, st);
+                                fp32_swiglu, combine_mode, out, ws, lay, st, h_plain);
     const int R = tokens * top_k;
     const int n_slots = routed->gate.n_slots;
     int32_t *seg_start = at<int32_t>(ws, lay.seg_start);
@@ -613,6 +618,50 @@ int locali_moe_expert_grouped(const locali_expert_arena *routed, const locali_ex
                        swiglu_limit, fp32_swiglu, combine_mode, out, workspace, lay, S(stream));
 }
 
+int locali_moe_expert_grouped_stages(const locali_expert_arena *routed, const locali_expert_arena *shared,
+                                     const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k,
+                                     int32_t n_experts, const int32_t *idx, const int32_t *slot_of_expert,
+                                     const float *weights, float swiglu_limit, int32_t fp32_swiglu,
+                                     int32_t combine_mode, void *out, void *h_out, void *y_out,
+                                     int32_t *route_pos_out, void *workspace, size_t workspace_bytes,
+                                     void *stream) {
+    if (tokens == 0) return 0;   // an empty batch is a no-op
+    int rc, dff = 0;
+    if (!x || !dtype16(x_dtype) || tokens < 1 || top_k < 1 || !idx || !slot_of_expert || !weights || !out ||
+        !h_out || !y_out || !route_pos_out || !workspace || n_experts < 1 || !routed)
+        return fail(LOCALI_E_ARG, "expert_grouped_stages: bad arguments");
+    const int d = routed->gate.cols;
+    if ((rc = check_arena(routed, "routed", x_dtype, d, &dff))) return rc;
+    if ((rc = check_shared(routed, shared))) return rc;
+    if (routed->gate.n_slots > kMaxSlots)
+        return fail(LOCALI_E_ARG, "expert_grouped_stages: n_slots > %d", kMaxSlots);
+    const Layout lay = layout(tokens, d, dff, n_experts, top_k, shared ? 1 : 0);
+    if (workspace_bytes < lay.total)
+        return fail(LOCALI_E_WORKSPACE, "expert_grouped_stages: workspace %zu < %zu bytes", workspace_bytes,
+                    lay.total);
+    const hipStream_t st = S(stream);
+    int32_t *route_slot = at<int32_t>(workspace, lay.route_slot);
+    hipError_t e = launch_route_slots(idx, tokens * top_k, n_experts, slot_of_expert, routed->gate.n_slots,
+                                      route_slot, st);
+    if (e != hipSuccess) return hip_fail(e, "route slot launch");
+    bool mfma = false;
+    if ((rc = run_grouped(routed, shared, x, x_dtype, tokens, top_k, n_experts, route_slot, weights, swiglu_limit,
+                          fp32_swiglu, combine_mode, out, workspace, lay, st, static_cast<uint16_t *>(h_out),
+                          &mfma)))
+        return rc;
+    const size_t R = static_cast<size_t>(tokens) * top_k, routes = R + (shared ? tokens : 0);
+    if (!mfma &&   // the VALU kernels keep h by position in the workspace
+        (e = hipMemcpyAsync(h_out, at<void>(workspace, lay.gh), routes * dff * sizeof(uint16_t),
+                            hipMemcpyDeviceToDevice, st)) != hipSuccess)
+        return hip_fail(e, "expert_grouped_stages h copy");
+    if ((e = hipMemcpyAsync(y_out, at<void>(workspace, lay.gy), routes * d * sizeof(uint16_t),
+                            hipMemcpyDeviceToDevice, st)) != hipSuccess ||
+        (e = hipMemcpyAsync(route_pos_out, at<void>(workspace, lay.route_pos), R * sizeof(int32_t),
+                            hipMemcpyDeviceToDevice, st)) != hipSuccess)
+        return hip_fail(e, "expert_grouped_stages copies");
+    return 0;
+}
+
 int locali_moe_combine(const void *y, const void *shared_y, const float *weights, int32_t dtype,
                        int32_t tokens, int32_t top_k, int32_t d, int32_t combine_mode, void *out,
                        void *stream) {
@@ -734,16 +783,21 @@ int locali_moe_arena_fill_batch(const locali_fill_piece *pieces, int32_t n, void
 }
 
 int locali_moe_arena_fill_slots(void *const *dst_base, const size_t *slot_bytes, int32_t n_arrays,
-                                const int32_t *slots, const void *const *src_host, int32_t n, void *stream) {
-    if (n < 0 || n_arrays < 1 || (n > 0 && (!dst_base || !slot_bytes || !slots || !src_host)))
+                                int32_t n_slots, const int32_t *slots, const void *const *src_host, int32_t n,
+                                void *stream) {
+    if (n < 0 || n_arrays < 1 || n_slots < 1 || (n > 0 && (!dst_base || !slot_bytes || !slots || !src_host)))
         return fail(LOCALI_E_ARG, "arena_fill_slots: bad arguments");
     for (int32_t a = 0; a < n_arrays; ++a)
         if (!dst_base[a]) return fail(LOCALI_E_ARG, "arena_fill_slots: null array %d", a);
+    // every argument is checked before the first copy is queued
+    for (int32_t i = 0; i < n; ++i) {
+        if (!src_host[i]) return fail(LOCALI_E_ARG, "arena_fill_slots: null source %d", i);
+        if (slots[i] < 0 || slots[i] >= n_slots)
+            return fail(LOCALI_E_ARG, "arena_fill_slots: slot %d of expert %d outside [0, %d)", slots[i], i, n_slots);
+    }
     FillQueue q(S(stream), "arena_fill_slots");
     for (int32_t i = 0; i < n; ++i) {
         const char *src = static_cast<const char *>(src_host[i]);
-        if (!src) return fail(LOCALI_E_ARG, "arena_fill_slots: null source %d", i);
-        if (slots[i] < 0) return fail(LOCALI_E_ARG, "arena_fill_slots: slot %d of expert %d", slots[i], i);
         const char *dev = static_cast<const char *>(device_view(src));
         size_t off = 0;
         for (int32_t a = 0; a < n_arrays; ++a) {

@@ -64,6 +64,7 @@ constexpr uint32_t kPubMaxSpins = 1u << 22;    // about a second of polling
 constexpr uint8_t kNowhere = 0, kProbation = 1, kProtected = 2;
 constexpr size_t kPlanMaxLds = 160 * 1024;
 constexpr size_t kPlanMaxDynamicLds = kPlanMaxLds - 4096;   // the rest is the kernel's static LDS
+constexpr size_t kDefaultLds = 64 * 1024;                   // per workgroup without the attribute
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -255,12 +256,23 @@ __device__ inline void copy_chunk(const DPlanFillArgs &a, const u32x4 *__restric
     }
 }
 
+// Every workgroup of the fused launch (the planner and each copy workgroup)
+// counts its exit; the last one to leave sets the publication word back to
+// zero for the next call. The planner counts too, so that a publication it
+// makes after copy workgroups gave up waiting cannot outlive the launch.
+__device__ inline void fused_exit(DPlanHeader *H) {
+    const int before = __hip_atomic_fetch_add(&H->exited, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (before == static_cast<int>(gridDim.x) - 1) {
+        __hip_atomic_store(&H->exited, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&H->pub, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // A copy workgroup of the fused kernel (blockIdx.x >= 1): chunks g, g + G,
 // ... of the misses' payloads in list order, each once the planner
 // workgroup has published its miss. Thread 0 polls the publication word and
 // hands it to the workgroup through LDS, so the branch stays uniform; every
-// workgroup leaves once the list is closed and its chunks are copied, and
-// the last one to leave sets the word back to zero for the next call.
+// workgroup leaves once the list is closed and its chunks are copied.
 __device__ void copy_workgroup(unsigned char *state, const DPlanLayout &G, const DPlanFillArgs &a,
                                const uint64_t *__restrict__ host_src, int layer, int E, PlanShared &sh) {
     DPlanHeader *H = reinterpret_cast<DPlanHeader *>(state);
@@ -304,13 +316,7 @@ __device__ void copy_workgroup(unsigned char *state, const DPlanLayout &G, const
         if (src) copy_chunk<kPlanThreads, kFusedUnits>(a, src, slot, c % chunks, units);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const int before = __hip_atomic_fetch_add(&H->exited, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        if (before == copiers - 1) {
-            __hip_atomic_store(&H->exited, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&H->pub, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
+    if (threadIdx.x == 0) fused_exit(H);
 }
 
 // Thread 0's planner state for one call (registers) and the list operations
@@ -385,7 +391,10 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     if (H->n_keys != n_keys || H->n_slots != n_slots || H->policy != policy || H->max_routes != max_routes) {
         if (tid == 0) {
             if (!H->error) H->error = LOCALI_DPLAN_E_CONFIG;
-            if (kFused) __hip_atomic_store(&H->pub, kPubClosed, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            if (kFused) {
+                __hip_atomic_store(&H->pub, kPubClosed, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                fused_exit(H);
+            }
         }
         return;
     }
@@ -668,6 +677,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
         H->calls += 1;
         if (sh.bad && !H->error) H->error = LOCALI_DPLAN_E_EXPERT;
         if (fails && !H->error) H->error = LOCALI_DPLAN_E_PLACE;
+        if (kFused) fused_exit(H);
     }
 }
 
@@ -779,14 +789,19 @@ int plan_launch(bool fused, void *state, int32_t key_capacity, int32_t slots, in
     if (lds > kPlanMaxDynamicLds)
         return dfail(LOCALI_E_ARG, "dplan_plan: %d slots need %zu bytes of LDS; at most %zu", slots, lds,
                      kPlanMaxDynamicLds);
-    static const hipError_t attr0 = hipFuncSetAttribute(reinterpret_cast<const void *>(&dplan_kernel<false>),
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                        static_cast<int>(kPlanMaxDynamicLds));
-    static const hipError_t attr1 = hipFuncSetAttribute(reinterpret_cast<const void *>(&dplan_kernel<true>),
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                        static_cast<int>(kPlanMaxDynamicLds));
-    const hipError_t attr = fused ? attr1 : attr0;
-    if (attr != hipSuccess) return dhip(attr, "dplan_plan attribute");
+    // Above the default 64 KiB per workgroup the kernels need the larger
+    // LDS allowance (gfx950: 160 KiB); requested once per kernel, and only by
+    // a state that needs it, so that small states run wherever 64 KiB do.
+    if (lds + (kPlanMaxLds - kPlanMaxDynamicLds) > kDefaultLds) {
+        static const hipError_t attr0 = hipFuncSetAttribute(reinterpret_cast<const void *>(&dplan_kernel<false>),
+                                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                            static_cast<int>(kPlanMaxDynamicLds));
+        static const hipError_t attr1 = hipFuncSetAttribute(reinterpret_cast<const void *>(&dplan_kernel<true>),
+                                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                            static_cast<int>(kPlanMaxDynamicLds));
+        const hipError_t attr = fused ? attr1 : attr0;
+        if (attr != hipSuccess) return dhip(attr, "dplan_plan attribute (LDS beyond 64 KiB per workgroup)");
+    }
     const hipStream_t st = static_cast<hipStream_t>(stream);
     unsigned char *sp = static_cast<unsigned char *>(state);
     if (fused)

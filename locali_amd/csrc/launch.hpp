@@ -43,6 +43,9 @@ struct MfmaVec {
     uint32_t *pairs;
     uint4 *fix;
     int64_t pairs_stride, fix_stride;
+    // optional (the grouped gate/up kernels' h, for stage-wise tests): the
+    // vectors' plain values, [vec][2 * pairs_stride]
+    uint16_t *plain;
 };
 
 struct RouterLaunch;

@@ -204,6 +204,7 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
             u += red[w][rt][1][p][n];
         }
         hs[p][q] = swiglu16<BF16>(round16<BF16>(g), round16<BF16>(u), limit, fp32_swiglu != 0);
+        if (hout.plain) hout.plain[static_cast<int64_t>(ti.first + p) * N + n0 + q] = hs[p][q];
     }
     const int vpw = 32 / down_bits, words = kSmallRows / vpw;
     float2 part = make_float2(0.f, 0.f);

@@ -434,10 +434,13 @@ __device__ __forceinline__ void wide_gateup_tile(const TileArgs &ta, const QProj
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int q = 16 * tb + 4 * kb + i;
-                hs[q][wave * 16 + nl] =
+                const uint16_t hv =
                     q < count ? swiglu16<BF16>(round16<BF16>(acc[0][tb][i]), round16<BF16>(acc[1][tb][i]), limit,
                                                fp32_swiglu != 0)
                               : static_cast<uint16_t>(0);
+                hs[q][wave * 16 + nl] = hv;
+                if (hout.plain && q < count)
+                    hout.plain[(first + q) * 2 * hout.pairs_stride + n0 + wave * 16 + nl] = hv;
             }
         }
     }

@@ -73,6 +73,7 @@ class V4ArenaStore(ArenaStore):
                                        n_experts=self.E, policy=policy, device=self.device)
             self._dplan_src = None
             self._dplan_base = None
+            self._dplan_pinned = 0   # distinct slots of the previous demand call
 
     def _key_id(self, key):
         layer, expert = key
@@ -221,8 +222,18 @@ class V4ArenaStore(ArenaStore):
         call's misses are copied by the same launch, each starting as soon
         as the planner has placed it, on the current stream."""
         t = self.tiers[0]
+        # The kernel cannot raise: a demanded key it could not place would
+        # read the zero slot. Calls that might not place every key are
+        # refused here, where the host planner would raise.
+        keys = min(int(expert_idx.numel()), self.E)
+        if not self.dplan.demand_fits(keys, self._dplan_pinned):
+            raise RuntimeError(f"device planner: a call of {keys} experts with {self._dplan_pinned} slots of "
+                               f"the previous call pinned may find no unpinned slot (probation holds "
+                               f"{self.dplan.probation_capacity} keys); use a larger arena or the host planner")
         src = self._dplan_sources(t)
-        return self.dplan.plan_fill(expert_idx, layer, self.top_k, self._slot_table(t), src)
+        slots = self.dplan.plan_fill(expert_idx, layer, self.top_k, self._slot_table(t), src)
+        self._dplan_pinned = keys
+        return slots
 
     def _dplan_counters(self):
         c, _ = self.dplan.read()

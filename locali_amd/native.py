@@ -148,6 +148,9 @@ class DevicePlanner:
         self.key_capacity, self.slots, self.n_experts = key_capacity, slots, n_experts
         self.policy = POLICIES[policy]
         self.max_routes = max_routes
+        # keys that probation holds when it is full (LFU-decay keeps every
+        # key there); see demand_fits
+        self.probation_capacity = slots - 1 - (protected_capacity if policy == "slru" else 0)
         lds = self._lib.locali_dplan_lds_bytes(slots, n_experts, self.policy)
         if lds > self.LDS_LIMIT:
             raise ValueError(f"device planner: {slots} slots x {n_experts} experts need {lds} bytes of LDS "
@@ -162,6 +165,21 @@ class DevicePlanner:
                                                  protected_capacity, self.policy, max_routes, _stream()),
                    "locali_dplan_init")
         self._table = None
+
+    @staticmethod
+    def placement_certain(keys: int, pinned: int, probation_capacity: int) -> bool:
+        """True when a call of `keys` distinct keys, with `pinned` slots of
+        the previous call pinned, places every key whatever the planner's
+        state (native/locali_core.c:113-180). A key finds no slot only when
+        every resident key is pinned and no free slot may be taken: under
+        SLRU that needs a full probation segment or no free slot, under
+        LFU-decay no free slot, and either way at least probation_capacity
+        resident keys. At most pinned + keys - 1 slots are pinned when the
+        call's last key is planned."""
+        return keys + pinned <= probation_capacity
+
+    def demand_fits(self, keys: int, pinned: int) -> bool:
+        return self.placement_certain(keys, pinned, self.probation_capacity)
 
     def plan(self, expert_idx, layer: int, top_k: int, *, touch_hits: bool = True, out=None):
         """Slots of the routes in expert_idx (device int32, any shape) for
@@ -183,7 +201,7 @@ class DevicePlanner:
 
     def _records(self, table):
         if self._table is None or self._table[0] is not table:
-            base, per = table
+            base, per = table[0], table[1]
             self._table = (table, (ctypes.c_void_p * len(base))(*base), (ctypes.c_size_t * len(per))(*per),
                            len(base))
         return self._table[1:]

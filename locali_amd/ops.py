@@ -383,6 +383,37 @@ def expert_grouped(arena: ExpertArenaT, shared: ExpertArenaT | None, x: torch.Te
     return out.reshape(x.shape)
 
 
+def expert_grouped_stages(arena: ExpertArenaT, shared: ExpertArenaT | None, x: torch.Tensor,
+                          idx: torch.Tensor, slot_of_expert: torch.Tensor, weights: torch.Tensor,
+                          ws: Workspace, *, n_experts=None, swiglu_limit=10.0, fp32_swiglu=False,
+                          combine_mode=COMBINE_ROUNDED):
+    """expert_grouped that also returns its intermediates
+    (locali_moe_expert_grouped_stages): (out, h [routes, d_ff], y [routes,
+    d_model]) with route r = t * top_k + j, and the shared expert's route of
+    token t at T * top_k + t."""
+    x2 = _flat(x)
+    T = x2.shape[0]
+    k = idx.shape[-1]
+    E = int(n_experts or slot_of_expert.numel())
+    routes = T * k + (T if shared is not None else 0)
+    buf = ws.reserve(T, arena.d_model, arena.d_ff, E, k, shared is not None)
+    out = torch.empty_like(x2)
+    h = torch.empty(routes, arena.d_ff, dtype=x2.dtype, device=x2.device)
+    y = torch.empty(routes, arena.d_model, dtype=x2.dtype, device=x2.device)
+    pos = torch.empty(T * k, dtype=torch.int32, device=x2.device)
+    a = arena.struct()
+    s = shared.struct() if shared is not None else None
+    rc = lib().locali_moe_expert_grouped_stages(ctypes.byref(a), ctypes.byref(s) if s is not None else None,
+                                                _ptr(x2), _dt(x2), T, k, E, _ptr(idx.contiguous()),
+                                                _ptr(slot_of_expert), _ptr(weights.contiguous()),
+                                                float(swiglu_limit), int(fp32_swiglu), int(combine_mode),
+                                                _ptr(out), _ptr(h), _ptr(y), _ptr(pos), _ptr(buf), buf.numel(),
+                                                _stream())
+    check(rc, "locali_moe_expert_grouped_stages")
+    order = torch.cat([pos.long(), torch.arange(T * k, routes, device=x2.device)])
+    return out.reshape(x.shape), h[order], y[order]
+
+
 def combine(y: torch.Tensor, weights: torch.Tensor, shared_y=None, mode=COMBINE_ROUNDED):
     T, k, d = y.shape
     out = torch.empty(T, d, dtype=y.dtype, device=y.device)
@@ -457,11 +488,11 @@ def arena_fill_batch_ptrs(pieces, stream) -> None:
 
 
 def slot_table(arrays) -> tuple:
-    """(dst_base, slot_bytes) ctypes arrays of slot-major device arrays, in
-    record order, for arena_fill_slots."""
+    """(dst_base, slot_bytes, n_slots) of slot-major device arrays, in record
+    order, for arena_fill_slots (n_slots: the smallest leading dimension)."""
     base = (ctypes.c_void_p * len(arrays))(*(a.data_ptr() for a in arrays))
     per = (ctypes.c_size_t * len(arrays))(*(a[0].numel() * a.element_size() for a in arrays))
-    return base, per
+    return base, per, min(int(a.shape[0]) for a in arrays)
 
 
 def arena_fill_slots(table, slots, sources, stream) -> None:
@@ -471,10 +502,10 @@ def arena_fill_slots(table, slots, sources, stream) -> None:
     sources go through the copy kernel; the host memory must stay until the
     stream has passed the copy."""
     n = len(slots)
-    base, per = table
+    base, per, n_slots = table
     sl = (ctypes.c_int32 * max(n, 1))(*slots)
     src = (ctypes.c_void_p * max(n, 1))(*sources)
-    rc = lib().locali_moe_arena_fill_slots(base, per, len(base), sl, src, n, stream.cuda_stream)
+    rc = lib().locali_moe_arena_fill_slots(base, per, len(base), n_slots, sl, src, n, stream.cuda_stream)
     check(rc, "locali_moe_arena_fill_slots")
 
 

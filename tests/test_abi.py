@@ -76,3 +76,18 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(_lib.LocaliError):
         _lib.lib()
+
+
+@pytest.mark.parametrize("slot", [-1, 97, 1 << 30])
+def test_fill_slots_refuses_a_slot_outside_the_arena(slot):
+    """A slot outside [0, n_slots) is an argument error, reported before any
+    copy is queued (the pointers are never dereferenced, so fakes do)."""
+    lib = _lib.lib()
+    n_arrays, n_slots = 9, 97
+    base = (ctypes.c_void_p * n_arrays)(*([0x1000] * n_arrays))
+    per = (ctypes.c_size_t * n_arrays)(*([4096] * n_arrays))
+    slots = (ctypes.c_int32 * 2)(3, slot)
+    src = (ctypes.c_void_p * 2)(0x2000, 0x3000)
+    rc = lib.locali_moe_arena_fill_slots(base, per, n_arrays, n_slots, slots, src, 2, None)
+    assert rc == -1
+    assert b"outside [0, 97)" in lib.locali_moe_last_error()

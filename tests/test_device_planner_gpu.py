@@ -174,3 +174,48 @@ def test_fused_plan_fill_equals_plan_then_fill(policy, multi):
         assert torch.equal(got, payload[[layer * E + e for e in routes]]), f"payload of call {c}"
         n_multi_miss += sum(not r.hit for r in want_res) > 1
     assert n_multi_miss > 20
+
+
+@pytest.mark.parametrize("policy,slots,n_calls,tokens", [
+    ("slru", 43 * 96 + 1, 43 * 14, (1, 1, 4, 16)),
+    ("lfu-decay", 43 * 96 + 1, 43 * 14, (1, 1, 4, 16)),
+    ("slru", 43 * 192 + 1, 43 * 30, (1, 4, 16, 16)),
+])
+def test_device_planner_at_the_stack_geometry(policy, slots, n_calls, tokens):
+    """The geometry the 43-layer bench leg runs: 43 layers x 256 experts
+    (11,008 keys) over 4,129 slots (and 8,257 under SLRU, beyond 8,000), the
+    store's protected segment (slots - 1) // 2 under SLRU. Each thread of
+    the planner workgroup then scans several slots per victim search, and the
+    slot state fills most of the LDS. Zipf(1.1) calls of 1 to 16 tokens
+    through the layers in order; every per-key result, every route's slot
+    and the counters equal the host planner's, and the arena churns."""
+    layers, E, top_k = 43, 256, 6
+    pcap = (slots - 1) // 2 if policy == "slru" else 0
+    rng = np.random.default_rng(slots + (1 if policy == "slru" else 2))
+    ranks = [rng.permutation(E) for _ in range(layers)]
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    calls = []
+    for c in range(n_calls):
+        routes = []
+        for _ in range(int(rng.choice(tokens))):
+            routes.extend(int(ranks[c % layers][i]) for i in rng.choice(E, size=top_k, replace=False, p=p))
+        calls.append((c % layers, routes))
+    expect = host_run(calls, layers, E, slots, pcap, policy, top_k)
+    dp = DevicePlanner(layers * E, slots, pcap, n_experts=E, policy=policy, max_routes=16 * top_k, device=DEV)
+    hits = misses = evictions = 0
+    for c, ((layer, routes), want_res) in enumerate(zip(calls, expect)):
+        rs = dp.plan(torch.tensor(routes, dtype=torch.int32, device=DEV), layer, top_k)
+        counters, got = dp.read(max_results=len(want_res))
+        assert counters["error"] == 0, (c, counters)
+        assert [(r.key, r.slot, r.evicted_key, r.hit, r.placed) for r in got] == \
+               [(r.key, r.slot, r.evicted_key, r.hit, r.placed) for r in want_res], f"call {c} layer {layer}"
+        slot_of = {r.key - layer * E: r.slot for r in want_res}
+        assert rs.cpu().tolist() == [slot_of[e] for e in routes], f"route slots of call {c}"
+        hits += sum(r.hit for r in want_res)
+        misses += sum(not r.hit for r in want_res)
+        evictions += sum(r.evicted_key >= 0 for r in want_res)
+    counters, _ = dp.read()
+    assert (counters["hits"], counters["misses"], counters["evictions"], counters["calls"]) == \
+           (hits, misses, evictions, n_calls)
+    assert evictions > 500 and hits > 1000, (hits, misses, evictions)

@@ -292,7 +292,9 @@ def test_device_planner_prefill_batches_equal_host_planner(tmp_path):
     steps = 16
     outs, counts = [], []
     for device_planner in (False, True):
-        stack = _Stack(tmp_path, layers=4, per_layer=64, policy="slru-all", seed=520, steps=steps,
+        # 96 usable slots per layer: probation (the half not protected) then
+        # holds the 96 routes of a call plus the previous call's 96 pinned
+        stack = _Stack(tmp_path, layers=4, per_layer=96, policy="slru-all", seed=520, steps=steps,
                        device_planner=device_planner)
         try:
             got = []
@@ -310,6 +312,23 @@ def test_device_planner_prefill_batches_equal_host_planner(tmp_path):
     assert counts[0] == counts[1] and counts[0][0] > 0 and counts[0][1] > 0
     for i, (a, b) in enumerate(zip(*outs)):
         assert torch.equal(a, b), f"call {i}"
+
+
+def test_device_planner_refuses_a_call_it_might_not_place(tmp_path):
+    """A device-planned call whose keys plus the previous call's pinned
+    slots exceed what probation holds could leave a demanded expert without
+    a slot, which the kernel would answer with the zero slot: V4ArenaMoE
+    raises before queueing anything instead. 4 layers x 2 usable slots (9
+    slots, 4 protected): a decode call's six experts do not fit probation's
+    four."""
+    banner("device planner refuses an unplaceable call")
+    stack = _Stack(tmp_path, layers=4, per_layer=2, policy="slru-all", seed=530, steps=1, device_planner=True)
+    try:
+        with pytest.raises(RuntimeError, match="may find no unpinned slot"):
+            stack.mods[0](stack.X[0, 0:1])
+        assert stack.store.stats()["misses"] == 0
+    finally:
+        stack.close()
 
 
 def test_cross_layer_prefetch_is_exact_and_accounted(tmp_path):

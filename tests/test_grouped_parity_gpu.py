@@ -1,0 +1,259 @@
+"""The grouped (prefill) matrix-core kernels held to the stated expert-output
+tolerance at the benchmarked shape: d_model 4096, 256 routed experts + the
+shared expert, d_ff 2048, 2-bit g64, T = 64 and 512, bf16 and fp16, Zipf(1.1)
+expert popularity.
+
+  * Pure expert outputs (dsv4_arena.py:223-235, one route per token, weight 1,
+    no shared expert; tests/test_dsv4_kernels.py:75 holds the reference's own
+    kernel to the same kind of check) within 1e-2 relative / 2e-3 absolute of
+    the fp32-accumulated C oracle; the few elements (under 1 %) that a
+    one-ulp rounding flip of h moves further must be explained by the
+    kernel's own h (_check_outputs). The shared expert's own tiles (every
+    position of the call, full 64-position tiles) are checked the same way:
+    with every routed weight 0 the combine returns round(0 + y_shared) =
+    y_shared exactly.
+  * Stage by stage on top-6 routing (locali_moe_expert_grouped_stages hands
+    out the kernels' own h and y): the down projection y within one unit in
+    the last place plus the fp32 summation bound 2^-12 sum |h W| of the exact
+    (fp64) product of the kernel's own h; gate/up + SwiGLU within the
+    propagated bound of the same kind from x. The checked routes are the
+    first and last position of every 64-position tile of the heaviest experts
+    and of the shared expert, tiles of 3..64 positions, and one- and
+    two-position tiles (the small-tile kernels): every tile kind and tile
+    boundary of the call.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import ATOL, RTOL, arena_numpy, banner, dt_name, ulp, values
+from locali_amd import ops, synth
+from oracle import affine, moe
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+D, E, DFF, K, GROUP, TILE = 4096, 256, 2048, 6, 64, 64
+FP32_SUM = 2.0 ** -12     # worst-case relative error of an fp32 sum of up to 4096 terms
+LIMIT = 10.0
+
+
+def _layer(seed, dtype):
+    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=2, group=GROUP, dtype=dtype, seed=seed, device=DEV)
+    shared = synth.expert_arena(1, D, DFF, bits_gate_up=2, group=GROUP, dtype=dtype, seed=seed + 1, device=DEV,
+                                zero_slot=False)
+    return arena, shared
+
+
+def _zipf_one(T, seed):
+    """One expert per token, popularity Zipf(1.1) over a seeded ranking."""
+    rng = np.random.default_rng(seed)
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    rank = rng.permutation(E)
+    return rank[rng.choice(E, size=T, p=p / p.sum())].astype(np.int32)
+
+
+def _segments(route_expert):
+    """expert -> its routes in grouped order (the dispatch's stable sort by
+    slot keeps route order within an expert)."""
+    seg: dict = {}
+    for r, e in enumerate(route_expert.tolist()):
+        seg.setdefault(int(e), []).append(r)
+    return seg
+
+
+def _tile_routes(seg, heavy=3, mid=3, small=3, seed=0):
+    """First and last route of every 64-position tile of the `heavy` most
+    used experts, of `mid` experts with 3..64 routes, and the last route of
+    `small` experts whose last tile has one or two positions."""
+    rng = np.random.default_rng(seed)
+    pick = set()
+
+    def ends(members):
+        for a in range(0, len(members), TILE):
+            tile = members[a:a + TILE]
+            pick.update((tile[0], tile[-1]))
+
+    by_count = sorted(seg, key=lambda e: -len(seg[e]))
+    for e in by_count[:heavy]:
+        ends(seg[e])
+    mids = [e for e in by_count if 3 <= len(seg[e]) <= TILE]
+    for e in rng.permutation(mids)[:mid]:
+        ends(seg[int(e)])
+    tails = [e for e in seg if len(seg[e]) % TILE in (1, 2)]
+    for e in rng.permutation(tails)[:small]:
+        pick.add(seg[int(e)][-1])
+    return sorted(pick)
+
+
+def _dense(proj, slot):
+    """fp64 dequantised matrix of one slot (2/4-bit whole codes per word),
+    vectorised; pinned to affine.dequant on its first rows."""
+    w, s, b, bits, group = proj
+    w, s, b = w[slot], s[slot], b[slot]
+    vpw = 32 // bits
+    shifts = (np.arange(vpw, dtype=np.uint32) * bits)[None, None, :]
+    q = ((w[:, :, None] >> shifts) & ((1 << bits) - 1)).reshape(w.shape[0], -1).astype(np.float64)
+    q = q.reshape(q.shape[0], -1, group)
+    dense = (q * s[:, :, None] + b[:, :, None]).reshape(w.shape[0], -1)
+    np.testing.assert_array_equal(dense[:4], affine.dequant(w[:4], s[:4], b[:4], bits, group))
+    return dense
+
+
+def _h_oracle(dense, xr, dt):
+    up = affine.round_to(dense["up_proj"] @ xr, dt)
+    gate = affine.round_to(dense["gate_proj"] @ xr, dt)
+    return moe.swiglu(gate, up, dt, limit=LIMIT)
+
+
+def _check_outputs(got, want, h_gpu, dense_of, x_of, tokens, dt, what):
+    """got within 1e-2 rel / 2e-3 abs of the fp32-accumulated oracle. h, the
+    SwiGLU output rounded to the activation dtype, flips by one unit in the
+    last place wherever two fp32 sums of its inputs straddle a rounding
+    midpoint (a few % of h, the oracle's own fp32 sums included), and in
+    bf16 one flip of a large h moves y by more than 2e-3. So an element
+    outside the tolerance is accepted only when it is explained that way:
+    against y_o, the exact down projection of the exact (fp64) oracle h_o,
+    it is within the tolerance plus sum_j |W_nj| |h_gpu_j - h_o_j|, and
+    h_gpu differs from h_o. Such elements must stay below 1 %."""
+    bad = np.abs(got - want) > ATOL + RTOL * np.abs(want)
+    for i in np.unique(np.argwhere(bad)[:, 0]):
+        t = tokens[i]
+        dense = dense_of(t)
+        h_o = _h_oracle(dense, x_of(t), dt)
+        dh = np.abs(h_gpu[t] - h_o)
+        assert dh.any(), f"{what}: token {t} outside the tolerance with h equal to the oracle's"
+        n = np.flatnonzero(bad[i])
+        y_o = affine.round_to(dense["down_proj"][n] @ h_o, dt)
+        bound = ATOL + RTOL * np.abs(y_o) + np.abs(dense["down_proj"][n]) @ dh
+        assert np.all(np.abs(got[i, n] - y_o) <= bound), \
+            f"{what}: token {t} columns {n[:4].tolist()} beyond the h-flip bound"
+    assert bad.mean() < 1e-2, f"{what}: {int(bad.sum())} elements outside the stated tolerance"
+    return int(bad.sum())
+
+
+@pytest.mark.parametrize("T,dtype", [(64, torch.bfloat16), (512, torch.bfloat16), (64, torch.float16),
+                                     (512, torch.float16)])
+def test_grouped_pure_expert_outputs(oracle_lib, T, dtype):
+    banner(f"grouped pure expert outputs T={T} {dtype}")
+    arena, shared = _layer(700 + T, dtype)
+    x = synth.activations(T, D, dtype, seed=710 + T, device=DEV)
+    experts = _zipf_one(T, seed=720 + T)
+    idx = torch.from_numpy(experts).reshape(T, 1).to(DEV)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    ws = ops.Workspace(DEV)
+    out, h, _ = ops.expert_grouped_stages(arena, None, x, idx, slot_of, torch.ones(T, 1, device=DEV), ws,
+                                          n_experts=E)
+    out_sh, h_sh, _ = ops.expert_grouped_stages(arena, shared, x, idx, slot_of, torch.zeros(T, 1, device=DEV),
+                                                ws, n_experts=E)
+    torch.cuda.synchronize()
+    seg = _segments(experts)
+    counts = sorted((len(v) for v in seg.values()), reverse=True)
+    assert counts[0] >= 3 and any(c <= 2 for c in counts)   # wide tiles and small tiles
+    if T <= 64:
+        tokens = list(range(T))
+    else:
+        tokens = sorted(set(_tile_routes(seg, heavy=4, mid=6, small=6, seed=T)) | set(range(0, T, TILE)) |
+                        set(range(TILE - 1, T, TILE)))
+    xs, got, got_sh, hg, hg_sh = values(x), values(out), values(out_sh), values(h), values(h_sh)
+    sh = arena_numpy(shared, float_meta=False)
+    dt = dt_name(dtype)
+    sh_dense = {}
+
+    def dense_routed(t):
+        return {p: _dense(a, 0) for p, a in arena_numpy(arena, slots=[int(experts[t]) + 1]).items()}
+
+    def dense_shared(t):
+        if not sh_dense:
+            sh_dense.update({p: _dense(a, 0) for p, a in arena_numpy(shared).items()})
+        return sh_dense
+
+    flips = 0
+    for c in range(0, len(tokens), 16):
+        tk = np.asarray(tokens[c:c + 16])
+        used = sorted(set((experts[tk] + 1).tolist()))
+        remap = {s: i for i, s in enumerate(used)}
+        sub = arena_numpy(arena, float_meta=False, slots=used)
+        slots = np.array([[remap[int(e) + 1]] for e in experts[tk]], dtype=np.int32)
+        want = oracle_lib.moe_layer(xs[tk], slots, np.ones((len(tk), 1)), sub, dt)
+        flips += _check_outputs(got[tk], want, hg, dense_routed, lambda t: xs[t], tk, dt,
+                                f"expert outputs T={T} {dt}")
+        want_sh = oracle_lib.moe_layer(xs[tk], np.zeros((len(tk), 1), np.int32), np.ones((len(tk), 1)), sh, dt)
+        flips += _check_outputs(got_sh[tk], want_sh, hg_sh[T:], dense_shared, lambda t: xs[t], tk, dt,
+                                f"shared expert outputs T={T} {dt}")
+    print(f"T={T} {dt}: {2 * len(tokens) * D} outputs checked, {flips} beyond the stated tolerance "
+          f"through h rounding flips")
+
+
+@pytest.mark.parametrize("T,dtype", [(64, torch.bfloat16), (512, torch.bfloat16), (64, torch.float16),
+                                     (512, torch.float16)])
+def test_grouped_stagewise_ulp(T, dtype):
+    """h and y of the grouped kernels against the exact oracle on their own
+    stage inputs (the bounds of test_expert_decode_stagewise_ulp): every
+    checked element within the bound, at least 95 % of h and 98 % of y
+    equal to the oracle's rounding (the matrix cores' fp32 sums round h
+    differently from the exact oracle a little more often than the decode
+    kernels do: 95.9 % of one route's h equal at T=512 in bf16)."""
+    banner(f"grouped stage-wise ulp T={T} {dtype}")
+    dt = dt_name(dtype)
+    arena, shared = _layer(800 + T, dtype)
+    x, w = synth.zipf_router_inputs(T, E, D, 1.1, dtype, seed=810 + T, device=DEV)
+    spec = ops.RouterSpec(w, K, routed_scale=1.5)
+    ws = ops.Workspace(DEV)
+    idx, wts, _ = ops.router(spec, x, ws)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    out, h, y = ops.expert_grouped_stages(arena, shared, x, idx, slot_of, wts, ws, n_experts=E)
+    ref = ops.expert_grouped(arena, shared, x, idx, slot_of, wts, ws, n_experts=E)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), "the stages entry point computes what expert_grouped does"
+    R = T * K
+    route_expert = idx.reshape(-1).cpu().numpy()
+    seg = _segments(route_expert)
+    routes = _tile_routes(seg, seed=T)
+    shared_tiles = sorted({R + t for a in range(0, T, TILE) for t in (a, min(a + TILE, T) - 1)})
+    routes += shared_tiles
+    assert any(len(seg[int(route_expert[r])]) <= 2 for r in routes if r < R), "a small tile is checked"
+    assert any(len(seg[int(route_expert[r])]) >= 3 for r in routes if r < R), "a 64-position tile is checked"
+    if T > TILE:
+        assert any(len(seg[int(route_expert[r])]) > TILE for r in routes if r < R), "a tile boundary is checked"
+    xs, hs, ys = values(x), values(h), values(y)
+    ar = arena_numpy(arena, slots=sorted({int(route_expert[r]) + 1 for r in routes if r < R}))
+    sha = arena_numpy(shared)
+    slot_index = {s: i for i, s in enumerate(sorted({int(route_expert[r]) + 1 for r in routes if r < R}))}
+    cache: dict = {}
+    worst, exact_h, exact_y = 0.0, [], []
+    for r in routes:
+        if r < R:
+            key = int(route_expert[r]) + 1
+            src, sl = ar, slot_index[key]
+        else:
+            key, src, sl = "shared", sha, 0
+        if key not in cache:
+            cache[key] = {p: _dense(src[p], sl) for p in src}
+        dense = cache[key]
+        xr = xs[r // K] if r < R else xs[r - R]
+        up = affine.round_to(dense["up_proj"] @ xr, dt)
+        gate = affine.round_to(dense["gate_proj"] @ xr, dt)
+        h_want = moe.swiglu(gate, up, dt, limit=LIMIT)
+        d_up = ulp(up, dtype) + FP32_SUM * (np.abs(dense["up_proj"]) @ np.abs(xr))
+        d_gate = ulp(gate, dtype) + FP32_SUM * (np.abs(dense["gate_proj"]) @ np.abs(xr))
+        gc = np.minimum(gate, LIMIT)
+        silu = gc / (1.0 + np.exp(-gc))
+        h_tol = 1.1 * np.minimum(np.abs(up), LIMIT) * d_gate + np.abs(silu) * d_up + 3 * ulp(h_want, dtype)
+        dh = np.abs(hs[r] - h_want)
+        what = f"T={T} {dt} route {r} ({'shared' if r >= R else 'expert %d' % (key - 1)})"
+        assert np.all(dh <= h_tol), f"h {what}: worst {np.max(dh / h_tol):.3g} of the bound"
+        assert np.mean(dh == 0) >= 0.95, f"h {what}: exact {np.mean(dh == 0):.4f}"
+        y_want = affine.round_to(dense["down_proj"] @ hs[r], dt)
+        y_tol = ulp(y_want, dtype) + FP32_SUM * (np.abs(dense["down_proj"]) @ np.abs(hs[r]))
+        dy = np.abs(ys[r] - y_want)
+        assert np.all(dy <= y_tol), f"y {what}: worst {np.max(dy / y_tol):.3g} of the bound"
+        assert np.mean(dy == 0) >= 0.98, f"y {what}: exact {np.mean(dy == 0):.4f}"
+        worst = max(worst, float(np.max(dh / h_tol)), float(np.max(dy / y_tol)))
+        exact_h.append(np.mean(dh == 0))
+        exact_y.append(np.mean(dy == 0))
+    print(f"T={T} {dt}: {len(routes)} routes of {len(cache)} experts checked stage by stage; h exact "
+          f"{min(exact_h):.4f}..{max(exact_h):.4f}, y exact {min(exact_y):.4f}..{max(exact_y):.4f}, "
+          f"worst {worst:.3g} of the bound")

@@ -320,6 +320,37 @@ def test_router_sigmoid_variant_and_canonical_order():
     assert list(tie_idx[0]) == [0, 1, 2, 3]
 
 
+def test_router_sigmoid_pinned_by_torch_and_a_hand_built_case():
+    """arena.py:501-506 pinned without the oracle's own formula: scores equal
+    torch.sigmoid of the logits, and a hand-built router where the selection
+    bias changes which experts are chosen but never enters the weights."""
+    import math
+
+    import torch
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 32))
+    w = rng.standard_normal((12, 32)) / 4
+    _, _, _, scores = moe.route(x, w, 4, score_func="sigmoid")
+    ref = torch.sigmoid(torch.from_numpy(x) @ torch.from_numpy(w).T).numpy()
+    np.testing.assert_allclose(scores, ref, rtol=1e-13, atol=0)
+    # logits [2, 1, 0, -1] (x = e0 .. e3 rows of the identity, times these)
+    gate = np.diag([2.0, 1.0, 0.0, -1.0])
+    xs = np.ones((1, 4))
+    sig = [1.0 / (1.0 + math.exp(-v)) for v in (2.0, 1.0, 0.0, -1.0)]
+    idx, wts, _, _ = moe.route(xs, gate, 2, score_func="sigmoid")
+    assert idx[0].tolist() == [0, 1]
+    np.testing.assert_allclose(wts[0], [sig[0] / (sig[0] + sig[1]), sig[1] / (sig[0] + sig[1])], rtol=1e-14)
+    # a bias of 5 on the weakest expert selects it first; its weight is
+    # still its own score, renormalised with the other chosen one
+    idx, wts, _, _ = moe.route(xs, gate, 2, bias=np.array([0.0, 0.0, 0.0, 5.0]), score_func="sigmoid")
+    assert idx[0].tolist() == [3, 0]
+    np.testing.assert_allclose(wts[0], [sig[3] / (sig[3] + sig[0]), sig[0] / (sig[3] + sig[0])], rtol=1e-14)
+    # routed_scale multiplies after the renormalisation
+    _, w2, _, _ = moe.route(xs, gate, 2, bias=np.array([0.0, 0.0, 0.0, 5.0]), score_func="sigmoid",
+                            routed_scale=2.5)
+    np.testing.assert_allclose(w2, 2.5 * wts, rtol=1e-14)
+
+
 def test_c_oracle_router_matches_numpy(oracle_lib):
     rng = np.random.default_rng(9)
     x = rng.standard_normal((6, 128)).astype(np.float32)

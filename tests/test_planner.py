@@ -16,6 +16,7 @@ import ctypes
 import json
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 import planner_traces as pt
@@ -226,3 +227,35 @@ def test_plan_each_equals_one_call_per_key_with_growing_pins(policy, slots, prot
             pinned = {r.slot for r in got if r.placed}
     with pytest.raises(ValueError):
         ours.plan_each([1, 99, 2])
+
+
+@pytest.mark.parametrize("policy", ["slru", "lfu-decay"])
+def test_device_planner_placement_bound_is_sound(policy):
+    """DevicePlanner.placement_certain, the host-side check that lets a
+    device-planned demand call proceed, never admits a call that the
+    compiled planner fails to place: random geometries and call sequences
+    under the store's convention (plan_each, the previous call's slots
+    pinned). The calls it refuses include every call that did fail, and
+    some did fail, so the check is not vacuous."""
+    from locali_amd.native import DevicePlanner
+    rng = np.random.default_rng(11 if policy == "slru" else 12)
+    failed = refused = 0
+    for _ in range(300):
+        slots = int(rng.integers(3, 24))
+        pcap = int(rng.integers(0, slots - 1)) if policy == "slru" else 0
+        n_keys = int(rng.integers(2, 40))
+        probation = slots - 1 - pcap
+        cache = NativeCache(n_keys, slots, pcap, policy=policy)
+        pinned = []
+        for _ in range(20):
+            k = int(rng.integers(1, min(n_keys, slots + 2) + 1))
+            keys = [int(v) for v in rng.choice(n_keys, size=k, replace=False)]
+            ok = DevicePlanner.placement_certain(len(keys), len(pinned), probation)
+            res = cache.plan_each(keys, pinned_slots=pinned)
+            placed = all(r.placed for r in res)
+            refused += not ok
+            failed += not placed
+            assert placed or not ok, (slots, pcap, keys, pinned)
+            pinned = sorted({r.slot for r in res if r.placed})
+        cache.close()
+    assert failed > 0 and refused >= failed

@@ -73,3 +73,55 @@ def test_noalloc_refuses_more_than_its_scratch():
     rc, *_ = _noalloc(spec, arena, None, slot_of, x)
     assert rc == -2
     assert b"static scratch holds" in _lib.lib().locali_moe_last_error()
+
+
+def _capture_first_main():
+    """Body of test_noalloc_first_call_under_graph_capture, run in a fresh
+    process so that the library's first noalloc call on the device (the
+    scratch lookup and its clear) happens while a graph is being captured."""
+    torch.cuda.set_device(0)
+    d, E, dff = 4096, 256, 2048
+    arena = synth.expert_arena(E + 1, d, dff, dtype=torch.bfloat16, seed=81, device=DEV)
+    shared = synth.expert_arena(1, d, dff, dtype=torch.bfloat16, seed=82, device=DEV, zero_slot=False)
+    w, bias = synth.uniform_router(E, d, torch.bfloat16, seed=83, device=DEV, bias_std=0.01)
+    spec = ops.RouterSpec(w, 6, routed_scale=1.5, score_bias=bias)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    xs = [synth.activations(1, d, torch.bfloat16, seed=84 + i, device=DEV) for i in range(3)]
+    x = xs[0].clone()
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        rc, out, idx, wts = _noalloc(spec, arena, shared, slot_of, x)
+    _lib.check(rc, "locali_moe_forward_noalloc (captured)")
+    for rep, xi in enumerate(xs):
+        x.copy_(xi)
+        g.replay()
+        torch.cuda.synchronize()
+        ref, ridx, rw = ops.forward(spec, arena, shared, slot_of, xi, ops.Workspace())
+        torch.cuda.synchronize()
+        assert torch.equal(idx, ridx) and torch.equal(wts, rw), f"replay {rep} routes"
+        assert torch.equal(out, ref), f"replay {rep} output"
+        # an eager noalloc call between replays shares the same scratch
+        rc2, out2, _, _ = _noalloc(spec, arena, shared, slot_of, xi)
+        _lib.check(rc2, "locali_moe_forward_noalloc (eager)")
+        torch.cuda.synchronize()
+        assert torch.equal(out2, ref), f"eager call after replay {rep}"
+    print("capture-first ok", flush=True)
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """The first noalloc call of a process made inside torch.cuda.graph
+    capture: every replay (inputs changed between replays, an eager noalloc
+    call after each) equals the workspace forward bit for bit."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    banner("forward_noalloc first call under graph capture (fresh process)")
+    here = Path(__file__).resolve().parent
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([str(here.parent), str(here)]))
+    proc = subprocess.run([sys.executable, "-c", "import test_zz_no_alloc as t; t._capture_first_main()"],
+                          cwd=here, env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                          timeout=110)
+    assert proc.returncode == 0 and "capture-first ok" in proc.stdout, proc.stdout[-3000:]
