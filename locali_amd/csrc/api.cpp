@@ -306,13 +306,13 @@ bool mfma_eligible(const locali_expert_arena *routed, const locali_expert_arena 
     return true;
 }
 
-// Small-tile kernels (mfma_small.hpp): groups of exactly 64, K of both
+// Small-tile kernels (mfma_small.hpp): groups of 64 or 128, K of both
 // stages a multiple of 512 and at most 4096, rows multiples of 32.
 constexpr int kSmallTileHost = 2;
 bool small_tiles_eligible(const locali_expert_arena *routed) {
     auto ok = [](const locali_qproj &p) {
-        return (p.bits == 2 || p.bits == 4) && p.group_size == 64 && p.cols % 512 == 0 && p.cols <= 4096 &&
-               p.rows % 32 == 0;
+        return (p.bits == 2 || p.bits == 4) && (p.group_size == 64 || p.group_size == 128) &&
+               (p.cols / p.group_size) % 8 == 0 && p.cols % 512 == 0 && p.cols <= 4096 && p.rows % 32 == 0;
     };
     return ok(routed->gate) && ok(routed->up) && ok(routed->down);
 }

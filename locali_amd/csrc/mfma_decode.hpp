@@ -50,6 +50,39 @@ struct DiagGeom {
     static_assert(BITS == 2 || BITS == 4, "2- and 4-bit codes");
 };
 
+// A workgroup's scales and biases (`arrays` arrays of `rows` rows of gpr
+// groups) move into LDS by whole lines as 16-byte pieces: piece c = (array,
+// row, part), gpr / 8 parts per row, row stride mrs bytes in LDS. With
+// groups of 128 there are half as many pieces as with 64; a thread whose
+// piece lies past the arrays loads a valid piece again (the loads stay
+// unconditional, so the vector-memory counter keeps counting them) and does
+// not store it.
+struct MetaPiece {
+    int arr;      // array index (clamped)
+    int off;      // u16 offset in the array's rows
+    int dst;      // LDS byte offset
+    bool store;
+};
+
+__device__ __forceinline__ MetaPiece meta_piece_of(int c, int arrays, int rows, int gpr, int mrs) {
+    const int ppr = gpr >> 3;
+    const int a = c / (rows * ppr), row = (c / ppr) % rows, pc = c % ppr;
+    MetaPiece m;
+    m.store = a < arrays;
+    m.arr = min(a, arrays - 1);
+    m.off = row * gpr + 8 * pc;
+    m.dst = (a * rows + row) * mrs + 16 * pc;
+    return m;
+}
+
+// log2 of the 16-byte units a group of `group` values spans (groups of 64
+// or 128): grp = unit >> units_per_group_log2.
+template <int BITS>
+__device__ __forceinline__ int units_per_group_log2(int group) {
+    constexpr int base = DiagGeom<BITS>::kUnitsPerGroup == 1 ? 0 : DiagGeom<BITS>::kUnitsPerGroup == 2 ? 1 : 2;
+    return base + (group == 128 ? 1 : 0);
+}
+
 // One window of a prepared vector in LDS: unit u's pairs at u * kStride
 // (padding spreads the eight units one step reads over distinct banks), then
 // a zeroed slot for the off-diagonal lanes, then the per-unit sums
@@ -219,29 +252,24 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     const int64_t gw_slot = shared ? sgate.w_slot : gate.w_slot, uw_slot = shared ? sup.w_slot : up.w_slot;
     const int64_t gm_slot = shared ? sgate.m_slot : gate.m_slot, um_slot = shared ? sup.m_slot : up.m_slot;
     const int n0 = blockIdx.x * 16 * RT;
-    const int wpr = K * BITS / 32, gpr = K / 64;
+    const int wpr = K * BITS / 32, gpr = K / gate.group;
     const int waves = blockDim.x >> 6;   // = K / 512
+    const int ug_log2 = units_per_group_log2<BITS>(gate.group);
     DiagSlice<BITS> &mw = win[wave];
 
     // Raw x of the window first (the prep waits only for it), then the
     // workgroup's scales and biases by whole lines, then the weights in
     // consumption order. The metadata geometry does not depend on the slot
     // and is worked out before any selection: thread i moves 16-byte pieces
-    // i and i + 64 * waves of the four arrays' rows, piece c = (array, row,
-    // part).
+    // i and i + 64 * waves of the four arrays' rows (meta_piece_of).
     uint32_t xw[16 / BITS];
     diag_prep_load<BITS>(xw, ra.x + static_cast<int64_t>(token) * K + wave * kDiagWindow, lane);
     const int mrs = 2 * gpr + 16;   // LDS bytes per metadata row
-    // 4 arrays x 16 RT rows x `waves` pieces: RT pieces per thread
-    int ma[RT], mo[RT], md[RT];
+    // 4 arrays x 16 RT rows x gpr / 8 pieces: at most RT pieces per thread
+    MetaPiece mp[RT];
 #pragma unroll
-    for (int q = 0; q < RT; ++q) {
-        const int c = static_cast<int>(threadIdx.x) + q * 64 * waves;
-        const int row = (c / waves) % (16 * RT), pc = c % waves;
-        ma[q] = c / (16 * RT * waves);
-        mo[q] = row * gpr + 8 * pc;   // u16 elements
-        md[q] = (ma[q] * 16 * RT + row) * mrs + 16 * pc;
-    }
+    for (int q = 0; q < RT; ++q)
+        mp[q] = meta_piece_of(static_cast<int>(threadIdx.x) + q * 64 * waves, 4, 16 * RT, gpr, mrs);
     if constexpr (SELECT) {
         __shared__ float2 stage[256];
         __shared__ int s_slot;
@@ -292,8 +320,8 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     u32x4 mv[RT];
 #pragma unroll
     for (int q = 0; q < RT; ++q) {
-        const uint16_t *arr = ma[q] == 0 ? m_gs : ma[q] == 1 ? m_gb : ma[q] == 2 ? m_us : m_ub;
-        mv[q] = *reinterpret_cast<const u32x4 *>(arr + mo[q]);
+        const uint16_t *arr = mp[q].arr == 0 ? m_gs : mp[q].arr == 1 ? m_gb : mp[q].arr == 2 ? m_us : m_ub;
+        mv[q] = *reinterpret_cast<const u32x4 *>(arr + mp[q].off);
     }
     sched_fence();
     const uint32_t wbytes = 4u * 16 * RT * wpr;
@@ -315,7 +343,8 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     sched_fence();
     if constexpr (!SELECT) diag_prep_store<BITS, BF16>(mw, xw, lane);
 #pragma unroll
-    for (int q = 0; q < RT; ++q) *reinterpret_cast<u32x4 *>(mlds + md[q]) = mv[q];
+    for (int q = 0; q < RT; ++q)
+        if (mp[q].store) *reinterpret_cast<u32x4 *>(mlds + mp[q].dst) = mv[q];
     __syncthreads();
     const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
     // diagonal A: lane (m, kb) feeds unit 8 line + 4 ((m / 2) % 2) + kb when m / 4 == kb
@@ -356,7 +385,7 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
         // the lane's unit 4 h + kb of this line, rows 8 i + n % 8 of each tile
         const int uB = 8 * line + 4 * hh + kb;
         const float2 us = mw.usum[uB];
-        const int grp = (G::kUnits * wave + uB) / G::kUnitsPerGroup;
+        const int grp = (G::kUnits * wave + uB) >> ug_log2;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll

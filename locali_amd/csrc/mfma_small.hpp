@@ -66,8 +66,9 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
     const int64_t gw_slot = shared ? sgate.w_slot : gate.w_slot, uw_slot = shared ? sup.w_slot : up.w_slot;
     const int64_t gm_slot = shared ? sgate.m_slot : gate.m_slot, um_slot = shared ? sup.m_slot : up.m_slot;
     const int n0 = blockIdx.x * kSmallRows;
-    const int wpr = K * BITS / 32, gpr = K / 64;
+    const int wpr = K * BITS / 32, gpr = K / gate.group;
     const int waves = blockDim.x >> 6;   // = K / 512
+    const int ug_log2 = units_per_group_log2<BITS>(gate.group);
     // tokens from the tile record when the dispatch packed them there
     static_assert(kSmallTile <= kPackedTokens, "small tiles carry packed tokens");
     const bool packed = !shared && (ti.packed & kTokensPacked);
@@ -93,15 +94,14 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
     const uint16_t *m_us = (shared ? sup.s : up.s) + sl * um_slot + mrow0;
     const uint16_t *m_ub = (shared ? sup.b : up.b) + sl * um_slot + mrow0;
     u32x4 mv0, mv1;
-    int md0, md1;
-    auto meta_piece = [&](int c, u32x4 &v, int &dst) {
-        const int a = c / (kSmallRows * waves), row = (c / waves) % kSmallRows, pc = c % waves;
-        const uint16_t *arr = a == 0 ? m_gs : a == 1 ? m_gb : a == 2 ? m_us : m_ub;
-        v = reinterpret_cast<const u32x4 *>(arr + static_cast<int64_t>(row) * gpr)[pc];
-        dst = (a * kSmallRows + row) * mrs + 16 * pc;
+    const MetaPiece mp0 = meta_piece_of(static_cast<int>(threadIdx.x), 4, kSmallRows, gpr, mrs);
+    const MetaPiece mp1 = meta_piece_of(static_cast<int>(threadIdx.x) + 64 * waves, 4, kSmallRows, gpr, mrs);
+    auto meta_load = [&](const MetaPiece &m) {
+        const uint16_t *arr = m.arr == 0 ? m_gs : m.arr == 1 ? m_gb : m.arr == 2 ? m_us : m_ub;
+        return *reinterpret_cast<const u32x4 *>(arr + m.off);
     };
-    meta_piece(static_cast<int>(threadIdx.x), mv0, md0);
-    meta_piece(static_cast<int>(threadIdx.x) + 64 * waves, mv1, md1);
+    mv0 = meta_load(mp0);
+    mv1 = meta_load(mp1);
     sched_fence();
     const uint32_t wbytes = 4u * kSmallRows * wpr;
     const int64_t wrow0 = static_cast<int64_t>(n0) * wpr;
@@ -121,8 +121,8 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
     sched_fence();
     diag_prep_store<BITS, BF16>(win[wave][0], xw[0], lane);
     if (count > 1) diag_prep_store<BITS, BF16>(win[wave][1], xw[1], lane);
-    *reinterpret_cast<u32x4 *>(mlds + md0) = mv0;
-    *reinterpret_cast<u32x4 *>(mlds + md1) = mv1;
+    if (mp0.store) *reinterpret_cast<u32x4 *>(mlds + mp0.dst) = mv0;
+    if (mp1.store) *reinterpret_cast<u32x4 *>(mlds + mp1.dst) = mv1;
     __syncthreads();
     const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
     // A lane (m, kb) feeds position m % 2's unit 8 line + 4 ((m / 2) % 2) + kb when m / 4 == kb
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
         const int uB = 8 * line + 4 * hh + kb;
         const float2 us0 = win[wave][0].usum[uB];
         const float2 us1 = win[wave][1].usum[uB];
-        const int grp = (G::kUnits * wave + uB) / G::kUnitsPerGroup;
+        const int grp = (G::kUnits * wave + uB) >> ug_log2;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -242,8 +242,9 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void down_small_kernel(
     const uint32_t *wp = shared ? sdown.w : down.w;
     const int64_t w_slot = shared ? sdown.w_slot : down.w_slot, m_slot = shared ? sdown.m_slot : down.m_slot;
     const int n0 = blockIdx.x * kSmallRows;
-    const int wpr = K * BITS / 32, gpr = K / 64;
+    const int wpr = K * BITS / 32, gpr = K / down.group;
     const int waves = blockDim.x >> 6;   // = K / 512
+    const int ug_log2 = units_per_group_log2<BITS>(down.group);
 
     // The window's prepared h of each position and the sums of the lane's
     // units (a 64-value unit adds its two 32-value halves), the scales and
@@ -271,14 +272,9 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void down_small_kernel(
     const int64_t mrow0 = static_cast<int64_t>(n0) * gpr;
     const uint16_t *m_s = (shared ? sdown.s : down.s) + sl * m_slot + mrow0;
     const uint16_t *m_b = (shared ? sdown.b : down.b) + sl * m_slot + mrow0;
-    u32x4 mv;
-    int md;
-    {
-        const int c = threadIdx.x;   // 2 arrays x 32 rows x waves pieces = 64 * waves
-        const int a = c / (kSmallRows * waves), row = (c / waves) % kSmallRows, pc = c % waves;
-        mv = reinterpret_cast<const u32x4 *>((a == 0 ? m_s : m_b) + static_cast<int64_t>(row) * gpr)[pc];
-        md = (a * kSmallRows + row) * mrs + 16 * pc;
-    }
+    // 2 arrays x 32 rows x gpr / 8 pieces: at most one per thread
+    const MetaPiece mp = meta_piece_of(static_cast<int>(threadIdx.x), 2, kSmallRows, gpr, mrs);
+    const u32x4 mv = *reinterpret_cast<const u32x4 *>((mp.arr == 0 ? m_s : m_b) + mp.off);
     sched_fence();
     const __amdgpu_buffer_rsrc_t w_rs =
         make_rsrc(wp + sl * w_slot + static_cast<int64_t>(n0) * wpr, 4u * kSmallRows * wpr);
@@ -300,7 +296,7 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void down_small_kernel(
             *reinterpret_cast<u32x4 *>(win[wave][p].pairs + (lane / LPU) * G::kStride + 16 * (lane % LPU)) = hv[p];
         if (lane < 4 * G::kSteps) win[wave][0].zero[lane] = 0u;
     }
-    *reinterpret_cast<u32x4 *>(mlds + md) = mv;
+    if (mp.store) *reinterpret_cast<u32x4 *>(mlds + mp.dst) = mv;
     __syncthreads();
     const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
     const int ap = nl & 1;
@@ -334,7 +330,7 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void down_small_kernel(
                     d[rt][i] = mfma_16x16x32<BF16>(a, diag_b<BITS, BF16, t>(wd[rt][2 * line + i], magic_v), d[rt][i]);
         });
         const int uB = 8 * line + 4 * hh + kb;
-        const int grp = (G::kUnits * wave + uB) / G::kUnitsPerGroup;
+        const int grp = (G::kUnits * wave + uB) >> ug_log2;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll

@@ -36,10 +36,10 @@ D, E, DFF, K, GROUP = 4096, 256, 2048, 6, 64
 TILE = 64            # positions per matrix-core tile (a tile of 1-2 takes the small-tile kernels)
 
 
-def _layer(seed, bits_down=2, dtype=torch.bfloat16):
-    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=2, bits_down=bits_down, group=GROUP,
+def _layer(seed, bits_down=2, dtype=torch.bfloat16, group=GROUP):
+    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=2, bits_down=bits_down, group=group,
                                dtype=dtype, seed=seed, device=DEV)
-    shared = synth.expert_arena(1, D, DFF, bits_gate_up=2, bits_down=bits_down, group=GROUP,
+    shared = synth.expert_arena(1, D, DFF, bits_gate_up=2, bits_down=bits_down, group=group,
                                 dtype=dtype, seed=seed + 1, device=DEV, zero_slot=False)
     return arena, shared
 
@@ -115,10 +115,12 @@ def _tile_sample(idx, T, heavy=6, mid=8, small=8, seed=0):
     return sorted(pick), seg
 
 
-@pytest.mark.parametrize("T,dtype", [(64, torch.bfloat16), (512, torch.bfloat16), (64, torch.float16)])
-def test_prefill_full_width_zipf(oracle_lib, T, dtype):
-    banner(f"full-width prefill T={T} zipf 1.1 {dtype}")
-    arena, shared = _layer(seed=300 + T, dtype=dtype)
+@pytest.mark.parametrize("T,dtype,group", [(64, torch.bfloat16, 64), (512, torch.bfloat16, 64),
+                                           (64, torch.float16, 64), (64, torch.bfloat16, 128),
+                                           (512, torch.bfloat16, 128)])
+def test_prefill_full_width_zipf(oracle_lib, T, dtype, group):
+    banner(f"full-width prefill T={T} zipf 1.1 {dtype} group {group}")
+    arena, shared = _layer(seed=300 + T, dtype=dtype, group=group)
     x, w = synth.zipf_router_inputs(T, E, D, 1.1, dtype, seed=310 + T, device=DEV)
     spec = ops.RouterSpec(w, K, routed_scale=1.5)
     slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)

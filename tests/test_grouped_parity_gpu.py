@@ -40,9 +40,9 @@ FP32_SUM = 2.0 ** -12     # worst-case relative error of an fp32 sum of up to 40
 LIMIT = 10.0
 
 
-def _layer(seed, dtype):
-    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=2, group=GROUP, dtype=dtype, seed=seed, device=DEV)
-    shared = synth.expert_arena(1, D, DFF, bits_gate_up=2, group=GROUP, dtype=dtype, seed=seed + 1, device=DEV,
+def _layer(seed, dtype, group=GROUP):
+    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=2, group=group, dtype=dtype, seed=seed, device=DEV)
+    shared = synth.expert_arena(1, D, DFF, bits_gate_up=2, group=group, dtype=dtype, seed=seed + 1, device=DEV,
                                 zero_slot=False)
     return arena, shared
 
@@ -134,11 +134,12 @@ def _check_outputs(got, want, h_gpu, dense_of, x_of, tokens, dt, what):
     return int(bad.sum())
 
 
-@pytest.mark.parametrize("T,dtype", [(64, torch.bfloat16), (512, torch.bfloat16), (64, torch.float16),
-                                     (512, torch.float16)])
-def test_grouped_pure_expert_outputs(oracle_lib, T, dtype):
-    banner(f"grouped pure expert outputs T={T} {dtype}")
-    arena, shared = _layer(700 + T, dtype)
+@pytest.mark.parametrize("T,dtype,group", [(64, torch.bfloat16, 64), (512, torch.bfloat16, 64),
+                                           (64, torch.float16, 64), (512, torch.float16, 64),
+                                           (512, torch.bfloat16, 128)])
+def test_grouped_pure_expert_outputs(oracle_lib, T, dtype, group):
+    banner(f"grouped pure expert outputs T={T} {dtype} group {group}")
+    arena, shared = _layer(700 + T, dtype, group)
     x = synth.activations(T, D, dtype, seed=710 + T, device=DEV)
     experts = _zipf_one(T, seed=720 + T)
     idx = torch.from_numpy(experts).reshape(T, 1).to(DEV)
@@ -187,18 +188,19 @@ def test_grouped_pure_expert_outputs(oracle_lib, T, dtype):
           f"through h rounding flips")
 
 
-@pytest.mark.parametrize("T,dtype", [(64, torch.bfloat16), (512, torch.bfloat16), (64, torch.float16),
-                                     (512, torch.float16)])
-def test_grouped_stagewise_ulp(T, dtype):
+@pytest.mark.parametrize("T,dtype,group", [(64, torch.bfloat16, 64), (512, torch.bfloat16, 64),
+                                           (64, torch.float16, 64), (512, torch.float16, 64),
+                                           (64, torch.bfloat16, 128), (512, torch.bfloat16, 128)])
+def test_grouped_stagewise_ulp(T, dtype, group):
     """h and y of the grouped kernels against the exact oracle on their own
     stage inputs (the bounds of test_expert_decode_stagewise_ulp): every
     checked element within the bound, at least 95 % of h and 98 % of y
     equal to the oracle's rounding (the matrix cores' fp32 sums round h
     differently from the exact oracle a little more often than the decode
     kernels do: 95.9 % of one route's h equal at T=512 in bf16)."""
-    banner(f"grouped stage-wise ulp T={T} {dtype}")
+    banner(f"grouped stage-wise ulp T={T} {dtype} group {group}")
     dt = dt_name(dtype)
-    arena, shared = _layer(800 + T, dtype)
+    arena, shared = _layer(800 + T, dtype, group)
     x, w = synth.zipf_router_inputs(T, E, D, 1.1, dtype, seed=810 + T, device=DEV)
     spec = ops.RouterSpec(w, K, routed_scale=1.5)
     ws = ops.Workspace(DEV)

@@ -194,6 +194,10 @@ DECODE_CASES = [
     (torch.bfloat16, 2, 2, 64, 4096, 2048),
     (torch.bfloat16, 2, 4, 64, 4096, 2048),
     (torch.float16, 2, 2, 64, 4096, 2048),
+    # groups of 128 (the real checkpoint's 2-bit experts) on the matrix cores
+    (torch.bfloat16, 2, 2, 128, 4096, 2048),
+    (torch.float16, 2, 2, 128, 4096, 2048),
+    (torch.bfloat16, 4, 4, 128, 4096, 2048),
     # 3-bit codes (the DSpark/MTP tier): 4-bit kernels widening 3-bit rows
     (torch.bfloat16, 3, 3, 64, 1024, 512),
     (torch.float16, 3, 3, 32, 1024, 512),
@@ -660,16 +664,19 @@ def test_decode_forward_in_separate_stages(T):
     assert torch.equal(rs, idx + 1)
 
 
-@pytest.mark.parametrize("d,dtype", [(4096, torch.bfloat16), (2048, torch.float16), (1024, torch.bfloat16)])
-def test_fused_router_rows_across_calls_and_replays(d, dtype):
+@pytest.mark.parametrize("d,dtype,dff", [(4096, torch.bfloat16, 1024), (2048, torch.float16, 1024),
+                                         (1024, torch.bfloat16, 1024), (4096, torch.bfloat16, 2048),
+                                         (4096, torch.float16, 2048)])
+def test_fused_router_rows_across_calls_and_replays(d, dtype, dff):
     """The decode forward computes the logits in router rows of its gate/up
     kernel and hands them over as tagged words. Consecutive calls on one
     workspace alternate between routers and between 1 and 2 tokens, so a call
     that read the previous call's words would route like that call: every
     call must equal the separate logits -> gate/up -> down chain bit for bit,
-    eagerly and under repeated graph replays."""
-    banner(f"fused router rows d={d} {dt_name(dtype)}")
-    E, dff, k = 256, 1024, 6
+    eagerly and under repeated graph replays (d_ff 1024 and the benchmarked
+    2048)."""
+    banner(f"fused router rows d={d} {dt_name(dtype)} dff={dff}")
+    E, k = 256, 6
     arena = synth.expert_arena(E + 1, d, dff, dtype=dtype, seed=91, device=DEV)
     shared = synth.expert_arena(1, d, dff, dtype=dtype, seed=92, device=DEV, zero_slot=False)
     specs = []
@@ -719,13 +726,16 @@ def test_fused_router_rows_across_calls_and_replays(d, dtype):
         torch.cuda.synchronize()
 
 
-def test_forward_full_width_decode(oracle_lib):
-    """d 4096, 256 experts + shared, d_ff 2048, 2-bit g64 bf16, 1 token; checked
-    against the C oracle (fp32) on the GPU's own routing."""
-    banner("forward C2")
+@pytest.mark.parametrize("group", [64, 128])
+def test_forward_full_width_decode(oracle_lib, group):
+    """d 4096, 256 experts + shared, d_ff 2048, 2-bit bf16 in groups of 64 and
+    of 128 (the real checkpoint's), 1 token; checked against the C oracle
+    (fp32) on the GPU's own routing."""
+    banner(f"forward C2 group {group}")
     d, E, dff, k = 4096, 256, 2048, 6
-    arena = synth.expert_arena(E + 1, d, dff, dtype=torch.bfloat16, seed=21, device=DEV)
-    shared = synth.expert_arena(1, d, dff, dtype=torch.bfloat16, seed=22, device=DEV, zero_slot=False)
+    arena = synth.expert_arena(E + 1, d, dff, group=group, dtype=torch.bfloat16, seed=21, device=DEV)
+    shared = synth.expert_arena(1, d, dff, group=group, dtype=torch.bfloat16, seed=22, device=DEV,
+                                zero_slot=False)
     w, _ = synth.uniform_router(E, d, torch.bfloat16, seed=23, device=DEV)
     spec = ops.RouterSpec(w, k, routed_scale=1.5)
     slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
@@ -747,3 +757,4 @@ def test_forward_full_width_decode(oracle_lib):
                                            return_terms=True)
         assert_close_terms(values(out), want, terms, f"C2 step {step}")
         assert exact_fraction(values(out), want) > 0.8
+
