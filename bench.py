@@ -11,20 +11,28 @@ and rotate over 64 copies of the router and shared expert, so that no step
 finds them in the 256 MB MALL (a model's layers each have their own).
 
 Also reported:
-  roofline      the dominant kernel (decode gate/up + SwiGLU), its average
-                launch duration from HIP events around a graph of back-to-back
-                launches on the replay stream, achieved algorithmic GB/s
-                against the 8 TB/s peak, and `traffic`: HBM bytes per launch
+  roofline      the dominant kernel, the step's first launch (router rows,
+                gate/up + SwiGLU, top-6 selection), its average launch
+                duration from HIP events around graphs of back-to-back steps
+                and of back-to-back down kernels on the replay stream,
+                achieved algorithmic GB/s against the 8 TB/s peak, and
+                `traffic`: HBM bytes per launch
                 measured by two rocprofv3 --pmc passes (FETCH_SIZE, then
                 WRITE_SIZE), each scaled by what the counter reads for a
                 reference kernel of known bytes -- a 256 MiB reduction and a
                 256 MiB fill (`--copy-calibration`) -- summarised by
                 `--summarize-pmc` into profiles/gateup_diag_kernel_decode_traffic.json
+  decode_g128   the decode leg with the real checkpoint's 2-bit experts in
+                groups of 128 (7,077,888 B per expert)
   prefill64, prefill512
                 64- and 512-token prefill on the same layer with Zipf(1.1)
                 expert popularity (grouped path): tokens/s, algorithmic GB/s
                 against 8 TB/s, and matrix-core utilisation (flops against
                 the 2.5 PFLOP/s dense bf16 peak)
+  prefill512_heavy_tiles
+                matrix-core utilisation on the heavy tiles alone: a 512-token
+                call's routes to experts with 64 or more positions, plus the
+                shared expert over those tokens
   mixed32       batched decode of 32 tokens on a layer with 2-bit gate/up
                 and 4-bit down projections, uniform routing: tokens/s and GB/s
   stack43       a 43-layer stack of full-width layers decoding through one
@@ -63,7 +71,9 @@ METRIC = "MoE-layer tokens/s at 1 GPU (decode & 64-tok prefill); achieved HBM GB
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0          # dense bf16
 TRAFFIC_FILE = ROOT / "profiles" / "gateup_diag_kernel_decode_traffic.json"
-GATEUP_KERNEL = "gateup_diag_kernel<2, true, true>"
+# the decode step's first launch: router rows, gate/up + SwiGLU and the top-6
+# selection in one kernel
+GATEUP_KERNEL = "gateup_diag_kernel<2, true, true, true>"
 COPY_BYTES = 256 << 20
 D, E, DFF, K_TOP, GROUP, BITS = 4096, 256, 2048, 6, 64, 2
 
@@ -73,6 +83,8 @@ def proj_bytes(rows, cols, bits=BITS, group=GROUP):
 
 
 EXPERT_BYTES = 2 * proj_bytes(DFF, D) + proj_bytes(D, DFF)          # 7,864,320
+# the real checkpoint's 2-bit experts come in groups of 128
+G128_EXPERT_BYTES = 2 * proj_bytes(DFF, D, group=128) + proj_bytes(D, DFF, group=128)   # 7,077,888
 MIXED_EXPERT_BYTES = 2 * proj_bytes(DFF, D) + proj_bytes(D, DFF, bits=4)   # 9,961,472
 GATEUP_ROUTE_BYTES = 2 * proj_bytes(DFF, D)                           # 5,242,880
 ROUTER_BYTES = E * D * 2
@@ -85,6 +97,9 @@ GATEUP_ALG_BYTES = (K_TOP + 1) * GATEUP_ROUTE_BYTES + D * 2 + (K_TOP + 1) * DFF 
 # the decode step's gate/up kernel also reads the token's logits and writes its
 # routes (expert, weight, slot)
 SELECT_ALG_BYTES = GATEUP_ALG_BYTES + E * 4 + 3 * K_TOP * 4                            # 36,738,120
+# ... and with its router rows it reads the router weight and hands the logits
+# over itself (one 8-byte tagged word per expert written; the routes read them)
+STEP_GATEUP_ALG_BYTES = GATEUP_ALG_BYTES + ROUTER_BYTES + E * 8 + 3 * K_TOP * 4         # 38,836,296
 
 
 def layer_flops(tokens):
@@ -168,17 +183,22 @@ def decode_graph_run(specs, arena, shareds, slot_of, X, ws, steps, warmup, use_g
 
 
 def stage_timing(specs, arena, shareds, slot_of, X, ws, m=40, replays=5):
-    """Average device time (s) of one launch of each kernel of the decode step
-    -- router logits, gate/up with the in-kernel top-6 selection, down +
-    combine -- and of the gate/up kernel fed with chosen routes (no
-    selection), for reference.
+    """Average device time (s) per launch of the decode step and of its
+    kernels. The step (`decode_step`, locali_moe_forward) is two launches:
+    gateup_diag_kernel<2, true, true, true> -- router rows, gate/up + SwiGLU
+    and the top-6 selection -- then down_combine_kernel. The first cannot run
+    alone (its router rows tag the logits with a generation the down kernel
+    advances), so its average is the step's less the down kernel's
+    (`gateup_router_select`). Also timed, for reference: the separate stages
+    of the same step (router logits kernel, gate/up selecting from those
+    logits, the gate/up kernel fed with chosen routes).
 
     Each stage is captured m times back to back (inputs 0..m-1, so every
     launch streams different experts) into its own HIP graph; HIP events on
     the replay stream bracket `replays` replays, and the per-launch average
     is elapsed / (replays * m) -- the same quantity rocprofv3 reports as a
-    kernel's average duration. Launch i uses router and shared expert
-    i % len(specs), as the decode leg does."""
+    kernel's average duration (plus the launch gap). Launch i uses router
+    and shared expert i % len(specs), as the decode leg does."""
     dev = X.device
     nl = len(specs)
     n_in = X.shape[0]
@@ -192,7 +212,12 @@ def stage_timing(specs, arena, shareds, slot_of, X, ws, m=40, replays=5):
     lbuf = torch.empty(E, dtype=torch.float32, device=dev)
     sel = [tuple(torch.empty(1, K_TOP, dtype=dt, device=dev) for dt in (torch.int32, torch.float32, torch.int32))
            for _ in range(m)]
+    outs = torch.empty(m, D, dtype=torch.bfloat16, device=dev)
+    sidx = torch.empty(m, K_TOP, dtype=torch.int32, device=dev)
+    swts = torch.empty(m, K_TOP, dtype=torch.float32, device=dev)
     stages = {
+        "decode_step": lambda i: ops.forward(specs[i % nl], arena, shareds[i % nl], slot_of, xs[i], ws,
+                                             out=outs[i:i + 1], idx=sidx[i:i + 1], weights=swts[i:i + 1]),
         "router_logits": lambda i: ops.router_logits(specs[i % nl], xs[i], lbuf),
         "gateup_select": lambda i: ops.decode_gateup_select(specs[i % nl], arena, shareds[i % nl], slot_of, xs[i],
                                                             logits[i], hidden, dws, idx=sel[i][0],
@@ -220,6 +245,7 @@ def stage_timing(specs, arena, shareds, slot_of, X, ws, m=40, replays=5):
         e1.record()
         torch.cuda.synchronize()
         res[name] = e0.elapsed_time(e1) / 1e3 / (replays * m)
+    res["gateup_router_select"] = res["decode_step"] - res["down_combine"]
     return res
 
 
@@ -413,6 +439,67 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetc
                         f"logits through copula noise of correlation {lookahead_rho}"}
 
 
+def decode_g128_run(specs, X, dev, steps, warmup, use_graph, seed):
+    """The decode leg on experts in groups of 128, the real checkpoint's
+    2-bit layout (7,077,888 B per expert): same router copies, inputs and
+    step as the headline leg, one g128 shared expert per router copy."""
+    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=BITS, group=128, dtype=torch.bfloat16,
+                               seed=seed, device=dev)
+    shareds = [synth.expert_arena(1, D, DFF, bits_gate_up=BITS, group=128, dtype=torch.bfloat16,
+                                  seed=seed + 1000 + 2 * i, device=dev, zero_slot=False) for i in range(len(specs))]
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=dev)
+    ws = ops.Workspace(dev)
+    ws.reserve(1, D, DFF, E, K_TOP, True)
+    secs, wall, _ = decode_graph_run(specs, arena, shareds, slot_of, X, ws, steps, warmup, use_graph)
+    del arena, shareds
+    torch.cuda.empty_cache()
+    layer = 7 * G128_EXPERT_BYTES + ROUTER_BYTES
+    value = steps / secs
+    return {"value": value, "unit": "tokens/s", "ms_per_step": secs / steps * 1e3, "steps": steps,
+            "expert_bytes": G128_EXPERT_BYTES, "layer_bytes_per_token": layer,
+            "layer_GBps": layer * value / 1e9, "layer_frac_of_hbm_peak": layer * value / 1e9 / HBM_PEAK_GBS,
+            "workload": "the headline decode layer with 2-bit affine experts in groups of 128 (bf16 scales/"
+                        "biases), the real checkpoint's expert layout"}
+
+
+def heavy_tiles_run(arena, shared, slot_of, dev, tokens, calls, seed):
+    """Matrix-core utilisation on the heavy tiles alone: the routes of one
+    Zipf(1.1) call of `tokens` tokens whose expert has at least 64 positions,
+    each as a one-route token (so every heavy expert keeps its tiles), plus
+    the shared expert over those tokens (full 64-position tiles)."""
+    x, w = synth.zipf_router_inputs(tokens, E, D, 1.1, torch.bfloat16, seed=seed, device=dev)
+    spec = ops.RouterSpec(w, K_TOP, routed_scale=1.5)
+    ws = ops.Workspace(dev)
+    idx, _, _ = ops.router(spec, x, ws)
+    counts = torch.bincount(idx.reshape(-1).long(), minlength=E)
+    heavy = (counts >= 64).nonzero().reshape(-1)
+    sel = torch.isin(idx.long(), heavy)
+    tok = sel.nonzero()[:, 0]
+    xh = x[tok].contiguous()
+    ih = idx[sel].reshape(-1, 1).contiguous()
+    n = xh.shape[0]
+    ones = torch.ones(n, 1, device=dev)
+    for _ in range(2):
+        ops.expert_grouped(arena, shared, xh, ih, slot_of, ones, ws, n_experts=E)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(calls):
+        ops.expert_grouped(arena, shared, xh, ih, slot_of, ones, ws, n_experts=E)
+    e1.record()
+    torch.cuda.synchronize()
+    per_call = e0.elapsed_time(e1) / 1e3 / calls
+    flops = 2 * (2 * n) * 3 * D * DFF            # n routed routes + n shared routes
+    tiles = int(sum((int(c) + 63) // 64 for c in counts[heavy].tolist())) + (n + 63) // 64
+    return {"from_tokens": tokens, "heavy_experts": int(heavy.numel()),
+            "positions_per_heavy_expert": sorted(counts[heavy].tolist(), reverse=True),
+            "routes": 2 * n, "tiles": tiles, "ms_per_call": per_call * 1e3,
+            "achieved_TFLOPs": flops / per_call / 1e12,
+            "mfma_utilisation": flops / per_call / 1e12 / MFMA_PEAK_TFLOPS,
+            "bytes_per_call": int((heavy.numel() + 1) * EXPERT_BYTES),
+            "frac_of_hbm_peak": (heavy.numel() + 1) * EXPERT_BYTES / per_call / 1e9 / HBM_PEAK_GBS}
+
+
 def cpu_baseline(arena, shared, spec, X, seconds):
     """C oracle on the host cores, decode tokens until `seconds` elapse on
     every core, then for half as long on one core."""
@@ -500,7 +587,7 @@ def summarize_pmc(fetch_csv, write_csv, out_path=TRAFFIC_FILE):
     write = per_kernel(write_csv, "WRITE_SIZE", "FillFunctor")
     res = {"kernel": GATEUP_KERNEL, "fetch": fetch, "write": write,
            "traffic_bytes_per_launch": fetch["bytes_per_launch"] + write["bytes_per_launch"],
-           "algorithmic_bytes_per_launch": SELECT_ALG_BYTES}
+           "algorithmic_bytes_per_launch": STEP_GATEUP_ALG_BYTES}
     Path(out_path).write_text(json.dumps(res, indent=1) + "\n")
     print(json.dumps(res, indent=1))
     return res
@@ -562,6 +649,8 @@ def main(argv=None):
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--prefill-sizes", default="64,512", help="tokens per prefill call, comma-separated")
     ap.add_argument("--skip-mixed", action="store_true")
+    ap.add_argument("--skip-g128", action="store_true")
+    ap.add_argument("--skip-heavy", action="store_true")
     ap.add_argument("--skip-stack", action="store_true")
     ap.add_argument("--stack-steps", type=int, default=128)
     ap.add_argument("--stack-warmup", type=int, default=16)
@@ -627,11 +716,15 @@ def main(argv=None):
     value = args.steps / secs
     layer_bytes = 7 * EXPERT_BYTES + ROUTER_BYTES
 
-    phase("stage timing (router logits, gate/up with selection, down+combine graphs)")
+    phase("stage timing (decode step, down + combine, separate stages)")
     st = stage_timing(specs, arena, shareds, slot_of, X, ws)
+    gate_bytes = STEP_GATEUP_ALG_BYTES
+    achieved = gate_bytes / st["gateup_router_select"] / 1e9
+    g128 = None
+    if not args.skip_g128:
+        phase("decode, experts in groups of 128 (graph replay)")
+        g128 = decode_g128_run(specs, X, dev, args.steps, args.warmup, not args.no_graph, args.seed + 50)
     del specs, shareds
-    gate_bytes = SELECT_ALG_BYTES
-    achieved = gate_bytes / st["gateup_select"] / 1e9
     result = {
         "metric": METRIC,
         "value": value,
@@ -662,29 +755,37 @@ def main(argv=None):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gateup_diag_kernel<2, true, true>: the decode step's gate/up + clamped SwiGLU "
-                      "on the matrix cores for 7 routes, each routed workgroup selecting its token's "
-                      "top-6 from the logits first (the kernel that runs in the timed step)",
+            "kernel": f"{GATEUP_KERNEL}: the decode step's first launch -- the shared expert's "
+                      "workgroups compute the router logits first (2 MiB gate), then the gate/up + clamped "
+                      "SwiGLU of 7 routes on the matrix cores, each routed workgroup selecting its "
+                      "token's top-6 from the logits",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": measured_traffic(),
             "algorithmic_bytes_per_launch": gate_bytes,
-            "avg_launch_us": st["gateup_select"] * 1e6,
+            "avg_launch_us": st["gateup_router_select"] * 1e6,
+            "measured_as": "decode_step - down_combine: HIP events around graphs of 40 back-to-back launches",
             "stage_us": {k: v * 1e6 for k, v in st.items()},
             "chosen_routes_variant": {
-                "kernel": "gateup_diag_kernel<2, true, false> (same kernel fed with chosen routes)",
+                "kernel": "gateup_diag_kernel<2, true, false, false> (the same kernel fed with chosen routes)",
                 "avg_launch_us": st["gateup_chosen_routes"] * 1e6,
                 "achieved": GATEUP_ALG_BYTES / st["gateup_chosen_routes"] / 1e9,
                 "frac": GATEUP_ALG_BYTES / st["gateup_chosen_routes"] / 1e9 / HBM_PEAK_GBS},
         },
     }
+    if g128 is not None:
+        result["decode_g128"] = g128
     if not args.skip_prefill:
         for tokens in (int(v) for v in args.prefill_sizes.split(",")):
             phase(f"prefill {tokens} tokens")
             result[f"prefill{tokens}"] = prefill_run(arena, shared, slot_of, dev, tokens,
                                                      args.prefill_calls, args.seed + 100)
+        if not args.skip_heavy:
+            phase("heavy tiles of a 512-token prefill")
+            result["prefill512_heavy_tiles"] = heavy_tiles_run(arena, shared, slot_of, dev, 512,
+                                                               args.prefill_calls, args.seed + 100)
     if not args.skip_mixed:
         phase("mixed 2/4-bit, 32 tokens")
         result["mixed32"] = mixed_run(dev, 32, args.prefill_calls, args.seed + 200)
