@@ -793,10 +793,46 @@ class ArenaMoE:
         slots = self._device_slots([[placed[e][1] for e in row] for row in ii], flat.device)
         return self._run_experts(t, flat, slots, gates, dtype)
 
+    def _gather(self, t, inputs, indices):
+        """Unweighted expert outputs of tier t, the reference's gather hook
+        (arena.py:674-681, dsv4_arena.py:168-235): inputs [n, 1, 1, d]
+        activations and indices [n, k] device slots of tier t give
+        [n, k, 1, d], entry (r, j) the expert of slot indices[r, j] applied
+        to inputs[r], in the tier's activation dtype (bf16 activations become
+        fp16 for a tier of fp16 metadata, as the reference casts them). Each
+        route is one row of a one-route call with weight 1, so an entry is
+        the expert's down output rounded once to that dtype.
+
+        The module's own calls fuse this with the combine (_run_experts).
+        When a subclass overrides _gather, every tier evaluation of __call__
+        goes through the override instead, and the library's combine then
+        takes its outputs in the order the fused kernels do."""
+        n, k = indices.shape
+        d = inputs.shape[-1]
+        x_in = inputs.reshape(n, d)
+        if x_in.dtype == torch.bfloat16 and self.store.use_f16(t):
+            x_in = x_in.to(torch.float16)
+        rows = x_in.repeat_interleave(k, dim=0).contiguous()
+        slots = indices.reshape(n * k, 1).to(torch.int32).contiguous()
+        y = self._routes(self.store.expert_arena(t), rows, slots, self._workspace())
+        return y.view(n, k, 1, d)
+
+    def _gather_overridden(self) -> bool:
+        return type(self)._gather is not ArenaMoE._gather
+
+    def _tier_routes(self, t, x_in, slots, ws):
+        """One route per row of x_in through tier t ([n, 1] slots): _routes,
+        or the subclass's _gather when it replaces the hook."""
+        if self._gather_overridden():
+            return self._gather(t, x_in[:, None, None, :], slots).reshape(x_in.shape[0], x_in.shape[-1])
+        return self._routes(self.store.expert_arena(t), x_in, slots, ws)
+
     def _run_experts(self, t, flat, slots, gates, dtype):
         """Tier t's expert kernels over device route slots [T, k]: the decode
         kernels up to two tokens, the slot-grouped kernels beyond."""
         from . import ops
+        if self._gather_overridden():
+            return self._combine_gathered(t, flat, slots, gates, dtype)
         T = flat.shape[0]
         arena = self.store.expert_arena(t)
         x_in = flat.contiguous()
@@ -813,6 +849,26 @@ class ArenaMoE:
             y = ops.expert_grouped(arena, self.shared_expert, x_in, slots, ident, w, ws, n_experts=n,
                                    swiglu_limit=self.swiglu_limit, fp32_swiglu=self.fp32_swiglu)
         return y.to(dtype)
+
+    def _combine_gathered(self, t, flat, slots, gates, dtype):
+        """The [T, k] routes through a subclass's _gather, then the single-tier
+        combine the fused kernels apply (each product of y and the rounded
+        weight rounded, summed in float32, one rounding), then the folded
+        shared expert with one more rounding."""
+        from . import ops
+        T, k = slots.shape
+        x_in = flat.contiguous()
+        if x_in.dtype == torch.bfloat16 and self.store.use_f16(t):
+            x_in = x_in.to(torch.float16)
+        y = self._gather(t, x_in[:, None, None, :], slots).reshape(T * k, -1).to(x_in.dtype)
+        route_pos = torch.arange(T * k, dtype=torch.int32, device=flat.device).view(T, k)
+        shared_y = None
+        if self.shared_expert is not None:
+            zero = torch.zeros(T, 1, dtype=torch.int32, device=flat.device)
+            shared_y = self._routes(self.shared_expert, x_in, zero, self._workspace())
+        out = ops.combine_routes(y, route_pos, gates.to(torch.float32).contiguous(), x_in.dtype,
+                                 shared_y=shared_y, mode=ops.COMBINE_ROUNDED)
+        return out.to(dtype)
 
     def _device_slots(self, rows, device):
         """[T, k] int32 slots on the device by an asynchronous copy from a
@@ -867,7 +923,6 @@ class ArenaMoE:
         dev = flat.device
         ready = [j for j, e in enumerate(row) if e not in pending]
         late = [j for j, e in enumerate(row) if e in pending]
-        arena = self.store.expert_arena(t)
         x_in = flat.contiguous()
         if self.store.use_f16(t) and x_in.dtype == torch.bfloat16:
             x_in = x_in.to(torch.float16)
@@ -875,7 +930,7 @@ class ArenaMoE:
 
         def run(pos):
             slots = self._device_slots([[placed[row[j]][1]] for j in pos], dev)
-            return self._routes(arena, x_in.expand(len(pos), -1).contiguous(), slots, ws)
+            return self._tier_routes(t, x_in.expand(len(pos), -1).contiguous(), slots, ws)
 
         y_ready = run(ready)
         self.store.wait(reads[t])
@@ -914,7 +969,7 @@ class ArenaMoE:
             x_in = flat.index_select(0, rows).contiguous()
             if self.store.use_f16(t) and x_in.dtype == torch.bfloat16:
                 x_in = x_in.to(torch.float16)
-            ys.append(self._routes(self.store.expert_arena(t), x_in, slots, ws))
+            ys.append(self._tier_routes(t, x_in, slots, ws))
             for i, rj in enumerate(ent):
                 entry[rj] = base + i
             base += len(ent)

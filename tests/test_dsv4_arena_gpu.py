@@ -381,6 +381,56 @@ def test_overlap_hits_splits_a_decode_call_and_stays_exact(ckpt, with_shared):
         store.close()
 
 
+@pytest.mark.parametrize("T", [1, 5])
+def test_gather_hook_follows_the_reference_contract(ckpt, oracle_lib, T):
+    """_gather(tier, inputs [n, 1, 1, d], indices [n, k]) -> [n, k, 1, d]
+    unweighted per-route expert outputs (reference arena.py:674-681,
+    dsv4_arena.py:168-235): each entry within the expert-output tolerance of
+    the oracle's expert on that route. A subclass that overrides _gather (the
+    reference's _apply -> _gather contract) is called through it by
+    __call__, and since each route's output and the combine's arithmetic are
+    the fused kernels', its layer output equals the module's own, with and
+    without a folded shared expert."""
+    from gpu_helpers import assert_close
+    from oracle import cref
+    truth, index, _ = ckpt
+    banner(f"v4 arena _gather hook T={T}")
+    store = V4ArenaStore(index, ceiling_gb=(E + 1) * _item(index) / 1e9 + 1e-6, threads=2)
+    calls = []
+
+    class Hooked(V4ArenaMoE):
+        def _gather(self, tier, inputs, indices):
+            calls.append((tier, tuple(inputs.shape), tuple(indices.shape)))
+            return super()._gather(tier, inputs, indices)
+
+    try:
+        g = torch.Generator().manual_seed(70 + T)
+        x = (torch.randn(T, D, generator=g) * 0.5).to(torch.bfloat16).cuda()
+        ind = torch.tensor([[1, 4], [4, 5], [0, 1], [2, 3], [5, 0]][:T], dtype=torch.int32, device="cuda")
+        sc = torch.tensor([[0.6, 0.4], [0.3, 0.7], [0.5, 0.5], [0.9, 0.1], [0.2, 0.8]][:T], device="cuda")
+        shared = _gpu(synth.expert_arena(1, D, DFF, bits_gate_up=2, group=64, dtype=torch.bfloat16,
+                                         seed=43, zero_slot=False))
+        for sh in (None, shared):
+            own = V4ArenaMoE(store, 0, FixedGate(ind, sc), K, swiglu_limit=10.0, shared_expert=sh)(x)
+            calls.clear()
+            hooked = Hooked(store, 0, FixedGate(ind, sc), K, swiglu_limit=10.0, shared_expert=sh)
+            got = hooked(x)
+            assert calls == [("cold", (T, 1, 1, D), (T, K))]
+            assert torch.equal(got, own), f"hooked layer output differs (shared={sh is not None})"
+        placed = store.slots_for(0, sorted(set(ind.reshape(-1).tolist())))
+        slots = torch.tensor([[placed[e][1] for e in row] for row in ind.tolist()], dtype=torch.int32,
+                             device="cuda")
+        y = V4ArenaMoE(store, 0, FixedGate(ind, sc), K, swiglu_limit=10.0)._gather(
+            "cold", x[:, None, None, :], slots)
+        assert y.shape == (T, K, 1, D) and y.dtype == torch.bfloat16
+        want = cref.load().moe_layer(x.float().cpu().numpy().repeat(K, axis=0),
+                                     ind.reshape(-1, 1).cpu().numpy(), np.ones((T * K, 1), np.float32),
+                                     arena_numpy(truth[0], float_meta=False), "bf16", limit=10.0)
+        assert_close(y.reshape(T * K, D).float().cpu().numpy(), want, "_gather vs oracle experts")
+    finally:
+        store.close()
+
+
 def test_two_tier_store_streams_cold_and_hot_layers(tmp_path):
     """An index extended with the DSpark/MTP stage (reference
     dsv4_index.py:146-249): main layers in the 2-bit cold tier, the stage as
