@@ -328,7 +328,7 @@ def mixed_run(dev, tokens, calls, seed):
 
 
 def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetch_k=None,
-              lookahead_rho=LOOKAHEAD_RHO, device_planner=False):
+              lookahead_rho=LOOKAHEAD_RHO, device_planner=False, mark=None):
     """Decode through a stack of full-width layers sharing one bounded arena,
     misses copied from pinned host memory (V4ArenaStore host_source).
 
@@ -344,7 +344,10 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetc
 
     device_planner: the planner runs on the GPU (same decisions), so a
     layer's router, planner, fills and expert kernels queue on the stream
-    with no per-layer host round trip."""
+    with no per-layer host round trip.
+
+    mark(suffix): called (after a device synchronize) when the timed tokens
+    start and when they end, for the bench's phase log."""
     import tempfile
     from locali_amd.dsv4_arena import V4ArenaMoE, V4ArenaStore, V4Gate
     tmp = tempfile.TemporaryDirectory()
@@ -399,6 +402,8 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetc
                 mods[layer](X[t, layer:layer + 1])
     torch.cuda.synchronize()
     store.reset_stats()
+    if mark:
+        mark("timed tokens")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     with torch.cuda.stream(compute):
@@ -409,6 +414,8 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetc
         e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    if mark:
+        mark("teardown")
     secs = e0.elapsed_time(e1) / 1e3
     st = store.stats()
     store.close()
@@ -597,12 +604,19 @@ def summarize_trace(trace_csv, phases_json):
     """Per-phase kernel table (markdown) from a rocprofv3 --kernel-trace CSV of
     a run made with --phase-log: kernels are assigned to the bench phase
     whose [start, next start) window holds their start timestamp (both
-    clocks are CLOCK_MONOTONIC nanoseconds)."""
+    clocks are CLOCK_MONOTONIC nanoseconds).
+
+    Each phase also gets the occupancy of the library's kernels over their
+    span (first start to last end): the time some host-to-HBM copy launch
+    (the fill kernels and the device planner's plan-and-copy launch) is
+    running, the time any library kernel is running, and the time no copy
+    launch is running."""
     import csv
     marks = json.loads(Path(phases_json).read_text())["phases"]
     bounds = [(name, t0, marks[i + 1][1] if i + 1 < len(marks) else float("inf"))
               for i, (name, t0) in enumerate(marks)]
     per = {name: {} for name, _, _ in bounds}
+    spans = {name: {"copy": [], "all": []} for name, _, _ in bounds}
     unassigned = 0
     for r in csv.DictReader(open(trace_csv)):
         t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
@@ -610,16 +624,40 @@ def summarize_trace(trace_csv, phases_json):
         for ph, a, b in bounds:
             if a <= t0 < b:
                 per[ph].setdefault(name, []).append((t1 - t0) / 1e3)
+                if "locali" in name or "dplan" in name:
+                    spans[ph]["all"].append((t0, t1))
+                    if "fill_kernel" in name or "dplan_kernel<true>" in name:
+                        spans[ph]["copy"].append((t0, t1))
                 break
         else:
             unassigned += 1
+
+    def union(iv):
+        tot, end = 0, None
+        for a, b in sorted(iv):
+            if end is None or a > end:
+                tot += b - a
+                end = b
+            elif b > end:
+                tot += b - end
+                end = b
+        return tot
+
     out = []
     for ph, _, _ in bounds:
         ks = per[ph]
         if not ks:
             continue
         total = sum(sum(v) for v in ks.values())
-        out += [f"### {ph}", "", "| kernel | calls | avg us | min us | max us | share of phase kernel time |",
+        out += [f"### {ph}", ""]
+        iv = spans[ph]
+        if iv["copy"]:
+            span = max(b for _, b in iv["all"]) - min(a for a, _ in iv["all"])
+            cu, au = union(iv["copy"]), union(iv["all"])
+            out += [f"Library kernels span {span / 1e6:.2f} ms: a host-to-HBM copy launch runs {cu / 1e6:.2f} ms "
+                    f"({100 * cu / span:.1f} %), some library kernel {au / 1e6:.2f} ms ({100 * au / span:.1f} %); "
+                    f"no copy launch runs for {(span - cu) / 1e6:.2f} ms ({100 * (span - cu) / span:.1f} %).", ""]
+        out += ["| kernel | calls | avg us | min us | max us | share of phase kernel time |",
                 "|---|---:|---:|---:|---:|---:|"]
         for name, v in sorted(ks.items(), key=lambda kv: -sum(kv[1])):
             if "locali" not in name and sum(v) < 0.01 * total:
@@ -659,6 +697,9 @@ def main(argv=None):
     ap.add_argument("--stack-prefetch", default="5",
                     help="comma-separated prefetch widths for extra slru-all stack legs with "
                          "cross-layer prefetch at depth 1 (0: none)")
+    ap.add_argument("--stack-device-prefetch", default="1,5",
+                    help="comma-separated prefetch widths for extra slru-all stack legs planned on the GPU "
+                         "with cross-layer prefetch at depth 1 (0: none)")
     ap.add_argument("--stack-device-planner", default="slru-all,lfu-decay",
                     help="comma-separated cache policies for extra stack legs planned on the GPU")
     ap.add_argument("--stack-lookahead-rho", type=float, default=LOOKAHEAD_RHO,
@@ -791,20 +832,21 @@ def main(argv=None):
         result["mixed32"] = mixed_run(dev, 32, args.prefill_calls, args.seed + 200)
     if not args.skip_stack:
         result["stack43"] = []
-        for policy in args.stack_policies.split(","):
-            phase(f"43-layer bounded arena, {policy}")
-            result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, policy,
-                                               args.seed + 300, lookahead_rho=args.stack_lookahead_rho))
+        def leg(label, policy, **kw):
+            phase(label)
+            result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, policy, args.seed + 300,
+                                               lookahead_rho=args.stack_lookahead_rho,
+                                               mark=lambda what: phase(f"{label}: {what}"), **kw))
+
+        for policy in (v for v in args.stack_policies.split(",") if v.strip()):
+            leg(f"43-layer bounded arena, {policy}", policy)
         for policy in (v for v in args.stack_device_planner.split(",") if v.strip()):
-            phase(f"43-layer bounded arena, {policy}, device planner")
-            result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, policy,
-                                               args.seed + 300, lookahead_rho=args.stack_lookahead_rho,
-                                               device_planner=True))
+            leg(f"43-layer bounded arena, {policy}, device planner", policy, device_planner=True)
         for k in (int(v) for v in args.stack_prefetch.split(",") if v.strip() and int(v)):
-            phase(f"43-layer bounded arena, slru-all, prefetch top-{k} at depth 1")
-            result["stack43"].append(stack_run(dev, args.stack_steps, args.stack_warmup, "slru-all",
-                                               args.seed + 300, prefetch_k=k,
-                                               lookahead_rho=args.stack_lookahead_rho))
+            leg(f"43-layer bounded arena, slru-all, prefetch top-{k} at depth 1", "slru-all", prefetch_k=k)
+        for k in (int(v) for v in args.stack_device_prefetch.split(",") if v.strip() and int(v)):
+            leg(f"43-layer bounded arena, slru-all, device planner, prefetch top-{k} at depth 1", "slru-all",
+                prefetch_k=k, device_planner=True)
     if not args.skip_cpu:
         phase("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(arena, shared, spec, X, args.cpu_seconds)

@@ -41,7 +41,7 @@ int locali_cache_plan_each(locali_cache *cache, const int32_t *keys, size_t key_
  * layer * n_experts + expert, slot 0 is reserved, and usable slots are handed
  * out highest-first, as the host planner. The kernel holds the slot state in
  * LDS: locali_dplan_lds_bytes(slots, n_experts, policy) must stay within
- * 156 KiB (about 11,000 slots under SLRU and 6,000 under LFU_DECAY for 256
+ * 156 KiB (about 10,000 slots under SLRU and 5,600 under LFU_DECAY for 256
  * experts); locali_dplan_plan refuses larger ones.
  *
  * locali_dplan_plan plans the distinct experts of expert_idx[routes] (device
@@ -72,6 +72,23 @@ int locali_cache_plan_each(locali_cache *cache, const int32_t *keys, size_t key_
  * is dispatched first; one that still waits after about a second gives up
  * and sets LOCALI_DPLAN_E_FILL.
  *
+ * locali_dplan_prefetch is the cross-layer prefetch call of the same planner
+ * (reference arena.py:518-541 over native/locali_core.c:259-313, as
+ * V4ArenaStore.submit(..., prefetch=True) makes it on the host): expert_idx
+ * and weights are `rows` rows of top_k routes of a lookahead routing (device
+ * int32 and fp32); the call's keys are, row by row, each row's take_k highest
+ * weights in descending order, equal weights in row order (every route in
+ * route order when take_k is 0 or >= top_k), deduplicated in first-appearance
+ * order. It plans them with hits left in place (touch_hits 0), the last
+ * demand call's slots pinned and not replaced, no LFU token tick, and keys it
+ * cannot place dropped without error; it writes no route slots, and counts
+ * its placed misses as prefetched. A later demand hit on a slot a prefetch
+ * filled counts as prefetch_used, its eviction before one as
+ * prefetch_wasted. With dst_base non-null the launch also copies the placed
+ * misses, as locali_dplan_plan_fill; with dst_base null it only plans
+ * (locali_dplan_fill copies afterwards). It must run in stream order with the
+ * state's other calls.
+ *
  * locali_dplan_read copies the counters (and up to max_results per-key
  * results of the last call) to the host and waits for the stream.
  */
@@ -89,6 +106,7 @@ typedef struct {
     int32_t error;
     int32_t probation, protected_, free_slots;
     int32_t last_keys, last_misses;
+    uint64_t prefetched, prefetch_used, prefetch_wasted;
 } locali_dplan_stats;
 
 size_t locali_dplan_state_bytes(int32_t key_capacity, int32_t slots, int32_t max_routes);
@@ -105,6 +123,10 @@ int locali_dplan_plan_fill(void *state, int32_t key_capacity, int32_t slots, int
                            const int32_t *expert_idx, int32_t routes, int32_t layer, int32_t n_experts,
                            int32_t top_k, int32_t touch_hits, int32_t *route_slot, void *const *dst_base,
                            const size_t *slot_bytes, int32_t n_arrays, const uint64_t *host_src, void *stream);
+int locali_dplan_prefetch(void *state, int32_t key_capacity, int32_t slots, int32_t policy, int32_t max_routes,
+                          const int32_t *expert_idx, const float *weights, int32_t rows, int32_t top_k,
+                          int32_t take_k, int32_t layer, int32_t n_experts, void *const *dst_base,
+                          const size_t *slot_bytes, int32_t n_arrays, const uint64_t *host_src, void *stream);
 int locali_dplan_host_view(const void *const *src_host, int32_t n, uint64_t *out);
 int locali_dplan_read(const void *state, locali_dplan_stats *stats, locali_cache_result *results,
                       int32_t max_results, void *stream);

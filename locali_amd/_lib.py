@@ -44,6 +44,9 @@ class DPlanStats(ctypes.Structure):
         ("free_slots", ctypes.c_int32),
         ("last_keys", ctypes.c_int32),
         ("last_misses", ctypes.c_int32),
+        ("prefetched", ctypes.c_uint64),
+        ("prefetch_used", ctypes.c_uint64),
+        ("prefetch_wasted", ctypes.c_uint64),
     ]
 
 
@@ -110,6 +113,8 @@ _SIGNATURES = {
                            _I, _P], ctypes.c_int),
     "locali_dplan_plan_fill": ([_P, _I, _I, _I, _I, _P, _I, _I, _I, _I, _I, _P, ctypes.POINTER(ctypes.c_void_p),
                                 ctypes.POINTER(ctypes.c_size_t), _I, _P, _P], ctypes.c_int),
+    "locali_dplan_prefetch": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_void_p),
+                               ctypes.POINTER(ctypes.c_size_t), _I, _P, _P], ctypes.c_int),
     "locali_dplan_host_view": ([ctypes.POINTER(ctypes.c_void_p), _I, ctypes.POINTER(ctypes.c_uint64)],
                                ctypes.c_int),
     "locali_dplan_read": ([_P, ctypes.POINTER(DPlanStats), ctypes.POINTER(CacheResult), _I, _P], ctypes.c_int),

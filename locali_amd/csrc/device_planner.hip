@@ -76,12 +76,13 @@ struct DPlanHeader {
     int32_t exited, pad[3];
     uint64_t rclock, lclock;
     uint64_t hits, misses, evictions, calls;
+    uint64_t prefetched, pf_used, pf_wasted;
 };
 
 __host__ __device__ constexpr size_t align256(size_t x) { return (x + 255) & ~size_t{255}; }
 
 struct DPlanLayout {
-    size_t slot_of, hot, lst, owner, where, rst, pinned, res, miss_e, miss_s, total;
+    size_t slot_of, hot, lst, owner, where, spf, rst, pinned, res, miss_e, miss_s, total;
 };
 
 __host__ __device__ inline DPlanLayout dplan_layout(int n_keys, int n_slots, int max_routes) {
@@ -97,6 +98,7 @@ __host__ __device__ inline DPlanLayout dplan_layout(int n_keys, int n_slots, int
     L.lst = take(sizeof(uint64_t) * n_keys);
     L.owner = take(sizeof(int32_t) * n_slots);
     L.where = take(sizeof(uint8_t) * n_slots);
+    L.spf = take(sizeof(uint8_t) * n_slots);
     L.rst = take(sizeof(uint64_t) * n_slots);
     L.pinned = take(sizeof(int32_t) * max_routes);
     L.res = take(sizeof(locali_cache_result) * max_routes);
@@ -107,14 +109,15 @@ __host__ __device__ inline DPlanLayout dplan_layout(int n_keys, int n_slots, int
 }
 
 // Dynamic LDS of one plan call: slot-indexed state (recency stamps, LFU
-// hotness and stamps for the LFU policy, owners, segments, pins), then the
+// hotness and stamps for the LFU policy, owners, segments, pins, the flag of
+// a slot whose key a prefetch placed and no demand call has used yet), then the
 // layer's experts (their keys' slots, hotness and stamps, first route, slot
 // chosen, the deduplicated list).
 struct PlanLds {
     uint64_t *rst, *lst, *klst;
     uint32_t *hot, *khot;
     int32_t *owner, *kslot, *first, *eslot, *want;
-    uint8_t *where, *pin, *dirty;
+    uint8_t *where, *pin, *dirty, *spf;
 };
 
 __host__ __device__ inline size_t plan_lds_bytes(int n_slots, int E, bool lfu) {
@@ -122,7 +125,7 @@ __host__ __device__ inline size_t plan_lds_bytes(int n_slots, int E, bool lfu) {
     if (lfu) b += sizeof(uint64_t) * n_slots + sizeof(uint32_t) * n_slots;   // lst, hot
     b += sizeof(uint32_t) * E;                                            // khot
     b += sizeof(int32_t) * n_slots + 4 * sizeof(int32_t) * E;            // owner, kslot, first, eslot, want
-    b += 3 * sizeof(uint8_t) * n_slots;                                   // where, pin, dirty
+    b += 4 * sizeof(uint8_t) * n_slots;                                   // where, pin, dirty, spf
     return (b + 15) & ~size_t{15};
 }
 
@@ -148,6 +151,7 @@ __device__ inline PlanLds carve(unsigned char *p, int n_slots, int E, bool lfu) 
     L.where = take(n_slots);
     L.pin = take(n_slots);
     L.dirty = take(n_slots);
+    L.spf = take(n_slots);
     return L;
 }
 
@@ -325,10 +329,11 @@ struct Planner {
     const PlanLds &L;
     int32_t *g_slot_of;
     int layer, E, pcap, prob_cap;
-    bool lfu;
+    bool lfu, prefetch;
     int32_t n_probation, n_protected;
     int32_t free_count;
     uint64_t rclock, lclock;
+    uint64_t pf_wasted = 0;
 
     __device__ Planner(const PlanLds &lds) : L(lds) {}
 
@@ -351,6 +356,7 @@ struct Planner {
         L.kslot[e] = s;
         g_slot_of[key] = s;
         L.owner[s] = key;
+        L.spf[s] = prefetch ? 1 : 0;
         push(s, kProbation);
         if (lfu) {
             L.hot[s] = L.khot[e];
@@ -360,6 +366,10 @@ struct Planner {
     // Frees slot v of its key; returns that key.
     __device__ int evict(int v) {
         const int k = L.owner[v];
+        if (L.spf[v]) {   // a prefetched key leaves unused
+            ++pf_wasted;
+            L.spf[v] = 0;
+        }
         unlink(v);
         g_slot_of[k] = -1;
         if (k >= layer * E && k < layer * E + E) L.kslot[k - layer * E] = -1;
@@ -368,8 +378,42 @@ struct Planner {
     }
 };
 
+// The keys of a call, in order. A demand call takes its routes' experts in
+// route order. A prefetch call reads rows of top_k routes with their gate
+// weights and takes, row by row, the `take` highest weights of each row in
+// descending order, equal weights in row order (a stable sort of the negated
+// weights); with take >= top_k it takes every route in route order.
+struct KeySeq {
+    const int32_t *idx;
+    const float *w;
+    int top_k, take;
+    bool ranked;
+
+    __device__ int at(int p) const {
+        if (!ranked) return idx[p];
+        const int row = p / take, q = p - row * take;
+        const int32_t *ri = idx + static_cast<int64_t>(row) * top_k;
+        const float *rw = w + static_cast<int64_t>(row) * top_k;
+        for (int j = 0; j < top_k; ++j) {
+            const float wj = rw[j];
+            int rank = 0;
+            for (int i = 0; i < top_k; ++i) {
+                const float wi = rw[i];
+                rank += (wi > wj || (wi == wj && i < j)) ? 1 : 0;
+            }
+            if (rank == q) return ri[j];
+        }
+        return -1;   // NaN weights rank nowhere: the call is marked (LOCALI_DPLAN_E_EXPERT)
+    }
+};
+
 // The planner's shape travels in the arguments (the launch sized its LDS by
-// them); a state whose header disagrees is left alone and marked. kFused:
+// them); a state whose header disagrees is left alone and marked. A
+// prefetch call (prefetch != 0; idx and weights are rows of top_k routes)
+// plans its keys with hits left in place, does not replace the pinned set
+// of the last demand call, skips the LFU token tick, drops keys it cannot
+// place, writes no route slots and counts its placements as prefetched
+// instead of hits and misses. kFused:
 // workgroup 0 plans and publishes each miss as it is decided, workgroups 1..
 // copy the published misses meanwhile (copy_workgroup).
 template <bool kFused>
@@ -378,7 +422,9 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
                                                              const int32_t *__restrict__ idx, int routes,
                                                              int layer, int E, int top_k, int touch_hits,
                                                              int32_t *__restrict__ route_slot, DPlanFillArgs fa,
-                                                             const uint64_t *__restrict__ host_src) {
+                                                             const uint64_t *__restrict__ host_src,
+                                                             const float *__restrict__ pf_weights, int take_k,
+                                                             int prefetch) {
     extern __shared__ __align__(16) unsigned char plds[];
     __shared__ PlanShared sh;
     DPlanHeader *H = reinterpret_cast<DPlanHeader *>(state);
@@ -404,6 +450,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     uint64_t *g_lst = reinterpret_cast<uint64_t *>(state + G.lst);
     int32_t *g_owner = reinterpret_cast<int32_t *>(state + G.owner);
     uint8_t *g_where = state + G.where;
+    uint8_t *g_spf = state + G.spf;
     uint64_t *g_rst = reinterpret_cast<uint64_t *>(state + G.rst);
     int32_t *g_pinned = reinterpret_cast<int32_t *>(state + G.pinned);
     locali_cache_result *g_res = reinterpret_cast<locali_cache_result *>(state + G.res);
@@ -411,15 +458,19 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     int32_t *g_miss_s = reinterpret_cast<int32_t *>(state + G.miss_s);
     const PlanLds L = carve(plds, n_slots, E, lfu);
     const int kbase = layer * E;
+    const int take = prefetch && take_k > 0 && take_k < top_k ? take_k : top_k;
+    const KeySeq seq{idx, pf_weights, top_k, take, take < top_k};
+    const int n_seq = take < top_k ? routes / top_k * take : routes;
 
-    // ---- state into LDS; the first routes and pins travel with it
+    // ---- state into LDS; the first keys and pins travel with it
     const int n_pinned_prev = H->n_pinned;
-    const int my_e = tid < routes ? idx[tid] : -1;
+    const int my_e = tid < n_seq ? seq.at(tid) : -1;
     const int my_pin = tid < n_pinned_prev ? g_pinned[tid] : 0;
     for (int s = tid; s < n_slots; s += kPlanThreads) {
         const int k = g_owner[s];
         L.owner[s] = k;
         L.where[s] = g_where[s];
+        L.spf[s] = g_spf[s];
         L.rst[s] = g_rst[s];
         L.pin[s] = 0;
         L.dirty[s] = 0;
@@ -438,10 +489,10 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     if (tid == 0) sh.bad = 0;
     __syncthreads();
 
-    // ---- the routes' experts in first-appearance order; the previous
+    // ---- the call's experts in first-appearance order; the previous
     // demand call's slots pinned
-    for (int r = tid; r < routes; r += kPlanThreads) {
-        const int e = r < kPlanThreads ? my_e : idx[r];
+    for (int r = tid; r < n_seq; r += kPlanThreads) {
+        const int e = r < kPlanThreads ? my_e : seq.at(r);
         if (e >= 0 && e < E) atomicMin(&L.first[e], r);
         else sh.bad = 1;
     }
@@ -451,12 +502,12 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     }
     __syncthreads();
     int carry = 0;
-    for (int r0 = 0; r0 < routes; r0 += kPlanThreads) {
+    for (int r0 = 0; r0 < n_seq; r0 += kPlanThreads) {
         const int r = r0 + tid;
         int e = -1;
         bool head = false;
-        if (r < routes) {
-            e = r0 == 0 ? my_e : idx[r];
+        if (r < n_seq) {
+            e = r0 == 0 ? my_e : seq.at(r);
             head = e >= 0 && e < E && L.first[e] == r;
         }
         const uint64_t m = __ballot(head);
@@ -474,7 +525,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     if (tid == 0) {
         sh.n_want = carry;
         int decay = 0;
-        if (lfu && layer == 0 && carry <= top_k) {
+        if (lfu && !prefetch && layer == 0 && carry <= top_k) {
             const uint32_t t = static_cast<uint32_t>(H->tokens_seen) + 1u;
             H->tokens_seen = static_cast<int32_t>(t);
             decay = t % 16u == 0u;
@@ -498,6 +549,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     P.layer = layer;
     P.E = E;
     P.lfu = lfu;
+    P.prefetch = prefetch != 0;
     P.pcap = H->protected_cap;
     P.prob_cap = H->probation_cap;
     P.n_probation = H->count_probation;
@@ -509,7 +561,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     int phase = kDone, e = 0, key = 0, slot = -1, evicted = -1, hit = 0, placed = 0;
     bool prob_full = false, have_free = false;
     int n_pin = 0, n_miss = 0, fails = 0;
-    uint64_t hits = 0, misses = 0, evictions = 0;
+    uint64_t hits = 0, misses = 0, evictions = 0, pf_used = 0;
     for (int i = 0; i < n_want; ++i) {
         if (tid == 0) {
             e = L.want[i];
@@ -537,6 +589,11 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
             if (s0 >= 0) {
                 hit = placed = 1;
                 slot = s0;
+                if (!prefetch && L.spf[s0]) {   // a demand call uses a prefetched key
+                    ++pf_used;
+                    L.spf[s0] = 0;
+                    L.dirty[s0] = 1;
+                }
                 if (touch_hits && !lfu) {
                     const uint8_t from = L.where[s0];
                     P.unlink(s0);
@@ -631,7 +688,7 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
             if (placed) {
                 L.eslot[e] = slot;
                 L.pin[slot] = 1;
-                g_pinned[n_pin++] = slot;
+                if (!prefetch) g_pinned[n_pin++] = slot;
                 if (!hit) {
                     g_miss_e[n_miss] = e;
                     g_miss_s[n_miss] = slot;
@@ -652,14 +709,17 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
     if (kFused && tid == 0) {
         __hip_atomic_store(&H->pub, n_miss | kPubClosed, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     }
-    for (int r = tid; r < routes; r += kPlanThreads) {
-        const int x = idx[r];
-        route_slot[r] = (x >= 0 && x < E) ? L.eslot[x] : 0;
+    if (!prefetch) {
+        for (int r = tid; r < routes; r += kPlanThreads) {
+            const int x = idx[r];
+            route_slot[r] = (x >= 0 && x < E) ? L.eslot[x] : 0;
+        }
     }
     for (int s = tid; s < n_slots; s += kPlanThreads) {
         if (!L.dirty[s]) continue;   // only the slots this call changed
         g_owner[s] = L.owner[s];
         g_where[s] = L.where[s];
+        g_spf[s] = L.spf[s];
         g_rst[s] = L.rst[s];
     }
     if (tid == 0) {
@@ -668,15 +728,21 @@ __global__ __launch_bounds__(kPlanThreads) void dplan_kernel(unsigned char *__re
         H->free_count = P.free_count;
         H->rclock = P.rclock;
         H->lclock = P.lclock;
-        H->n_pinned = n_pin;
+        if (!prefetch) H->n_pinned = n_pin;
         H->n_want = n_want;
         H->n_miss = n_miss;
-        H->hits += hits;
-        H->misses += misses;
+        if (prefetch) {
+            H->prefetched += n_miss;
+        } else {
+            H->hits += hits;
+            H->misses += misses;
+        }
+        H->pf_used += pf_used;
+        H->pf_wasted += P.pf_wasted;
         H->evictions += evictions;
         H->calls += 1;
         if (sh.bad && !H->error) H->error = LOCALI_DPLAN_E_EXPERT;
-        if (fails && !H->error) H->error = LOCALI_DPLAN_E_PLACE;
+        if (fails && !prefetch && !H->error) H->error = LOCALI_DPLAN_E_PLACE;
         if (kFused) fused_exit(H);
     }
 }
@@ -689,6 +755,7 @@ __global__ __launch_bounds__(256) void dplan_init_kernel(unsigned char *__restri
     uint64_t *lst = reinterpret_cast<uint64_t *>(state + G.lst);
     int32_t *owner = reinterpret_cast<int32_t *>(state + G.owner);
     uint8_t *where = state + G.where;
+    uint8_t *spf = state + G.spf;
     uint64_t *rst = reinterpret_cast<uint64_t *>(state + G.rst);
     const int stride = gridDim.x * blockDim.x;
     for (int k = blockIdx.x * blockDim.x + threadIdx.x; k < n_keys; k += stride) {
@@ -699,6 +766,7 @@ __global__ __launch_bounds__(256) void dplan_init_kernel(unsigned char *__restri
     for (int s = blockIdx.x * blockDim.x + threadIdx.x; s < n_slots; s += stride) {
         owner[s] = -1;
         where[s] = kNowhere;
+        spf[s] = 0;
         rst[s] = 0u;
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -769,16 +837,26 @@ int fill_args(void *const *dst_base, const size_t *slot_bytes, int32_t n_arrays,
     return 0;
 }
 
+// The prefetch form of a call: the rows' gate weights and how many of each
+// row's highest to take (0: every route).
+struct PrefetchArgs {
+    const float *weights = nullptr;
+    int32_t take_k = 0;
+    bool on = false;
+};
+
 // One planner launch: a single workgroup, or (fused) the planner workgroup
 // and kFusedCopiers copy workgroups.
 int plan_launch(bool fused, void *state, int32_t key_capacity, int32_t slots, int32_t policy, int32_t max_routes,
                 const int32_t *expert_idx, int32_t routes, int32_t layer, int32_t n_experts, int32_t top_k,
                 int32_t touch_hits, int32_t *route_slot, const DPlanFillArgs &fa, const uint64_t *host_src,
-                void *stream) {
+                void *stream, const PrefetchArgs &pf = PrefetchArgs{}) {
     if (routes == 0) return 0;
-    if (!state || !expert_idx || !route_slot || routes < 0 || routes > max_routes || n_experts < 1 ||
+    if (!state || !expert_idx || (!route_slot && !pf.on) || routes < 0 || routes > max_routes || n_experts < 1 ||
         n_experts > LOCALI_DPLAN_MAX_EXPERTS || layer < 0 || top_k < 1)
         return dfail(LOCALI_E_ARG, "dplan_plan: bad arguments");
+    if (pf.on && (routes % top_k || pf.take_k < 0 || (pf.take_k > 0 && pf.take_k < top_k && !pf.weights)))
+        return dfail(LOCALI_E_ARG, "dplan_prefetch: bad arguments");
     if (static_cast<int64_t>(layer + 1) * n_experts > key_capacity)
         return dfail(LOCALI_E_ARG, "dplan_plan: layer %d x %d experts outside %d keys", layer, n_experts,
                      key_capacity);
@@ -807,11 +885,11 @@ int plan_launch(bool fused, void *state, int32_t key_capacity, int32_t slots, in
     if (fused)
         hipLaunchKernelGGL(dplan_kernel<true>, dim3(1 + kFusedCopiers), dim3(kPlanThreads), lds, st, sp, key_capacity,
                            slots, policy, max_routes, expert_idx, routes, layer, n_experts, top_k,
-                           touch_hits ? 1 : 0, route_slot, fa, host_src);
+                           touch_hits ? 1 : 0, route_slot, fa, host_src, pf.weights, pf.take_k, pf.on ? 1 : 0);
     else
         hipLaunchKernelGGL(dplan_kernel<false>, dim3(1), dim3(kPlanThreads), lds, st, sp, key_capacity, slots,
                            policy, max_routes, expert_idx, routes, layer, n_experts, top_k, touch_hits ? 1 : 0,
-                           route_slot, fa, host_src);
+                           route_slot, fa, host_src, pf.weights, pf.take_k, pf.on ? 1 : 0);
     const hipError_t e = hipGetLastError();
     return e != hipSuccess ? dhip(e, "dplan_plan launch") : 0;
 }
@@ -882,6 +960,27 @@ int locali_dplan_plan_fill(void *state, int32_t key_capacity, int32_t slots, int
                        top_k, touch_hits, route_slot, a, host_src, stream);
 }
 
+int locali_dplan_prefetch(void *state, int32_t key_capacity, int32_t slots, int32_t policy, int32_t max_routes,
+                          const int32_t *expert_idx, const float *weights, int32_t rows, int32_t top_k,
+                          int32_t take_k, int32_t layer, int32_t n_experts, void *const *dst_base,
+                          const size_t *slot_bytes, int32_t n_arrays, const uint64_t *host_src, void *stream) {
+    if (rows == 0) return 0;
+    if (rows < 0 || top_k < 1 || static_cast<int64_t>(rows) * top_k > max_routes)
+        return dfail(LOCALI_E_ARG, "dplan_prefetch: bad arguments");
+    PrefetchArgs pf;
+    pf.weights = weights;
+    pf.take_k = take_k;
+    pf.on = true;
+    const bool fused = dst_base != nullptr;
+    DPlanFillArgs a{};
+    if (fused) {
+        if (!host_src) return dfail(LOCALI_E_ARG, "dplan_prefetch: bad arguments");
+        if (const int rc = fill_args(dst_base, slot_bytes, n_arrays, &a, "dplan_prefetch")) return rc;
+    }
+    return plan_launch(fused, state, key_capacity, slots, policy, max_routes, expert_idx, rows * top_k, layer,
+                       n_experts, top_k, 0, nullptr, a, host_src, stream, pf);
+}
+
 int locali_dplan_host_view(const void *const *src_host, int32_t n, uint64_t *out) {
     if (n < 0 || (n > 0 && (!src_host || !out))) return dfail(LOCALI_E_ARG, "dplan_host_view: bad arguments");
     for (int32_t i = 0; i < n; ++i) {
@@ -916,6 +1015,9 @@ int locali_dplan_read(const void *state, locali_dplan_stats *stats, locali_cache
     stats->free_slots = h.free_count;
     stats->last_keys = h.n_want;
     stats->last_misses = h.n_miss;
+    stats->prefetched = h.prefetched;
+    stats->prefetch_used = h.pf_used;
+    stats->prefetch_wasted = h.pf_wasted;
     if (max_results > 0 && h.n_want > 0) {
         const int32_t n = h.n_want < max_results ? h.n_want : max_results;
         const DPlanLayout G = dplan_layout(h.n_keys, h.n_slots, h.max_routes);

@@ -41,8 +41,8 @@ class V4ArenaStore(ArenaStore):
         """device_planner: plan on the GPU (native.DevicePlanner) with the
         compiled planner's rules and fill misses from host_source's pinned
         payloads in the same stream, so that V4ArenaMoE calls never wait for
-        the host (one tier, host_source required, no cross-layer prefetch;
-        counters are read from the device by stats())."""
+        the host (one tier, host_source required; cross-layer prefetch runs
+        on the fill stream; counters are read from the device by stats())."""
         config = json.loads(Path(index_path).read_text())
         self.expert_quant = config.get("quantization", {})
         for tier, q in self.expert_quant.items():
@@ -74,6 +74,7 @@ class V4ArenaStore(ArenaStore):
             self._dplan_src = None
             self._dplan_base = None
             self._dplan_pinned = 0   # distinct slots of the previous demand call
+            self._pf_event = None    # the fill stream's last prefetch call
 
     def _key_id(self, key):
         layer, expert = key
@@ -231,11 +232,62 @@ class V4ArenaStore(ArenaStore):
                                f"the previous call pinned may find no unpinned slot (probation holds "
                                f"{self.dplan.probation_capacity} keys); use a larger arena or the host planner")
         src = self._dplan_sources(t)
+        self._after_prefetch()
         slots = self.dplan.plan_fill(expert_idx, layer, self.top_k, self._slot_table(t), src)
         self._dplan_pinned = keys
         return slots
 
+    def _after_prefetch(self):
+        """The current stream waits for the prefetch calls queued on the fill
+        stream: the planner state is used by one call at a time, in the
+        reference's order, and their copies have landed before a later
+        demand call can use their slots."""
+        if self._pf_event is not None:
+            ops.current_stream(self.device).wait_event(self._pf_event)
+            self._pf_event = None
+
+    def device_lookahead(self, ahead, x, input_ids=None):
+        """The lookahead routings of a cross-layer prefetch: [(layer,
+        prefetch_k, indices, weights)] for each (module, prefetch_k) of
+        `ahead`. When every module routes through its V4Gate they run on the
+        fill stream beside this layer's router, each with the store's own
+        router workspace (the gate's workspace belongs to its layer's demand
+        call on the current stream); any other gate routes on the current
+        stream, whose state only its own calls are known to keep in order."""
+        plain = all(type(blk).route is V4ArenaMoE.route and isinstance(blk.gate, V4Gate) for blk, _ in ahead)
+        if not plain:
+            return [(blk.layer, k) + tuple(blk.route(x, input_ids)) for blk, k in ahead]
+        fs, cur = self.fill_stream, ops.current_stream(self.device)
+        fs.wait_stream(cur)          # x and the workspace's last use are behind
+        for t in (x, input_ids):
+            if isinstance(t, torch.Tensor) and t.is_cuda:
+                t.record_stream(fs)
+        ws = self.__dict__.get("_look_ws")
+        if ws is None:
+            ws = self._look_ws = ops.Workspace(self.device)
+        with torch.cuda.stream(fs):
+            return [(blk.layer, k) + tuple(blk.gate(x, input_ids, ws=ws)) for blk, k in ahead]
+
+    def device_prefetch(self, looks):
+        """Queue the prefetch calls of one layer call on the fill stream, after
+        the demand call already queued on the current stream (the reference's
+        order: demand, then the nearest layer first). Each plans and copies
+        in one launch (locali_dplan_prefetch); the next demand call waits for
+        them (_after_prefetch)."""
+        t = self.tiers[0]
+        fs, cur = self.fill_stream, ops.current_stream(self.device)
+        fs.wait_stream(cur)
+        src = self._dplan_sources(t)
+        with torch.cuda.stream(fs):
+            for layer, k, idx, w in looks:
+                self.dplan.prefetch(idx.to(torch.int32), w.to(torch.float32), layer, self.top_k, k or 0,
+                                    self._slot_table(t), src)
+            ev = torch.cuda.Event()
+            ev.record(fs)
+        self._pf_event = ev
+
     def _dplan_counters(self):
+        self._after_prefetch()
         c, _ = self.dplan.read()
         if c["error"]:
             what = {1: "a route's expert outside the layer", 2: "a demanded expert found no unpinned slot",
@@ -256,10 +308,13 @@ class V4ArenaStore(ArenaStore):
             c = self._dplan_counters()
             base = self._dplan_base or {k: 0 for k in c}
             hits, misses = c["hits"] - base["hits"], c["misses"] - base["misses"]
+            pf = c["prefetched"] - base["prefetched"]
             st.update(hits=hits, misses=misses, hit_rate=hits / (hits + misses) if hits + misses else 0.0,
                       evictions=c["evictions"] - base["evictions"],
-                      bytes_read=misses * self.item[self.tiers[0]], scheduler="device",
-                      protected={self.tiers[0]: c["protected_"]})
+                      bytes_read=(misses + pf) * self.item[self.tiers[0]], scheduler="device",
+                      protected={self.tiers[0]: c["protected_"]}, prefetched=pf,
+                      prefetch_used=c["prefetch_used"] - base["prefetch_used"],
+                      prefetch_wasted=c["prefetch_wasted"] - base["prefetch_wasted"])
         return st
 
     def _protected_size(self, t):
@@ -297,11 +352,14 @@ class V4Gate:
     def weight(self):
         return self.spec.weight
 
-    def __call__(self, x, input_ids=None):
+    def __call__(self, x, input_ids=None, ws=None):
+        """ws: a router workspace to use instead of the gate's own (a caller
+        routing on another stream than the gate's layer)."""
         lead = x.shape[:-1]
         if self.spec.tid2eid is not None and input_ids is None:
             raise ValueError("hash-routed gate needs input_ids")
-        idx, w, _ = ops.router(self.spec, x.reshape(-1, x.shape[-1]), self.ws, input_ids=input_ids)
+        idx, w, _ = ops.router(self.spec, x.reshape(-1, x.shape[-1]), ws if ws is not None else self.ws,
+                                  input_ids=input_ids)
         return idx.reshape(*lead, self.top_k), w.reshape(*lead, self.top_k)
 
 
@@ -341,15 +399,22 @@ class V4ArenaMoE(ArenaMoE):
         for the device; otherwise ArenaMoE's host-planned call."""
         if self.store.dplan is None:
             return super().__call__(x, input_ids)
-        if self.nxt is not None or self.nxt2 is not None:
-            raise ValueError("cross-layer prefetch plans on the host; the device planner does not take it")
         shape = x.shape
         flat = x.reshape(-1, shape[-1])
         if flat.shape[0] == 0:
             return torch.zeros(shape, dtype=x.dtype, device=x.device)
+        # Cross-layer prefetch (reference arena.py:518-541): the lookahead
+        # gates run on the fill stream beside this layer's router, and their
+        # planner calls follow this layer's demand call there, so that their
+        # copies overlap this layer's experts.
+        ahead = [(blk, k) for blk, k in ((self.nxt, self.prefetch_k), (self.nxt2, self.prefetch_k2))
+                 if blk is not None]
+        looks = self.store.device_lookahead(ahead, x, input_ids) if ahead else None
         inds, gates = self.route(x, input_ids)
         T = flat.shape[0]
         slots = self.store.device_plan(self.layer, inds.reshape(T, self.top_k))
+        if looks:
+            self.store.device_prefetch(looks)
         out = self._run_experts(self.store.tiers[0], flat, slots, gates.reshape(T, self.top_k), x.dtype)
         return out.reshape(shape).to(x.dtype)
 

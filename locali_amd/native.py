@@ -237,6 +237,35 @@ class DevicePlanner:
                    "locali_dplan_plan_fill")
         return out.view(expert_idx.shape)
 
+    def prefetch(self, expert_idx, weights, layer: int, top_k: int, take_k: int = 0, table=None, host_src=None):
+        """The cross-layer prefetch call (locali_dplan_prefetch): expert_idx
+        (device int32) and weights (device fp32) are rows of top_k routes of
+        a lookahead routing; each row's take_k highest weights (ties in row
+        order; every route when take_k is 0 or >= top_k) are planned with
+        hits left in place and the last demand call's slots pinned, and keys
+        that find no slot are dropped. With table and host_src the same
+        launch copies the placed misses (as plan_fill); otherwise fill()
+        copies them afterwards."""
+        import torch
+        from .ops import _stream
+        idx = expert_idx.reshape(-1, top_k)
+        w = weights.reshape(-1, top_k)
+        if idx.dtype != torch.int32 or not idx.is_cuda or w.dtype != torch.float32 or not w.is_cuda:
+            raise ValueError("device planner: prefetch takes device int32 experts and float32 weights")
+        if idx.shape != w.shape:
+            raise ValueError("device planner: prefetch experts and weights differ in shape")
+        idx, w = idx.contiguous(), w.contiguous()
+        if table is not None:
+            bases, pers, n = self._records(table)
+            src = host_src.data_ptr()
+        else:
+            bases, pers, n, src = None, None, 0, None
+        _lib.check(self._lib.locali_dplan_prefetch(self.state.data_ptr(), self.key_capacity, self.slots, self.policy,
+                                                     self.max_routes, idx.data_ptr(), w.data_ptr(), idx.shape[0],
+                                                     top_k, int(take_k or 0), layer, self.n_experts, bases, pers,
+                                                     n, src, _stream()),
+                   "locali_dplan_prefetch")
+
     @staticmethod
     def host_view(pointers) -> list[int]:
         """Device-visible addresses of pinned host payloads (raises for any

@@ -219,3 +219,124 @@ def test_device_planner_at_the_stack_geometry(policy, slots, n_calls, tokens):
     assert (counters["hits"], counters["misses"], counters["evictions"], counters["calls"]) == \
            (hits, misses, evictions, n_calls)
     assert evictions > 500 and hits > 1000, (hits, misses, evictions)
+
+
+def prefetch_calls(rng, n_calls, layers, E, top_k, tokens=(1, 1, 3)):
+    """Alternating demand and prefetch calls, as a layer call with a depth-1
+    cross-layer prefetch makes them: ("demand", layer, routes) then
+    ("prefetch", layer + 1, (idx [T, top_k], weights [T, top_k])) for a
+    lookahead routing of T tokens whose weights come from a few values, so
+    that equal weights are common."""
+    ranks = [rng.permutation(E) for _ in range(layers)]
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    seq = []
+    for c in range(n_calls):
+        layer = c % layers
+        routes = [int(ranks[layer][i]) for i in rng.choice(E, size=top_k, replace=False, p=p)]
+        seq.append(("demand", layer, routes))
+        nxt = (layer + 1) % layers
+        T = int(rng.choice(tokens))
+        idx = np.stack([ranks[nxt][rng.choice(E, size=top_k, replace=False, p=p)] for _ in range(T)])
+        w = rng.choice(np.array([0.05, 0.1, 0.2, 0.3], np.float32), size=(T, top_k))
+        seq.append(("prefetch", nxt, (idx.astype(np.int32), w.astype(np.float32))))
+    return seq
+
+
+def host_prefetch_run(seq, layers, E, slots, pcap, policy, top_k, take_k):
+    """The host store's convention (V4ArenaStore.submit / _place_keys and
+    ArenaStore's prefetch counters): a demand call pins the previous demand
+    call's slots, touches hits and replaces the pinned set; a prefetch call
+    plans the lookahead's take_k highest-weight experts per row
+    (_lookahead_experts, deduplicated in order) with hits untouched and the
+    same pins, and leaves the pinned set alone. Counters: hits and misses of
+    demand calls, evictions of both, placed prefetch misses, demand hits on a
+    prefetched key (used) and evictions of one before such a hit (wasted)."""
+    from locali_amd.arena import _lookahead_experts
+    cache = NativeCache(layers * E, slots, pcap, policy=policy)
+    pinned, flag, out = (), {}, []
+    cnt = dict(hits=0, misses=0, evictions=0, prefetched=0, prefetch_used=0, prefetch_wasted=0)
+    for kind, layer, what in seq:
+        if kind == "demand":
+            want = list(dict.fromkeys(what))
+            if layer == 0 and len(want) <= top_k:
+                cache.note_token()
+            res = cache.plan_each([layer * E + e for e in want], pinned_slots=pinned, touch_hits=True)
+            pinned = tuple(r.slot for r in res if r.placed)
+        else:
+            idx, w = what
+            want = list(dict.fromkeys(_lookahead_experts(idx.reshape(-1), w.reshape(-1).view(np.int32), top_k,
+                                                         take_k)))
+            res = cache.plan_each([layer * E + e for e in want], pinned_slots=pinned, touch_hits=False)
+        for r in res:
+            if r.evicted_key >= 0:
+                cnt["evictions"] += 1
+                if flag.get(r.slot):
+                    cnt["prefetch_wasted"] += 1
+            if kind == "demand":
+                if r.hit:
+                    cnt["hits"] += 1
+                    if flag.get(r.slot):
+                        cnt["prefetch_used"] += 1
+                else:
+                    cnt["misses"] += 1
+                if r.placed:
+                    flag[r.slot] = 0
+            elif r.placed and not r.hit:
+                cnt["prefetched"] += 1
+                flag[r.slot] = 1
+        out.append(res)
+    cache.close()
+    return out, cnt
+
+
+@pytest.mark.parametrize("policy,slots,pcap,take_k,fused", [
+    ("slru", 40, 12, 1, False),
+    ("slru", 40, 12, 2, True),
+    ("slru", 48, 0, 0, False),
+    ("lfu-decay", 40, 0, 1, True),
+    ("lfu-decay", 48, 0, 6, False),
+])
+def test_device_prefetch_matches_host_prefetch(policy, slots, pcap, take_k, fused):
+    """locali_dplan_prefetch beside demand calls against the host store's
+    convention: per-key results of every call (the take_k highest weights
+    per row with ties in row order, the pins of the last demand call, hits
+    untouched, unplaceable keys dropped), demand route slots, and the
+    counters including prefetched / used / wasted. Fused: the launch also
+    copies the placed misses, and each lands in its slot byte for byte."""
+    layers, E, top_k, n_calls = 4, 48, 6, 150
+    rng = np.random.default_rng(slots + pcap + 10 * take_k + fused)
+    seq = prefetch_calls(rng, n_calls, layers, E, top_k)
+    expect, cnt = host_prefetch_run(seq, layers, E, slots, pcap, policy, top_k, take_k)
+    dp = DevicePlanner(layers * E, slots, pcap, n_experts=E, policy=policy, max_routes=64, device=DEV)
+    sizes = [2048, 256]
+    payload = torch.randint(0, 256, (layers * E, sum(sizes)), dtype=torch.uint8).pin_memory()
+    arrays = [torch.zeros(slots, sz, dtype=torch.uint8, device=DEV) for sz in sizes]
+    table = ([a.data_ptr() for a in arrays], sizes)
+    host_src = torch.tensor(DevicePlanner.host_view([payload[k].data_ptr() for k in range(layers * E)]),
+                            dtype=torch.uint64, device=DEV)
+    for c, ((kind, layer, what), want_res) in enumerate(zip(seq, expect)):
+        if kind == "demand":
+            idx = torch.tensor(what, dtype=torch.int32, device=DEV)
+            rs = dp.plan_fill(idx, layer, top_k, table, host_src) if fused else dp.plan(idx, layer, top_k)
+            slot_of = {r.key - layer * E: r.slot for r in want_res}
+            assert rs.cpu().tolist() == [slot_of[e] for e in what], f"route slots of call {c}"
+        else:
+            idx, w = (torch.from_numpy(a).to(DEV) for a in what)
+            if fused:
+                dp.prefetch(idx, w, layer, top_k, take_k, table, host_src)
+            else:
+                dp.prefetch(idx, w, layer, top_k, take_k)
+        counters, got = dp.read(max_results=len(want_res))
+        assert counters["error"] == 0, (c, counters)
+        assert [(r.key, r.slot, r.evicted_key, r.hit, r.placed) for r in got] == \
+               [(r.key, r.slot, r.evicted_key, r.hit, r.placed) for r in want_res], f"{kind} call {c} layer {layer}"
+        if fused:
+            for r in want_res:
+                if r.placed and not r.hit:
+                    landed = torch.cat([a[r.slot].cpu() for a in arrays])
+                    assert torch.equal(landed, payload[r.key]), f"{kind} call {c}: key {r.key} in slot {r.slot}"
+    counters, _ = dp.read()
+    assert {k: counters[k] for k in cnt} == cnt
+    assert counters["calls"] == len(seq)
+    assert cnt["prefetched"] > 20 and cnt["prefetch_used"] > 10 and cnt["evictions"] > 20, cnt

@@ -356,3 +356,33 @@ def test_cross_layer_prefetch_is_exact_and_accounted(tmp_path):
         assert st["prefetch_used"] + st["prefetch_wasted"] <= st["prefetched"]
     finally:
         stack.close()
+
+
+def test_cross_layer_prefetch_device_planner_equals_host_planner(tmp_path):
+    """The same cross-layer prefetch (depth 1: the three highest-gate
+    experts of the next layer's routing on the current input; depth 2: all
+    six of the layer after) planned on the GPU: the lookahead gates run on
+    the fill stream, and the prefetch planner calls and their copies follow
+    each layer's demand call there (locali_dplan_prefetch). Every layer call
+    equals the resident weights bit for bit, and hits, misses, evictions,
+    bytes and the prefetch counters equal the host-planned run's."""
+    banner("full-width stack with cross-layer prefetch, device planner")
+    steps = 12
+    counts = []
+    for device_planner in (False, True):
+        stack = _Stack(tmp_path, layers=4, per_layer=16, policy="slru-all", seed=600, steps=steps,
+                       predict_next=True, device_planner=device_planner)
+        try:
+            for layer, mod in enumerate(stack.mods):
+                mod.nxt = stack.mods[layer + 1] if layer + 1 < stack.layers else None
+                mod.prefetch_k = 3
+                mod.nxt2 = stack.mods[layer + 2] if layer + 2 < stack.layers else None
+                mod.prefetch_k2 = None
+            _run_stack(stack, steps)
+            st = stack.store.stats()
+            counts.append(tuple(st[k] for k in ("hits", "misses", "evictions", "bytes_read", "prefetched",
+                                                "prefetch_used", "prefetch_wasted")))
+        finally:
+            stack.close()
+    assert counts[0] == counts[1], counts
+    assert counts[0][4] > 0 and counts[0][5] > 0
