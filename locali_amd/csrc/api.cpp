@@ -57,8 +57,9 @@ bool dtype16(int32_t dt) { return dt == LOCALI_DT_F16 || dt == LOCALI_DT_BF16; }
 // Workspace layout for up to T tokens.
 struct Layout {
     size_t sync_gen, sync_logits, logits, route_slot, hidden, hprep, seg_start, seg_tile, sorted_route, route_pos,
-        tiles, n_tiles, gh, gy, mx, mh, total;
+        tiles, n_tiles, tile_tok, gh, gy, mx, mh, total;
     int max_tiles;
+    int wide_tiles;   // tiles of the matrix-core path that tile_tok holds
 };
 
 // Bytes of one prepared vector of K values, for any bit width (pairs take at
@@ -108,6 +109,9 @@ Layout layout(int T, int d, int dff, int E, int k, int has_shared) {
     L.route_pos = take(sizeof(int32_t) * R);
     L.tiles = take(sizeof(int32_t) * 4 * L.max_tiles);
     L.n_tiles = take(sizeof(int32_t));
+    // the matrix-core path's tiles of up to kWideTokens positions: their tokens
+    L.wide_tiles = grouped_max_tiles(T, k, has_shared ? 1 : 0, E, kWideTokens);
+    L.tile_tok = take(sizeof(int32_t) * kWideTokens * static_cast<size_t>(L.wide_tiles));
     L.gh = take(sizeof(uint16_t) * static_cast<size_t>(routes) * dff);
     L.gy = take(sizeof(uint16_t) * static_cast<size_t>(routes) * d);
     L.mx = take(mfma_batch_bytes(T, d));
@@ -281,7 +285,8 @@ int check_decode_args(const locali_expert_arena *routed, const locali_expert_are
 }
 
 // The matrix-core grouped path needs 2- or 4-bit codes (gate and up alike),
-// groups of a multiple of 64 with a multiple of 8 per row, rows in multiples
+// groups of a multiple of 64 with a multiple of 8 per row and at most
+// kWideMetaMaxGroups (96: K up to 6144 in groups of 64), rows in multiples
 // of 128, columns in multiples of kMfmaColsAlign, its staged scales, biases
 // and sums within the LDS of a workgroup, and prepared inputs (2 bytes per value) below 2 GiB so
 // that its buffer offsets stay 31-bit; the shared expert must match the
@@ -293,7 +298,8 @@ bool mfma_eligible(const locali_expert_arena *routed, const locali_expert_arena 
         return false;
     auto ok = [](const locali_qproj &p) {
         return (p.bits == 2 || p.bits == 4) && p.group_size % 64 == 0 && p.rows % kWideRows == 0 &&
-               p.cols % kMfmaColsAlign == 0 && (p.cols / p.group_size) % 8 == 0;
+               p.cols % kMfmaColsAlign == 0 && (p.cols / p.group_size) % 8 == 0 &&
+               p.cols / p.group_size <= kWideMetaMaxGroups;
     };
     if (!ok(routed->gate) || !ok(routed->up) || !ok(routed->down)) return false;
     if (wide_lds_bytes(routed->gate.cols, 2) > kWideMaxLds || wide_lds_bytes(routed->down.cols, 1) > kWideMaxLds)
@@ -330,21 +336,25 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     int32_t *n_tiles = at<int32_t>(ws, lay.n_tiles);
     uint16_t *gy = at<uint16_t>(ws, lay.gy);
     const int max_tiles = grouped_max_tiles(tokens, top_k, shared ? 1 : 0, n_experts, kWideTokens);
-    if (max_tiles > lay.max_tiles) return fail(LOCALI_E_WORKSPACE, "grouped: tile list too small");
+    if (max_tiles > lay.max_tiles || max_tiles > lay.wide_tiles)
+        return fail(LOCALI_E_WORKSPACE, "grouped: tile list too small");
     // Tiles of one or two positions go to the small-tile kernels when the
     // shapes allow; the 64-position kernels skip them. The dispatch packs
-    // such a tile's tokens into its record.
+    // such a tile's tokens into its record, and writes every routed tile's
+    // tokens by position for the 64-position kernels.
     const bool small = small_tiles_eligible(routed);
+    int32_t *tile_tok = at<int32_t>(ws, lay.tile_tok);
     hipError_t e = launch_dispatch(route_slot, R, n_slots, shared ? tokens : 0, kWideTokens,
                                    at<int32_t>(ws, lay.seg_start), at<int32_t>(ws, lay.sorted_route),
-                                   route_pos, tiles, n_tiles, max_tiles, st,
-                                   small ? at<int32_t>(ws, lay.seg_tile) : nullptr, top_k);
+                                   route_pos, tiles, n_tiles, max_tiles, st, at<int32_t>(ws, lay.seg_tile), top_k,
+                                   small, tile_tok);
     if (e != hipSuccess) return hip_fail(e, "dispatch launch");
     MfmaLaunch L{};
     L.ta.x = static_cast<const uint16_t *>(x);
     L.ta.tiles = tiles;
     L.ta.n_tiles = n_tiles;
     L.ta.sorted_route = at<int32_t>(ws, lay.sorted_route);
+    L.ta.tile_tok = tile_tok;
     L.ta.R = R;
     L.ta.top_k = top_k;
     L.gate = to_dev(routed->gate);

@@ -8,11 +8,15 @@
 //                           (seg_start), per-slot tile counts and the tile
 //                           list (slot, first position, token count); the
 //                           shared expert, when present, is one more segment
-//                           holding every token, placed after the routed ones;
+//                           holding every token, whose tiles come first in the
+//                           list (the longest tiles start with the launch);
 //                           routes outside the arena get route_pos -1
 //   dispatch_place_kernel   one wave per slot: walks the routes 512 at a time
 //                           with ballots and writes sorted_route / route_pos
-//                           in route order (stable)
+//                           in route order (stable), and on request each
+//                           routed tile's tokens by position (tile_tok), so
+//                           that a tile kernel reads them beside the tile's
+//                           record instead of after it
 //   combine_kernel          out[t] = round(sum_j round(y[pos(t,j)] * w)) (+ shared)
 #include "mfma_grouped.hpp"
 
@@ -25,6 +29,8 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
     const int32_t *__restrict__ route_slot, int R, int n_slots, int n_shared_tokens, int tile_tokens,
     int32_t *__restrict__ seg_start, int32_t *__restrict__ tiles, int32_t *__restrict__ n_tiles,
     int max_tiles, int32_t *__restrict__ route_pos, int32_t *__restrict__ seg_tile, int small_pack) {
+    // the shared expert's tiles first, then the routed segments in slot order
+    const int n_shared_tiles = (n_shared_tokens + tile_tokens - 1) / tile_tokens;
     extern __shared__ int32_t cnt[];              // [n_slots + 1]
     __shared__ int32_t wsum[kDispatchThreads / 64];
     __shared__ int32_t carry;
@@ -68,9 +74,9 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
                     seg_start[s] = excl;
                 } else {
                     int pos = seg_start[s];
-                    if (seg_tile) seg_tile[s] = excl;
+                    if (seg_tile) seg_tile[s] = n_shared_tiles + excl;
                     for (int q = 0; q < v; ++q) {
-                        const int tile = excl + q;
+                        const int tile = n_shared_tiles + excl + q;
                         if (tiles && tile < max_tiles) {
                             const int first = pos + q * tile_tokens;
                             tiles[4 * tile + 0] = s;
@@ -91,37 +97,35 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
         __syncthreads();
     }
     if (tid == 0) {
-        int nt = carry;
         // shared expert: positions R .. R + n_shared_tokens, slot marker -2
-        for (int q = 0; q * tile_tokens < n_shared_tokens; ++q) {
-            if (tiles && nt < max_tiles) {
-                tiles[4 * nt + 0] = -2;
-                tiles[4 * nt + 1] = R + q * tile_tokens;
-                tiles[4 * nt + 2] = min(tile_tokens, n_shared_tokens - q * tile_tokens);
-                tiles[4 * nt + 3] = 0;
+        for (int q = 0; q < n_shared_tiles; ++q) {
+            if (tiles && q < max_tiles) {
+                tiles[4 * q + 0] = -2;
+                tiles[4 * q + 1] = R + q * tile_tokens;
+                tiles[4 * q + 2] = min(tile_tokens, n_shared_tokens - q * tile_tokens);
+                tiles[4 * q + 3] = 0;
             }
-            ++nt;
         }
-        if (n_tiles) *n_tiles = min(nt, max_tiles);
+        if (n_tiles) *n_tiles = min(n_shared_tiles + carry, max_tiles);
     }
 }
 
 __global__ __launch_bounds__(256) void dispatch_place_kernel(
     const int32_t *__restrict__ route_slot, int R, int n_slots, const int32_t *__restrict__ seg_start,
     int32_t *__restrict__ sorted_route, int32_t *__restrict__ route_pos, const int32_t *__restrict__ seg_tile,
-    int32_t *__restrict__ tiles, int max_tiles, int top_k) {
+    int32_t *__restrict__ tiles, int max_tiles, int top_k, int small_pack, int32_t *__restrict__ tile_tok,
+    int tile_tokens) {
     const int lane = threadIdx.x & 63;
     const int s = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (s >= n_slots) return;
     const int base = seg_start[s], end = seg_start[s + 1];
     if (base == end) return;
+    const int tile0 = seg_tile ? seg_tile[s] : -1;   // the segment's first tile
     // a slot of at most kPackedTokens routes: its tile's tokens, 15 bits each
     // in position order, go into the tile record (see the count kernel)
     int32_t *packed = nullptr;
-    if (seg_tile && end - base <= kPackedTokens) {
-        const int tile = seg_tile[s];
-        if (tile >= 0 && tile < max_tiles) packed = &tiles[4 * tile + 3];
-    }
+    if (small_pack && end - base <= kPackedTokens && tile0 >= 0 && tile0 < max_tiles) packed = &tiles[4 * tile0 + 3];
+    if (tile0 < 0) tile_tok = nullptr;
     // 8 x 64 routes per pass: the loads of a pass are in flight together,
     // then the ballots place them in route order
     constexpr int U = 8;
@@ -143,6 +147,10 @@ __global__ __launch_bounds__(256) void dispatch_place_kernel(
                 sorted_route[p] = r;
                 if (route_pos) route_pos[r] = p;
                 if (packed) atomicOr(packed, (r / top_k) << (kTokenBits * (p - base)));
+                if (tile_tok) {
+                    const int q = p - base, tile = tile0 + q / tile_tokens;
+                    if (tile < max_tiles) tile_tok[static_cast<int64_t>(tile) * tile_tokens + q % tile_tokens] = r / top_k;
+                }
             }
             pos += __popcll(m);
         }
@@ -310,11 +318,13 @@ int grouped_max_tiles(int tokens, int top_k, int n_shared, int E, int tile_token
 hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
                            int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
                            int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,
-                           hipStream_t st, int32_t *seg_tile, int top_k) {
+                           hipStream_t st, int32_t *seg_tile, int top_k, bool pack_small, int32_t *tile_tok) {
     if (n_slots < 1 || n_slots > kMaxDispatchSlots) return hipErrorInvalidValue;
     // tokens fit the packed field (and the tiles exist to hold it)
-    const int pack = seg_tile && tiles && top_k > 0 && R / top_k < (1 << kTokenBits) && tile_tokens > kPackedTokens;
-    if (!pack) seg_tile = nullptr;
+    const int pack = pack_small && seg_tile && tiles && top_k > 0 && R / top_k < (1 << kTokenBits) &&
+                     tile_tokens > kPackedTokens;
+    if (!tiles || top_k < 1) tile_tok = nullptr;
+    if (!pack && !tile_tok) seg_tile = nullptr;
     const size_t lds = sizeof(int32_t) * (n_slots + 1);
     hipLaunchKernelGGL(dispatch_count_kernel, dim3(1), dim3(kDispatchThreads), lds, st, route_slot, R,
                        n_slots, n_shared_tokens, tile_tokens, seg_start, tiles, n_tiles, max_tiles, route_pos,
@@ -322,7 +332,8 @@ hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(dispatch_place_kernel, dim3((n_slots + 3) / 4), dim3(256), 0, st, route_slot, R,
-                       n_slots, seg_start, sorted_route, route_pos, seg_tile, tiles, max_tiles, top_k > 0 ? top_k : 1);
+                       n_slots, seg_start, sorted_route, route_pos, seg_tile, tiles, max_tiles, top_k > 0 ? top_k : 1,
+                       pack, tile_tok, tile_tokens);
     return hipGetLastError();
 }
 

@@ -21,6 +21,7 @@ struct TileArgs {
     const int32_t *sorted_route;  // [R]
     int32_t R, top_k;
     int32_t n_vec;                // vectors in the MFMA kernels' input array (bounds of its loads)
+    const int32_t *tile_tok;      // [max_tiles, 64] routed tiles' tokens by position (MFMA path)
     int32_t min_count;            // MFMA kernels: skip tiles of fewer positions (the small-tile kernels' share)
 };
 
@@ -277,7 +278,8 @@ hipError_t launch_grouped_kernels(int which, const GroupedKernelLaunch &L, hipSt
 hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
                            int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
                            int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,
-                           hipStream_t st, int32_t *seg_tile = nullptr, int top_k = 0);
+                           hipStream_t st, int32_t *seg_tile = nullptr, int top_k = 0, bool pack_small = false,
+                           int32_t *tile_tok = nullptr);
 hipError_t launch_route_slots(const int32_t *idx, int R, int E, const int32_t *slot_of_expert,
                               int n_slots, int32_t *route_slot, hipStream_t st);
 hipError_t launch_combine(const uint16_t *y, const int32_t *route_pos, const uint16_t *shared_y,

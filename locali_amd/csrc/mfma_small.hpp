@@ -32,14 +32,18 @@ struct SmallTileInfo {
 
 // The tile's slot and positions, or false when this workgroup has nothing to
 // do (past the list, a large tile, an invalid entry).
+// The record and the tile count are read together: the grid has one row per
+// possible tile, so the record is in bounds.
 __device__ __forceinline__ bool small_tile(const TileArgs &ta, int tile, int n_slots, SmallTileInfo &t) {
-    if (tile >= *ta.n_tiles) return false;
-    t.slot = ta.tiles[4 * tile];
-    t.first = ta.tiles[4 * tile + 1];
-    t.count = ta.tiles[4 * tile + 2];
-    t.packed = ta.tiles[4 * tile + 3];
+    const int4 rec = reinterpret_cast<const int4 *>(ta.tiles)[tile];
+    const int nt = *ta.n_tiles;
+    asm volatile("" ::"s"(rec.x), "s"(rec.y), "s"(rec.z), "s"(rec.w), "s"(nt));
+    t.slot = rec.x;
+    t.first = rec.y;
+    t.count = rec.z;
+    t.packed = rec.w;
     t.shared = t.slot == -2;
-    if (t.count <= 0 || t.count > kSmallTile) return false;
+    if (tile >= nt || t.count <= 0 || t.count > kSmallTile) return false;
     return t.shared || (t.slot >= 0 && t.slot < n_slots && t.first >= 0 && t.first + t.count <= ta.R);
 }
 

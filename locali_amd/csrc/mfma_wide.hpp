@@ -101,12 +101,16 @@ struct WideLds {
 // entry per 64-value block (bpg blocks per group). With P pieces per row
 // dividing 64, a wave's 64 items are 64 / P rows x all P pieces of each
 // (whole 128-byte lines per load instruction): lane l holds row l % (64 / P),
-// piece l / (64 / P). Loads go
-// out for every thread on every pass (past the last item they repeat it), so
-// the waits that follow count loads exactly.
+// piece l / (64 / P). One pass covers every item (kWideMetaMaxGroups groups
+// per row at most, which the host checks), and loads go out for every thread
+// (past the last item they repeat it), so that the waits that follow count
+// loads exactly: the loop's first wait is for its first weight chunk, not
+// for every chunk in flight.
+constexpr int kWideMetaPass = 2;
+constexpr int kWideMetaMaxGroups = kWideMetaPass * kWideThreads * 8 / kWideRows;
 template <int NPROJ>
 struct WideMetaStage {
-    static constexpr int U = 2;
+    static constexpr int U = kWideMetaPass;
     uint4 v[U][2 * NPROJ];
     int items;
 
@@ -220,11 +224,11 @@ __device__ __forceinline__ void wide_b(const BlockW<MfmaGeom<BITS, BF16>::kWPL> 
 // marr: their scales and biases (see WideMetaStage); vec(p) the
 // prepared-input vector of position p < count. Returns with the compute
 // waves' acc[j] filled and every wave past the last barrier.
-template <int BITS, bool BF16, int NPROJ, int NACT, typename VecOf>
-__device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const WideLds<NPROJ> &L, int *tok,
+template <int BITS, bool BF16, int NPROJ, int NACT, typename TokOf>
+__device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const WideLds<NPROJ> &L, const int32_t *tt,
                                           const uint32_t *const (&w)[NPROJ],
                                           const uint16_t *const (&marr)[2 * NPROJ], const MfmaVec &in, int n_vec,
-                                          VecOf vec, int K, int group, int count) {
+                                          TokOf tokof, int K, int group, int count) {
     using G = MfmaGeom<BITS, BF16>;
     constexpr int WPL = G::kWPL, CB = G::kCB, SPC = CB / 2;
     const int nblk = K / 64, nsteps = nblk / 2, nchunks = nblk / CB;
@@ -237,28 +241,19 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
 #pragma unroll
         for (int tb = 0; tb < NACT; ++tb) acc[j][tb] = mf32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // Prologue. The loader waves fetch the positions' vectors, then their
-    // first activation stages; the compute waves issue their first weight
-    // chunks; every wave helps to stage the scales and biases of the whole
-    // K range (independent of the vectors, so those loads overlap).
+    // Prologue. What the loop's first step needs goes out first, since a
+    // CU's loads leave in issue order at the rate the memory system drains
+    // them: every wave's share of the scales and biases of the whole K range
+    // and the compute waves' first two weight chunks, the loader waves' first
+    // activation stage (addresses from the dispatch's token list, no
+    // barrier); then the loaders' later stages; the compute waves' other
+    // chunks only once stage 0 and the metadata are in LDS.
     WideMetaStage<NPROJ> ms;
-    ms.items = kWideRows * (gpr / 8);
-    const int mpass = WideMetaStage<NPROJ>::U * kWideThreads;
-    auto stage_meta = [&]() {
-        ms.store(L.meta, bpg, 0, gpr);
-        for (int base = mpass; base < ms.items; base += mpass) {
-            ms.load(marr, gpr, base);
-            ms.store(L.meta, bpg, base, gpr);
-        }
-    };
+    ms.items = kWideRows * (gpr / 8);   // at most U * kWideThreads: one pass
+    auto stage_meta = [&]() { ms.store(L.meta, bpg, 0, gpr); };
 
     if (wave >= kWideCompute) {
         const int lt = threadIdx.x - 64 * kWideCompute;
-        int my_tok = 0;
-        if (lt < 16 * NACT) my_tok = vec(min(lt, count - 1));
-        ms.load(marr, gpr, 0);
-        if (lt < 16 * NACT) tok[lt] = my_tok;
-        __syncthreads();
         WideLoader<NACT> ld;
         ld.rs = make_rsrc(in.pairs, static_cast<uint32_t>(4 * in.pairs_stride * n_vec));
         ld.frs = make_rsrc(in.fix, static_cast<uint32_t>(sizeof(uint4) * in.fix_stride * n_vec));
@@ -266,14 +261,22 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
         ld.p0 = lt >> 4;
         ld.fp = min(lt >> 1, 16 * NACT - 1);
         ld.fb = lt & 1;
+        // positions past the tile's count read token 0's vector (results
+        // discarded); so does a lane that stores no fixup operand
 #pragma unroll
-        for (int i = 0; i < NACT; ++i)
-            ld.off[i] = 4u * static_cast<uint32_t>(tok[ld.p0 + 16 * i] * in.pairs_stride) + 16u * ld.part;
-        ld.foff = static_cast<uint32_t>(sizeof(uint4) * (tok[ld.fp] * in.fix_stride + ld.fb));
+        for (int i = 0; i < NACT; ++i) {
+            const int p = ld.p0 + 16 * i;
+            const int t = p < count ? tokof(p, tt) : 0;
+            ld.off[i] = 4u * static_cast<uint32_t>(t * in.pairs_stride) + 16u * ld.part;
+        }
+        const int tf = lt < 32 * NACT && ld.fp < count ? tokof(ld.fp, tt) : 0;
+        ld.foff = static_cast<uint32_t>(sizeof(uint4) * (tf * in.fix_stride + ld.fb));
         constexpr int SETS = WideDepth<NACT>::kSets;
         WideLoad<NACT> r[SETS];
+        ld.load(r[0], 0, nsteps);
+        ms.load(marr, gpr, 0);
 #pragma unroll
-        for (int q = 0; q < SETS; ++q) ld.load(r[q], q, nsteps);
+        for (int q = 1; q < SETS; ++q) ld.load(r[q], q, nsteps);
         stage_meta();
         ld.store(r[0], L.a[0], L.fix[0], lt);
         __syncthreads();
@@ -304,16 +307,18 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
         for (int j = 0; j < NPROJ; ++j)
             dst[j] = __builtin_amdgcn_raw_buffer_load_b128(wrs[j], w_off | past, c * 64, kAuxStream);
     };
-    // the scales and biases first: the loop waits for all of them, and the
-    // in-order load counter then lets the first weight chunks land behind
+    // the scales and biases first (staging waits for them), then two weight
+    // chunks; the other chunks behind stage 0 and the metadata
+    constexpr int FIRST = RING < 2 ? RING : 2;
     ms.load(marr, gpr, 0);
 #pragma unroll
-    for (int q = 0; q < RING; ++q) load_w(ring[q], q);
-    stage_meta();
+    for (int q = 0; q < FIRST; ++q) load_w(ring[q], q);
     const uint32_t magic_v = opaque_vgpr(G::P::kMagic);
     const int row = wave * 16 + nl;
-    __syncthreads();   // the loaders' vectors
+    stage_meta();
     __syncthreads();   // stage 0 and the scales / biases
+#pragma unroll
+    for (int q = FIRST; q < RING; ++q) load_w(ring[q], q);
     for (int c0 = 0; c0 < nchunks; c0 += RING) {
 #pragma unroll
         for (int q = 0; q < RING; ++q) {
@@ -391,27 +396,32 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
     }
 }
 
-// Tiles are taken from the end of the list first: the shared expert's tiles,
-// which the dispatch appends and which hold every position (full 64-position
-// tiles, the longest workgroups), start with the launch instead of forming
-// its tail.
+// Workgroup row y takes tile y. The dispatch lists the shared expert's tiles
+// first: they hold every position (full 64-position tiles, the longest
+// workgroups) and start with the launch instead of forming its tail. The
+// record and the tile count are read together (the grid has one row per
+// possible tile, so the record is in bounds), one dependent load fewer before
+// the workgroup knows its tile.
 __device__ __forceinline__ bool wide_tile(const TileArgs &ta, int n_slots, int &slot, int &first, int &count,
                                           bool &shared) {
-    const int tile = *ta.n_tiles - 1 - static_cast<int>(blockIdx.y);
-    if (tile < 0) return false;
-    slot = ta.tiles[4 * tile];
-    first = ta.tiles[4 * tile + 1];
-    count = ta.tiles[4 * tile + 2];
+    const int tile = static_cast<int>(blockIdx.y);
+    const int4 rec = reinterpret_cast<const int4 *>(ta.tiles)[tile];
+    const int nt = *ta.n_tiles;
+    // the record and the count before the decision: neither load waits for the other
+    asm volatile("" ::"s"(rec.x), "s"(rec.y), "s"(rec.z), "s"(nt));
+    slot = rec.x;
+    first = rec.y;
+    count = rec.z;
     shared = slot == -2;
-    return !(count <= 0 || count > kWideTokens || count < ta.min_count ||
+    return !(tile >= nt || count <= 0 || count > kWideTokens || count < ta.min_count ||
              (!shared && (slot < 0 || slot >= n_slots || first < 0 || first + count > ta.R)));
 }
 
 template <int BITS, bool BF16, int NACT>
 __device__ __forceinline__ void wide_gateup_tile(const TileArgs &ta, const QProj &pg, const QProj &pu, int sl,
-                                                 bool shared, int first, int count, const MfmaVec &xin,
-                                                 const MfmaVec &hout, int down_bits, float limit, int fp32_swiglu,
-                                                 unsigned char *wlds, int *tok) {
+                                                 bool shared, int first, int count,
+                                                 const MfmaVec &xin, const MfmaVec &hout, int down_bits, float limit,
+                                                 int fp32_swiglu, unsigned char *wlds) {
     const int K = pg.cols;
     const WideLds<2> L(wlds, K);
     const int n0 = blockIdx.x * kWideRows;
@@ -422,8 +432,11 @@ __device__ __forceinline__ void wide_gateup_tile(const TileArgs &ta, const QProj
     const uint16_t *const marr[4] = {pg.s + sl * pg.m_slot + r0, pg.b + sl * pg.m_slot + r0,
                                      pu.s + sl * pu.m_slot + r0, pu.b + sl * pu.m_slot + r0};
     mf32x4_t acc[2][NACT];
-    wide_body<BITS, BF16, 2, NACT>(acc, L, tok, w, marr, xin, ta.n_vec,
-                                   [&](int p) { return tile_token(ta, shared, first + p); }, K, pg.group, count);
+    // position p's token: the shared expert's tiles hold tokens in order; a
+    // routed tile's come from the dispatch's list
+    wide_body<BITS, BF16, 2, NACT>(acc, L, ta.tile_tok + static_cast<int64_t>(blockIdx.y) * kWideTokens, w, marr, xin,
+                                   ta.n_vec, [&](int p, const int32_t *t) { return shared ? first + p - ta.R : t[p]; },
+                                   K, pg.group, count);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nl = lane & 15, kb = lane >> 4;
     // h of the tile's positions x the workgroup's 128 rows, in LDS (stage 0's
     // activations are no longer read: every wave has passed the last barrier)
@@ -474,22 +487,20 @@ __global__ __launch_bounds__(kWideThreads) void wide_gateup_kernel(TileArgs ta, 
     int slot, first, count;
     bool shared;
     if (!wide_tile(ta, gate.n_slots, slot, first, count, shared)) return;
-    int *tok = reinterpret_cast<int *>(wlds + wide_tok_offset(gate.cols, 2));
     const QProj pg = shared ? sgate : gate;
     const QProj pu = shared ? sup : up;
     const int sl = shared ? 0 : slot;
     switch ((count + 15) >> 4) {
-    case 1: wide_gateup_tile<BITS, BF16, 1>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds, tok); break;
-    case 2: wide_gateup_tile<BITS, BF16, 2>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds, tok); break;
-    case 3: wide_gateup_tile<BITS, BF16, 3>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds, tok); break;
-    default: wide_gateup_tile<BITS, BF16, 4>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds, tok); break;
+    case 1: wide_gateup_tile<BITS, BF16, 1>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
+    case 2: wide_gateup_tile<BITS, BF16, 2>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
+    case 3: wide_gateup_tile<BITS, BF16, 3>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
+    default: wide_gateup_tile<BITS, BF16, 4>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
     }
 }
 
 template <int BITS, bool BF16, int NACT>
 __device__ __forceinline__ void wide_down_tile(const TileArgs &ta, const QProj &p, int sl, int first, int count,
-                                               const MfmaVec &hin, uint16_t *__restrict__ y, unsigned char *wlds,
-                                               int *tok) {
+                                               const MfmaVec &hin, uint16_t *__restrict__ y, unsigned char *wlds) {
     const int N = p.rows, K = p.cols;
     const WideLds<1> L(wlds, K);
     const int n0 = blockIdx.x * kWideRows;
@@ -498,8 +509,8 @@ __device__ __forceinline__ void wide_down_tile(const TileArgs &ta, const QProj &
     const uint32_t *const w[1] = {p.w + sl * p.w_slot + static_cast<int64_t>(n0) * wpr};
     const uint16_t *const marr[2] = {p.s + sl * p.m_slot + r0, p.b + sl * p.m_slot + r0};
     mf32x4_t acc[1][NACT];
-    wide_body<BITS, BF16, 1, NACT>(acc, L, tok, w, marr, hin, ta.n_vec, [&](int q) { return first + q; }, K, p.group,
-                                   count);
+    wide_body<BITS, BF16, 1, NACT>(acc, L, nullptr, w, marr, hin, ta.n_vec,
+                                   [&](int q, const int32_t *) { return first + q; }, K, p.group, count);
     const int wave = threadIdx.x >> 6;
     if (wave >= kWideCompute) return;
     const int lane = threadIdx.x & 63, nl = lane & 15, kb = lane >> 4;
@@ -521,14 +532,13 @@ __global__ __launch_bounds__(kWideThreads) void wide_down_kernel(TileArgs ta, QP
     int slot, first, count;
     bool shared;
     if (!wide_tile(ta, down.n_slots, slot, first, count, shared)) return;
-    int *tok = reinterpret_cast<int *>(wlds + wide_tok_offset(down.cols, 1));
     const QProj p = shared ? sdown : down;
     const int sl = shared ? 0 : slot;
     switch ((count + 15) >> 4) {
-    case 1: wide_down_tile<BITS, BF16, 1>(ta, p, sl, first, count, hin, y, wlds, tok); break;
-    case 2: wide_down_tile<BITS, BF16, 2>(ta, p, sl, first, count, hin, y, wlds, tok); break;
-    case 3: wide_down_tile<BITS, BF16, 3>(ta, p, sl, first, count, hin, y, wlds, tok); break;
-    default: wide_down_tile<BITS, BF16, 4>(ta, p, sl, first, count, hin, y, wlds, tok); break;
+    case 1: wide_down_tile<BITS, BF16, 1>(ta, p, sl, first, count, hin, y, wlds); break;
+    case 2: wide_down_tile<BITS, BF16, 2>(ta, p, sl, first, count, hin, y, wlds); break;
+    case 3: wide_down_tile<BITS, BF16, 3>(ta, p, sl, first, count, hin, y, wlds); break;
+    default: wide_down_tile<BITS, BF16, 4>(ta, p, sl, first, count, hin, y, wlds); break;
     }
 }
 
