@@ -446,6 +446,65 @@ def stack_run(dev, steps, warmup, policy, seed, layers=43, per_layer=96, prefetc
                         f"logits through copula noise of correlation {lookahead_rho}"}
 
 
+DOWN_ROUTE_BYTES = proj_bytes(D, DFF)                                 # 2,621,440
+
+
+def streaming_floor_run(dev, m=40, replays=5, rotate=16):
+    """The decode step's memory traffic with nothing else: per step three
+    dependent launches of locali_moe_stream_read (16-byte non-temporal loads,
+    no arithmetic) over the router's 2 MiB, the 7 routes' gate/up bytes and
+    the 7 routes' down bytes, each from its own buffer; steps rotate over
+    `rotate` buffer sets (914 MB, far past the 256 MB MALL) so every read is
+    cold, as the decode leg's are. Graphs of m steps (and of m launches of
+    each stage alone) are timed with HIP events on the replay stream."""
+    from locali_amd import _lib
+    lib = _lib.lib()
+    sizes = {"router": ROUTER_BYTES, "gateup": (K_TOP + 1) * GATEUP_ROUTE_BYTES,
+             "down": (K_TOP + 1) * DOWN_ROUTE_BYTES}
+    bufs = [{k: torch.empty(v, dtype=torch.uint8, device=dev) for k, v in sizes.items()} for _ in range(rotate)]
+    sink = torch.zeros(65535, dtype=torch.int32, device=dev)
+
+    def launch(buf):
+        blocks = min(65535, (buf.numel() // 16 + 1023) // 1024)
+        _lib.check(lib.locali_moe_stream_read(buf.data_ptr(), buf.numel(), sink.data_ptr(), blocks, ops._stream()),
+                   "locali_moe_stream_read")
+
+    def timed(fn):
+        for i in range(2):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(m):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / (replays * m)
+
+    def step(i):
+        for k in ("router", "gateup", "down"):
+            launch(bufs[i % rotate][k])
+
+    out = {"step_us": timed(step) * 1e6}
+    for k in sizes:
+        t = timed(lambda i, k=k: launch(bufs[i % rotate][k]))
+        out[f"{k}_us"] = t * 1e6
+        out[f"{k}_GBps"] = sizes[k] / t / 1e9
+    out["bytes_per_step"] = sum(sizes.values())
+    out["step_GBps"] = out["bytes_per_step"] / (out["step_us"] * 1e-6) / 1e9
+    out["workload"] = ("three dependent streaming reads per step (router 2 MiB, 7 routes' gate/up "
+                       "36.7 MB, 7 routes' down 18.4 MB), cold buffers, no arithmetic")
+    del bufs
+    torch.cuda.empty_cache()
+    return out
+
+
 def decode_g128_run(specs, X, dev, steps, warmup, use_graph, seed):
     """The decode leg on experts in groups of 128, the real checkpoint's
     2-bit layout (7,077,888 B per expert): same router copies, inputs and
@@ -761,6 +820,8 @@ def main(argv=None):
     st = stage_timing(specs, arena, shareds, slot_of, X, ws)
     gate_bytes = STEP_GATEUP_ALG_BYTES
     achieved = gate_bytes / st["gateup_router_select"] / 1e9
+    phase("streaming floor of the decode step (three dependent streaming reads)")
+    floor = streaming_floor_run(dev)
     g128 = None
     if not args.skip_g128:
         phase("decode, experts in groups of 128 (graph replay)")
@@ -816,6 +877,7 @@ def main(argv=None):
                 "frac": GATEUP_ALG_BYTES / st["gateup_chosen_routes"] / 1e9 / HBM_PEAK_GBS},
         },
     }
+    result["decode_streaming_floor"] = floor
     if g128 is not None:
         result["decode_g128"] = g128
     if not args.skip_prefill:

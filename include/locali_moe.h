@@ -328,6 +328,14 @@ int locali_moe_forward_noalloc(const locali_router *router, const locali_expert_
                                int32_t fp32_swiglu, void *out, int32_t *idx, float *weights,
                                void *stream);
 
+/* No counterpart in the reference: a measurement helper. Reads `bytes`
+ * (a multiple of 16, 16-byte aligned) of device memory once with the expert
+ * kernels' 16-byte non-temporal loads and computes nothing (sink: `blocks`
+ * words the kernel practically never writes). Timed over the decode step's
+ * byte counts in dependent launches, it is the streaming floor the decode
+ * kernels are compared with. */
+int locali_moe_stream_read(const void *src, size_t bytes, uint32_t *sink, int32_t blocks, void *stream);
+
 const char *locali_moe_last_error(void);
 
 #ifdef __cplusplus

@@ -113,6 +113,7 @@ _SIGNATURES = {
                            _I, _P], ctypes.c_int),
     "locali_dplan_plan_fill": ([_P, _I, _I, _I, _I, _P, _I, _I, _I, _I, _I, _P, ctypes.POINTER(ctypes.c_void_p),
                                 ctypes.POINTER(ctypes.c_size_t), _I, _P, _P], ctypes.c_int),
+    "locali_moe_stream_read": ([_P, _SZ, _P, _I, _P], ctypes.c_int),
     "locali_dplan_prefetch": ([_P, _I, _I, _I, _I, _P, _P, _I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_void_p),
                                ctypes.POINTER(ctypes.c_size_t), _I, _P, _P], ctypes.c_int),
     "locali_dplan_host_view": ([ctypes.POINTER(ctypes.c_void_p), _I, ctypes.POINTER(ctypes.c_uint64)],
