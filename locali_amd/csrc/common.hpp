@@ -153,6 +153,31 @@ template <> struct Pairs<4, false> {
                                           {8, 0x00F000F0u, 3, 7, -4, -4}};
 };
 
+// 3-bit codes split over a word's halves (spread3_halves: values 0-3 in bits
+// 0-11 and 4-7 in bits 16-27, three bits each; bits 12-15 of each half are
+// not read): shifts 0, 3, 6, 9, the 4-bit order and unscaled activations.
+template <> struct Pairs<3, true> {
+    static constexpr bool kSubtract = false;  // magic removed per group
+    static constexpr int kCount = 4;
+    static constexpr uint32_t kMagic = 0x43004300u;
+    static constexpr float kMagicValue = 128.0f;
+    static constexpr PairSpec kSpec[4] = {{0, 0x00070007u, 0, 4, 0, 0},
+                                          {3, 0x00070007u, 1, 5, 0, 0},
+                                          {6, 0x00070007u, 2, 6, 0, 0},
+                                          {9, 0x00070007u, 3, 7, 0, 0}};
+};
+
+template <> struct Pairs<3, false> {
+    static constexpr bool kSubtract = true;   // magic removed by v_pk_add_f16
+    static constexpr int kCount = 4;
+    static constexpr uint32_t kMagic = 0x64006400u;
+    static constexpr float kMagicValue = 1024.0f;
+    static constexpr PairSpec kSpec[4] = {{0, 0x00070007u, 0, 4, 0, 0},
+                                          {3, 0x00070007u, 1, 5, 0, 0},
+                                          {6, 0x00070007u, 2, 6, 0, 0},
+                                          {9, 0x00070007u, 3, 7, 0, 0}};
+};
+
 // 8-bit, bf16: a byte does not fit the 7-bit mantissa, so each byte is two
 // nibble fields (the high nibble weighs 16). Values 0..3 of the word.
 template <> struct Pairs<8, true> {

@@ -37,7 +37,8 @@ static hipError_t decode_dispatch(int which, const QProj &p, const DecodeLaunch 
 }
 
 hipError_t launch_gateup_decode(const DecodeLaunch &L, hipStream_t st) {
-    if (gateup_diag_eligible(L)) return L.gate.bits == 2 ? decode_diag_b2(L, st) : decode_diag_b4(L, st);
+    if (gateup_diag_eligible(L))
+        return L.gate.bits == 2 ? decode_diag_b2(L, st) : L.gate.bits == 3 ? decode_diag_b3(L, st) : decode_diag_b4(L, st);
     return decode_dispatch(0, L.gate, L, st);
 }
 

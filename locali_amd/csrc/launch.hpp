@@ -91,25 +91,28 @@ int group_parts(const QProj &p);
 
 // Matrix-core decode gate/up kernel (mfma_decode.hpp): one wave per
 // 512-value window of K and 16-row tile, workgroups of 2 tiles and K / 512
-// waves. It takes 2- or 4-bit codes (gate and up alike) with groups of 64 or
-// 128 (a metadata row of whole 16-byte pieces), K a multiple of 512 and at
-// most 4096, d_ff a multiple of 32, and a down
-// projection of 2 or 4 bits (its epilogue prepares whole words of the down
-// input, the decode layout the down kernel reads). The shared expert has the
-// routed experts' shapes and quantisation.
+// waves. It takes 2-, 3- or 4-bit codes (gate and up alike; 3-bit rows are
+// widened to 4-bit codes as they arrive) with groups of 64 or 128 (a
+// metadata row of whole 16-byte pieces), K a multiple of 512 and at most
+// 4096, d_ff a multiple of 32, and a down projection of 2, 3 or 4 bits (its
+// epilogue prepares whole words of the down input, the decode layout the
+// down kernel reads). The shared expert has the routed experts' shapes and
+// quantisation.
 constexpr int kDiagWindow = 512;
 constexpr int kDiagGateUpTiles = 2;
 constexpr int kDiagGateUpMaxWaves = 8;
 
 inline bool gateup_diag_eligible(const DecodeLaunch &L) {
     auto ok = [](const QProj &p) {
-        return (p.bits == 2 || p.bits == 4) && (p.group == 64 || p.group == 128) && (p.cols / p.group) % 8 == 0 &&
-               p.cols % kDiagWindow == 0;
+        return (p.bits == 2 || p.bits == 3 || p.bits == 4) && (p.group == 64 || p.group == 128) &&
+               (p.cols / p.group) % 8 == 0 && p.cols % kDiagWindow == 0;
     };
-    return ok(L.gate) && ok(L.up) && L.gate.bits == L.up.bits && (L.down.bits == 2 || L.down.bits == 4) &&
+    return ok(L.gate) && ok(L.up) && L.gate.bits == L.up.bits &&
+           (L.down.bits == 2 || L.down.bits == 3 || L.down.bits == 4) &&
            L.gate.cols / kDiagWindow <= kDiagGateUpMaxWaves && L.gate.rows % (16 * kDiagGateUpTiles) == 0;
 }
 hipError_t decode_diag_b2(const DecodeLaunch &L, hipStream_t st);
+hipError_t decode_diag_b3(const DecodeLaunch &L, hipStream_t st);
 hipError_t decode_diag_b4(const DecodeLaunch &L, hipStream_t st);
 
 // ---- router ------------------------------------------------------------------

@@ -38,8 +38,14 @@
 
 namespace locali {
 
+// 3-bit gate/up rows staged in LDS: a 192-byte window row padded to 52
+// words, one 16-row tile a wave at a time
+constexpr int kDiag3RowWords = 52;
+constexpr size_t kDiag3WaveBytes = 4 * kDiag3RowWords * 16;
+
 template <int BITS>
 struct DiagGeom {
+    // BITS: the width the kernels compute in (3-bit codes are widened to 4)
     static constexpr int kUnitVals = 128 / BITS;            // values per 16-byte unit
     static constexpr int kUnits = kDiagWindow / kUnitVals;  // units per window row (8 or 16)
     static constexpr int kLines = kUnits / 8;               // 128-byte lines per window row
@@ -114,16 +120,17 @@ __device__ __forceinline__ void diag_prep_load(uint32_t (&ww)[16 / BITS], const 
 // Prepares the wave's window (a word per lane; 2-bit: lanes 0-31) into its
 // slice; the words of a unit are consecutive lanes, so the unit sums meet by
 // butterfly. The slice is the wave's own: its LDS writes are ordered before
-// its later reads without a workgroup barrier.
-template <int BITS, bool BF16>
+// its later reads without a workgroup barrier. PB: the pair layout of the
+// weights (3 for 3-bit codes in the 4-bit geometry).
+template <int BITS, bool BF16, int PB = BITS>
 __device__ __forceinline__ void diag_prep_store(DiagSlice<BITS> &sl, const uint32_t (&ww)[16 / BITS], int lane) {
     using G = DiagGeom<BITS>;
-    using P = Pairs<BITS, BF16>;
+    using P = Pairs<PB, BF16>;
     constexpr int VPW = 32 / BITS, WORDS = kDiagWindow / VPW, WPU = G::kUnitVals / VPW;
     float2 part = make_float2(0.f, 0.f);
     const int u = lane / WPU, wu = lane % WPU;
     if (lane < WORDS)
-        prep_vals<BITS, BF16>(ww, reinterpret_cast<uint32_t *>(sl.pairs + u * G::kStride) + wu * P::kCount, 1,
+        prep_vals<BITS, BF16, PB>(ww, reinterpret_cast<uint32_t *>(sl.pairs + u * G::kStride) + wu * P::kCount, 1,
                               part);
 #pragma unroll
     for (int m = 1; m < WPU; m <<= 1) {
@@ -211,10 +218,14 @@ template <int BITS, bool BF16, bool SELECT, bool ROUTER>
 __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     RouteArgs ra, QProj gate, QProj up, QProj sgate, QProj sup, uint16_t *__restrict__ h,
     PrepVec hout, int down_bits, float limit, int fp32_swiglu, RouterLaunch sel) {
-    using G = DiagGeom<BITS>;
+    // 3-bit codes run in the 4-bit geometry: each 16-byte unit of 4-bit
+    // codes is a 12-byte piece of the 3-bit row, its words' values split
+    // over their halves on arrival (the Pairs<3, *> layout)
+    constexpr int CB = BITS == 3 ? 4 : BITS;
+    using G = DiagGeom<CB>;
     constexpr int RT = kDiagGateUpTiles;
     constexpr int NI = 2 * G::kLines;   // loads per (tile, projection): row halves x lines
-    __shared__ __align__(16) DiagSlice<BITS> win[kDiagGateUpMaxWaves];
+    __shared__ __align__(16) DiagSlice<CB> win[kDiagGateUpMaxWaves];
     __shared__ float red[kDiagGateUpMaxWaves][RT][2][16];
     __shared__ __align__(16) uint16_t hs[16 * RT];
     // scales and biases of the workgroup's rows: [gs, gb, us, ub][row][K / 64]
@@ -254,16 +265,16 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     const int n0 = blockIdx.x * 16 * RT;
     const int wpr = K * BITS / 32, gpr = K / gate.group;
     const int waves = blockDim.x >> 6;   // = K / 512
-    const int ug_log2 = units_per_group_log2<BITS>(gate.group);
-    DiagSlice<BITS> &mw = win[wave];
+    const int ug_log2 = units_per_group_log2<CB>(gate.group);
+    DiagSlice<CB> &mw = win[wave];
 
     // Raw x of the window first (the prep waits only for it), then the
     // workgroup's scales and biases by whole lines, then the weights in
     // consumption order. The metadata geometry does not depend on the slot
     // and is worked out before any selection: thread i moves 16-byte pieces
     // i and i + 64 * waves of the four arrays' rows (meta_piece_of).
-    uint32_t xw[16 / BITS];
-    diag_prep_load<BITS>(xw, ra.x + static_cast<int64_t>(token) * K + wave * kDiagWindow, lane);
+    uint32_t xw[16 / CB];
+    diag_prep_load<CB>(xw, ra.x + static_cast<int64_t>(token) * K + wave * kDiagWindow, lane);
     const int mrs = 2 * gpr + 16;   // LDS bytes per metadata row
     // 4 arrays x 16 RT rows x gpr / 8 pieces: at most RT pieces per thread
     MetaPiece mp[RT];
@@ -280,8 +291,8 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
                 if (wave == 0)
                     tag = sync_tag(__hip_atomic_load(sel.sync_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
             // wave 1 also prepares wave 0's window while wave 0 selects
-            uint32_t xw0[16 / BITS];
-            if (wave == 1) diag_prep_load<BITS>(xw0, ra.x + static_cast<int64_t>(token) * K, lane);
+            uint32_t xw0[16 / CB];
+            if (wave == 1) diag_prep_load<CB>(xw0, ra.x + static_cast<int64_t>(token) * K, lane);
             sched_fence();
             if (wave == 0) {
                 // this route needs choice j only; the workgroup that stores the
@@ -298,15 +309,15 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
                 const int sj = __builtin_amdgcn_readlane(o.slot, j);
                 if (lane == 0) s_slot = sj;
                 if (store) select_store(sel, token, o);
-                if (waves == 1) diag_prep_store<BITS, BF16>(mw, xw, lane);
+                if (waves == 1) diag_prep_store<CB, BF16, BITS>(mw, xw, lane);
             } else {
-                diag_prep_store<BITS, BF16>(mw, xw, lane);
-                if (wave == 1) diag_prep_store<BITS, BF16>(win[0], xw0, lane);
+                diag_prep_store<CB, BF16, BITS>(mw, xw, lane);
+                if (wave == 1) diag_prep_store<CB, BF16, BITS>(win[0], xw0, lane);
             }
             __syncthreads();
             slot = s_slot;
         } else {
-            diag_prep_store<BITS, BF16>(mw, xw, lane);
+            diag_prep_store<CB, BF16, BITS>(mw, xw, lane);
         }
     }
     sched_fence();
@@ -330,22 +341,70 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_diag_kernel(
     const __amdgpu_buffer_rsrc_t uw_rs = make_rsrc(uwp + sl * uw_slot + wrow0, wbytes);
     // load q = 2 * line + i: row 8 i + n % 8 of the tile, unit 4 h + kb of the line
     u32x4 wg[RT][NI], wu[RT][NI];
+    // 3-bit codes: a window row is 192 bytes, twelve 16-byte pieces, and a
+    // unit is 12 of them. Loads of single units would cover lines in part
+    // (and be requested as partial lines); the wave reads its 16 RT window
+    // rows whole instead, piece f = 64 j + lane of the rows' piece list in
+    // load j (a tile's 16 rows are 3 loads), stages them in LDS one tile of
+    // one projection at a time after the metadata barrier, and reads each
+    // unit's three words back to split them.
+    constexpr int P3 = kDiagWindow * 3 / 8 / 16;   // pieces per window row
+    constexpr int NP3 = BITS == 3 ? 16 * RT * P3 / 64 : 1;
+    static_assert(BITS != 3 || 16 * RT * P3 % 64 == 0, "whole loads per projection");
+    u32x4 pg[NP3], pu[NP3];
+    if constexpr (BITS == 3) {
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int q = 0; q < NI; ++q) {
-            const int i = q & 1, line = q >> 1;
-            const uint32_t wo = 4u * static_cast<uint32_t>((16 * rt + 8 * i + r8) * wpr) + 128u * line +
-                                16u * (4 * hh + kb);
-            wg[rt][q] = __builtin_amdgcn_raw_buffer_load_b128(gw_rs, wo, 128 * G::kLines * wave, kAuxStream);
-            wu[rt][q] = __builtin_amdgcn_raw_buffer_load_b128(uw_rs, wo, 128 * G::kLines * wave, kAuxStream);
+        for (int j = 0; j < NP3; ++j) {
+            const int f = 64 * j + lane, row = f / P3, pc = f - P3 * row;
+            const uint32_t wo = 4u * static_cast<uint32_t>(row * wpr) + 16u * pc;
+            pg[j] = __builtin_amdgcn_raw_buffer_load_b128(gw_rs, wo, 16 * P3 * wave, kAuxStream);
+            pu[j] = __builtin_amdgcn_raw_buffer_load_b128(uw_rs, wo, 16 * P3 * wave, kAuxStream);
         }
+    } else {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int q = 0; q < NI; ++q) {
+                const int i = q & 1, line = q >> 1;
+                const uint32_t wo = 4u * static_cast<uint32_t>((16 * rt + 8 * i + r8) * wpr) + 128u * line +
+                                    16u * (4 * hh + kb);
+                wg[rt][q] = __builtin_amdgcn_raw_buffer_load_b128(gw_rs, wo, 128 * G::kLines * wave, kAuxStream);
+                wu[rt][q] = __builtin_amdgcn_raw_buffer_load_b128(uw_rs, wo, 128 * G::kLines * wave, kAuxStream);
+            }
+    }
     sched_fence();
-    if constexpr (!SELECT) diag_prep_store<BITS, BF16>(mw, xw, lane);
+    if constexpr (!SELECT) diag_prep_store<CB, BF16, BITS>(mw, xw, lane);
 #pragma unroll
     for (int q = 0; q < RT; ++q)
         if (mp[q].store) *reinterpret_cast<u32x4 *>(mlds + mp[q].dst) = mv[q];
     __syncthreads();
+    if constexpr (BITS == 3) {
+        // the wave's own tile of rows in dynamic LDS (kDiag3RowWords words a
+        // row, padded from 48 to spread the unit reads over the banks); each
+        // tile's pieces overwrite the previous tile's after its reads
+        extern __shared__ __align__(16) uint32_t stage3[];
+        uint32_t *sw = stage3 + wave * (16 * kDiag3RowWords);
+        constexpr int JT = NP3 / RT;   // loads per tile
+        static_assert(16 * P3 == 64 * JT, "a tile's rows are whole loads");
+        auto widen = [&](const u32x4(&pc)[NP3], u32x4(&out)[RT][NI]) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+                for (int jj = 0; jj < JT; ++jj) {
+                    const int f = 64 * jj + lane, row = f / P3;
+                    *reinterpret_cast<u32x4 *>(sw + kDiag3RowWords * row + 4 * (f - P3 * row)) = pc[JT * rt + jj];
+                }
+#pragma unroll
+                for (int q = 0; q < NI; ++q) {
+                    const int i = q & 1, line = q >> 1;
+                    const uint32_t *u = sw + kDiag3RowWords * (8 * i + r8) + 3 * (8 * line + 4 * hh + kb);
+                    out[rt][q] = spread3_halves(u[0], u[1], u[2]);
+                }
+            }
+        };
+        widen(pg, wg);
+        widen(pu, wu);
+    }
     const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
     // diagonal A: lane (m, kb) feeds unit 8 line + 4 ((m / 2) % 2) + kb when m / 4 == kb
     const bool diag = (nl >> 2) == kb;
@@ -437,16 +496,19 @@ template <int BITS, bool BF16>
 hipError_t launch_gateup_diag(const DecodeLaunch &L, hipStream_t st) {
     const int waves = L.gate.cols / kDiagWindow;
     const int rr = L.sel ? L.sel->router_rows - L.sel->router_shared_rows : 0;
+    // the down kernel reads its input prepared in the width it computes in
+    const int down_bits = lane_bits(L.down.bits);
+    const size_t lds = BITS == 3 ? waves * kDiag3WaveBytes : 0;
     dim3 grid(L.gate.rows / (16 * kDiagGateUpTiles), L.routes + rr);
     if (L.sel && L.sel->router_rows > 0)
-        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, true, true>), grid, dim3(64 * waves), 0, st, L.ra,
-                           L.gate, L.up, L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu, *L.sel);
+        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, true, true>), grid, dim3(64 * waves), lds, st, L.ra,
+                           L.gate, L.up, L.sgate, L.sup, L.h, L.hprep, down_bits, L.limit, L.fp32_swiglu, *L.sel);
     else if (L.sel)
-        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, true, false>), grid, dim3(64 * waves), 0, st, L.ra,
-                           L.gate, L.up, L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu, *L.sel);
+        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, true, false>), grid, dim3(64 * waves), lds, st, L.ra,
+                           L.gate, L.up, L.sgate, L.sup, L.h, L.hprep, down_bits, L.limit, L.fp32_swiglu, *L.sel);
     else
-        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, false, false>), grid, dim3(64 * waves), 0, st, L.ra,
-                           L.gate, L.up, L.sgate, L.sup, L.h, L.hprep, L.down.bits, L.limit, L.fp32_swiglu,
+        hipLaunchKernelGGL((gateup_diag_kernel<BITS, BF16, false, false>), grid, dim3(64 * waves), lds, st, L.ra,
+                           L.gate, L.up, L.sgate, L.sup, L.h, L.hprep, down_bits, L.limit, L.fp32_swiglu,
                            RouterLaunch{});
     return hipGetLastError();
 }

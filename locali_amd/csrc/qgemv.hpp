@@ -66,10 +66,12 @@ __device__ __forceinline__ uint16_t scale_pow2(uint16_t v) {
 // Prepare one word's worth of activations (VPW values at `src`).
 // Prepare one word's worth of activations (32 / BITS values, given as 16-bit
 // pairs in ww) into its pairs and partial sums (corr, xs).
-template <int BITS, bool BF16>
+// PB: the pair layout the products read (BITS, or 3 for 3-bit codes split
+// over the halves of 4-bit-sized words).
+template <int BITS, bool BF16, int PB = BITS>
 __device__ __forceinline__ void prep_vals(const uint32_t (&ww)[16 / BITS], uint32_t *pairs,
                                           int pair_stride, float2 &part) {
-    using P = Pairs<BITS, BF16>;
+    using P = Pairs<PB, BF16>;
     constexpr int VPW = 32 / BITS;
     uint16_t vals[VPW];
 #pragma unroll
@@ -276,6 +278,18 @@ __device__ __forceinline__ uint32_t spread3_word(uint32_t v) {
     v = (v & 0x00000FFFu) | ((v << 4) & 0x0FFF0000u);
     v = (v & 0x003F003Fu) | ((v << 2) & 0x3F003F00u);
     return (v & 0x07070707u) | ((v << 1) & 0x70707070u);
+}
+
+// A 32-value chunk of 3-bit codes with each word's eight values split over
+// its halves (values 0-3 at bits 0-11, 4-7 at bits 16-27; bits 12-15 and
+// 28-31 hold other values' bits), the layout Pairs<3, *> reads: one shift
+// and one bit select a word.
+__device__ __forceinline__ uint32_t spread3_half(uint32_t v) {
+    return ((v << 4) & 0xFFFF0000u) | (v & 0x0000FFFFu);
+}
+__device__ __forceinline__ u32x4 spread3_halves(uint32_t w0, uint32_t w1, uint32_t w2) {
+    return u32x4{spread3_half(w0), spread3_half(__builtin_amdgcn_alignbit(w1, w0, 24)),
+                 spread3_half(__builtin_amdgcn_alignbit(w2, w1, 16)), spread3_half(w2 >> 8)};
 }
 
 // A 32-value chunk of 3-bit codes (three words of the row's little-endian

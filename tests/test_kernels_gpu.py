@@ -199,10 +199,13 @@ DECODE_CASES = [
     (torch.float16, 2, 2, 128, 4096, 2048),
     (torch.bfloat16, 4, 4, 128, 4096, 2048),
     # 3-bit codes (the DSpark/MTP tier): 4-bit kernels widening 3-bit rows
+    # (the matrix-core gate/up for groups of 64 and 128, VALU for 32)
     (torch.bfloat16, 3, 3, 64, 1024, 512),
     (torch.float16, 3, 3, 32, 1024, 512),
     (torch.bfloat16, 2, 3, 64, 1024, 512),
     (torch.bfloat16, 3, 2, 64, 4096, 2048),
+    (torch.bfloat16, 3, 3, 64, 4096, 2048),
+    (torch.float16, 3, 3, 128, 4096, 2048),
 ]
 
 
@@ -664,21 +667,22 @@ def test_decode_forward_in_separate_stages(T):
     assert torch.equal(rs, idx + 1)
 
 
-@pytest.mark.parametrize("d,dtype,dff", [(4096, torch.bfloat16, 1024), (2048, torch.float16, 1024),
-                                         (1024, torch.bfloat16, 1024), (4096, torch.bfloat16, 2048),
-                                         (4096, torch.float16, 2048)])
-def test_fused_router_rows_across_calls_and_replays(d, dtype, dff):
+@pytest.mark.parametrize("d,dtype,dff,bits", [(4096, torch.bfloat16, 1024, 2), (2048, torch.float16, 1024, 2),
+                                              (1024, torch.bfloat16, 1024, 2), (4096, torch.bfloat16, 2048, 2),
+                                              (4096, torch.float16, 2048, 2), (4096, torch.bfloat16, 2048, 3)])
+def test_fused_router_rows_across_calls_and_replays(d, dtype, dff, bits):
     """The decode forward computes the logits in router rows of its gate/up
     kernel and hands them over as tagged words. Consecutive calls on one
     workspace alternate between routers and between 1 and 2 tokens, so a call
     that read the previous call's words would route like that call: every
     call must equal the separate logits -> gate/up -> down chain bit for bit,
     eagerly and under repeated graph replays (d_ff 1024 and the benchmarked
-    2048)."""
-    banner(f"fused router rows d={d} {dt_name(dtype)} dff={dff}")
+    2048; 2-bit codes and the 3-bit MTP tier's)."""
+    banner(f"fused router rows d={d} {dt_name(dtype)} dff={dff} bits={bits}")
     E, k = 256, 6
-    arena = synth.expert_arena(E + 1, d, dff, dtype=dtype, seed=91, device=DEV)
-    shared = synth.expert_arena(1, d, dff, dtype=dtype, seed=92, device=DEV, zero_slot=False)
+    arena = synth.expert_arena(E + 1, d, dff, bits_gate_up=bits, dtype=dtype, seed=91, device=DEV)
+    shared = synth.expert_arena(1, d, dff, bits_gate_up=bits, dtype=dtype, seed=92, device=DEV,
+                                zero_slot=False)
     specs = []
     for i in range(3):
         w, bias = synth.uniform_router(E, d, dtype, seed=93 + i, device=DEV, bias_std=0.01)
@@ -726,16 +730,18 @@ def test_fused_router_rows_across_calls_and_replays(d, dtype, dff):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("group", [64, 128])
-def test_forward_full_width_decode(oracle_lib, group):
-    """d 4096, 256 experts + shared, d_ff 2048, 2-bit bf16 in groups of 64 and
-    of 128 (the real checkpoint's), 1 token; checked against the C oracle
-    (fp32) on the GPU's own routing."""
-    banner(f"forward C2 group {group}")
+@pytest.mark.parametrize("group,bits", [(64, 2), (128, 2), (64, 3)])
+def test_forward_full_width_decode(oracle_lib, group, bits):
+    """d 4096, 256 experts + shared, d_ff 2048, bf16, 2-bit in groups of 64
+    and of 128 (the real checkpoint's) and 3-bit in groups of 64 (the MTP
+    tier's width), 1 token; checked against the C oracle (fp32) on the GPU's
+    own routing."""
+    banner(f"forward C2 group {group} bits {bits}")
     d, E, dff, k = 4096, 256, 2048, 6
-    arena = synth.expert_arena(E + 1, d, dff, group=group, dtype=torch.bfloat16, seed=21, device=DEV)
-    shared = synth.expert_arena(1, d, dff, group=group, dtype=torch.bfloat16, seed=22, device=DEV,
-                                zero_slot=False)
+    arena = synth.expert_arena(E + 1, d, dff, bits_gate_up=bits, group=group, dtype=torch.bfloat16, seed=21,
+                               device=DEV)
+    shared = synth.expert_arena(1, d, dff, bits_gate_up=bits, group=group, dtype=torch.bfloat16, seed=22,
+                                device=DEV, zero_slot=False)
     w, _ = synth.uniform_router(E, d, torch.bfloat16, seed=23, device=DEV)
     spec = ops.RouterSpec(w, k, routed_scale=1.5)
     slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
@@ -755,6 +761,6 @@ def test_forward_full_width_decode(oracle_lib, group):
         want, terms = oracle_lib.moe_layer(values(x), np.vectorize(remap.get)(slots),
                                            wts.cpu().numpy(), sub, "bf16", shared=sh,
                                            return_terms=True)
-        assert_close_terms(values(out), want, terms, f"C2 step {step}")
+        assert_close_terms(values(out), want, terms, f"C2 bits {bits} step {step}")
         assert exact_fraction(values(out), want) > 0.8
 
