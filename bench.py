@@ -24,6 +24,9 @@ Also reported:
                 `--summarize-pmc` into profiles/gateup_diag_kernel_decode_traffic.json
   decode_g128   the decode leg with the real checkpoint's 2-bit experts in
                 groups of 128 (7,077,888 B per expert)
+  decode_3bit_g128
+                the decode leg with the DSpark/MTP tier's experts: 3-bit codes
+                in groups of 128 (10,223,616 B per expert)
   prefill64, prefill512
                 64- and 512-token prefill on the same layer with Zipf(1.1)
                 expert popularity (grouped path): tokens/s, algorithmic GB/s
@@ -86,6 +89,8 @@ EXPERT_BYTES = 2 * proj_bytes(DFF, D) + proj_bytes(D, DFF)          # 7,864,320
 # the real checkpoint's 2-bit experts come in groups of 128
 G128_EXPERT_BYTES = 2 * proj_bytes(DFF, D, group=128) + proj_bytes(D, DFF, group=128)   # 7,077,888
 MIXED_EXPERT_BYTES = 2 * proj_bytes(DFF, D) + proj_bytes(D, DFF, bits=4)   # 9,961,472
+# the checkpoint's DSpark/MTP tier: 3-bit experts in groups of 128
+B3_EXPERT_BYTES = 2 * proj_bytes(DFF, D, bits=3, group=128) + proj_bytes(D, DFF, bits=3, group=128)   # 10,223,616
 GATEUP_ROUTE_BYTES = 2 * proj_bytes(DFF, D)                           # 5,242,880
 ROUTER_BYTES = E * D * 2
 # copula correlation between the next layer's gate applied to the current
@@ -505,13 +510,14 @@ def streaming_floor_run(dev, m=40, replays=5, rotate=16):
     return out
 
 
-def decode_g128_run(specs, X, dev, steps, warmup, use_graph, seed):
-    """The decode leg on experts in groups of 128, the real checkpoint's
-    2-bit layout (7,077,888 B per expert): same router copies, inputs and
-    step as the headline leg, one g128 shared expert per router copy."""
-    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=BITS, group=128, dtype=torch.bfloat16,
+def decode_format_run(specs, X, dev, steps, warmup, use_graph, seed, bits, group, expert_bytes, workload):
+    """The decode leg on experts of another format (`bits`-bit codes in
+    groups of `group`, expert_bytes per expert): same router copies, inputs
+    and step as the headline leg, one shared expert of that format per
+    router copy."""
+    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=bits, group=group, dtype=torch.bfloat16,
                                seed=seed, device=dev)
-    shareds = [synth.expert_arena(1, D, DFF, bits_gate_up=BITS, group=128, dtype=torch.bfloat16,
+    shareds = [synth.expert_arena(1, D, DFF, bits_gate_up=bits, group=group, dtype=torch.bfloat16,
                                   seed=seed + 1000 + 2 * i, device=dev, zero_slot=False) for i in range(len(specs))]
     slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=dev)
     ws = ops.Workspace(dev)
@@ -519,13 +525,12 @@ def decode_g128_run(specs, X, dev, steps, warmup, use_graph, seed):
     secs, wall, _ = decode_graph_run(specs, arena, shareds, slot_of, X, ws, steps, warmup, use_graph)
     del arena, shareds
     torch.cuda.empty_cache()
-    layer = 7 * G128_EXPERT_BYTES + ROUTER_BYTES
+    layer = 7 * expert_bytes + ROUTER_BYTES
     value = steps / secs
     return {"value": value, "unit": "tokens/s", "ms_per_step": secs / steps * 1e3, "steps": steps,
-            "expert_bytes": G128_EXPERT_BYTES, "layer_bytes_per_token": layer,
+            "expert_bytes": expert_bytes, "layer_bytes_per_token": layer,
             "layer_GBps": layer * value / 1e9, "layer_frac_of_hbm_peak": layer * value / 1e9 / HBM_PEAK_GBS,
-            "workload": "the headline decode layer with 2-bit affine experts in groups of 128 (bf16 scales/"
-                        "biases), the real checkpoint's expert layout"}
+            "workload": workload}
 
 
 def heavy_tiles_run(arena, shared, slot_of, dev, tokens, calls, seed):
@@ -747,6 +752,7 @@ def main(argv=None):
     ap.add_argument("--prefill-sizes", default="64,512", help="tokens per prefill call, comma-separated")
     ap.add_argument("--skip-mixed", action="store_true")
     ap.add_argument("--skip-g128", action="store_true")
+    ap.add_argument("--skip-3bit", action="store_true")
     ap.add_argument("--skip-heavy", action="store_true")
     ap.add_argument("--skip-stack", action="store_true")
     ap.add_argument("--stack-steps", type=int, default=128)
@@ -822,10 +828,19 @@ def main(argv=None):
     achieved = gate_bytes / st["gateup_router_select"] / 1e9
     phase("streaming floor of the decode step (three dependent streaming reads)")
     floor = streaming_floor_run(dev)
-    g128 = None
+    g128 = b3 = None
     if not args.skip_g128:
         phase("decode, experts in groups of 128 (graph replay)")
-        g128 = decode_g128_run(specs, X, dev, args.steps, args.warmup, not args.no_graph, args.seed + 50)
+        g128 = decode_format_run(specs, X, dev, args.steps, args.warmup, not args.no_graph, args.seed + 50,
+                                 BITS, 128, G128_EXPERT_BYTES,
+                                 "the headline decode layer with 2-bit affine experts in groups of 128 "
+                                 "(bf16 scales/biases), the real checkpoint's expert layout")
+    if not args.skip_3bit:
+        phase("decode, 3-bit experts in groups of 128 (graph replay)")
+        b3 = decode_format_run(specs, X, dev, args.steps, args.warmup, not args.no_graph, args.seed + 60,
+                               3, 128, B3_EXPERT_BYTES,
+                               "the headline decode layer with 3-bit affine experts in groups of 128 "
+                               "(bf16 scales/biases), the checkpoint's DSpark/MTP tier layout")
     del specs, shareds
     result = {
         "metric": METRIC,
@@ -880,6 +895,8 @@ def main(argv=None):
     result["decode_streaming_floor"] = floor
     if g128 is not None:
         result["decode_g128"] = g128
+    if b3 is not None:
+        result["decode_3bit_g128"] = b3
     if not args.skip_prefill:
         for tokens in (int(v) for v in args.prefill_sizes.split(",")):
             phase(f"prefill {tokens} tokens")

@@ -185,9 +185,11 @@ int locali_moe_decode_down_combine(const locali_expert_arena *routed,
  *                                  expert -> slot lookup of arena.py:558-567),
  *                                  writing idx, weights, route_slot [tokens,
  *                                  top_k] and hidden; tokens <= 2, n_experts
- *                                  <= 256, gate/up of 2- or 4-bit codes in
- *                                  groups of 64, d_model a multiple of 512 up
- *                                  to 4096; the workspace is laid out as for
+ *                                  <= 256, gate/up of 2-, 3- or 4-bit codes
+ *                                  in groups of 64 or 128, d_model a multiple
+ *                                  of 512 up to 4096, d_ff a multiple of 32
+ *                                  and a down projection of 2, 3 or 4 bits;
+ *                                  the workspace is laid out as for
  *                                  locali_moe_decode_gateup, and
  *                                  locali_moe_decode_down_combine on the same
  *                                  workspace then finishes the layer. */

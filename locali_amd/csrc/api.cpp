@@ -865,8 +865,9 @@ int locali_moe_decode_gateup_select(const locali_router *router, const locali_ex
     const DecodeLaunch DL = decode_launch(routed, shared, x, x_dtype, tokens, k, route_slot, weights, swiglu_limit,
                                           fp32_swiglu, LOCALI_COMBINE_ROUNDED, hidden, nullptr, workspace, lay);
     if (!router_select_fusable(RL) || !gateup_diag_eligible(DL))
-        return fail(LOCALI_E_ARG, "decode_gateup_select: needs n_experts <= 256 and a gate/up of 2- or 4-bit "
-                                  "codes in groups of 64 with d_model a multiple of 512 up to 4096");
+        return fail(LOCALI_E_ARG, "decode_gateup_select: needs n_experts <= 256, a gate/up of 2-, 3- or 4-bit "
+                                  "codes in groups of 64 or 128 with d_model a multiple of 512 up to 4096 and "
+                                  "d_ff a multiple of 32, and a down projection of 2, 3 or 4 bits");
     return run_decode(routed, shared, x, x_dtype, tokens, k, route_slot, weights, swiglu_limit, fp32_swiglu,
                       LOCALI_COMBINE_ROUNDED, hidden, nullptr, S(stream), 1, workspace, lay, &RL);
 }
