@@ -46,6 +46,9 @@ struct MfmaVec {
     // optional (the grouped gate/up kernels' h, for stage-wise tests): the
     // vectors' plain values, [vec][2 * pairs_stride]
     uint16_t *plain;
+    // optional (the 64-position gate/up kernel's h, for the small-tile down
+    // kernel): each 32 values' sums (corr, xs), [vec][2 * pairs_stride / 32]
+    float2 *sum32;
 };
 
 struct RouterLaunch;

@@ -177,6 +177,7 @@ struct MfmaLaunch {
     int32_t fp32_swiglu;
     int32_t max_tiles;
     int32_t tokens, routes;
+    int32_t min_count_down;       // the down stage's ta.min_count (its small tiles take more positions)
 };
 
 // Prepared pairs and per-64 sums of the tokens' x for the gate/up stage.

@@ -1,14 +1,19 @@
 // Grouped expert kernels for small tiles -- one or two positions of one slot
-// -- on the matrix cores (prefill, batched decode).
+// for gate/up, one to four for down -- on the matrix cores (prefill, batched
+// decode).
 //
 // The design of the decode gate/up kernel (mfma_decode.hpp): a wave owns a
 // 512-value window of K for 32 rows, its 16-byte weight loads cover whole
 // 128-byte lines, and the A operand is "diagonal". Its spare row bit carries
 // the second position: A row m = 4 kb + 2 h + p holds position p's x' for
 // k-lane kb's unit 4 h + kb, so D[4 kb + 2 h + p][n] is position p's dot with
-// lane (n, kb)'s unit -- two positions for the MFMA work of one. Under Zipf
-// routing most experts of a prefill get one or two tokens; the 16-position
-// tiles of the larger ones go to mfma_grouped.hpp.
+// lane (n, kb)'s unit -- two positions for the MFMA work of one. The down
+// kernel also takes tiles of three or four positions, feeding both pairs'
+// MFMAs from each expanded weight register (measured: 3.2 against the
+// 64-position down kernel's 2.2 TB/s on such tiles; the gate/up kernel was
+// slower than its 64-position kernel there). Under Zipf routing most experts
+// of a prefill get one to four tokens; the tiles of the larger ones go to
+// mfma_wide.hpp.
 //
 //   gateup_small_kernel  h[pos] = swiglu(up(x_t), gate(x_t)) for the tile's
 //                        positions; x is prepared per wave in LDS; the epilogue
@@ -22,7 +27,8 @@
 
 namespace locali {
 
-constexpr int kSmallTile = 2;   // positions per small tile
+constexpr int kSmallGateUpTile = 2;   // positions of a small gate/up tile
+constexpr int kSmallDownTile = 4;     // positions of a small down tile: one or two pairs
 constexpr int kSmallRows = 32;  // rows per workgroup (2 tiles of 16)
 
 struct SmallTileInfo {
@@ -34,7 +40,8 @@ struct SmallTileInfo {
 // do (past the list, a large tile, an invalid entry).
 // The record and the tile count are read together: the grid has one row per
 // possible tile, so the record is in bounds.
-__device__ __forceinline__ bool small_tile(const TileArgs &ta, int tile, int n_slots, SmallTileInfo &t) {
+__device__ __forceinline__ bool small_tile(const TileArgs &ta, int tile, int n_slots, int max_count,
+                                           SmallTileInfo &t) {
     const int4 rec = reinterpret_cast<const int4 *>(ta.tiles)[tile];
     const int nt = *ta.n_tiles;
     asm volatile("" ::"s"(rec.x), "s"(rec.y), "s"(rec.z), "s"(rec.w), "s"(nt));
@@ -43,7 +50,7 @@ __device__ __forceinline__ bool small_tile(const TileArgs &ta, int tile, int n_s
     t.count = rec.z;
     t.packed = rec.w;
     t.shared = t.slot == -2;
-    if (tile >= nt || t.count <= 0 || t.count > kSmallTile) return false;
+    if (tile >= nt || t.count <= 0 || t.count > max_count) return false;
     return t.shared || (t.slot >= 0 && t.slot < n_slots && t.first >= 0 && t.first + t.count <= ta.R);
 }
 
@@ -55,12 +62,12 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
     using G = DiagGeom<BITS>;
     constexpr int RT = kSmallRows / 16;
     constexpr int NI = 2 * G::kLines;
-    __shared__ __align__(16) DiagSlice<BITS> win[kDiagGateUpMaxWaves][kSmallTile];
-    __shared__ float red[kDiagGateUpMaxWaves][RT][2][kSmallTile][16];
-    __shared__ __align__(16) uint16_t hs[kSmallTile][kSmallRows];
+    __shared__ __align__(16) DiagSlice<BITS> win[kDiagGateUpMaxWaves][kSmallGateUpTile];
+    __shared__ float red[kDiagGateUpMaxWaves][RT][2][kSmallGateUpTile][16];
+    __shared__ __align__(16) uint16_t hs[kSmallGateUpTile][kSmallRows];
     __shared__ __align__(16) uint8_t mlds[4 * kSmallRows * (2 * (4096 / 64) + 16)];
     SmallTileInfo ti;
-    if (!small_tile(ta, blockIdx.y, gate.n_slots, ti)) return;
+    if (!small_tile(ta, blockIdx.y, gate.n_slots, kSmallGateUpTile, ti)) return;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nl = lane & 15, kb = lane >> 4, hh = nl >> 3, r8 = nl & 7;
     const bool shared = ti.shared;
@@ -74,11 +81,11 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
     const int waves = blockDim.x >> 6;   // = K / 512
     const int ug_log2 = units_per_group_log2<BITS>(gate.group);
     // tokens from the tile record when the dispatch packed them there
-    static_assert(kSmallTile <= kPackedTokens, "small tiles carry packed tokens");
+    static_assert(kSmallGateUpTile <= kPackedTokens, "small tiles carry packed tokens");
     const bool packed = !shared && (ti.packed & kTokensPacked);
-    int tok[kSmallTile];
+    int tok[kSmallGateUpTile];
 #pragma unroll
-    for (int p = 0; p < kSmallTile; ++p) {
+    for (int p = 0; p < kSmallGateUpTile; ++p) {
         const int q = min(p, count - 1);
         tok[p] = packed ? (ti.packed >> (kTokenBits * q)) & ((1 << kTokenBits) - 1)
                         : tile_token(ta, shared, ti.first + q);
@@ -86,9 +93,9 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
 
     // Raw x of the window of each position, the workgroup's scales and biases
     // by whole lines, then the weights in consumption order.
-    uint32_t xw[kSmallTile][16 / BITS];
+    uint32_t xw[kSmallGateUpTile][16 / BITS];
 #pragma unroll
-    for (int p = 0; p < kSmallTile; ++p)
+    for (int p = 0; p < kSmallGateUpTile; ++p)
         diag_prep_load<BITS>(xw[p], ta.x + static_cast<int64_t>(tok[p]) * K + wave * kDiagWindow, lane);
     sched_fence();
     const int mrs = 2 * gpr + 16;
@@ -134,13 +141,13 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
     const bool feed = (nl >> 2) == kb && ap < count;
     const int ah = (nl >> 1) & 1;
     const int as = kSmallRows * mrs / 2;
-    float accg[RT][2][kSmallTile], accu[RT][2][kSmallTile];
+    float accg[RT][2][kSmallGateUpTile], accu[RT][2][kSmallGateUpTile];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int p = 0; p < kSmallTile; ++p) accg[rt][i][p] = accu[rt][i][p] = 0.f;
+            for (int p = 0; p < kSmallGateUpTile; ++p) accg[rt][i][p] = accu[rt][i][p] = 0.f;
 #pragma unroll
     for (int line = 0; line < G::kLines; ++line) {
         const int uA = 8 * line + 4 * ah + kb;
@@ -188,7 +195,7 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void gateup_small_kernel(
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int p = 0; p < kSmallTile; ++p) {
+            for (int p = 0; p < kSmallGateUpTile; ++p) {
                 const float g = diag_row_sum(accg[rt][i][p]);
                 const float u = diag_row_sum(accu[rt][i][p]);
                 if (lane < 8) {
@@ -233,11 +240,12 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void down_small_kernel(
     using G = DiagGeom<BITS>;
     constexpr int RT = kSmallRows / 16;
     constexpr int NI = 2 * G::kLines;
-    __shared__ __align__(16) DiagSlice<BITS> win[kDiagGateUpMaxWaves][kSmallTile];
-    __shared__ float red[kDiagGateUpMaxWaves][RT][kSmallTile][16];
+    extern __shared__ __align__(16) uint8_t small_win[];
+    auto win = reinterpret_cast<DiagSlice<BITS>(*)[kSmallDownTile]>(small_win);
+    __shared__ float red[kDiagGateUpMaxWaves][RT][kSmallDownTile][16];
     __shared__ __align__(16) uint8_t mlds[2 * kSmallRows * (2 * (4096 / 64) + 16)];
     SmallTileInfo ti;
-    if (!small_tile(ta, blockIdx.y, down.n_slots, ti)) return;
+    if (!small_tile(ta, blockIdx.y, down.n_slots, kSmallDownTile, ti)) return;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nl = lane & 15, kb = lane >> 4, hh = nl >> 3, r8 = nl & 7;
     const bool shared = ti.shared;
@@ -253,10 +261,10 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void down_small_kernel(
     // The window's prepared h of each position and the sums of the lane's
     // units (a 64-value unit adds its two 32-value halves), the scales and
     // biases by whole lines, then the weights.
-    u32x4 hv[kSmallTile];
-    float2 hsum[kSmallTile][G::kLines];
+    u32x4 hv[kSmallDownTile];
+    float2 hsum[kSmallDownTile][G::kLines];
 #pragma unroll
-    for (int p = 0; p < kSmallTile; ++p) {
+    for (int p = 0; p < kSmallDownTile; ++p) {
         const int pos = ti.first + min(p, count - 1);
         hv[p] = reinterpret_cast<const u32x4 *>(hin.pairs + pos * hin.pairs_stride + wave * (kDiagWindow / 2))[lane];
 #pragma unroll
@@ -296,71 +304,94 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void down_small_kernel(
     {
         constexpr int LPU = G::kUnitPairs / 4;   // lanes per unit
 #pragma unroll
-        for (int p = 0; p < kSmallTile; ++p)
+        for (int p = 0; p < kSmallDownTile; ++p)
             *reinterpret_cast<u32x4 *>(win[wave][p].pairs + (lane / LPU) * G::kStride + 16 * (lane % LPU)) = hv[p];
         if (lane < 4 * G::kSteps) win[wave][0].zero[lane] = 0u;
     }
     if (mp.store) *reinterpret_cast<u32x4 *>(mlds + mp.dst) = mv;
     __syncthreads();
-    const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
     const int ap = nl & 1;
-    const bool feed = (nl >> 2) == kb && ap < count;
     const int ah = (nl >> 1) & 1;
     const int as = kSmallRows * mrs / 2;
-    float acc[RT][2][kSmallTile];
+    auto compute = [&](auto npc) {
+        constexpr int NPR = decltype(npc)::value;   // position pairs
+        const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
+        bool feed[NPR];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
+        for (int pr = 0; pr < NPR; ++pr) feed[pr] = (nl >> 2) == kb && 2 * pr + ap < count;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int rt = 0; rt < RT; ++rt) {
+            float acc[2][2 * NPR];
 #pragma unroll
-            for (int p = 0; p < kSmallTile; ++p) acc[rt][i][p] = 0.f;
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int line = 0; line < G::kLines; ++line) {
-        const int uA = 8 * line + 4 * ah + kb;
-        const uint8_t *abase = feed ? win[wave][ap].pairs + uA * G::kStride
-                                    : reinterpret_cast<const uint8_t *>(win[wave][0].zero);
-        mf32x4_t d[RT][2];
+                for (int p = 0; p < 2 * NPR; ++p) acc[i][p] = 0.f;
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
+            for (int line = 0; line < G::kLines; ++line) {
+                const int uA = 8 * line + 4 * ah + kb;
+                const uint8_t *abase[NPR];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) d[rt][i] = mf32x4_t{0.f, 0.f, 0.f, 0.f};
-        static_for<0, G::kSteps>([&](auto tc) {
-            constexpr int t = decltype(tc)::value;
-            const u32x4 a = reinterpret_cast<const u32x4 *>(abase)[t];
+                for (int pr = 0; pr < NPR; ++pr)
+                    abase[pr] = feed[pr] ? win[wave][2 * pr + ap].pairs + uA * G::kStride
+                                         : reinterpret_cast<const uint8_t *>(win[wave][0].zero);
+                mf32x4_t d[NPR][2];
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
+                for (int pr = 0; pr < NPR; ++pr)
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    d[rt][i] = mfma_16x16x32<BF16>(a, diag_b<BITS, BF16, t>(wd[rt][2 * line + i], magic_v), d[rt][i]);
-        });
-        const int uB = 8 * line + 4 * hh + kb;
-        const int grp = (G::kUnits * wave + uB) >> ug_log2;
+                    for (int i = 0; i < 2; ++i) d[pr][i] = mf32x4_t{0.f, 0.f, 0.f, 0.f};
+                static_for<0, G::kSteps>([&](auto tc) {
+                    constexpr int t = decltype(tc)::value;
+                    u32x4 a[NPR];
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
+                    for (int pr = 0; pr < NPR; ++pr) a[pr] = reinterpret_cast<const u32x4 *>(abase[pr])[t];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const uint16_t *m0 = reinterpret_cast<const uint16_t *>(mlds + (16 * rt + 8 * i + r8) * mrs) + grp;
-                const uint16_t s = m0[0], b = m0[as];
-                acc[rt][i][0] += diag_fix<BF16>(hh ? d[rt][i][2] : d[rt][i][0], s, b, hsum[0][line]);
-                acc[rt][i][1] += diag_fix<BF16>(hh ? d[rt][i][3] : d[rt][i][1], s, b, hsum[1][line]);
+                    for (int i = 0; i < 2; ++i) {
+                        const u32x4 b = diag_b<BITS, BF16, t>(wd[rt][2 * line + i], magic_v);
+#pragma unroll
+                        for (int pr = 0; pr < NPR; ++pr) d[pr][i] = mfma_16x16x32<BF16>(a[pr], b, d[pr][i]);
+                    }
+                });
+                const int uB = 8 * line + 4 * hh + kb;
+                const int grp = (G::kUnits * wave + uB) >> ug_log2;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint16_t *m0 =
+                        reinterpret_cast<const uint16_t *>(mlds + (16 * rt + 8 * i + r8) * mrs) + grp;
+                    const uint16_t s = m0[0], b = m0[as];
+#pragma unroll
+                    for (int pr = 0; pr < NPR; ++pr) {
+                        acc[i][2 * pr] += diag_fix<BF16>(hh ? d[pr][i][2] : d[pr][i][0], s, b, hsum[2 * pr][line]);
+                        acc[i][2 * pr + 1] +=
+                            diag_fix<BF16>(hh ? d[pr][i][3] : d[pr][i][1], s, b, hsum[2 * pr + 1][line]);
+                    }
+                }
             }
-    }
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int p = 0; p < kSmallTile; ++p) {
-                const float v = diag_row_sum(acc[rt][i][p]);
-                if (lane < 8) red[wave][rt][p][8 * i + lane] = v;
-            }
+                for (int p = 0; p < 2 * NPR; ++p) {
+                    const float v = diag_row_sum(acc[i][p]);
+                    if (lane < 8) red[wave][rt][p][8 * i + lane] = v;
+                }
+        }
+    };
+    if (count > 2)
+        compute(std::integral_constant<int, 2>{});
+    else
+        compute(std::integral_constant<int, 1>{});
     __syncthreads();
-    if (wave != 0 || lane >= kSmallRows * count) return;
-    const int p = lane / kSmallRows, q = lane % kSmallRows, rt = q >> 4, n = q & 15;
-    float v = 0.f;
-    for (int w = 0; w < waves; ++w) v += red[w][rt][p][n];
-    y[static_cast<int64_t>(ti.first + p) * N + n0 + q] = from_float<BF16>(v);
+    if (wave != 0) return;
+    for (int e = lane; e < kSmallRows * count; e += 64) {
+        const int p = e / kSmallRows, q = e % kSmallRows, rt = q >> 4, n = q & 15;
+        float v = 0.f;
+        for (int w = 0; w < waves; ++w) v += red[w][rt][p][n];
+        y[static_cast<int64_t>(ti.first + p) * N + n0 + q] = from_float<BF16>(v);
+    }
 }
+
+// The down kernel's windows in dynamic LDS at the most waves (K = 4096).
+template <int BITS>
+constexpr size_t kSmallDownMaxWinLds = kDiagGateUpMaxWaves * kSmallDownTile * sizeof(DiagSlice<BITS>);
 
 // which: 3 = gate/up of small tiles, 4 = down of small tiles.
 template <int BITS, bool BF16>
@@ -373,8 +404,14 @@ hipError_t launch_small_stage(int which, const MfmaLaunch &L, hipStream_t st) {
                            L.fp32_swiglu);
     } else {
         dim3 grid(L.down.rows / kSmallRows, L.max_tiles);
-        hipLaunchKernelGGL((down_small_kernel<BITS, BF16>), grid, dim3(64 * (L.down.cols / kDiagWindow)), 0, st,
-                           ta, L.down, L.sdown, L.hmid, L.hsum32, L.y);
+        const int waves = L.down.cols / kDiagWindow;
+        const size_t lds = waves * kSmallDownTile * sizeof(DiagSlice<BITS>);
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&down_small_kernel<BITS, BF16>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmallDownMaxWinLds<BITS>));
+        if (attr != hipSuccess) return attr;
+        hipLaunchKernelGGL((down_small_kernel<BITS, BF16>), grid, dim3(64 * waves), lds, st, ta, L.down, L.sdown,
+                           L.hmid, L.hsum32, L.y);
     }
     return hipGetLastError();
 }

@@ -461,7 +461,8 @@ __device__ __forceinline__ void wide_gateup_tile(const TileArgs &ta, const QProj
     // Prepared h for the down projection: rows [n0, n0 + 128) are whole words
     // and two whole 64-blocks of every position's h; the sums of a block's
     // words meet by butterfly over consecutive lanes.
-    const int vpw_d = 32 / down_bits, wpw = kWideRows / vpw_d, wpb = 64 / vpw_d;
+    const int vpw_d = 32 / down_bits, wpw = kWideRows / vpw_d, wpb = 64 / vpw_d, w32 = 32 / vpw_d;
+    const int n32 = pg.rows / 32;
     for (int u0 = 0; u0 < 16 * NACT * wpw; u0 += kWideThreads) {
         const int uu = u0 + static_cast<int>(threadIdx.x), q = uu / wpw, wd = uu % wpw;
         float2 part = make_float2(0.f, 0.f);
@@ -474,6 +475,10 @@ __device__ __forceinline__ void wide_gateup_tile(const TileArgs &ta, const QProj
         for (int m = 1; m < wpb; m <<= 1) {
             part.x += __shfl_xor(part.x, m, 64);
             part.y += __shfl_xor(part.y, m, 64);
+            // the 32-value sums once the butterfly has met them (the small
+            // down kernel's operands)
+            if (2 * m == w32 && hout.sum32 && mine && wd % w32 == 0)
+                hout.sum32[(first + q) * n32 + (n0 + wd * vpw_d) / 32] = part;
         }
         if (mine && wd % wpb == 0) hout.fix[(first + q) * hout.fix_stride + n0 / 64 + wd / wpb] = make_fix<BF16>(part);
     }
@@ -556,6 +561,7 @@ hipError_t launch_wide_stage(int which, const MfmaLaunch &L, hipStream_t st) {
                            st, ta, L.gate, L.up, L.sgate, L.sup, L.xin, L.hmid, L.down.bits, L.limit, L.fp32_swiglu);
     } else {
         ta.n_vec = L.routes;
+        ta.min_count = L.min_count_down;
         static const hipError_t attr = hipFuncSetAttribute(
             reinterpret_cast<const void *>(&wide_down_kernel<BITS, BF16>),
             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kWideMaxLds));

@@ -2,7 +2,7 @@
 + 1 shared expert, d_ff 2048, group 64, bf16 scales/biases.
 
   * 64- and 512-token prefill with Zipf(1.1) expert popularity (the grouped
-    path: matrix-core 64-position tiles and one/two-position small tiles at
+    path: matrix-core 64-position tiles and one- to four-position small tiles at
     K 4096 / 2048, the whole-K metadata staging and the tile list at these
     counts), 2-bit gate/up/down;
   * 32-token batched decode with 2-bit gate/up and 4-bit down projections;
@@ -33,7 +33,7 @@ from oracle import moe
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 D, E, DFF, K, GROUP = 4096, 256, 2048, 6, 64
-TILE = 64            # positions per matrix-core tile (a tile of 1-2 takes the small-tile kernels)
+TILE = 64            # positions per matrix-core tile (a tile of 1-4 takes the small-tile kernels)
 
 
 def _layer(seed, bits_down=2, dtype=torch.bfloat16, group=GROUP):
@@ -85,11 +85,13 @@ def _oracle_check(oracle_lib, arena, shared, x, slots, wts, out, tokens, what, c
         assert exact_fraction(np.concatenate(same), True) > exact
 
 
-def _tile_sample(idx, T, heavy=6, mid=8, small=8, seed=0):
+def _tile_sample(idx, T, heavy=6, mid=8, small=8, quad=4, seed=0):
     """Tokens covering every tile kind: the first and last position of every
     64-position tile of the `heavy` most-routed experts and of the shared
     expert (a segment of all T tokens), first/last of `mid` experts with
-    3..64 positions, and `small` tokens of one- or two-position tiles."""
+    5..64 positions, `small` tokens of one- or two-position tiles, and every
+    token of `quad` three- or four-position tiles (the small-tile kernels'
+    two-pass tiles)."""
     rng = np.random.default_rng(seed)
     seg: dict = {}
     for t in range(T):
@@ -106,12 +108,16 @@ def _tile_sample(idx, T, heavy=6, mid=8, small=8, seed=0):
     by_count = sorted(seg, key=lambda e: -len(seg[e]))
     for e in by_count[:heavy]:
         ends(seg[e])
-    mids = [e for e in by_count if 3 <= len(seg[e]) <= TILE]
+    mids = [e for e in by_count if 5 <= len(seg[e]) <= TILE]
     for e in rng.permutation(mids)[:mid]:
         ends(seg[int(e)])
     tails = [e for e in seg if len(seg[e]) % TILE in (1, 2)]
     for e in rng.permutation(tails)[:small]:
         pick.add(seg[int(e)][-1])
+    quads = [e for e in seg if len(seg[e]) % TILE in (3, 4)]
+    for e in rng.permutation(quads)[:quad]:
+        members = seg[int(e)]
+        pick.update(members[len(members) - len(members) % TILE:])
     return sorted(pick), seg
 
 

@@ -18,9 +18,10 @@ expert popularity.
     (fp64) product of the kernel's own h; gate/up + SwiGLU within the
     propagated bound of the same kind from x. The checked routes are the
     first and last position of every 64-position tile of the heaviest experts
-    and of the shared expert, tiles of 3..64 positions, and one- and
-    two-position tiles (the small-tile kernels): every tile kind and tile
-    boundary of the call.
+    and of the shared expert, tiles of 5..64 positions, one- and two-position
+    tiles and every position of three- and four-position tiles (the
+    small-tile kernels, whose second pair of positions takes a second pass):
+    every tile kind and tile boundary of the call.
 """
 
 from __future__ import annotations
@@ -64,10 +65,12 @@ def _segments(route_expert):
     return seg
 
 
-def _tile_routes(seg, heavy=3, mid=3, small=3, seed=0):
+def _tile_routes(seg, heavy=3, mid=3, small=3, quad=3, seed=0):
     """First and last route of every 64-position tile of the `heavy` most
-    used experts, of `mid` experts with 3..64 routes, and the last route of
-    `small` experts whose last tile has one or two positions."""
+    used experts, of `mid` experts with 5..64 routes, the last route of
+    `small` experts whose last tile has one or two positions, and every
+    route of the last tile of `quad` experts whose last tile has three or
+    four positions."""
     rng = np.random.default_rng(seed)
     pick = set()
 
@@ -79,12 +82,16 @@ def _tile_routes(seg, heavy=3, mid=3, small=3, seed=0):
     by_count = sorted(seg, key=lambda e: -len(seg[e]))
     for e in by_count[:heavy]:
         ends(seg[e])
-    mids = [e for e in by_count if 3 <= len(seg[e]) <= TILE]
+    mids = [e for e in by_count if 5 <= len(seg[e]) <= TILE]
     for e in rng.permutation(mids)[:mid]:
         ends(seg[int(e)])
     tails = [e for e in seg if len(seg[e]) % TILE in (1, 2)]
     for e in rng.permutation(tails)[:small]:
         pick.add(seg[int(e)][-1])
+    quads = [e for e in seg if len(seg[e]) % TILE in (3, 4)]
+    for e in rng.permutation(quads)[:quad]:
+        members = seg[int(e)]
+        pick.update(members[len(members) - len(members) % TILE:])
     return sorted(pick)
 
 
@@ -152,7 +159,8 @@ def test_grouped_pure_expert_outputs(oracle_lib, T, dtype, group):
     torch.cuda.synchronize()
     seg = _segments(experts)
     counts = sorted((len(v) for v in seg.values()), reverse=True)
-    assert counts[0] >= 3 and any(c <= 2 for c in counts)   # wide tiles and small tiles
+    # wide tiles, small tiles and two-pass small tiles
+    assert counts[0] >= 5 and any(c <= 2 for c in counts) and any(c in (3, 4) for c in counts)
     if T <= 64:
         tokens = list(range(T))
     else:
@@ -217,7 +225,8 @@ def test_grouped_stagewise_ulp(T, dtype, group):
     shared_tiles = sorted({R + t for a in range(0, T, TILE) for t in (a, min(a + TILE, T) - 1)})
     routes += shared_tiles
     assert any(len(seg[int(route_expert[r])]) <= 2 for r in routes if r < R), "a small tile is checked"
-    assert any(len(seg[int(route_expert[r])]) >= 3 for r in routes if r < R), "a 64-position tile is checked"
+    assert any(len(seg[int(route_expert[r])]) in (3, 4) for r in routes if r < R), "a two-pass small tile is checked"
+    assert any(len(seg[int(route_expert[r])]) >= 5 for r in routes if r < R), "a 64-position tile is checked"
     if T > TILE:
         assert any(len(seg[int(route_expert[r])]) > TILE for r in routes if r < R), "a tile boundary is checked"
     xs, hs, ys = values(x), values(h), values(y)
