@@ -314,8 +314,12 @@ bool mfma_eligible(const locali_expert_arena *routed, const locali_expert_arena 
 
 // Small-tile kernels (mfma_small.hpp): groups of 64 or 128, K of both
 // stages a multiple of 512 and at most 4096, rows multiples of 32.
-// positions of the small-tile kernels' tiles: gate/up, down
-constexpr int kSmallGateUpTileHost = 2, kSmallDownTileHost = 4;
+// Positions of the small-tile kernels' tiles: gate/up 2; down 2, or 4 in
+// calls of at least kSmallDown4Tokens tokens, where tiles of three and four
+// positions are common under skewed routing (the four-position down kernel is
+// faster than the 64-position one on those tiles and slower than the
+// two-position one on the rest).
+constexpr int kSmallGateUpTileHost = 2, kSmallDown4Tokens = 256;
 bool small_tiles_eligible(const locali_expert_arena *routed) {
     auto ok = [](const locali_qproj &p) {
         return (p.bits == 2 || p.bits == 4) && (p.group_size == 64 || p.group_size == 128) &&
@@ -339,9 +343,9 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     const int max_tiles = grouped_max_tiles(tokens, top_k, shared ? 1 : 0, n_experts, kWideTokens);
     if (max_tiles > lay.max_tiles || max_tiles > lay.wide_tiles)
         return fail(LOCALI_E_WORKSPACE, "grouped: tile list too small");
-    // Tiles of one or two positions (gate/up) and of one to four (down) go
-    // to the small-tile kernels when the shapes allow; the 64-position
-    // kernels skip them. The dispatch packs the tokens of a tile of one or
+    // Tiles of one or two positions (gate/up; down: up to four in calls of
+    // many tokens) go to the small-tile kernels when the shapes allow; the
+    // 64-position kernels skip them. The dispatch packs the tokens of a tile of one or
     // two positions into its record, and writes every routed tile's tokens by
     // position for the 64-position kernels.
     const bool small = small_tiles_eligible(routed);
@@ -370,9 +374,11 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     L.hmid = mfma_batch(at<void>(ws, lay.mh), routes, routed->down.cols);
     L.hmid.plain = h_plain;
     L.hsum32 = at<float2>(ws, lay.gh);   // the VALU path's h buffer is free here
-    // the small down kernel also takes tiles whose h the 64-position gate/up
-    // kernel writes (three or four positions): that kernel writes their sums
-    if (small) L.hmid.sum32 = L.hsum32;
+    L.small_down_positions = tokens >= kSmallDown4Tokens ? 4 : 2;
+    // the four-position small down kernel also takes tiles whose h the
+    // 64-position gate/up kernel writes (three or four positions): that
+    // kernel writes their sums
+    if (small && L.small_down_positions > 2) L.hmid.sum32 = L.hsum32;
     L.y = gy;
     L.limit = limit;
     L.fp32_swiglu = fp32_swiglu;
@@ -381,7 +387,7 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     L.routes = routes;
     const bool bf16 = x_dtype == LOCALI_DT_BF16;
     L.ta.min_count = small ? kSmallGateUpTileHost + 1 : 0;
-    L.min_count_down = small ? kSmallDownTileHost + 1 : 0;
+    L.min_count_down = small ? L.small_down_positions + 1 : 0;
     const int order[5] = {0, 1, 3, 2, 4};
     for (int which : order) {
         if (which >= 3 && !small) continue;

@@ -177,7 +177,8 @@ struct MfmaLaunch {
     int32_t fp32_swiglu;
     int32_t max_tiles;
     int32_t tokens, routes;
-    int32_t min_count_down;       // the down stage's ta.min_count (its small tiles take more positions)
+    int32_t min_count_down;       // the down stage's ta.min_count (its small tiles may take more positions)
+    int32_t small_down_positions; // positions of the down stage's small tiles: 2 or 4 (mfma_small.hpp)
 };
 
 // Prepared pairs and per-64 sums of the tokens' x for the gate/up stage.

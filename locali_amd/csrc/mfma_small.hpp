@@ -7,19 +7,22 @@
 // 128-byte lines, and the A operand is "diagonal". Its spare row bit carries
 // the second position: A row m = 4 kb + 2 h + p holds position p's x' for
 // k-lane kb's unit 4 h + kb, so D[4 kb + 2 h + p][n] is position p's dot with
-// lane (n, kb)'s unit -- two positions for the MFMA work of one. The down
-// kernel also takes tiles of three or four positions, feeding both pairs'
-// MFMAs from each expanded weight register (measured: 3.2 against the
-// 64-position down kernel's 2.2 TB/s on such tiles; the gate/up kernel was
-// slower than its 64-position kernel there). Under Zipf routing most experts
-// of a prefill get one to four tokens; the tiles of the larger ones go to
-// mfma_wide.hpp.
+// lane (n, kb)'s unit -- two positions for the MFMA work of one. For calls of
+// many tokens the down stage takes tiles of up to four positions instead
+// (down_small4_kernel: both pairs' MFMAs on each expanded weight register;
+// measured 3.2 against the 64-position down kernel's 2.2 TB/s on such tiles,
+// but slower than down_small_kernel on one- and two-position tiles, which
+// dominate calls of few tokens; the gate/up kernel for three or four
+// positions was slower than its 64-position kernel there). Under Zipf routing
+// most experts of a prefill get one to four tokens; the tiles of the larger
+// ones go to mfma_wide.hpp.
 //
 //   gateup_small_kernel  h[pos] = swiglu(up(x_t), gate(x_t)) for the tile's
 //                        positions; x is prepared per wave in LDS; the epilogue
 //                        writes h's prepared pairs (the MFMA layout) and sums
 //                        per 32 values (the workgroup owns 32 rows).
 //   down_small_kernel    y[pos] = round(down(h[pos])) for 32 output rows.
+//   down_small4_kernel   the same for tiles of up to four positions.
 // Reference arithmetic: dsv4_arena.py:168-235 (expert).
 #pragma once
 
@@ -240,6 +243,143 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void down_small_kernel(
     using G = DiagGeom<BITS>;
     constexpr int RT = kSmallRows / 16;
     constexpr int NI = 2 * G::kLines;
+    __shared__ __align__(16) DiagSlice<BITS> win[kDiagGateUpMaxWaves][kSmallGateUpTile];
+    __shared__ float red[kDiagGateUpMaxWaves][RT][kSmallGateUpTile][16];
+    __shared__ __align__(16) uint8_t mlds[2 * kSmallRows * (2 * (4096 / 64) + 16)];
+    SmallTileInfo ti;
+    if (!small_tile(ta, blockIdx.y, down.n_slots, kSmallGateUpTile, ti)) return;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nl = lane & 15, kb = lane >> 4, hh = nl >> 3, r8 = nl & 7;
+    const bool shared = ti.shared;
+    const int sl = shared ? 0 : ti.slot, count = ti.count;
+    const int N = down.rows, K = down.cols;
+    const uint32_t *wp = shared ? sdown.w : down.w;
+    const int64_t w_slot = shared ? sdown.w_slot : down.w_slot, m_slot = shared ? sdown.m_slot : down.m_slot;
+    const int n0 = blockIdx.x * kSmallRows;
+    const int wpr = K * BITS / 32, gpr = K / down.group;
+    const int waves = blockDim.x >> 6;   // = K / 512
+    const int ug_log2 = units_per_group_log2<BITS>(down.group);
+
+    // The window's prepared h of each position and the sums of the lane's
+    // units (a 64-value unit adds its two 32-value halves), the scales and
+    // biases by whole lines, then the weights.
+    u32x4 hv[kSmallGateUpTile];
+    float2 hsum[kSmallGateUpTile][G::kLines];
+#pragma unroll
+    for (int p = 0; p < kSmallGateUpTile; ++p) {
+        const int pos = ti.first + min(p, count - 1);
+        hv[p] = reinterpret_cast<const u32x4 *>(hin.pairs + pos * hin.pairs_stride + wave * (kDiagWindow / 2))[lane];
+#pragma unroll
+        for (int line = 0; line < G::kLines; ++line) {
+            const int u = G::kUnits * wave + 8 * line + 4 * hh + kb;   // unit of K
+            const float2 *hp = hsum32 + static_cast<int64_t>(pos) * (K / 32) + u * (G::kUnitVals / 32);
+            if constexpr (G::kUnitVals == 64) {
+                const float4 s2 = reinterpret_cast<const float4 *>(hp)[0];
+                hsum[p][line] = make_float2(s2.x + s2.z, s2.y + s2.w);
+            } else {
+                hsum[p][line] = hp[0];
+            }
+        }
+    }
+    sched_fence();
+    const int mrs = 2 * gpr + 16;
+    const int64_t mrow0 = static_cast<int64_t>(n0) * gpr;
+    const uint16_t *m_s = (shared ? sdown.s : down.s) + sl * m_slot + mrow0;
+    const uint16_t *m_b = (shared ? sdown.b : down.b) + sl * m_slot + mrow0;
+    // 2 arrays x 32 rows x gpr / 8 pieces: at most one per thread
+    const MetaPiece mp = meta_piece_of(static_cast<int>(threadIdx.x), 2, kSmallRows, gpr, mrs);
+    const u32x4 mv = *reinterpret_cast<const u32x4 *>((mp.arr == 0 ? m_s : m_b) + mp.off);
+    sched_fence();
+    const __amdgpu_buffer_rsrc_t w_rs =
+        make_rsrc(wp + sl * w_slot + static_cast<int64_t>(n0) * wpr, 4u * kSmallRows * wpr);
+    u32x4 wd[RT][NI];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int q = 0; q < NI; ++q) {
+            const int i = q & 1, line = q >> 1;
+            const uint32_t wo = 4u * static_cast<uint32_t>((16 * rt + 8 * i + r8) * wpr) + 128u * line +
+                                16u * (4 * hh + kb);
+            wd[rt][q] = __builtin_amdgcn_raw_buffer_load_b128(w_rs, wo, 128 * G::kLines * wave, kAuxStream);
+        }
+    sched_fence();
+    {
+        constexpr int LPU = G::kUnitPairs / 4;   // lanes per unit
+#pragma unroll
+        for (int p = 0; p < kSmallGateUpTile; ++p)
+            *reinterpret_cast<u32x4 *>(win[wave][p].pairs + (lane / LPU) * G::kStride + 16 * (lane % LPU)) = hv[p];
+        if (lane < 4 * G::kSteps) win[wave][0].zero[lane] = 0u;
+    }
+    if (mp.store) *reinterpret_cast<u32x4 *>(mlds + mp.dst) = mv;
+    __syncthreads();
+    const uint32_t magic_v = opaque_vgpr(Pairs<BITS, BF16>::kMagic);
+    const int ap = nl & 1;
+    const bool feed = (nl >> 2) == kb && ap < count;
+    const int ah = (nl >> 1) & 1;
+    const int as = kSmallRows * mrs / 2;
+    float acc[RT][2][kSmallGateUpTile];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int p = 0; p < kSmallGateUpTile; ++p) acc[rt][i][p] = 0.f;
+#pragma unroll
+    for (int line = 0; line < G::kLines; ++line) {
+        const int uA = 8 * line + 4 * ah + kb;
+        const uint8_t *abase = feed ? win[wave][ap].pairs + uA * G::kStride
+                                    : reinterpret_cast<const uint8_t *>(win[wave][0].zero);
+        mf32x4_t d[RT][2];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) d[rt][i] = mf32x4_t{0.f, 0.f, 0.f, 0.f};
+        static_for<0, G::kSteps>([&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            const u32x4 a = reinterpret_cast<const u32x4 *>(abase)[t];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    d[rt][i] = mfma_16x16x32<BF16>(a, diag_b<BITS, BF16, t>(wd[rt][2 * line + i], magic_v), d[rt][i]);
+        });
+        const int uB = 8 * line + 4 * hh + kb;
+        const int grp = (G::kUnits * wave + uB) >> ug_log2;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint16_t *m0 = reinterpret_cast<const uint16_t *>(mlds + (16 * rt + 8 * i + r8) * mrs) + grp;
+                const uint16_t s = m0[0], b = m0[as];
+                acc[rt][i][0] += diag_fix<BF16>(hh ? d[rt][i][2] : d[rt][i][0], s, b, hsum[0][line]);
+                acc[rt][i][1] += diag_fix<BF16>(hh ? d[rt][i][3] : d[rt][i][1], s, b, hsum[1][line]);
+            }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int p = 0; p < kSmallGateUpTile; ++p) {
+                const float v = diag_row_sum(acc[rt][i][p]);
+                if (lane < 8) red[wave][rt][p][8 * i + lane] = v;
+            }
+    __syncthreads();
+    if (wave != 0 || lane >= kSmallRows * count) return;
+    const int p = lane / kSmallRows, q = lane % kSmallRows, rt = q >> 4, n = q & 15;
+    float v = 0.f;
+    for (int w = 0; w < waves; ++w) v += red[w][rt][p][n];
+    y[static_cast<int64_t>(ti.first + p) * N + n0 + q] = from_float<BF16>(v);
+}
+
+
+template <int BITS, bool BF16>
+__global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void down_small4_kernel(
+    TileArgs ta, QProj down, QProj sdown, MfmaVec hin, const float2 *__restrict__ hsum32,
+    uint16_t *__restrict__ y) {
+    using G = DiagGeom<BITS>;
+    constexpr int RT = kSmallRows / 16;
+    constexpr int NI = 2 * G::kLines;
     extern __shared__ __align__(16) uint8_t small_win[];
     auto win = reinterpret_cast<DiagSlice<BITS>(*)[kSmallDownTile]>(small_win);
     __shared__ float red[kDiagGateUpMaxWaves][RT][kSmallDownTile][16];
@@ -389,11 +529,13 @@ __global__ __launch_bounds__(64 * kDiagGateUpMaxWaves) void down_small_kernel(
     }
 }
 
-// The down kernel's windows in dynamic LDS at the most waves (K = 4096).
+// The four-position down kernel's windows in dynamic LDS at the most waves
+// (K = 4096).
 template <int BITS>
 constexpr size_t kSmallDownMaxWinLds = kDiagGateUpMaxWaves * kSmallDownTile * sizeof(DiagSlice<BITS>);
 
-// which: 3 = gate/up of small tiles, 4 = down of small tiles.
+// which: 3 = gate/up of small tiles, 4 = down of small tiles (of up to
+// L.small_down_positions positions: 2 or kSmallDownTile).
 template <int BITS, bool BF16>
 hipError_t launch_small_stage(int which, const MfmaLaunch &L, hipStream_t st) {
     TileArgs ta = L.ta;
@@ -402,16 +544,20 @@ hipError_t launch_small_stage(int which, const MfmaLaunch &L, hipStream_t st) {
         hipLaunchKernelGGL((gateup_small_kernel<BITS, BF16>), grid, dim3(64 * (L.gate.cols / kDiagWindow)), 0, st,
                            ta, L.gate, L.up, L.sgate, L.sup, L.hmid, L.hsum32, L.down.bits, L.limit,
                            L.fp32_swiglu);
-    } else {
+    } else if (L.small_down_positions == kSmallDownTile) {
         dim3 grid(L.down.rows / kSmallRows, L.max_tiles);
         const int waves = L.down.cols / kDiagWindow;
         const size_t lds = waves * kSmallDownTile * sizeof(DiagSlice<BITS>);
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&down_small_kernel<BITS, BF16>),
+            reinterpret_cast<const void *>(&down_small4_kernel<BITS, BF16>),
             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmallDownMaxWinLds<BITS>));
         if (attr != hipSuccess) return attr;
-        hipLaunchKernelGGL((down_small_kernel<BITS, BF16>), grid, dim3(64 * waves), lds, st, ta, L.down, L.sdown,
+        hipLaunchKernelGGL((down_small4_kernel<BITS, BF16>), grid, dim3(64 * waves), lds, st, ta, L.down, L.sdown,
                            L.hmid, L.hsum32, L.y);
+    } else {
+        dim3 grid(L.down.rows / kSmallRows, L.max_tiles);
+        hipLaunchKernelGGL((down_small_kernel<BITS, BF16>), grid, dim3(64 * (L.down.cols / kDiagWindow)), 0, st,
+                           ta, L.down, L.sdown, L.hmid, L.hsum32, L.y);
     }
     return hipGetLastError();
 }

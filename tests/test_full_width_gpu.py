@@ -140,8 +140,30 @@ def test_prefill_full_width_zipf(oracle_lib, T, dtype, group):
         tokens, seg = _tile_sample(ih, T, seed=T)
         counts = sorted((len(v) for v in seg.values()), reverse=True)
         assert counts[0] > 2 * TILE and any(c % TILE in (1, 2) for c in counts)
+        assert any(c % TILE in (3, 4) for c in counts)   # the four-position small down tiles
     _oracle_check(oracle_lib, arena, shared, x, (ih + 1).astype(np.int32), wts.cpu().numpy(), out,
                   tokens, f"C3 T={T} {dtype}", dtype=dtype)
+
+
+def test_mixed_2_4_bit_prefill_full_width(oracle_lib):
+    """256 tokens, Zipf(1.1) routing, gate/up 2-bit and down 4-bit: the call
+    size from which the down stage's small tiles take up to four positions
+    (the 4-bit four-position kernel), checked on every tile kind."""
+    banner("full-width mixed 2/4-bit T=256 zipf 1.1")
+    T = 256
+    arena, shared = _layer(seed=420, bits_down=4)
+    x, w = synth.zipf_router_inputs(T, E, D, 1.1, torch.bfloat16, seed=421, device=DEV)
+    spec = ops.RouterSpec(w, K, routed_scale=1.5)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    out, idx, wts = ops.forward(spec, arena, shared, slot_of, x, ops.Workspace())
+    torch.cuda.synchronize()
+    _check_routes(x, w, idx, wts)
+    ih = idx.cpu().numpy()
+    tokens, seg = _tile_sample(ih, T, seed=T)
+    counts = [len(v) for v in seg.values()]
+    assert any(c in (3, 4) for c in counts) and any(c <= 2 for c in counts) and max(counts) > TILE
+    _oracle_check(oracle_lib, arena, shared, x, (ih + 1).astype(np.int32), wts.cpu().numpy(), out,
+                  tokens, "mixed 2/4-bit T=256")
 
 
 def test_mixed_2_4_bit_batched_decode_full_width(oracle_lib):
