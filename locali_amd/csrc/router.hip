@@ -18,8 +18,8 @@
 //                        v_mfma_f32_32x32x16, K split kRouterSplits ways into
 //                        partial sums that the selection adds in fixed order
 //                        (enough workgroups to stream the 2 MiB gate at 64
-//                        tokens); each stage's loads overlap the previous
-//                        stage's MFMAs.
+//                        tokens); each lane loads its operands directly, the
+//                        next chunk's loads overlapping the current MFMAs.
 //   router_select_kernel one wave per token: scores, top-k (DPP arg-max over
 //                        (value, ~expert) keys), weights, slots.
 #include "router_select.hpp"
@@ -143,52 +143,47 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(u32x4 a, u32x4 b, f32x16_t c) {
 
 template <bool BF16>
 __global__ __launch_bounds__(256) void router_mfma_kernel(RouterLaunch L) {
-    constexpr int KT = 64;                       // K per LDS stage
-    constexpr int PAD = 8;                       // 16-bit elements of row padding
-    __shared__ uint16_t xs[64][KT + PAD];
-    __shared__ uint16_t ws[64][KT + PAD];
+    // Each lane loads its own operands in the MFMA layout (A: token row
+    // lane % 32, B: expert row lane % 32, 8 values at k + 8 (lane / 32)),
+    // four MFMAs' worth a chunk, the next chunk's loads issued before the
+    // current chunk's MFMAs; no LDS staging and no barrier, so a workgroup
+    // waits for about one memory round trip. The loads are unconditional
+    // (the last chunk's successor re-reads the last chunk).
+    constexpr int CH = 4;                        // MFMAs per chunk
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
     const int split = blockIdx.z;
     const int kspan = L.d / kRouterSplits;
-    const int kbeg = split * kspan, kend = kbeg + kspan;
-    const uint16_t *gw = static_cast<const uint16_t *>(L.gate_w);
+    const int nmf = kspan / 16;                  // MFMAs of the split, a multiple of CH
     const int wt = (wave & 1) * 32, we = (wave >> 1) * 32;   // wave sub-tile
-    f32x16_t acc = {};
-    // Stage k0 + KT is loaded into registers while stage k0 is multiplied:
-    // a thread moves pieces c = threadIdx.x + 256 i (i < kPer) of x and of W.
-    constexpr int kPer = 64 * KT / 8 / 256;
-    uint4 xv[kPer], wv[kPer];
-    auto load_stage = [&](int k0) {
+    // rows past the tokens / experts repeat the last one; their results are
+    // not stored
+    const int tr = min(t0 + wt + (lane & 31), L.tokens - 1), er = min(e0 + we + (lane & 31), L.E - 1);
+    const int koff = split * kspan + (lane >> 5) * 8;
+    const uint16_t *xr = L.x + static_cast<int64_t>(tr) * L.d + koff;
+    const uint16_t *wr = static_cast<const uint16_t *>(L.gate_w) + static_cast<int64_t>(er) * L.d + koff;
+    u32x4 a0[CH], b0[CH], a1[CH], b1[CH];
+    auto load = [&](u32x4(&a)[CH], u32x4(&b)[CH], int m0) {
+        const int m = min(m0, nmf - CH);
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int c = threadIdx.x + 256 * i, row = c / (KT / 8), col = (c % (KT / 8)) * 8;
-            const int tr = min(t0 + row, L.tokens - 1), er = min(e0 + row, L.E - 1);
-            xv[i] = *reinterpret_cast<const uint4 *>(L.x + static_cast<int64_t>(tr) * L.d + k0 + col);
-            wv[i] = *reinterpret_cast<const uint4 *>(gw + static_cast<int64_t>(er) * L.d + k0 + col);
+        for (int q = 0; q < CH; ++q) {
+            a[q] = *reinterpret_cast<const u32x4 *>(xr + 16 * (m + q));
+            b[q] = *reinterpret_cast<const u32x4 *>(wr + 16 * (m + q));
         }
     };
-    load_stage(kbeg);
-    for (int k0 = kbeg; k0 < kend; k0 += KT) {
-        // rows past the tokens / experts repeat the last one; their results
-        // are not stored
+    f32x16_t acc = {};
+    auto run = [&](const u32x4(&a)[CH], const u32x4(&b)[CH]) {
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int c = threadIdx.x + 256 * i, row = c / (KT / 8), col = (c % (KT / 8)) * 8;
-            *reinterpret_cast<uint4 *>(&xs[row][col]) = xv[i];
-            *reinterpret_cast<uint4 *>(&ws[row][col]) = wv[i];
-        }
-        __syncthreads();
-        load_stage(min(k0 + KT, kend - KT));
-#pragma unroll
-        for (int kk = 0; kk < KT; kk += 16) {
-            const int kofs = kk + (lane >> 5) * 8;
-            const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[wt + (lane & 31)][kofs]);
-            const u32x4 b = *reinterpret_cast<const u32x4 *>(&ws[we + (lane & 31)][kofs]);
-            acc = mfma32x32x16<BF16>(a, b, acc);
-        }
-        __syncthreads();
+        for (int q = 0; q < CH; ++q) acc = mfma32x32x16<BF16>(a[q], b[q], acc);
+    };
+    load(a0, b0, 0);
+    for (int m = 0; m < nmf; m += 2 * CH) {
+        load(a1, b1, m + CH);
+        run(a0, b0);
+        if (m + CH >= nmf) break;
+        load(a0, b0, m + 2 * CH);
+        run(a1, b1);
     }
     // D layout (32x32): lane holds column n = lane % 32 (expert) and rows
     // 8*(i/4) + 4*(lane/32) + (i%4) (tokens) for i < 16.
