@@ -350,12 +350,14 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     // position for the 64-position kernels.
     const bool small = small_tiles_eligible(routed);
     int32_t *tile_tok = at<int32_t>(ws, lay.tile_tok);
-    hipError_t e = launch_dispatch(route_slot, R, n_slots, shared ? tokens : 0, kWideTokens,
-                                   at<int32_t>(ws, lay.seg_start), at<int32_t>(ws, lay.sorted_route),
-                                   route_pos, tiles, n_tiles, max_tiles, st, at<int32_t>(ws, lay.seg_tile), top_k,
-                                   small, tile_tok);
-    if (e != hipSuccess) return hip_fail(e, "dispatch launch");
+    // the dispatch's count step; its placement step runs in one launch with
+    // the preparation of x (launch_mfma stage 5)
     MfmaLaunch L{};
+    hipError_t e = launch_dispatch_count(route_slot, R, n_slots, shared ? tokens : 0, kWideTokens,
+                                         at<int32_t>(ws, lay.seg_start), at<int32_t>(ws, lay.sorted_route),
+                                         route_pos, tiles, n_tiles, max_tiles, st, at<int32_t>(ws, lay.seg_tile),
+                                         top_k, small, tile_tok, &L.place);
+    if (e != hipSuccess) return hip_fail(e, "dispatch launch");
     L.ta.x = static_cast<const uint16_t *>(x);
     L.ta.tiles = tiles;
     L.ta.n_tiles = n_tiles;
@@ -388,7 +390,9 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     const bool bf16 = x_dtype == LOCALI_DT_BF16;
     L.ta.min_count = small ? kSmallGateUpTileHost + 1 : 0;
     L.min_count_down = small ? L.small_down_positions + 1 : 0;
-    const int order[5] = {0, 1, 3, 2, 4};
+    // 5: placement + preparation of x; 1, 3: gate/up (64-position, small
+    // tiles); 2, 4: down
+    const int order[5] = {5, 1, 3, 2, 4};
     for (int which : order) {
         if (which >= 3 && !small) continue;
         if ((e = launch_mfma(which, bf16, L, st)) != hipSuccess) return hip_fail(e, "grouped MFMA launch");

@@ -11,7 +11,9 @@
 //                           holding every token, whose tiles come first in the
 //                           list (the longest tiles start with the launch);
 //                           routes outside the arena get route_pos -1
-//   dispatch_place_kernel   one wave per slot: walks the routes 512 at a time
+//   dispatch_place_kernel   (dispatch_place_block; the matrix-core path runs it
+//                           in one launch with the preparation of x)
+//                           one wave per slot: walks the routes 512 at a time
 //                           with ballots and writes sorted_route / route_pos
 //                           in route order (stable), and on request each
 //                           routed tile's tokens by position (tile_tok), so
@@ -110,51 +112,8 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_count_kernel(
     }
 }
 
-__global__ __launch_bounds__(256) void dispatch_place_kernel(
-    const int32_t *__restrict__ route_slot, int R, int n_slots, const int32_t *__restrict__ seg_start,
-    int32_t *__restrict__ sorted_route, int32_t *__restrict__ route_pos, const int32_t *__restrict__ seg_tile,
-    int32_t *__restrict__ tiles, int max_tiles, int top_k, int small_pack, int32_t *__restrict__ tile_tok,
-    int tile_tokens) {
-    const int lane = threadIdx.x & 63;
-    const int s = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (s >= n_slots) return;
-    const int base = seg_start[s], end = seg_start[s + 1];
-    if (base == end) return;
-    const int tile0 = seg_tile ? seg_tile[s] : -1;   // the segment's first tile
-    // a slot of at most kPackedTokens routes: its tile's tokens, 15 bits each
-    // in position order, go into the tile record (see the count kernel)
-    int32_t *packed = nullptr;
-    if (small_pack && end - base <= kPackedTokens && tile0 >= 0 && tile0 < max_tiles) packed = &tiles[4 * tile0 + 3];
-    if (tile0 < 0) tile_tok = nullptr;
-    // 8 x 64 routes per pass: the loads of a pass are in flight together,
-    // then the ballots place them in route order
-    constexpr int U = 8;
-    int pos = base;
-    for (int r0 = 0; r0 < R && pos < end; r0 += 64 * U) {
-        int v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int r = r0 + 64 * u + lane;
-            v[u] = r < R ? route_slot[r] : -1;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int r = r0 + 64 * u + lane;
-            const bool mine = v[u] == s;
-            const uint64_t m = __ballot(mine);
-            if (mine) {
-                const int p = pos + __popcll(m & ((1ull << lane) - 1ull));
-                sorted_route[p] = r;
-                if (route_pos) route_pos[r] = p;
-                if (packed) atomicOr(packed, (r / top_k) << (kTokenBits * (p - base)));
-                if (tile_tok) {
-                    const int q = p - base, tile = tile0 + q / tile_tokens;
-                    if (tile < max_tiles) tile_tok[static_cast<int64_t>(tile) * tile_tokens + q % tile_tokens] = r / top_k;
-                }
-            }
-            pos += __popcll(m);
-        }
-    }
+__global__ __launch_bounds__(256) void dispatch_place_kernel(PlaceArgs a) {
+    dispatch_place_block(a, static_cast<int>(blockIdx.x));
 }
 
 // expert id -> slot, fused with the route list.
@@ -297,8 +256,9 @@ hipError_t mfma_b2(int which, bool bf16, const MfmaLaunch &L, hipStream_t st);
 hipError_t mfma_b4(int which, bool bf16, const MfmaLaunch &L, hipStream_t st);
 
 // which: 0 = prepare x, 1 = gate/up + SwiGLU (+ prepared h), 2 = down,
-// 3 / 4 = gate/up / down of the small tiles. Gate and up share the prepared
-// x, so they must share a bit width.
+// 3 / 4 = gate/up / down of the small tiles, 5 = the dispatch's placement
+// step (L.place) and the preparation of x in one launch. Gate and up share
+// the prepared x, so they must share a bit width.
 hipError_t launch_mfma(int which, bool bf16, const MfmaLaunch &L, hipStream_t st) {
     const int bits = which == 2 || which == 4 ? L.down.bits : L.gate.bits;
     switch (bits) {
@@ -315,10 +275,11 @@ int grouped_max_tiles(int tokens, int top_k, int n_shared, int E, int tile_token
            n_shared * ((tokens + tile_tokens - 1) / tile_tokens) + 1;
 }
 
-hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
-                           int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
-                           int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,
-                           hipStream_t st, int32_t *seg_tile, int top_k, bool pack_small, int32_t *tile_tok) {
+hipError_t launch_dispatch_count(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
+                                 int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
+                                 int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,
+                                 hipStream_t st, int32_t *seg_tile, int top_k, bool pack_small,
+                                 int32_t *tile_tok, PlaceArgs *place) {
     if (n_slots < 1 || n_slots > kMaxDispatchSlots) return hipErrorInvalidValue;
     // tokens fit the packed field (and the tiles exist to hold it)
     const int pack = pack_small && seg_tile && tiles && top_k > 0 && R / top_k < (1 << kTokenBits) &&
@@ -329,11 +290,22 @@ hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_
     hipLaunchKernelGGL(dispatch_count_kernel, dim3(1), dim3(kDispatchThreads), lds, st, route_slot, R,
                        n_slots, n_shared_tokens, tile_tokens, seg_start, tiles, n_tiles, max_tiles, route_pos,
                        seg_tile, pack);
-    hipError_t e = hipGetLastError();
+    *place = PlaceArgs{route_slot, R, n_slots, seg_start, sorted_route, route_pos, seg_tile, tiles, max_tiles,
+                       top_k > 0 ? top_k : 1, pack, tile_tok, tile_tokens};
+    return hipGetLastError();
+}
+
+hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
+                           int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
+                           int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,
+                           hipStream_t st, int32_t *seg_tile, int top_k, bool pack_small, int32_t *tile_tok) {
+    PlaceArgs a;
+    hipError_t e = launch_dispatch_count(route_slot, R, n_slots, n_shared_tokens, tile_tokens, seg_start,
+                                         sorted_route, route_pos, tiles, n_tiles, max_tiles, st, seg_tile, top_k,
+                                         pack_small, tile_tok, &a);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(dispatch_place_kernel, dim3((n_slots + 3) / 4), dim3(256), 0, st, route_slot, R,
-                       n_slots, seg_start, sorted_route, route_pos, seg_tile, tiles, max_tiles, top_k > 0 ? top_k : 1,
-                       pack, tile_tok, tile_tokens);
+    hipLaunchKernelGGL(dispatch_place_kernel, dim3((n_slots + kPlaceSlotsPerBlock - 1) / kPlaceSlotsPerBlock),
+                       dim3(64 * kPlaceSlotsPerBlock), 0, st, a);
     return hipGetLastError();
 }
 

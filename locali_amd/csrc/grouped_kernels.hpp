@@ -275,6 +275,77 @@ hipError_t grouped_geometry(int which, int cpr, const GroupedKernelLaunch &L, hi
 }
 
 hipError_t launch_grouped_kernels(int which, const GroupedKernelLaunch &L, hipStream_t st);
+
+// The dispatch's placement step (stable sort of the routes by slot, see
+// grouped.hip): its arguments, and its body for one 256-thread block (one
+// wave per slot), shared by its own kernel and by the matrix-core path's
+// fused place + input preparation launch.
+struct PlaceArgs {
+    const int32_t *route_slot;
+    int R, n_slots;
+    const int32_t *seg_start;
+    int32_t *sorted_route, *route_pos;
+    const int32_t *seg_tile;
+    int32_t *tiles;
+    int max_tiles, top_k, small_pack;
+    int32_t *tile_tok;
+    int tile_tokens;
+};
+constexpr int kPlaceSlotsPerBlock = 4;   // waves of a 256-thread block
+
+__device__ __forceinline__ void dispatch_place_block(const PlaceArgs &a, int block) {
+    const int lane = threadIdx.x & 63;
+    const int s = block * kPlaceSlotsPerBlock + (threadIdx.x >> 6);
+    if (s >= a.n_slots) return;
+    const int base = a.seg_start[s], end = a.seg_start[s + 1];
+    if (base == end) return;
+    const int tile0 = a.seg_tile ? a.seg_tile[s] : -1;   // the segment's first tile
+    // a slot of at most kPackedTokens routes: its tile's tokens, kTokenBits
+    // bits each in position order, go into the tile record (see the count
+    // kernel)
+    int32_t *packed = nullptr;
+    if (a.small_pack && end - base <= kPackedTokens && tile0 >= 0 && tile0 < a.max_tiles)
+        packed = &a.tiles[4 * tile0 + 3];
+    int32_t *tile_tok = tile0 < 0 ? nullptr : a.tile_tok;
+    // 8 x 64 routes per pass: the loads of a pass are in flight together,
+    // then the ballots place them in route order
+    constexpr int U = 8;
+    int pos = base;
+    for (int r0 = 0; r0 < a.R && pos < end; r0 += 64 * U) {
+        int v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int r = r0 + 64 * u + lane;
+            v[u] = r < a.R ? a.route_slot[r] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int r = r0 + 64 * u + lane;
+            const bool mine = v[u] == s;
+            const uint64_t m = __ballot(mine);
+            if (mine) {
+                const int p = pos + __popcll(m & ((1ull << lane) - 1ull));
+                a.sorted_route[p] = r;
+                if (a.route_pos) a.route_pos[r] = p;
+                if (packed) atomicOr(packed, (r / a.top_k) << (kTokenBits * (p - base)));
+                if (tile_tok) {
+                    const int q = p - base, tile = tile0 + q / a.tile_tokens;
+                    if (tile < a.max_tiles)
+                        tile_tok[static_cast<int64_t>(tile) * a.tile_tokens + q % a.tile_tokens] = r / a.top_k;
+                }
+            }
+            pos += __popcll(m);
+        }
+    }
+}
+
+// The count step alone (one workgroup), filling `place` with the placement
+// step's arguments (the caller launches it, possibly fused with other work).
+hipError_t launch_dispatch_count(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
+                                 int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
+                                 int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,
+                                 hipStream_t st, int32_t *seg_tile, int top_k, bool pack_small,
+                                 int32_t *tile_tok, PlaceArgs *place);
 hipError_t launch_dispatch(const int32_t *route_slot, int R, int n_slots, int n_shared_tokens,
                            int tile_tokens, int32_t *seg_start, int32_t *sorted_route,
                            int32_t *route_pos, int32_t *tiles, int32_t *n_tiles, int max_tiles,

@@ -6,8 +6,9 @@
 namespace locali {
 
 hipError_t mfma_b4(int which, bool bf16, const MfmaLaunch &L, hipStream_t st) {
-    if (which >= 3) return bf16 ? launch_small_stage<4, true>(which, L, st) : launch_small_stage<4, false>(which, L, st);
-    if (which >= 1) return bf16 ? launch_wide_stage<4, true>(which, L, st) : launch_wide_stage<4, false>(which, L, st);
+    if (which == 5) return bf16 ? launch_place_prep<4, true>(L, st) : launch_place_prep<4, false>(L, st);
+    if (which == 3 || which == 4) return bf16 ? launch_small_stage<4, true>(which, L, st) : launch_small_stage<4, false>(which, L, st);
+    if (which == 1 || which == 2) return bf16 ? launch_wide_stage<4, true>(which, L, st) : launch_wide_stage<4, false>(which, L, st);
     return bf16 ? launch_mfma_prep<4, true>(L, st) : launch_mfma_prep<4, false>(L, st);
 }
 

@@ -84,11 +84,11 @@ __device__ __forceinline__ u32x4 fix_b(uint32_t sb) {
 // One thread per (vector, word); the W64 words of a 64-block are consecutive
 // lanes, so their sums meet by butterfly.
 template <int BITS, bool BF16>
-__global__ __launch_bounds__(256) void mfma_prep_kernel(const uint16_t *__restrict__ v, int n_vec, int K,
-                                                        MfmaVec out) {
+__device__ __forceinline__ void mfma_prep_block(const uint16_t *__restrict__ v, int n_vec, int K, const MfmaVec &out,
+                                                int block) {
     using G = MfmaGeom<BITS, BF16>;
     const int words = K / G::kVPW;
-    const int u = blockIdx.x * blockDim.x + threadIdx.x;
+    const int u = block * 256 + static_cast<int>(threadIdx.x);
     const int vec = u / words, w = u % words;
     float2 part = make_float2(0.f, 0.f);
     if (vec < n_vec)
@@ -100,6 +100,25 @@ __global__ __launch_bounds__(256) void mfma_prep_kernel(const uint16_t *__restri
         part.y += __shfl_xor(part.y, m, 64);
     }
     if (vec < n_vec && w % G::kW64 == 0) out.fix[vec * out.fix_stride + w / G::kW64] = make_fix<BF16>(part);
+}
+
+template <int BITS, bool BF16>
+__global__ __launch_bounds__(256) void mfma_prep_kernel(const uint16_t *__restrict__ v, int n_vec, int K,
+                                                        MfmaVec out) {
+    mfma_prep_block<BITS, BF16>(v, n_vec, K, out, static_cast<int>(blockIdx.x));
+}
+
+// The dispatch's placement step and the preparation of the tokens' x in one
+// launch: neither depends on the other, and each alone leaves most of the
+// GPU idle. Blocks [0, place_blocks) place, the rest prepare.
+template <int BITS, bool BF16>
+__global__ __launch_bounds__(256) void place_prep_kernel(PlaceArgs pa, int place_blocks, const uint16_t *__restrict__ v,
+                                                         int n_vec, int K, MfmaVec out) {
+    const int b = static_cast<int>(blockIdx.x);
+    if (b < place_blocks)
+        dispatch_place_block(pa, b);
+    else
+        mfma_prep_block<BITS, BF16>(v, n_vec, K, out, b - place_blocks);
 }
 
 // Buffer resources: one 128-bit descriptor per array, held in SGPRs, so a
@@ -178,6 +197,7 @@ struct MfmaLaunch {
     int32_t max_tiles;
     int32_t tokens, routes;
     int32_t min_count_down;       // the down stage's ta.min_count (its small tiles may take more positions)
+    PlaceArgs place;              // the dispatch's placement step (launched with the preparation)
     int32_t small_down_positions; // positions of the down stage's small tiles: 2 or 4 (mfma_small.hpp)
 };
 
@@ -188,6 +208,18 @@ hipError_t launch_mfma_prep(const MfmaLaunch &L, hipStream_t st) {
     const int64_t threads = static_cast<int64_t>(L.tokens) * words;
     hipLaunchKernelGGL((mfma_prep_kernel<BITS, BF16>), dim3((threads + 255) / 256), dim3(256), 0, st, L.ta.x,
                        L.tokens, L.gate.cols, L.xin);
+    return hipGetLastError();
+}
+
+// The dispatch's placement step (L.place) fused with that preparation.
+template <int BITS, bool BF16>
+hipError_t launch_place_prep(const MfmaLaunch &L, hipStream_t st) {
+    const int words = L.gate.cols / MfmaGeom<BITS, BF16>::kVPW;
+    const int64_t threads = static_cast<int64_t>(L.tokens) * words;
+    const int place_blocks = (L.place.n_slots + kPlaceSlotsPerBlock - 1) / kPlaceSlotsPerBlock;
+    const int64_t blocks = place_blocks + (threads + 255) / 256;
+    hipLaunchKernelGGL((place_prep_kernel<BITS, BF16>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                       L.place, place_blocks, L.ta.x, L.tokens, L.gate.cols, L.xin);
     return hipGetLastError();
 }
 
