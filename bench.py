@@ -265,7 +265,10 @@ def prefill_run(arena, shared, slot_of, dev, tokens, calls, seed):
     out = torch.empty(tokens, D, dtype=torch.bfloat16, device=dev)
     idx = torch.empty(tokens, K_TOP, dtype=torch.int32, device=dev)
     wts = torch.empty(tokens, K_TOP, dtype=torch.float32, device=dev)
-    for x in batches[:2]:
+    # one untimed pass over the same calls first: the timed pass then sees
+    # the steady state of a serving loop (address translation of the arena's
+    # pages and clocks warm after the legs before it), not a cold start
+    for x in batches:
         ops.forward(spec, arena, shared, slot_of, x, ws, out=out, idx=idx, weights=wts)
     torch.cuda.synchronize()
     distinct = []
@@ -308,7 +311,7 @@ def mixed_run(dev, tokens, calls, seed):
     out = torch.empty(tokens, D, dtype=torch.bfloat16, device=dev)
     idx = torch.empty(tokens, K_TOP, dtype=torch.int32, device=dev)
     wts = torch.empty(tokens, K_TOP, dtype=torch.float32, device=dev)
-    for x in xs[:2]:
+    for x in xs:                           # one untimed pass first (as prefill_run)
         ops.forward(spec, arena, shared, slot_of, x, ws, out=out, idx=idx, weights=wts)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
