@@ -145,6 +145,29 @@ def test_prefill_full_width_zipf(oracle_lib, T, dtype, group):
                   tokens, f"C3 T={T} {dtype}", dtype=dtype)
 
 
+def test_prefill_full_width_long_call(oracle_lib):
+    """2048 tokens (a long prompt), Zipf(1.1) routing, 2-bit g64 bf16: tile
+    lists of thousands of tiles (experts of hundreds of positions, several
+    64-position tiles each), the four-position small down tiles, and the
+    shared expert's 32 tiles, checked on every tile kind against the C
+    oracle."""
+    banner("full-width prefill T=2048 zipf 1.1")
+    T = 2048
+    arena, shared = _layer(seed=440)
+    x, w = synth.zipf_router_inputs(T, E, D, 1.1, torch.bfloat16, seed=441, device=DEV)
+    spec = ops.RouterSpec(w, K, routed_scale=1.5)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    out, idx, wts = ops.forward(spec, arena, shared, slot_of, x, ops.Workspace())
+    torch.cuda.synchronize()
+    _check_routes(x, w, idx, wts)
+    ih = idx.cpu().numpy()
+    tokens, seg = _tile_sample(ih, T, heavy=4, mid=6, small=6, quad=3, seed=T)
+    counts = [len(v) for v in seg.values()]
+    assert max(counts) > 4 * TILE and any(1 <= c % TILE <= 4 for c in counts)
+    _oracle_check(oracle_lib, arena, shared, x, (ih + 1).astype(np.int32), wts.cpu().numpy(), out,
+                  tokens, "C3 T=2048")
+
+
 def test_mixed_2_4_bit_prefill_full_width(oracle_lib):
     """256 tokens, Zipf(1.1) routing, gate/up 2-bit and down 4-bit: the call
     size from which the down stage's small tiles take up to four positions
