@@ -32,6 +32,10 @@ Also reported:
                 expert popularity (grouped path): tokens/s, algorithmic GB/s
                 against 8 TB/s, and matrix-core utilisation (flops against
                 the 2.5 PFLOP/s dense bf16 peak)
+  prefill64_3bit_g128, prefill512_3bit_g128
+                the same prefill calls on the DSpark/MTP tier's experts (3-bit
+                codes in groups of 128, the 64-position matrix-core kernels
+                for tiles of every size)
   prefill512_heavy_tiles
                 matrix-core utilisation on the heavy tiles alone: a 512-token
                 call's routes to experts with 64 or more positions, plus the
@@ -254,8 +258,9 @@ def stage_timing(specs, arena, shareds, slot_of, X, ws, m=40, replays=5):
     return res
 
 
-def prefill_run(arena, shared, slot_of, dev, tokens, calls, seed):
-    """Zipf(1.1) routing through the real router (x . Wg == Zipf logits)."""
+def prefill_run(arena, shared, slot_of, dev, tokens, calls, seed, expert_bytes=EXPERT_BYTES):
+    """Zipf(1.1) routing through the real router (x . Wg == Zipf logits);
+    expert_bytes: bytes of one expert in the arena's format."""
     batches = []
     for c in range(calls):
         x, w = synth.zipf_router_inputs(tokens, E, D, 1.1, torch.bfloat16, seed=seed + c, device=dev)
@@ -283,7 +288,7 @@ def prefill_run(arena, shared, slot_of, dev, tokens, calls, seed):
         i, _, _ = ops.router(spec, x, ws)
         distinct.append(int(torch.unique(i).numel()))
     u = sum(distinct) / len(distinct)
-    algo = (u + 1) * EXPERT_BYTES + ROUTER_BYTES + tokens * D * 2 * 2
+    algo = (u + 1) * expert_bytes + ROUTER_BYTES + tokens * D * 2 * 2
     per_call = secs / calls
     flops = layer_flops(tokens)
     t_roof = max(algo / (HBM_PEAK_GBS * 1e9), flops / (MFMA_PEAK_TFLOPS * 1e12))
@@ -905,6 +910,17 @@ def main(argv=None):
             phase(f"prefill {tokens} tokens")
             result[f"prefill{tokens}"] = prefill_run(arena, shared, slot_of, dev, tokens,
                                                      args.prefill_calls, args.seed + 100)
+        if not args.skip_3bit:
+            a3 = synth.expert_arena(E + 1, D, DFF, bits_gate_up=3, group=128, dtype=torch.bfloat16,
+                                    seed=args.seed + 61, device=dev)
+            s3 = synth.expert_arena(1, D, DFF, bits_gate_up=3, group=128, dtype=torch.bfloat16,
+                                    seed=args.seed + 62, device=dev, zero_slot=False)
+            for tokens in (int(v) for v in args.prefill_sizes.split(",")):
+                phase(f"prefill {tokens} tokens, 3-bit experts in groups of 128")
+                result[f"prefill{tokens}_3bit_g128"] = prefill_run(a3, s3, slot_of, dev, tokens, args.prefill_calls,
+                                                                   args.seed + 100, B3_EXPERT_BYTES)
+            del a3, s3
+            torch.cuda.empty_cache()
         if not args.skip_heavy:
             phase("heavy tiles of a 512-token prefill")
             result["prefill512_heavy_tiles"] = heavy_tiles_run(arena, shared, slot_of, dev, 512,

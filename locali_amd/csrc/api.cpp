@@ -284,7 +284,8 @@ int check_decode_args(const locali_expert_arena *routed, const locali_expert_are
     return 0;
 }
 
-// The matrix-core grouped path needs 2- or 4-bit codes (gate and up alike),
+// The matrix-core grouped path needs 2-, 3- or 4-bit codes (gate and up
+// alike; 3-bit rows run on the 4-bit 64-position kernels, every tile size),
 // groups of a multiple of 64 with a multiple of 8 per row and at most
 // kWideMetaMaxGroups (96: K up to 6144 in groups of 64), rows in multiples
 // of 128, columns in multiples of kMfmaColsAlign, its staged scales, biases
@@ -297,7 +298,7 @@ bool mfma_eligible(const locali_expert_arena *routed, const locali_expert_arena 
         2 * routes * routed->down.cols >= (int64_t{1} << 31))
         return false;
     auto ok = [](const locali_qproj &p) {
-        return (p.bits == 2 || p.bits == 4) && p.group_size % 64 == 0 && p.rows % kWideRows == 0 &&
+        return (p.bits == 2 || p.bits == 3 || p.bits == 4) && p.group_size % 64 == 0 && p.rows % kWideRows == 0 &&
                p.cols % kMfmaColsAlign == 0 && (p.cols / p.group_size) % 8 == 0 &&
                p.cols / p.group_size <= kWideMetaMaxGroups;
     };
@@ -394,7 +395,7 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     // tiles); 2, 4: down
     const int order[5] = {5, 1, 3, 2, 4};
     for (int which : order) {
-        if (which >= 3 && !small) continue;
+        if ((which == 3 || which == 4) && !small) continue;
         if ((e = launch_mfma(which, bf16, L, st)) != hipSuccess) return hip_fail(e, "grouped MFMA launch");
     }
     const int d = routed->down.rows;

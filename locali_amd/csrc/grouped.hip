@@ -253,6 +253,7 @@ hipError_t launch_grouped_kernels(int which, const GroupedKernelLaunch &L, hipSt
 }
 
 hipError_t mfma_b2(int which, bool bf16, const MfmaLaunch &L, hipStream_t st);
+hipError_t mfma_b3(int which, bool bf16, const MfmaLaunch &L, hipStream_t st);
 hipError_t mfma_b4(int which, bool bf16, const MfmaLaunch &L, hipStream_t st);
 
 // which: 0 = prepare x, 1 = gate/up + SwiGLU (+ prepared h), 2 = down,
@@ -263,6 +264,7 @@ hipError_t launch_mfma(int which, bool bf16, const MfmaLaunch &L, hipStream_t st
     const int bits = which == 2 || which == 4 ? L.down.bits : L.gate.bits;
     switch (bits) {
     case 2: return mfma_b2(which, bf16, L, st);
+    case 3: return mfma_b3(which, bf16, L, st);
     case 4: return mfma_b4(which, bf16, L, st);
     default: return hipErrorInvalidValue;
     }

@@ -165,6 +165,22 @@ __device__ __forceinline__ void transpose_words(u32x4 &x) {
     }
 }
 
+// A lane's share of one chunk of a row as it arrives from memory: the 16
+// bytes of the 2- and 4-bit layouts, or (SB = 3: 3-bit codes computed in the
+// 4-bit geometry) the 12 bytes of the same 32 values, widened to the 4-bit
+// words by chunk_words once they have landed.
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+template <int SB>
+using ChunkRaw = typename std::conditional<SB == 3, u32x3, u32x4>::type;
+
+template <int SB>
+__device__ __forceinline__ u32x4 chunk_words(const ChunkRaw<SB> &r) {
+    if constexpr (SB == 3)
+        return spread3_chunk(r[0], r[1], r[2]);
+    else
+        return r;
+}
+
 template <int WPL>
 __device__ __forceinline__ BlockW<WPL> block_words(const u32x4 &x, int j) {
     BlockW<WPL> o;

@@ -223,8 +223,11 @@ __device__ __forceinline__ void wide_b(const BlockW<MfmaGeom<BITS, BF16>::kWPL> 
 // waves' loop. w[j]: projection j's weight words of the workgroup's rows;
 // marr: their scales and biases (see WideMetaStage); vec(p) the
 // prepared-input vector of position p < count. Returns with the compute
-// waves' acc[j] filled and every wave past the last barrier.
-template <int BITS, bool BF16, int NPROJ, int NACT, typename TokOf>
+// waves' acc[j] filled and every wave past the last barrier. SB: bits of the
+// stored codes (BITS, or 3 for 3-bit rows computed in the 4-bit geometry: a
+// lane's 32 values of a chunk arrive as 12 bytes and are widened when the
+// chunk is consumed).
+template <int BITS, bool BF16, int NPROJ, int NACT, int SB, typename TokOf>
 __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const WideLds<NPROJ> &L, const int32_t *tt,
                                           const uint32_t *const (&w)[NPROJ],
                                           const uint16_t *const (&marr)[2 * NPROJ], const MfmaVec &in, int n_vec,
@@ -234,7 +237,8 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
     const int nblk = K / 64, nsteps = nblk / 2, nchunks = nblk / CB;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, nl = lane & 15, kb = lane >> 4;
-    const int wpr = K / G::kVPW;
+    static_assert(SB == BITS || (SB == 3 && BITS == 4), "3-bit codes run in the 4-bit geometry");
+    const int wpr = K * SB / 32;
     const int gpr = K / group, bpg = group / 64;
 #pragma unroll
     for (int j = 0; j < NPROJ; ++j)
@@ -298,14 +302,21 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
     __amdgpu_buffer_rsrc_t wrs[NPROJ];
 #pragma unroll
     for (int j = 0; j < NPROJ; ++j) wrs[j] = make_rsrc(w[j], wbytes);
-    const uint32_t w_off = 4u * static_cast<uint32_t>((wave * 16 + nl) * wpr) + 16u * kb;
+    // a chunk of a row (128 or 256 values) is 64 bytes, 16 a lane; of 3-bit
+    // codes 48 bytes, 12 a lane
+    constexpr int kLaneBytes = SB == 3 ? 12 : 16;
+    const uint32_t w_off = 4u * static_cast<uint32_t>((wave * 16 + nl) * wpr) + kLaneBytes * kb;
     constexpr int RING = WideDepth<NACT>::kRing;
-    u32x4 ring[RING][NPROJ];
-    auto load_w = [&](u32x4 (&dst)[NPROJ], int c) {
+    ChunkRaw<SB> ring[RING][NPROJ];
+    auto load_w = [&](ChunkRaw<SB> (&dst)[NPROJ], int c) {
         const uint32_t past = c < nchunks ? 0u : kPastEnd;
 #pragma unroll
-        for (int j = 0; j < NPROJ; ++j)
-            dst[j] = __builtin_amdgcn_raw_buffer_load_b128(wrs[j], w_off | past, c * 64, kAuxStream);
+        for (int j = 0; j < NPROJ; ++j) {
+            if constexpr (SB == 3)
+                dst[j] = __builtin_amdgcn_raw_buffer_load_b96(wrs[j], w_off | past, c * 48, kAuxStream);
+            else
+                dst[j] = __builtin_amdgcn_raw_buffer_load_b128(wrs[j], w_off | past, c * 64, kAuxStream);
+        }
     };
     // the scales and biases first (staging waits for them), then two weight
     // chunks; the other chunks behind stage 0 and the metadata
@@ -324,9 +335,12 @@ __device__ __forceinline__ void wide_body(mf32x4_t (&acc)[NPROJ][NACT], const Wi
         for (int q = 0; q < RING; ++q) {
             const int c = c0 + q;
             if (c < nchunks) {
-                u32x4(&wt)[NPROJ] = ring[q];
+                u32x4 wt[NPROJ];
 #pragma unroll
-                for (int j = 0; j < NPROJ; ++j) transpose_words<WPL>(wt[j]);
+                for (int j = 0; j < NPROJ; ++j) {
+                    wt[j] = chunk_words<SB>(ring[q][j]);
+                    transpose_words<WPL>(wt[j]);
+                }
 #pragma unroll
                 for (int sp = 0; sp < SPC; ++sp) {
                     const int s = c * SPC + sp;
@@ -417,7 +431,7 @@ __device__ __forceinline__ bool wide_tile(const TileArgs &ta, int n_slots, int &
              (!shared && (slot < 0 || slot >= n_slots || first < 0 || first + count > ta.R)));
 }
 
-template <int BITS, bool BF16, int NACT>
+template <int BITS, bool BF16, int SB, int NACT>
 __device__ __forceinline__ void wide_gateup_tile(const TileArgs &ta, const QProj &pg, const QProj &pu, int sl,
                                                  bool shared, int first, int count,
                                                  const MfmaVec &xin, const MfmaVec &hout, int down_bits, float limit,
@@ -425,7 +439,7 @@ __device__ __forceinline__ void wide_gateup_tile(const TileArgs &ta, const QProj
     const int K = pg.cols;
     const WideLds<2> L(wlds, K);
     const int n0 = blockIdx.x * kWideRows;
-    const int wpr = K / MfmaGeom<BITS, BF16>::kVPW, gpr = K / pg.group;
+    const int wpr = K * SB / 32, gpr = K / pg.group;
     const int64_t r0 = static_cast<int64_t>(n0) * gpr;
     const uint32_t *const w[2] = {pg.w + sl * pg.w_slot + static_cast<int64_t>(n0) * wpr,
                                   pu.w + sl * pu.w_slot + static_cast<int64_t>(n0) * wpr};
@@ -434,7 +448,7 @@ __device__ __forceinline__ void wide_gateup_tile(const TileArgs &ta, const QProj
     mf32x4_t acc[2][NACT];
     // position p's token: the shared expert's tiles hold tokens in order; a
     // routed tile's come from the dispatch's list
-    wide_body<BITS, BF16, 2, NACT>(acc, L, ta.tile_tok + static_cast<int64_t>(blockIdx.y) * kWideTokens, w, marr, xin,
+    wide_body<BITS, BF16, 2, NACT, SB>(acc, L, ta.tile_tok + static_cast<int64_t>(blockIdx.y) * kWideTokens, w, marr, xin,
                                    ta.n_vec, [&](int p, const int32_t *t) { return shared ? first + p - ta.R : t[p]; },
                                    K, pg.group, count);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nl = lane & 15, kb = lane >> 4;
@@ -484,7 +498,7 @@ __device__ __forceinline__ void wide_gateup_tile(const TileArgs &ta, const QProj
     }
 }
 
-template <int BITS, bool BF16>
+template <int BITS, bool BF16, int SB>
 __global__ __launch_bounds__(kWideThreads) void wide_gateup_kernel(TileArgs ta, QProj gate, QProj up, QProj sgate,
                                                                    QProj sup, MfmaVec xin, MfmaVec hout,
                                                                    int down_bits, float limit, int fp32_swiglu) {
@@ -496,25 +510,25 @@ __global__ __launch_bounds__(kWideThreads) void wide_gateup_kernel(TileArgs ta, 
     const QProj pu = shared ? sup : up;
     const int sl = shared ? 0 : slot;
     switch ((count + 15) >> 4) {
-    case 1: wide_gateup_tile<BITS, BF16, 1>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
-    case 2: wide_gateup_tile<BITS, BF16, 2>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
-    case 3: wide_gateup_tile<BITS, BF16, 3>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
-    default: wide_gateup_tile<BITS, BF16, 4>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
+    case 1: wide_gateup_tile<BITS, BF16, SB, 1>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
+    case 2: wide_gateup_tile<BITS, BF16, SB, 2>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
+    case 3: wide_gateup_tile<BITS, BF16, SB, 3>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
+    default: wide_gateup_tile<BITS, BF16, SB, 4>(ta, pg, pu, sl, shared, first, count, xin, hout, down_bits, limit, fp32_swiglu, wlds); break;
     }
 }
 
-template <int BITS, bool BF16, int NACT>
+template <int BITS, bool BF16, int SB, int NACT>
 __device__ __forceinline__ void wide_down_tile(const TileArgs &ta, const QProj &p, int sl, int first, int count,
                                                const MfmaVec &hin, uint16_t *__restrict__ y, unsigned char *wlds) {
     const int N = p.rows, K = p.cols;
     const WideLds<1> L(wlds, K);
     const int n0 = blockIdx.x * kWideRows;
-    const int wpr = K / MfmaGeom<BITS, BF16>::kVPW, gpr = K / p.group;
+    const int wpr = K * SB / 32, gpr = K / p.group;
     const int64_t r0 = static_cast<int64_t>(n0) * gpr;
     const uint32_t *const w[1] = {p.w + sl * p.w_slot + static_cast<int64_t>(n0) * wpr};
     const uint16_t *const marr[2] = {p.s + sl * p.m_slot + r0, p.b + sl * p.m_slot + r0};
     mf32x4_t acc[1][NACT];
-    wide_body<BITS, BF16, 1, NACT>(acc, L, nullptr, w, marr, hin, ta.n_vec,
+    wide_body<BITS, BF16, 1, NACT, SB>(acc, L, nullptr, w, marr, hin, ta.n_vec,
                                    [&](int q, const int32_t *) { return first + q; }, K, p.group, count);
     const int wave = threadIdx.x >> 6;
     if (wave >= kWideCompute) return;
@@ -530,7 +544,7 @@ __device__ __forceinline__ void wide_down_tile(const TileArgs &ta, const QProj &
     }
 }
 
-template <int BITS, bool BF16>
+template <int BITS, bool BF16, int SB>
 __global__ __launch_bounds__(kWideThreads) void wide_down_kernel(TileArgs ta, QProj down, QProj sdown, MfmaVec hin,
                                                                  uint16_t *__restrict__ y) {
     extern __shared__ __align__(16) unsigned char wlds[];
@@ -540,34 +554,37 @@ __global__ __launch_bounds__(kWideThreads) void wide_down_kernel(TileArgs ta, QP
     const QProj p = shared ? sdown : down;
     const int sl = shared ? 0 : slot;
     switch ((count + 15) >> 4) {
-    case 1: wide_down_tile<BITS, BF16, 1>(ta, p, sl, first, count, hin, y, wlds); break;
-    case 2: wide_down_tile<BITS, BF16, 2>(ta, p, sl, first, count, hin, y, wlds); break;
-    case 3: wide_down_tile<BITS, BF16, 3>(ta, p, sl, first, count, hin, y, wlds); break;
-    default: wide_down_tile<BITS, BF16, 4>(ta, p, sl, first, count, hin, y, wlds); break;
+    case 1: wide_down_tile<BITS, BF16, SB, 1>(ta, p, sl, first, count, hin, y, wlds); break;
+    case 2: wide_down_tile<BITS, BF16, SB, 2>(ta, p, sl, first, count, hin, y, wlds); break;
+    case 3: wide_down_tile<BITS, BF16, SB, 3>(ta, p, sl, first, count, hin, y, wlds); break;
+    default: wide_down_tile<BITS, BF16, SB, 4>(ta, p, sl, first, count, hin, y, wlds); break;
     }
 }
 
-template <int BITS, bool BF16>
+// SB: bits of the stored codes (3: 3-bit rows on the 4-bit kernels).
+template <int BITS, bool BF16, int SB = BITS>
 hipError_t launch_wide_stage(int which, const MfmaLaunch &L, hipStream_t st) {
     TileArgs ta = L.ta;
     if (which == 1) {
         ta.n_vec = L.tokens;
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&wide_gateup_kernel<BITS, BF16>),
+            reinterpret_cast<const void *>(&wide_gateup_kernel<BITS, BF16, SB>),
             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kWideMaxLds));
         if (attr != hipSuccess) return attr;
         dim3 grid(L.gate.rows / kWideRows, L.max_tiles);
-        hipLaunchKernelGGL((wide_gateup_kernel<BITS, BF16>), grid, dim3(kWideThreads), wide_lds_bytes(L.gate.cols, 2),
-                           st, ta, L.gate, L.up, L.sgate, L.sup, L.xin, L.hmid, L.down.bits, L.limit, L.fp32_swiglu);
+        // the epilogue prepares h in the geometry the down stage computes in
+        hipLaunchKernelGGL((wide_gateup_kernel<BITS, BF16, SB>), grid, dim3(kWideThreads),
+                           wide_lds_bytes(L.gate.cols, 2), st, ta, L.gate, L.up, L.sgate, L.sup, L.xin, L.hmid,
+                           lane_bits(L.down.bits), L.limit, L.fp32_swiglu);
     } else {
         ta.n_vec = L.routes;
         ta.min_count = L.min_count_down;
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&wide_down_kernel<BITS, BF16>),
+            reinterpret_cast<const void *>(&wide_down_kernel<BITS, BF16, SB>),
             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kWideMaxLds));
         if (attr != hipSuccess) return attr;
         dim3 grid(L.down.rows / kWideRows, L.max_tiles);
-        hipLaunchKernelGGL((wide_down_kernel<BITS, BF16>), grid, dim3(kWideThreads), wide_lds_bytes(L.down.cols, 1),
+        hipLaunchKernelGGL((wide_down_kernel<BITS, BF16, SB>), grid, dim3(kWideThreads), wide_lds_bytes(L.down.cols, 1),
                            st, ta, L.down, L.sdown, L.hmid, L.y);
     }
     return hipGetLastError();

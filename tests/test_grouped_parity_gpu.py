@@ -1,7 +1,8 @@
 """The grouped (prefill) matrix-core kernels held to the stated expert-output
 tolerance at the benchmarked shape: d_model 4096, 256 routed experts + the
 shared expert, d_ff 2048, 2-bit g64, T = 64 and 512, bf16 and fp16, Zipf(1.1)
-expert popularity.
+expert popularity; also 2-bit g128 and 3-bit g128 (the DSpark/MTP tier's
+experts, whose tiles of every size take the 64-position kernels).
 
   * Pure expert outputs (dsv4_arena.py:223-235, one route per token, weight 1,
     no shared expert; tests/test_dsv4_kernels.py:75 holds the reference's own
@@ -41,9 +42,9 @@ FP32_SUM = 2.0 ** -12     # worst-case relative error of an fp32 sum of up to 40
 LIMIT = 10.0
 
 
-def _layer(seed, dtype, group=GROUP):
-    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=2, group=group, dtype=dtype, seed=seed, device=DEV)
-    shared = synth.expert_arena(1, D, DFF, bits_gate_up=2, group=group, dtype=dtype, seed=seed + 1, device=DEV,
+def _layer(seed, dtype, group=GROUP, bits=2):
+    arena = synth.expert_arena(E + 1, D, DFF, bits_gate_up=bits, group=group, dtype=dtype, seed=seed, device=DEV)
+    shared = synth.expert_arena(1, D, DFF, bits_gate_up=bits, group=group, dtype=dtype, seed=seed + 1, device=DEV,
                                 zero_slot=False)
     return arena, shared
 
@@ -96,13 +97,24 @@ def _tile_routes(seg, heavy=3, mid=3, small=3, quad=3, seed=0):
 
 
 def _dense(proj, slot):
-    """fp64 dequantised matrix of one slot (2/4-bit whole codes per word),
-    vectorised; pinned to affine.dequant on its first rows."""
+    """fp64 dequantised matrix of one slot (2/4-bit whole codes per word;
+    3-bit: 32 codes per 3 words of the row's bit stream), vectorised; pinned
+    to affine.dequant on its first rows."""
     w, s, b, bits, group = proj
     w, s, b = w[slot], s[slot], b[slot]
-    vpw = 32 // bits
-    shifts = (np.arange(vpw, dtype=np.uint32) * bits)[None, None, :]
-    q = ((w[:, :, None] >> shifts) & ((1 << bits) - 1)).reshape(w.shape[0], -1).astype(np.float64)
+    if bits == 3:
+        t = w.reshape(w.shape[0], -1, 3).astype(np.uint64)
+        # code i of a 3-word piece: bits 3i .. 3i + 2, read from the 64-bit
+        # window of words (3i // 32, 3i // 32 + 1)
+        win = np.stack([t[..., 0] | (t[..., 1] << np.uint64(32)), t[..., 1] | (t[..., 2] << np.uint64(32)),
+                        t[..., 2]], axis=-1)
+        i = np.arange(32)
+        q = (win[..., (3 * i) // 32] >> ((3 * i) % 32).astype(np.uint64)) & np.uint64(7)
+        q = q.reshape(w.shape[0], -1).astype(np.float64)
+    else:
+        vpw = 32 // bits
+        shifts = (np.arange(vpw, dtype=np.uint32) * bits)[None, None, :]
+        q = ((w[:, :, None] >> shifts) & ((1 << bits) - 1)).reshape(w.shape[0], -1).astype(np.float64)
     q = q.reshape(q.shape[0], -1, group)
     dense = (q * s[:, :, None] + b[:, :, None]).reshape(w.shape[0], -1)
     np.testing.assert_array_equal(dense[:4], affine.dequant(w[:4], s[:4], b[:4], bits, group))
@@ -124,7 +136,10 @@ def _check_outputs(got, want, h_gpu, dense_of, x_of, tokens, dt, what):
     outside the tolerance is accepted only when it is explained that way:
     against y_o, the exact down projection of the exact (fp64) oracle h_o,
     it is within the tolerance plus sum_j |W_nj| |h_gpu_j - h_o_j|, and
-    h_gpu differs from h_o. Such elements must stay below 1 %."""
+    h_gpu differs from h_o. Returns how many elements needed that
+    explanation; the caller holds them below 1 % of the call's checked
+    outputs (one flip of a large h moves a few % of its token's outputs past
+    2e-3, so a handful of tokens can hold most of them)."""
     bad = np.abs(got - want) > ATOL + RTOL * np.abs(want)
     for i in np.unique(np.argwhere(bad)[:, 0]):
         t = tokens[i]
@@ -137,16 +152,16 @@ def _check_outputs(got, want, h_gpu, dense_of, x_of, tokens, dt, what):
         bound = ATOL + RTOL * np.abs(y_o) + np.abs(dense["down_proj"][n]) @ dh
         assert np.all(np.abs(got[i, n] - y_o) <= bound), \
             f"{what}: token {t} columns {n[:4].tolist()} beyond the h-flip bound"
-    assert bad.mean() < 1e-2, f"{what}: {int(bad.sum())} elements outside the stated tolerance"
     return int(bad.sum())
 
 
-@pytest.mark.parametrize("T,dtype,group", [(64, torch.bfloat16, 64), (512, torch.bfloat16, 64),
-                                           (64, torch.float16, 64), (512, torch.float16, 64),
-                                           (512, torch.bfloat16, 128)])
-def test_grouped_pure_expert_outputs(oracle_lib, T, dtype, group):
-    banner(f"grouped pure expert outputs T={T} {dtype} group {group}")
-    arena, shared = _layer(700 + T, dtype, group)
+@pytest.mark.parametrize("T,dtype,group,bits", [(64, torch.bfloat16, 64, 2), (512, torch.bfloat16, 64, 2),
+                                                (64, torch.float16, 64, 2), (512, torch.float16, 64, 2),
+                                                (512, torch.bfloat16, 128, 2), (64, torch.bfloat16, 128, 3),
+                                                (512, torch.bfloat16, 128, 3)])
+def test_grouped_pure_expert_outputs(oracle_lib, T, dtype, group, bits):
+    banner(f"grouped pure expert outputs T={T} {dtype} group {group} bits {bits}")
+    arena, shared = _layer(700 + T, dtype, group, bits)
     x = synth.activations(T, D, dtype, seed=710 + T, device=DEV)
     experts = _zipf_one(T, seed=720 + T)
     idx = torch.from_numpy(experts).reshape(T, 1).to(DEV)
@@ -192,23 +207,26 @@ def test_grouped_pure_expert_outputs(oracle_lib, T, dtype, group):
         want_sh = oracle_lib.moe_layer(xs[tk], np.zeros((len(tk), 1), np.int32), np.ones((len(tk), 1)), sh, dt)
         flips += _check_outputs(got_sh[tk], want_sh, hg_sh[T:], dense_shared, lambda t: xs[t], tk, dt,
                                 f"shared expert outputs T={T} {dt}")
-    print(f"T={T} {dt}: {2 * len(tokens) * D} outputs checked, {flips} beyond the stated tolerance "
+    checked = 2 * len(tokens) * D
+    print(f"T={T} {dt}: {checked} outputs checked, {flips} beyond the stated tolerance "
           f"through h rounding flips")
+    assert flips < 1e-2 * checked, f"T={T} {dt}: {flips} of {checked} elements outside the stated tolerance"
 
 
-@pytest.mark.parametrize("T,dtype,group", [(64, torch.bfloat16, 64), (512, torch.bfloat16, 64),
-                                           (64, torch.float16, 64), (512, torch.float16, 64),
-                                           (64, torch.bfloat16, 128), (512, torch.bfloat16, 128)])
-def test_grouped_stagewise_ulp(T, dtype, group):
+@pytest.mark.parametrize("T,dtype,group,bits", [(64, torch.bfloat16, 64, 2), (512, torch.bfloat16, 64, 2),
+                                                (64, torch.float16, 64, 2), (512, torch.float16, 64, 2),
+                                                (64, torch.bfloat16, 128, 2), (512, torch.bfloat16, 128, 2),
+                                                (512, torch.bfloat16, 128, 3), (64, torch.float16, 128, 3)])
+def test_grouped_stagewise_ulp(T, dtype, group, bits):
     """h and y of the grouped kernels against the exact oracle on their own
     stage inputs (the bounds of test_expert_decode_stagewise_ulp): every
     checked element within the bound, at least 95 % of h and 98 % of y
     equal to the oracle's rounding (the matrix cores' fp32 sums round h
     differently from the exact oracle a little more often than the decode
     kernels do: 95.9 % of one route's h equal at T=512 in bf16)."""
-    banner(f"grouped stage-wise ulp T={T} {dtype} group {group}")
+    banner(f"grouped stage-wise ulp T={T} {dtype} group {group} bits {bits}")
     dt = dt_name(dtype)
-    arena, shared = _layer(800 + T, dtype, group)
+    arena, shared = _layer(800 + T, dtype, group, bits)
     x, w = synth.zipf_router_inputs(T, E, D, 1.1, dtype, seed=810 + T, device=DEV)
     spec = ops.RouterSpec(w, K, routed_scale=1.5)
     ws = ops.Workspace(DEV)

@@ -430,7 +430,8 @@ def test_fp32_combine_mode_in_the_layer_kernels(T):
 @pytest.mark.parametrize("bits", [(2, 2), (3, 3)])
 def test_expert_grouped_swiglu_modes_and_limit(fp32_swiglu, bits):
     """The grouped kernels' SwiGLU epilogues (matrix-core 64-position and
-    small tiles for 2-bit, VALU for 3-bit) with the clamp driven (x scaled
+    small tiles for 2-bit, 64-position tiles of every size for 3-bit) with
+    the clamp driven (x scaled
     by 4) at limits 10 and 0.5, and with it off (limit 0, unscaled x: with
     no clamp the scaled inputs make h large enough that a last-place flip of
     one h value moves y past the combine-term bound), op by op in the
@@ -472,6 +473,35 @@ def test_expert_grouped_matches_oracle(T, dtype, bits):
     for t in range(0, T, 2):            # skew: expert 0 in every other token
         if not (idx[t] == 0).any():
             idx[t, 0] = 0
+    slot_of = (torch.arange(E, dtype=torch.int32) + 1)
+    wts = torch.rand(T, k, generator=gen)
+    out = ops.expert_grouped(_dev(arena), _dev(shared), x.to(DEV), idx.to(DEV), slot_of.to(DEV),
+                             wts.to(DEV), ops.Workspace())
+    torch.cuda.synchronize()
+    want, terms = _oracle_layer(x, idx.numpy(), wts.numpy(), arena, {e: e + 1 for e in range(E)},
+                                dtype, shared=shared, return_terms=True)
+    assert_close_terms(values(out), want, terms, "grouped")
+    assert close_fraction(values(out), want, dtype) > 0.8
+
+
+@pytest.mark.parametrize("T,dtype,bits,group,d,dff", [(9, torch.bfloat16, (8, 8), 64, 1024, 512),
+                                                      (12, torch.float16, (2, 2), 32, 1024, 512),
+                                                      (5, torch.bfloat16, (3, 3), 32, 1024, 512),
+                                                      (20, torch.bfloat16, (4, 8), 128, 1024, 512)])
+def test_expert_grouped_other_shapes_match_oracle(T, dtype, bits, group, d, dff):
+    """The formats the matrix-core grouped kernels do not take (8-bit codes,
+    groups of 32) on the VALU grouped kernels, with the shared expert and a
+    skewed expert."""
+    banner(f"grouped other shapes T={T} {dtype} {bits} g{group} d{d} dff{dff}")
+    E, k = 16, 4
+    arena = synth.expert_arena(E + 1, d, dff, bits_gate_up=bits[0], bits_down=bits[1], group=group, dtype=dtype,
+                               seed=T + 300)
+    shared = synth.expert_arena(1, d, dff, bits_gate_up=bits[0], bits_down=bits[1], group=group, dtype=dtype,
+                                seed=T + 301, zero_slot=False)
+    x = synth.activations(T, d, dtype, seed=T + 302)
+    gen = torch.Generator().manual_seed(T + 303)
+    idx = torch.stack([torch.randperm(E, generator=gen)[:k] for _ in range(T)]).to(torch.int32)
+    idx[: (2 * T) // 3, 0] = 5
     slot_of = (torch.arange(E, dtype=torch.int32) + 1)
     wts = torch.rand(T, k, generator=gen)
     out = ops.expert_grouped(_dev(arena), _dev(shared), x.to(DEV), idx.to(DEV), slot_of.to(DEV),
