@@ -329,6 +329,56 @@ bool small_tiles_eligible(const locali_expert_arena *routed) {
     return ok(routed->gate) && ok(routed->up) && ok(routed->down);
 }
 
+// Second stream of the grouped matrix-core path, one per host thread and
+// device (the events are reused call after call, so calls from one thread
+// stay ordered; threads never share a set). Created on the first grouped call
+// that is not under stream capture; calls that must not allocate
+// (set_no_alloc_call) and calls made before it exists under capture keep
+// every kernel on the caller's stream. Default priority, non-blocking.
+struct AuxStream {
+    hipStream_t s = nullptr;
+    hipEvent_t ev[4] = {};
+    bool failed = false;
+};
+constexpr int kAuxMaxDevices = 64;
+// Calls of fewer tokens keep one stream: their kernels are short and
+// latency-bound, and the fork and joins cost more than the overlap gives.
+constexpr int kAuxStreamTokens = 256;
+thread_local AuxStream g_aux[kAuxMaxDevices];
+thread_local bool g_no_alloc_call = false;
+
+AuxStream *aux_stream(hipStream_t st) {
+    if (g_no_alloc_call) return nullptr;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kAuxMaxDevices) return nullptr;
+    AuxStream &a = g_aux[dev];
+    if (a.s) return &a;
+    if (a.failed) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    hipStream_t s = nullptr;
+    bool ok = hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess;
+    for (int i = 0; ok && i < 4; ++i) ok = hipEventCreateWithFlags(&a.ev[i], hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+        for (hipEvent_t &ev : a.ev)
+            if (ev) (void)hipEventDestroy(ev), ev = nullptr;
+        if (s) (void)hipStreamDestroy(s);
+        (void)hipGetLastError();
+        a.failed = true;
+        return nullptr;
+    }
+    a.s = s;
+    return &a;
+}
+
+}  // namespace
+
+namespace locali {
+void set_no_alloc_call(bool on) { g_no_alloc_call = on; }
+}  // namespace locali
+
+namespace {
+
 int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_arena *shared,
                      const void *x, int32_t x_dtype, int32_t tokens, int32_t top_k, int32_t n_experts,
                      const int32_t *route_slot, const float *weights, float limit,
@@ -393,10 +443,31 @@ int run_grouped_mfma(const locali_expert_arena *routed, const locali_expert_aren
     L.min_count_down = small ? L.small_down_positions + 1 : 0;
     // 5: placement + preparation of x; 1, 3: gate/up (64-position, small
     // tiles); 2, 4: down
-    const int order[5] = {5, 1, 3, 2, 4};
-    for (int which : order) {
-        if ((which == 3 || which == 4) && !small) continue;
-        if ((e = launch_mfma(which, bf16, L, st)) != hipSuccess) return hip_fail(e, "grouped MFMA launch");
+    AuxStream *ax = small && tokens >= kAuxStreamTokens ? aux_stream(st) : nullptr;
+    if (!ax) {
+        const int order[5] = {5, 1, 3, 2, 4};
+        for (int which : order) {
+            if ((which == 3 || which == 4) && !small) continue;
+            if ((e = launch_mfma(which, bf16, L, st)) != hipSuccess) return hip_fail(e, "grouped MFMA launch");
+        }
+    } else {
+        // the small-tile kernels on the second stream beside the 64-position
+        // ones: gate/up pair after 5, down pair after both gate/ups (the
+        // small down kernel also reads h of tiles the 64-position gate/up
+        // kernel wrote), joined before the combine
+        const hipStream_t sa = ax->s;
+        if ((e = launch_mfma(5, bf16, L, st)) != hipSuccess) return hip_fail(e, "grouped MFMA launch");
+        if ((e = hipEventRecord(ax->ev[0], st)) != hipSuccess || (e = hipStreamWaitEvent(sa, ax->ev[0], 0)) != hipSuccess)
+            return hip_fail(e, "grouped fork");
+        if ((e = launch_mfma(1, bf16, L, st)) != hipSuccess || (e = launch_mfma(3, bf16, L, sa)) != hipSuccess)
+            return hip_fail(e, "grouped MFMA launch");
+        if ((e = hipEventRecord(ax->ev[1], sa)) != hipSuccess || (e = hipStreamWaitEvent(st, ax->ev[1], 0)) != hipSuccess ||
+            (e = hipEventRecord(ax->ev[2], st)) != hipSuccess || (e = hipStreamWaitEvent(sa, ax->ev[2], 0)) != hipSuccess)
+            return hip_fail(e, "grouped join");
+        if ((e = launch_mfma(2, bf16, L, st)) != hipSuccess || (e = launch_mfma(4, bf16, L, sa)) != hipSuccess)
+            return hip_fail(e, "grouped MFMA launch");
+        if ((e = hipEventRecord(ax->ev[3], sa)) != hipSuccess || (e = hipStreamWaitEvent(st, ax->ev[3], 0)) != hipSuccess)
+            return hip_fail(e, "grouped join");
     }
     const int d = routed->down.rows;
     e = launch_combine(gy, route_pos, shared ? gy + static_cast<int64_t>(R) * d : nullptr, weights, tokens,

@@ -13,6 +13,9 @@
 
 namespace locali {
 int set_error(int code, const char *msg);
+// Keeps the grouped path's kernels on the caller's stream (no second stream
+// or events are created) for the calling thread while set.
+void set_no_alloc_call(bool on);
 }
 
 namespace {
@@ -84,6 +87,9 @@ extern "C" int locali_moe_forward_noalloc(const locali_router *router, const loc
     const hipStream_t st = static_cast<hipStream_t>(stream);
     void *ws = nullptr;
     if (const int rc = scratch_of_current_device(&ws, st)) return rc;
-    return locali_moe_forward(router, routed, shared, slot_of_expert, x, x_dtype, tokens, input_ids,
-                              swiglu_limit, fp32_swiglu, out, idx, weights, ws, kScratchBytes, stream);
+    locali::set_no_alloc_call(true);
+    const int rc = locali_moe_forward(router, routed, shared, slot_of_expert, x, x_dtype, tokens, input_ids,
+                                      swiglu_limit, fp32_swiglu, out, idx, weights, ws, kScratchBytes, stream);
+    locali::set_no_alloc_call(false);
+    return rc;
 }

@@ -145,6 +145,58 @@ def test_prefill_full_width_zipf(oracle_lib, T, dtype, group):
                   tokens, f"C3 T={T} {dtype}", dtype=dtype)
 
 
+def test_prefill_two_streams_eager_and_graph_replays():
+    """Calls of 256 tokens or more run the small-tile kernels on a second
+    stream beside the 64-position ones (fork after the preparation, join
+    before the down pair and before the combine). Back-to-back eager calls
+    on different inputs (the fork's events are reused) give each call's own
+    result bit for bit, and a captured call replays bit-exact three times
+    with eager calls in between. Parity of the same path with the C oracle
+    is the 512-token case above."""
+    T = 512
+    banner(f"two-stream grouped path T={T}: eager pairs and graph replays")
+    arena, shared = _layer(seed=901)
+    xa, w = synth.zipf_router_inputs(T, E, D, 1.1, torch.bfloat16, seed=902, device=DEV)
+    xb, _ = synth.zipf_router_inputs(T, E, D, 1.1, torch.bfloat16, seed=903, device=DEV)
+    xb = xb.flip(0).contiguous()   # other tokens, same router
+    spec = ops.RouterSpec(w, K, routed_scale=1.5)
+    slot_of = torch.arange(1, E + 1, dtype=torch.int32, device=DEV)
+    ws = ops.Workspace()
+    ref_a = [t.clone() for t in ops.forward(spec, arena, shared, slot_of, xa, ws)]
+    torch.cuda.synchronize()
+    ref_b = [t.clone() for t in ops.forward(spec, arena, shared, slot_of, xb, ws)]
+    torch.cuda.synchronize()
+    assert not torch.equal(ref_a[0], ref_b[0])
+    outs = []
+    for x in (xa, xb, xa, xb):           # back to back, one synchronisation at the end
+        outs.append([t.clone() for t in ops.forward(spec, arena, shared, slot_of, x, ws)])
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        ref = ref_a if i % 2 == 0 else ref_b
+        for got, want in zip(o, ref):
+            assert torch.equal(got, want), f"eager call {i}"
+    xin = xa.clone()
+    out = torch.empty(T, D, dtype=torch.bfloat16, device=DEV)
+    idx = torch.empty(T, K, dtype=torch.int32, device=DEV)
+    wts = torch.empty(T, K, dtype=torch.float32, device=DEV)
+    ws_g = ops.Workspace()
+    ops.forward(spec, arena, shared, slot_of, xin, ws_g, out=out, idx=idx, weights=wts)   # sizes the workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.forward(spec, arena, shared, slot_of, xin, ws_g, out=out, idx=idx, weights=wts)
+    for r, x in enumerate((xa, xb, xa)):
+        xin.copy_(x)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        ref = ref_a if r % 2 == 0 else ref_b
+        assert torch.equal(out, ref[0]) and torch.equal(idx, ref[1]) and torch.equal(wts, ref[2]), f"replay {r}"
+        e_out = ops.forward(spec, arena, shared, slot_of, xb if r % 2 == 0 else xa, ws)[0]   # eager work between
+        torch.cuda.synchronize()
+        assert torch.equal(e_out, (ref_b if r % 2 == 0 else ref_a)[0]), f"eager call after replay {r}"
+
+
 def test_prefill_full_width_long_call(oracle_lib):
     """2048 tokens (a long prompt), Zipf(1.1) routing, 2-bit g64 bf16: tile
     lists of thousands of tiles (experts of hundreds of positions, several
