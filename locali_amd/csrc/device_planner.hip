@@ -871,6 +871,15 @@ int plan_launch(bool fused, void *state, int32_t key_capacity, int32_t slots, in
     // LDS allowance (gfx950: 160 KiB); requested once per kernel, and only by
     // a state that needs it, so that small states run wherever 64 KiB do.
     if (lds + (kPlanMaxLds - kPlanMaxDynamicLds) > kDefaultLds) {
+        // the device's own per-workgroup limit first: on a part with less LDS
+        // than gfx950's the call fails here with the figures, not at launch
+        int dev = 0, optin = 0;
+        hipError_t qe = hipGetDevice(&dev);
+        if (qe == hipSuccess) qe = hipDeviceGetAttribute(&optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
+        if (qe != hipSuccess) return dhip(qe, "dplan_plan LDS limit query");
+        if (lds + (kPlanMaxLds - kPlanMaxDynamicLds) > static_cast<size_t>(optin))
+            return dfail(LOCALI_E_ARG, "dplan_plan: %d slots need %zu bytes of LDS; this device allows %d per workgroup",
+                         slots, lds + (kPlanMaxLds - kPlanMaxDynamicLds), optin);
         static const hipError_t attr0 = hipFuncSetAttribute(reinterpret_cast<const void *>(&dplan_kernel<false>),
                                                             hipFuncAttributeMaxDynamicSharedMemorySize,
                                                             static_cast<int>(kPlanMaxDynamicLds));
