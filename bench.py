@@ -688,7 +688,7 @@ def summarize_trace(trace_csv, phases_json):
     bounds = [(name, t0, marks[i + 1][1] if i + 1 < len(marks) else float("inf"))
               for i, (name, t0) in enumerate(marks)]
     per = {name: {} for name, _, _ in bounds}
-    spans = {name: {"copy": [], "all": []} for name, _, _ in bounds}
+    spans = {name: {"copy": [], "all": [], "wide": [], "small": [], "combine": 0} for name, _, _ in bounds}
     unassigned = 0
     for r in csv.DictReader(open(trace_csv)):
         t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
@@ -700,6 +700,12 @@ def summarize_trace(trace_csv, phases_json):
                     spans[ph]["all"].append((t0, t1))
                     if "fill_kernel" in name or "dplan_kernel<true>" in name:
                         spans[ph]["copy"].append((t0, t1))
+                    if "wide_" in name:
+                        spans[ph]["wide"].append((t0, t1))
+                    elif "_small" in name:
+                        spans[ph]["small"].append((t0, t1))
+                    elif "combine8" in name:
+                        spans[ph]["combine"] += 1
                 break
         else:
             unassigned += 1
@@ -729,6 +735,16 @@ def summarize_trace(trace_csv, phases_json):
             out += [f"Library kernels span {span / 1e6:.2f} ms: a host-to-HBM copy launch runs {cu / 1e6:.2f} ms "
                     f"({100 * cu / span:.1f} %), some library kernel {au / 1e6:.2f} ms ({100 * au / span:.1f} %); "
                     f"no copy launch runs for {(span - cu) / 1e6:.2f} ms ({100 * (span - cu) / span:.1f} %).", ""]
+        if iv["wide"] and iv["small"] and iv["combine"]:
+            # grouped calls (one combine each): kernel time against the time
+            # some library kernel runs, and the time a 64-position and a
+            # small-tile kernel run together (the second stream's overlap)
+            n = iv["combine"]
+            both = union(iv["wide"]) + union(iv["small"]) - union(iv["wide"] + iv["small"])
+            ksum = sum(b - a for a, b in iv["all"])
+            out += [f"Grouped calls: {n}; library kernel time {ksum / n / 1e3:.1f} us per call, some library kernel "
+                    f"running {union(iv['all']) / n / 1e3:.1f} us per call, a 64-position and a small-tile kernel "
+                    f"running together {both / n / 1e3:.1f} us per call.", ""]
         out += ["| kernel | calls | avg us | min us | max us | share of phase kernel time |",
                 "|---|---:|---:|---:|---:|---:|"]
         for name, v in sorted(ks.items(), key=lambda kv: -sum(kv[1])):
