@@ -4,12 +4,18 @@
  * All pointers are device pointers unless stated otherwise; `stream` is a
  * hipStream_t passed as void* (NULL = the default stream). Every entry point
  * validates shapes on the host, launches asynchronously, never synchronises
- * and never allocates; scratch memory comes from a caller-owned workspace
+ * and never allocates device memory; scratch memory comes from a caller-owned workspace
  * whose size locali_moe_workspace_bytes() reports and which must be
  * zero-filled once before first use (the library leaves its counters at zero
  * after every call). Return value: 0 on success, a negative LOCALI_E_* code
  * otherwise; locali_moe_last_error() describes the last failure on the
- * calling thread. A call with tokens == 0 is an empty batch: it returns 0
+ * calling thread. Grouped calls (locali_moe_forward, locali_moe_expert_grouped)
+ * of 256 tokens or more run their small-tile kernels on a second stream of
+ * the library's beside `stream`, forked from and joined back into `stream`
+ * by events, so the call stays ordered on `stream` and can be captured into
+ * a graph; that stream and its four events are created once per host thread
+ * and device, on the first such call made outside stream capture
+ * (locali_moe_forward_noalloc never creates them and keeps one stream). A call with tokens == 0 is an empty batch: it returns 0
  * and touches nothing (the reference returns an empty output).
  *
  * What each entry point replaces in the reference (MLX) implementation:
