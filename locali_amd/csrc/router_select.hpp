@@ -208,6 +208,15 @@ constexpr uint32_t kSyncMaxSpins = 1u << 18;
 template <int M>
 __device__ __forceinline__ bool poll_logits(const uint64_t *row, int E, uint32_t tag, float (&lg)[M]) {
     const int lane = threadIdx.x & 63;
+    // while the logits are still being computed, poll one word (the row's
+    // last expert; every lane reads the same address: one request a wave)
+    // instead of the whole row, so that hundreds of polling waves do not
+    // load the memory path the router rows' stores and weights take
+    for (uint32_t spin = 0; spin < kSyncMaxSpins; ++spin) {
+        const uint64_t w = __hip_atomic_load(row + (E - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (static_cast<uint32_t>(w >> 32) == tag) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
     for (uint32_t spin = 0;; ++spin) {
         bool ok = true;
 #pragma unroll
