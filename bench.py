@@ -650,8 +650,12 @@ def summarize_pmc(fetch_csv, write_csv, out_path=TRAFFIC_FILE):
 
     def per_kernel(path, counter, ref_name):
         rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+        # the reference launches are the run's only ones of this name that
+        # count at least a quarter of COPY_BYTES (other fills and
+        # reductions of the run are far smaller)
         refs = [float(r["Counter_Value"]) for r in rows
-                if ref_name in r["Kernel_Name"] and int(r["Grid_Size"]) >= 1 << 16]
+                if ref_name in r["Kernel_Name"] and int(r["Grid_Size"]) >= 1 << 16
+                and float(r["Counter_Value"]) >= COPY_BYTES / 1024 / 4]
         target = [float(r["Counter_Value"]) for r in rows if GATEUP_KERNEL in r["Kernel_Name"]]
         if not refs or not target:
             raise SystemExit(f"{path}: no {counter} rows for {ref_name} and/or {GATEUP_KERNEL}")
